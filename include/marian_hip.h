@@ -1,0 +1,230 @@
+/*
+ * marian_hip.h — C ABI of the MI355X (gfx950) Q8 greedy translation backend.
+ *
+ * The ABI sits at the reference's token-level engine boundary, below its
+ * text adapter.  Reference interfaces each entry point replaces (paths relative
+ * to the marian-edge checkout):
+ *
+ *   marian_hip_engine_create   Q8CpuEngine::load / load_owned
+ *                              crates/marian-cpu/src/q8_engine.rs:162-174, 828-877
+ *                              (the caller hands over parsed, already-quantized
+ *                              weights; the engine copies them to HBM)
+ *   marian_hip_translate_token_ids
+ *                              Q8CpuEngine::translate_token_ids
+ *                              crates/marian-cpu/src/q8_engine.rs:353-466, and the
+ *                              CpuTokenEngine trait crates/marian-cpu/src/backend.rs:48-57;
+ *                              output = BatchOutput crates/marian-cpu/src/engine.rs:80-85
+ *   marian_hip_is_ready        TranslationBackend::is_ready
+ *                              crates/marian-core/src/backend.rs:16-18
+ *   marian_hip_info            TranslationBackend::info / BackendInfo
+ *                              crates/marian-core/src/backend.rs:8, types.rs:49-58
+ *   marian_hip_last_error      BackendError message (types.rs:60-70); the wasm
+ *                              ABI's error slot (marian-worker-wasm/src/lib.rs:381-389)
+ *   marian_hip_engine_destroy  Drop of the engine on its owner thread
+ *                              (crates/marian-core/src/backend.rs:3-6)
+ *
+ * Op-level entry points (device pointers, caller's stream) replace the
+ * reference's building blocks and exist so each kernel can be checked and timed
+ * on its own:
+ *   marian_hip_quantize_rows   quantize_symmetric_u8_into q8_gemm.rs:569-590
+ *   marian_hip_q8_linear       Q8Linear::run_into q8_gemm.rs:380-448 (+ the
+ *                              exact kernel q8_avx2.rs:125-229)
+ *   marian_hip_residual_layer_norm  residual_layer_norm_into tensor.rs:132-155
+ *   marian_hip_attention       attention_into tensor.rs:251-318
+ *   marian_hip_vocab_argmax    select_token q8_engine.rs:749-790
+ *   marian_hip_positions       sinusoidal_positions crates/marian-model/src/position.rs:5-21
+ *
+ * Threading: one engine handle belongs to one owner thread (the reference
+ * backend is deliberately !Send, backend.rs:3-6).  The engine owns one HIP
+ * stream.  Nothing here locks.
+ *
+ * Status codes: 0 success; negative values below.  Invalid input and
+ * output-buffer errors do not affect readiness; a HIP runtime error makes the
+ * engine permanently not ready (like the Metal backend's poisoning,
+ * crates/marian-metal/src/engine.rs:113-125).
+ */
+#ifndef MARIAN_HIP_H
+#define MARIAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MARIAN_HIP_ABI_VERSION 1
+
+enum {
+  MARIAN_HIP_OK = 0,
+  MARIAN_HIP_ERR_INVALID_INPUT = -1, /* BackendError::InvalidInput */
+  MARIAN_HIP_ERR_MODEL = -2,         /* BackendError::Model */
+  MARIAN_HIP_ERR_INFERENCE = -3,     /* BackendError::Inference (e.g. non-finite activation) */
+  MARIAN_HIP_ERR_DEVICE = -4,        /* HIP runtime failure; engine becomes not ready */
+  MARIAN_HIP_ERR_BUFFER = -5,        /* caller's output buffer too small */
+  MARIAN_HIP_ERR_NOT_READY = -6      /* engine was poisoned by an earlier device error */
+};
+
+/* Translate flags. */
+enum {
+  MARIAN_HIP_FLAG_IGNORE_EOS = 1u << 0,         /* token 0 does not finish a row */
+  MARIAN_HIP_FLAG_NO_GENERATION_MASK = 1u << 1  /* also score ids 1 and 7..38
+                                                   (shortlist.rs:169-176 masks them) */
+};
+
+/* One Q8 dense layer.  weight is [out, in] int8, input-contiguous (the
+ * reference's canonical layout, legacy_q8.rs:82-89); mult[n] is the
+ * per-output-channel multiplier with real_w = q / mult (legacy_q8.rs:466-495
+ * uses one multiplier per tensor); bias is fp32 [out]. */
+typedef struct {
+  const int8_t* weight;
+  const float* mult;
+  const float* bias;
+} marian_hip_linear;
+
+typedef struct {
+  marian_hip_linear qkv; /* [3d, d] rows Q, K, V (q8_engine.rs:528-530 as one GEMM) */
+  marian_hip_linear out; /* [d, d] */
+  const float* ln1_scale;
+  const float* ln1_bias;
+  marian_hip_linear ffn1; /* [F, d], ReLU */
+  marian_hip_linear ffn2; /* [d, F] */
+  const float* ln2_scale;
+  const float* ln2_bias;
+} marian_hip_encoder_layer;
+
+typedef struct {
+  marian_hip_linear self_qkv; /* [3d, d] */
+  marian_hip_linear self_out; /* [d, d] */
+  const float* ln1_scale;
+  const float* ln1_bias;
+  marian_hip_linear cross_q;   /* [d, d] (q8_engine.rs:410) */
+  marian_hip_linear cross_kv;  /* [2d, d] on the encoder output (q8_engine.rs:560-567) */
+  marian_hip_linear cross_out; /* [d, d] */
+  const float* ln2_scale;
+  const float* ln2_bias;
+  marian_hip_linear ffn1;
+  marian_hip_linear ffn2;
+  const float* ln3_scale;
+  const float* ln3_bias;
+} marian_hip_decoder_layer;
+
+/* Host-side model description; every pointer is host memory owned by the
+ * caller and only read during marian_hip_engine_create. */
+typedef struct {
+  uint32_t vocab, dim, heads, ffn_dim, encoder_layers, decoder_layers;
+  const int8_t* embedding;     /* [vocab, dim]: source and target embedding and
+                                  the tied output projection */
+  const float* embedding_mult; /* [vocab] per-row multiplier */
+  const float* output_bias;    /* [vocab] */
+  const marian_hip_encoder_layer* encoder;
+  const marian_hip_decoder_layer* decoder;
+} marian_hip_model;
+
+/* Work limits (crates/marian-cpu/src/limits.rs:3-7 and q8_engine.rs:369-379).
+ * 0 disables a cap.  Reference values: factor 2, steps 256, position 4096,
+ * batch 256, source tokens 256, padded cells 65536. */
+typedef struct {
+  uint32_t max_length_factor;
+  uint32_t max_generation_steps;
+  uint32_t max_position; /* must be <= 4096 (the position table) */
+  uint32_t max_batch;
+  uint32_t max_source_tokens;
+  uint64_t max_padded_cells;
+} marian_hip_limits;
+
+typedef struct marian_hip_engine marian_hip_engine;
+
+/* Copies the model to device `device` and builds the position table. */
+int marian_hip_engine_create(const marian_hip_model* model, const marian_hip_limits* limits,
+                             int device, marian_hip_engine** out_engine);
+void marian_hip_engine_destroy(marian_hip_engine* engine);
+
+/* Greedy translation of a packed batch.
+ *   tokens[n_tokens]: source ids; offsets[n_offsets]: cu_seqlens with
+ *   offsets[0] = 0, offsets[B] = n_tokens, every row >= 1 token;
+ *   max_output_tokens[B]: requested budget per row.
+ * Outputs (host memory): out_tokens (capacity out_cap) receives the generated
+ * ids of every row back to back, including a final EOS 0 when one is emitted;
+ * out_offsets[B+1] the row boundaries; *out_len the total.  On
+ * MARIAN_HIP_ERR_BUFFER, *out_len holds the capacity needed.  The bound
+ * sum_b min(max_output_tokens[b], caps) is always enough. */
+int marian_hip_translate_token_ids(marian_hip_engine* engine, const int32_t* tokens,
+                                   size_t n_tokens, const uint32_t* offsets, size_t n_offsets,
+                                   const uint32_t* max_output_tokens, uint32_t flags,
+                                   int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                                   size_t* out_len);
+
+int marian_hip_is_ready(const marian_hip_engine* engine);
+/* Last error message of this engine ("" if none); valid until the next call. */
+const char* marian_hip_last_error(const marian_hip_engine* engine);
+/* BackendInfo fields, e.g. name "hip", device "AMD Instinct MI355X (gfx950)",
+ * precision "q8". Writes a NUL-terminated JSON object into buf. */
+int marian_hip_info(const marian_hip_engine* engine, char* buf, size_t cap);
+
+/* Timing of the last translate call, in milliseconds (events on the engine's
+ * stream): total (upload to host-visible tokens), encoder, decode loop, the
+ * summed device time of the vocabulary projection + argmax kernel and the
+ * number of its launches, and the number of decode steps run. */
+typedef struct {
+  double total_ms, encoder_ms, decode_ms;
+  double vocab_kernel_ms;
+  uint32_t vocab_kernel_launches;
+  uint32_t decode_steps;
+  uint32_t max_active_rows;
+  uint64_t generated_tokens;
+} marian_hip_stats;
+int marian_hip_last_stats(const marian_hip_engine* engine, marian_hip_stats* stats);
+/* When enabled, the engine records events around each vocab kernel launch so
+ * marian_hip_stats.vocab_kernel_ms is filled (small overhead). */
+int marian_hip_set_kernel_timing(marian_hip_engine* engine, int enabled);
+
+/* ---- op-level entry points: device pointers, `stream` is a hipStream_t or
+ * NULL for the default stream.  They return MARIAN_HIP_ERR_INVALID_INPUT for
+ * shapes the kernels do not support. ------------------------------------- */
+
+/* q[m,:] = clamp(rne(x[m,:]*a[m]), -127, 127), a[m] = 127/max|x[m,:]| (1 for
+ * an all-zero row).  err (device int, may be NULL) is set to 1 when a
+ * non-finite value is seen. */
+int marian_hip_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, float* a,
+                             int* err, void* stream);
+
+/* y = (x quantized per row) @ W^T dequantized + bias (+ReLU).
+ * x fp32 [M,K] (NULL when xq/xa are given pre-quantized), W int8 [N,K],
+ * out_i32 [M,N] optional (exact accumulators), out_f32 [M,N] optional.
+ * K must be a multiple of 64. */
+int marian_hip_q8_linear(const float* x, const int8_t* xq, const float* xa, int64_t M,
+                         int64_t K, const int8_t* w, const float* w_mult, const float* bias,
+                         int64_t N, int relu, int32_t* out_i32, float* out_f32, int* err,
+                         void* stream);
+
+/* out = LN(x + r) (eps 1e-6), optional int8 quantization of out (q, a). */
+int marian_hip_residual_layer_norm(const float* x, const float* r, const float* scale,
+                                   const float* bias, int64_t rows, int64_t dim, float* out,
+                                   int8_t* q, float* a, int* err, void* stream);
+
+/* Variable-length attention, one query row per (row, head) wave:
+ * query row i belongs to sequence seq_of_row[i] and attends over key rows
+ * [cu_k[s], cu_k[s+1]); max_keys bounds every range (at most 4096).
+ * Row strides in elements.  in_bf16 != 0 reads q/k/v as
+ * bfloat16 (converted exactly to fp32); out is fp32 [rows, heads*64]. */
+int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
+                         const int32_t* seq_of_row, const uint32_t* cu_k, int64_t rows,
+                         int64_t heads, int64_t max_keys, int in_bf16, float* out, int64_t ldo,
+                         void* stream);
+
+/* Vocabulary projection + bias + generation mask + argmax per row:
+ * token[m] = argmax_v (acc[m,v] * (1/(xa[m]*mult[v])) + bias[v]) with ties to
+ * the lowest id; logits [M,V] optional.  xq/xa are the quantized rows. */
+int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                            const int8_t* emb, const float* emb_mult, const float* bias,
+                            int64_t V, uint32_t flags, int32_t* token, float* logits,
+                            void* stream);
+
+/* Host: sinusoidal position table [count, dim] (fp32), as the engine builds it. */
+int marian_hip_positions(uint32_t dim, uint32_t count, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,731 @@
+// engine.hip — the marian-hip engine: device-resident Q8 weights, a packed
+// (padding-free) encoder, and a greedy decode loop whose active set is
+// compacted on the device every step.
+//
+// Reference behaviour restated here: Q8CpuEngine::translate_token_ids
+// (crates/marian-cpu/src/q8_engine.rs:353-466) with validate_batch (:468-509)
+// and validate_work_shape (:1103-1119).  Differences in execution (not in
+// results): sequences are packed by cu_seqlens instead of padded to the longest
+// one, finished rows leave the active set instead of being recomputed, and the
+// per-step token selection runs on the device.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/marian_hip.h"
+#include "device_common.h"
+#include "kernels.h"
+
+using namespace mh;
+
+namespace {
+
+struct Lin {
+  const int8_t* w = nullptr;
+  const float* mult = nullptr;
+  const float* bias = nullptr;
+  int N = 0, K = 0;
+};
+struct EncLayer {
+  Lin qkv, out, ffn1, ffn2;
+  const float *ln1_s, *ln1_b, *ln2_s, *ln2_b;
+};
+struct DecLayer {
+  Lin self_qkv, self_out, cross_q, cross_kv, cross_out, ffn1, ffn2;
+  const float *ln1_s, *ln1_b, *ln2_s, *ln2_b, *ln3_s, *ln3_b;
+};
+
+// Grow-only device buffers reused across calls (the reference pools its
+// scratch too, q8_engine.rs:733-747).
+enum Buf {
+  B_META, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
+  B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DOQ, B_DOA, B_DY, B_DH, B_DHQ, B_DHA,
+  B_PART, B_OUT, B_COUNT, B_COUNT_
+};
+
+uint32_t host_positions(uint32_t dim, uint32_t count, float* out) {
+  if (dim < 4 || dim % 2) return 1;
+  const uint32_t half = dim / 2;
+  volatile float ten_thousand = 10000.0f;  // evaluated by libm at run time
+  const float ln10k = std::log((float)ten_thousand);
+  for (uint32_t p = 0; p < count; ++p)
+    for (uint32_t i = 0; i < half; ++i) {
+      const float f = std::exp(-(float)i * ln10k / (float)(half - 1));
+      const float arg = (float)p * f;
+      out[(size_t)p * dim + i] = std::sin(arg);
+      out[(size_t)p * dim + half + i] = std::cos(arg);
+    }
+  return 0;
+}
+
+}  // namespace
+
+struct marian_hip_engine {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint32_t V = 0, d = 0, H = 0, F = 0, Le = 0, Ld = 0;
+  float emb_scale = 1.0f;
+  marian_hip_limits limits{};
+  bool ready = true;
+  bool kernel_timing = false;
+  std::string error;
+  std::string device_name;
+
+  void* weights = nullptr;
+  Lin emb;
+  std::vector<EncLayer> enc;
+  std::vector<DecLayer> dec;
+  float* pos = nullptr;
+
+  void* buf[B_COUNT_] = {};
+  size_t cap[B_COUNT_] = {};
+  int* err_flag = nullptr;
+  int* pinned = nullptr;  // host-visible n_active polls
+  hipEvent_t ev[5] = {};  // start, encoder end, decode end, two poll slots
+  std::vector<hipEvent_t> vocab_ev;
+  marian_hip_stats stats{};
+
+  int fail(int code, const char* fmt, ...) {
+    char msg[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+    error = msg;
+    if (code == MARIAN_HIP_ERR_DEVICE) ready = false;
+    return code;
+  }
+  int hip_fail(hipError_t e, const char* what) {
+    return fail(MARIAN_HIP_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+  }
+  // Returns nullptr on failure (error recorded).
+  void* get(Buf b, size_t bytes) {
+    bytes = std::max<size_t>(bytes, 256);
+    if (cap[b] >= bytes) return buf[b];
+    if (buf[b]) {
+      hipStreamSynchronize(stream);
+      hipFree(buf[b]);
+      buf[b] = nullptr;
+      cap[b] = 0;
+    }
+    const size_t want = bytes + bytes / 4;
+    if (hipMalloc(&buf[b], want) != hipSuccess) {
+      buf[b] = nullptr;
+      return nullptr;
+    }
+    cap[b] = want;
+    return buf[b];
+  }
+};
+
+#define MH_HIP(expr)                                   \
+  do {                                                 \
+    hipError_t e_ = (expr);                            \
+    if (e_ != hipSuccess) return E->hip_fail(e_, #expr); \
+  } while (0)
+
+extern "C" {
+
+int marian_hip_positions(uint32_t dim, uint32_t count, float* out) {
+  if (!out || host_positions(dim, count, out)) return MARIAN_HIP_ERR_INVALID_INPUT;
+  return MARIAN_HIP_OK;
+}
+
+int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits* limits,
+                             int device, marian_hip_engine** out_engine) {
+  if (!m || !out_engine) return MARIAN_HIP_ERR_INVALID_INPUT;
+  *out_engine = nullptr;
+  if (!m->embedding || !m->embedding_mult || !m->output_bias || !m->vocab || !m->heads ||
+      m->dim != m->heads * kHeadDim || m->dim % 64 || m->dim > 1024 || m->ffn_dim % 64 ||
+      (m->encoder_layers && !m->encoder) || (m->decoder_layers && !m->decoder) ||
+      m->heads > 16)
+    return MARIAN_HIP_ERR_MODEL;
+  auto* E = new marian_hip_engine();
+  E->device = device;
+  E->V = m->vocab;
+  E->d = m->dim;
+  E->H = m->heads;
+  E->F = m->ffn_dim;
+  E->Le = m->encoder_layers;
+  E->Ld = m->decoder_layers;
+  E->emb_scale = std::sqrt((float)m->dim);
+  if (limits) {
+    E->limits = *limits;
+  } else {
+    E->limits = marian_hip_limits{2, 256, 4096, 256, 256, 65536};
+  }
+  if (E->limits.max_position > (uint32_t)kMaxPosition || E->limits.max_position == 0)
+    E->limits.max_position = kMaxPosition;
+
+  auto cleanup_fail = [&](int code) {
+    marian_hip_engine_destroy(E);
+    return code;
+  };
+  if (hipSetDevice(device) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess)
+    E->device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+
+  // Pack every tensor into one host staging buffer (256-byte aligned pieces),
+  // then copy to HBM once.
+  std::vector<char> host;
+  struct Fix {
+    size_t off;
+    const void** dst;
+  };
+  std::vector<Fix> fixes;
+  auto add = [&](const void* src, size_t bytes, const void** dst) {
+    size_t off = (host.size() + 255) & ~size_t(255);
+    host.resize(off + bytes);
+    std::memcpy(host.data() + off, src, bytes);
+    fixes.push_back({off, dst});
+  };
+  auto add_lin = [&](const marian_hip_linear& l, int N, int K, Lin& out) -> bool {
+    if (!l.weight || !l.mult || !l.bias) return false;
+    out.N = N;
+    out.K = K;
+    add(l.weight, (size_t)N * K, (const void**)&out.w);
+    add(l.mult, (size_t)N * 4, (const void**)&out.mult);
+    add(l.bias, (size_t)N * 4, (const void**)&out.bias);
+    return true;
+  };
+  auto add_vec = [&](const float* v, size_t n, const float** dst) -> bool {
+    if (!v) return false;
+    add(v, n * 4, (const void**)dst);
+    return true;
+  };
+  const int d = (int)E->d, F = (int)E->F, V = (int)E->V;
+  bool ok = true;
+  E->emb.N = V;
+  E->emb.K = d;
+  add(m->embedding, (size_t)V * d, (const void**)&E->emb.w);
+  add(m->embedding_mult, (size_t)V * 4, (const void**)&E->emb.mult);
+  add(m->output_bias, (size_t)V * 4, (const void**)&E->emb.bias);
+  E->enc.resize(E->Le);
+  E->dec.resize(E->Ld);
+  for (uint32_t l = 0; l < E->Le; ++l) {
+    const marian_hip_encoder_layer& s = m->encoder[l];
+    EncLayer& t = E->enc[l];
+    ok = ok && add_lin(s.qkv, 3 * d, d, t.qkv) && add_lin(s.out, d, d, t.out) &&
+         add_lin(s.ffn1, F, d, t.ffn1) && add_lin(s.ffn2, d, F, t.ffn2) &&
+         add_vec(s.ln1_scale, d, &t.ln1_s) && add_vec(s.ln1_bias, d, &t.ln1_b) &&
+         add_vec(s.ln2_scale, d, &t.ln2_s) && add_vec(s.ln2_bias, d, &t.ln2_b);
+  }
+  for (uint32_t l = 0; l < E->Ld; ++l) {
+    const marian_hip_decoder_layer& s = m->decoder[l];
+    DecLayer& t = E->dec[l];
+    ok = ok && add_lin(s.self_qkv, 3 * d, d, t.self_qkv) &&
+         add_lin(s.self_out, d, d, t.self_out) && add_lin(s.cross_q, d, d, t.cross_q) &&
+         add_lin(s.cross_kv, 2 * d, d, t.cross_kv) && add_lin(s.cross_out, d, d, t.cross_out) &&
+         add_lin(s.ffn1, F, d, t.ffn1) && add_lin(s.ffn2, d, F, t.ffn2) &&
+         add_vec(s.ln1_scale, d, &t.ln1_s) && add_vec(s.ln1_bias, d, &t.ln1_b) &&
+         add_vec(s.ln2_scale, d, &t.ln2_s) && add_vec(s.ln2_bias, d, &t.ln2_b) &&
+         add_vec(s.ln3_scale, d, &t.ln3_s) && add_vec(s.ln3_bias, d, &t.ln3_b);
+  }
+  if (!ok) return cleanup_fail(MARIAN_HIP_ERR_MODEL);
+  // Every weight multiplier must be finite and positive, and no weight -128
+  // (q8_gemm.rs:96-101 rejects both).
+  {
+    const float* em = m->embedding_mult;
+    for (int v = 0; v < V; ++v)
+      if (!(std::isfinite(em[v]) && em[v] > 0.0f)) return cleanup_fail(MARIAN_HIP_ERR_MODEL);
+  }
+  std::vector<float> posv((size_t)kMaxPosition * d);
+  host_positions(E->d, kMaxPosition, posv.data());
+  add(posv.data(), posv.size() * 4, (const void**)&E->pos);
+
+  if (hipMalloc(&E->weights, host.size()) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  if (hipMemcpy(E->weights, host.data(), host.size(), hipMemcpyHostToDevice) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  for (const Fix& f : fixes) *f.dst = (const char*)E->weights + f.off;
+
+  if (hipMalloc(&E->err_flag, sizeof(int)) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  if (hipHostMalloc((void**)&E->pinned, 64 * sizeof(int)) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  for (auto& ev : E->ev)
+    if (hipEventCreate(&ev) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  *out_engine = E;
+  return MARIAN_HIP_OK;
+}
+
+void marian_hip_engine_destroy(marian_hip_engine* E) {
+  if (!E) return;
+  hipSetDevice(E->device);
+  if (E->stream) hipStreamSynchronize(E->stream);
+  for (int b = 0; b < B_COUNT_; ++b)
+    if (E->buf[b]) hipFree(E->buf[b]);
+  if (E->weights) hipFree(E->weights);
+  if (E->err_flag) hipFree(E->err_flag);
+  if (E->pinned) hipHostFree(E->pinned);
+  for (auto& ev : E->ev)
+    if (ev) hipEventDestroy(ev);
+  for (auto& ev : E->vocab_ev) hipEventDestroy(ev);
+  if (E->stream) hipStreamDestroy(E->stream);
+  delete E;
+}
+
+int marian_hip_is_ready(const marian_hip_engine* E) { return E && E->ready ? 1 : 0; }
+
+const char* marian_hip_last_error(const marian_hip_engine* E) {
+  return E ? E->error.c_str() : "null engine";
+}
+
+int marian_hip_info(const marian_hip_engine* E, char* buf, size_t cap) {
+  if (!E || !buf || !cap) return MARIAN_HIP_ERR_INVALID_INPUT;
+  const int n = snprintf(buf, cap,
+                         "{\"name\":\"hip\",\"device\":\"%s\",\"model\":\"transformer-q8 d=%u "
+                         "heads=%u ffn=%u enc=%u dec=%u vocab=%u\",\"precision\":\"q8\","
+                         "\"attention\":\"varlen-fused\",\"supports_batching\":true}",
+                         E->device_name.c_str(), E->d, E->H, E->F, E->Le, E->Ld, E->V);
+  return (n < 0 || (size_t)n >= cap) ? MARIAN_HIP_ERR_BUFFER : MARIAN_HIP_OK;
+}
+
+int marian_hip_last_stats(const marian_hip_engine* E, marian_hip_stats* s) {
+  if (!E || !s) return MARIAN_HIP_ERR_INVALID_INPUT;
+  *s = E->stats;
+  return MARIAN_HIP_OK;
+}
+
+int marian_hip_set_kernel_timing(marian_hip_engine* E, int enabled) {
+  if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
+  E->kernel_timing = enabled != 0;
+  return MARIAN_HIP_OK;
+}
+
+int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
+                                   const uint32_t* offsets, size_t n_offsets,
+                                   const uint32_t* max_output_tokens, uint32_t flags,
+                                   int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                                   size_t* out_len) {
+  if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
+  E->error.clear();
+  if (!E->ready) return E->fail(MARIAN_HIP_ERR_NOT_READY, "engine is not ready after a device error");
+  if (!offsets || !max_output_tokens || !out_offsets || (n_tokens && !tokens))
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "null input pointer");
+  // ---- validation (q8_engine.rs:468-509, 1103-1119) ----
+  if (n_offsets < 2 || offsets[0] != 0 || offsets[n_offsets - 1] != n_tokens)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "invalid packed batch offsets");
+  const size_t B = n_offsets - 1;
+  const marian_hip_limits& lim = E->limits;
+  if (lim.max_batch && B > lim.max_batch)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "batch contains %zu sentences; maximum is %u", B,
+                   lim.max_batch);
+  if (B > (size_t)kMaxRowsPerCall)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "batch contains %zu sentences; this engine handles %d per call",
+                   B, kMaxRowsPerCall);
+  size_t Lmax = 0;
+  for (size_t b = 0; b < B; ++b) {
+    if (offsets[b + 1] <= offsets[b])
+      return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "each input must contain at least one token");
+    Lmax = std::max<size_t>(Lmax, offsets[b + 1] - offsets[b]);
+  }
+  if (lim.max_source_tokens && Lmax > lim.max_source_tokens)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "source has %zu tokens; maximum is %u", Lmax,
+                   lim.max_source_tokens);
+  if (lim.max_padded_cells && (uint64_t)B * Lmax * Lmax > lim.max_padded_cells)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "padded attention work is %llu cells; maximum is %llu",
+                   (unsigned long long)((uint64_t)B * Lmax * Lmax),
+                   (unsigned long long)lim.max_padded_cells);
+  if (Lmax > (size_t)kMaxPosition)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "source longer than the position table");
+  for (size_t i = 0; i < n_tokens; ++i)
+    if (tokens[i] < 0 || (uint32_t)tokens[i] >= E->V)
+      return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "source token %d is outside vocabulary %u",
+                     tokens[i], E->V);
+
+  const uint32_t maxpos = std::min<uint32_t>(lim.max_position, kMaxPosition);
+  std::vector<uint32_t> limit(B);
+  uint32_t gen_limit = 0;
+  uint64_t total_cap = 0;
+  for (size_t b = 0; b < B; ++b) {
+    uint64_t l = max_output_tokens[b];
+    const uint64_t len = offsets[b + 1] - offsets[b];
+    if (lim.max_length_factor) l = std::min<uint64_t>(l, len * lim.max_length_factor);
+    if (lim.max_generation_steps) l = std::min<uint64_t>(l, lim.max_generation_steps);
+    l = std::min<uint64_t>(l, maxpos);
+    limit[b] = (uint32_t)l;
+    gen_limit = std::max(gen_limit, limit[b]);
+    total_cap += l;
+  }
+
+  hipError_t he = hipSetDevice(E->device);
+  if (he != hipSuccess) return E->hip_fail(he, "hipSetDevice");
+  hipStream_t s = E->stream;
+  const int d = (int)E->d, F = (int)E->F, H = (int)E->H;
+  const int T = (int)n_tokens, Bi = (int)B;
+  E->stats = marian_hip_stats{};
+
+  // ---- host metadata -> one upload ----
+  std::vector<int32_t> positions(T), seq_of_row(T), act0;
+  std::vector<int64_t> kv_base(B);
+  int64_t run = 0;
+  for (size_t b = 0; b < B; ++b) {
+    for (uint32_t i = offsets[b]; i < offsets[b + 1]; ++i) {
+      positions[i] = (int32_t)(i - offsets[b]);
+      seq_of_row[i] = (int32_t)b;
+    }
+    kv_base[b] = run;
+    run += limit[b];
+    if (limit[b] > 0) act0.push_back((int32_t)b);
+  }
+  const int n_active0 = (int)act0.size();
+  act0.resize(B, 0);
+  // layout: tokens | positions | seq_of_row | cu | limit | act | n_active | kv_base
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  size_t o_tok = 0, o_pos = align(o_tok + 4 * (size_t)T), o_seq = align(o_pos + 4 * (size_t)T),
+         o_cu = align(o_seq + 4 * (size_t)T), o_lim = align(o_cu + 4 * (B + 1)),
+         o_act = align(o_lim + 4 * B), o_nact = align(o_act + 4 * B),
+         o_kvb = align(o_nact + 4), o_prev = align(o_kvb + 8 * B), meta_bytes = align(o_prev + 4 * B);
+  std::vector<char> meta(meta_bytes, 0);
+  std::memcpy(meta.data() + o_tok, tokens, 4 * (size_t)T);
+  std::memcpy(meta.data() + o_pos, positions.data(), 4 * (size_t)T);
+  std::memcpy(meta.data() + o_seq, seq_of_row.data(), 4 * (size_t)T);
+  std::memcpy(meta.data() + o_cu, offsets, 4 * (B + 1));
+  std::memcpy(meta.data() + o_lim, limit.data(), 4 * B);
+  std::memcpy(meta.data() + o_act, act0.data(), 4 * B);
+  std::memcpy(meta.data() + o_nact, &n_active0, 4);
+  std::memcpy(meta.data() + o_kvb, kv_base.data(), 8 * B);
+  std::vector<int32_t> prev0(B, -1);
+  std::memcpy(meta.data() + o_prev, prev0.data(), 4 * B);
+
+  const size_t cache_rows = std::max<uint64_t>(total_cap, 1);
+  char* dmeta = (char*)E->get(B_META, meta_bytes);
+  float* X0 = (float*)E->get(B_X0, 4ull * T * d);
+  float* X1 = (float*)E->get(B_X1, 4ull * T * d);
+  int8_t* XQ = (int8_t*)E->get(B_XQ, (size_t)T * d);
+  float* XA = (float*)E->get(B_XA, 4ull * T);
+  float* QKV = (float*)E->get(B_QKV, 12ull * T * d);
+  int8_t* OQ = (int8_t*)E->get(B_OQ, (size_t)T * d);
+  float* OA = (float*)E->get(B_OA, 4ull * T);
+  float* Y = (float*)E->get(B_Y, 4ull * T * d);
+  float* Hb = (float*)E->get(B_H, 4ull * T * F);
+  int8_t* HQ = (int8_t*)E->get(B_HQ, (size_t)T * F);
+  float* HA = (float*)E->get(B_HA, 4ull * T);
+  float* CKV = (float*)E->get(B_CKV, 8ull * T * d * std::max<uint32_t>(E->Ld, 1));
+  float* KC = (float*)E->get(B_KC, 4ull * cache_rows * d * std::max<uint32_t>(E->Ld, 1));
+  float* VC = (float*)E->get(B_VC, 4ull * cache_rows * d * std::max<uint32_t>(E->Ld, 1));
+  float* DX0 = (float*)E->get(B_DX0, 4ull * B * d);
+  float* DX1 = (float*)E->get(B_DX1, 4ull * B * d);
+  int8_t* DXQ = (int8_t*)E->get(B_DXQ, B * d);
+  float* DXA = (float*)E->get(B_DXA, 4ull * B);
+  float* DQ = (float*)E->get(B_DQ, 4ull * B * d);
+  int8_t* DOQ = (int8_t*)E->get(B_DOQ, B * d);
+  float* DOA = (float*)E->get(B_DOA, 4ull * B);
+  float* DY = (float*)E->get(B_DY, 4ull * B * d);
+  float* DH = (float*)E->get(B_DH, 4ull * B * F);
+  int8_t* DHQ = (int8_t*)E->get(B_DHQ, B * F);
+  float* DHA = (float*)E->get(B_DHA, 4ull * B);
+  const int nparts = skinny_groups((int)E->V);
+  uint64_t* PART = (uint64_t*)E->get(B_PART, 8ull * B * nparts);
+  int32_t* OUT = (int32_t*)E->get(B_OUT, 4ull * cache_rows);
+  uint32_t* COUNT = (uint32_t*)E->get(B_COUNT, 4ull * B);
+  for (int b = 0; b < B_COUNT_; ++b)
+    if (!E->buf[b]) return E->fail(MARIAN_HIP_ERR_DEVICE, "device allocation failed");
+
+  int32_t* d_tok = (int32_t*)(dmeta + o_tok);
+  int32_t* d_pos = (int32_t*)(dmeta + o_pos);
+  int32_t* d_seq = (int32_t*)(dmeta + o_seq);
+  uint32_t* d_cu = (uint32_t*)(dmeta + o_cu);
+  uint32_t* d_lim = (uint32_t*)(dmeta + o_lim);
+  int* d_act = (int*)(dmeta + o_act);
+  int* d_nact = (int*)(dmeta + o_nact);
+  int64_t* d_kvb = (int64_t*)(dmeta + o_kvb);
+  int32_t* d_prev = (int32_t*)(dmeta + o_prev);
+
+  MH_HIP(hipEventRecord(E->ev[0], s));
+  MH_HIP(hipMemcpyAsync(dmeta, meta.data(), meta_bytes, hipMemcpyHostToDevice, s));
+  MH_HIP(hipMemsetAsync(E->err_flag, 0, sizeof(int), s));
+  MH_HIP(hipMemsetAsync(COUNT, 0, 4 * B, s));
+
+  // ---- encoder over packed rows ----
+  {
+    EmbedArgs ea;
+    ea.emb = E->emb.w;
+    ea.emb_mult = E->emb.mult;
+    ea.pos = E->pos;
+    ea.scale = E->emb_scale;
+    ea.d = d;
+    ea.tokens = d_tok;
+    ea.positions = d_pos;
+    ea.rows = T;
+    ea.x = X0;
+    ea.xq = XQ;
+    ea.xa = XA;
+    ea.err = E->err_flag;
+    MH_HIP(launch_embed(ea, s));
+  }
+  auto gemm = [&](const int8_t* A, const float* a, int M, const Lin& L, float* out, int relu) {
+    GemmArgs g;
+    g.A = A;
+    g.a = a;
+    g.lda = L.K;
+    g.M = M;
+    g.K = L.K;
+    g.W = L.w;
+    g.wmult = L.mult;
+    g.bias = L.bias;
+    g.N = L.N;
+    Epilogue e;
+    e.out = out;
+    e.ldo = L.N;
+    e.relu = relu;
+    return launch_gemm_store(g, e, s);
+  };
+  for (uint32_t l = 0; l < E->Le; ++l) {
+    const EncLayer& L = E->enc[l];
+    MH_HIP(gemm(XQ, XA, T, L.qkv, QKV, 0));
+    AttnArgs aa;
+    aa.mode = ATT_SEQ;
+    aa.q = QKV;
+    aa.ldq = 3 * d;
+    aa.k = QKV + d;
+    aa.v = QKV + 2 * d;
+    aa.ldkv = 3 * d;
+    aa.heads = H;
+    aa.rows = T;
+    aa.seq_of_row = d_seq;
+    aa.cu = d_cu;
+    aa.max_keys = (int)Lmax;
+    aa.q8 = OQ;
+    aa.qa = OA;
+    aa.err = E->err_flag;
+    MH_HIP(launch_attention(aa, s));
+    MH_HIP(gemm(OQ, OA, T, L.out, Y, 0));
+    MH_HIP(launch_residual_ln(Y, X0, L.ln1_s, L.ln1_b, T, nullptr, d, X1, XQ, XA, E->err_flag, s));
+    MH_HIP(gemm(XQ, XA, T, L.ffn1, Hb, 1));
+    MH_HIP(launch_quantize_rows(Hb, F, T, nullptr, F, HQ, F, HA, E->err_flag, s));
+    MH_HIP(gemm(HQ, HA, T, L.ffn2, Y, 0));
+    MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, XQ, XA, E->err_flag, s));
+  }
+  for (uint32_t l = 0; l < E->Ld; ++l)
+    MH_HIP(gemm(XQ, XA, T, E->dec[l].cross_kv, CKV + (size_t)l * T * 2 * d, 0));
+  MH_HIP(hipEventRecord(E->ev[1], s));
+
+  // ---- greedy decode with device-side active set ----
+  if (E->kernel_timing) {
+    while (E->vocab_ev.size() < 2ull * gen_limit) {
+      hipEvent_t ev;
+      MH_HIP(hipEventCreate(&ev));
+      E->vocab_ev.push_back(ev);
+    }
+  }
+  std::vector<uint32_t> remaining(gen_limit + 1, 0);  // rows with limit > t
+  for (size_t b = 0; b < B; ++b) remaining[0] += limit[b] > 0;
+  {
+    std::vector<uint32_t> ends(gen_limit + 1, 0);
+    for (size_t b = 0; b < B; ++b) ends[limit[b]]++;
+    for (uint32_t t = 1; t <= gen_limit; ++t) remaining[t] = remaining[t - 1] - ends[t];
+  }
+  auto dgemm = [&](const int8_t* A, const float* a, const Lin& L, int mode, const Epilogue& e) {
+    GemmArgs g;
+    g.A = A;
+    g.a = a;
+    g.lda = L.K;
+    g.M = Bi;
+    g.M_dev = d_nact;
+    g.K = L.K;
+    g.W = L.w;
+    g.wmult = L.mult;
+    g.bias = L.bias;
+    g.N = L.N;
+    return launch_gemm_skinny(g, mode, e, s);
+  };
+  auto store_epi = [&](float* out, int ldo, int relu) {
+    Epilogue e;
+    e.out = out;
+    e.ldo = ldo;
+    e.relu = relu;
+    return e;
+  };
+  // Poll the active count every kPoll steps without blocking; stop launching
+  // once it has reached zero (rows can end early on EOS).
+  constexpr uint32_t kPoll = 8;
+  int poll_slot = 0;
+  uint32_t steps = 0;
+  uint32_t vocab_launches = 0;
+  bool done = n_active0 == 0;
+  for (uint32_t t = 0; t < gen_limit && !done; ++t) {
+    const int rows_ub = (int)remaining[t];
+    if (rows_ub == 0) break;
+    {
+      EmbedArgs ea;
+      ea.emb = E->emb.w;
+      ea.emb_mult = E->emb.mult;
+      ea.pos = E->pos;
+      ea.scale = E->emb_scale;
+      ea.d = d;
+      ea.act = d_act;
+      ea.prev = d_prev;
+      ea.step = (int)t;
+      ea.rows = rows_ub;
+      ea.rows_dev = d_nact;
+      ea.x = DX0;
+      ea.xq = DXQ;
+      ea.xa = DXA;
+      ea.err = E->err_flag;
+      MH_HIP(launch_embed(ea, s));
+    }
+    for (uint32_t l = 0; l < E->Ld; ++l) {
+      const DecLayer& L = E->dec[l];
+      float* kc = KC + (size_t)l * cache_rows * d;
+      float* vc = VC + (size_t)l * cache_rows * d;
+      {
+        Epilogue e;
+        e.out = DQ;
+        e.ldo = d;
+        e.kcache = kc;
+        e.vcache = vc;
+        e.act = d_act;
+        e.kv_base = d_kvb;
+        e.step = (int)t;
+        e.d = d;
+        MH_HIP(dgemm(DXQ, DXA, L.self_qkv, EPI_QKV_CACHE, e));
+      }
+      AttnArgs sa;
+      sa.mode = ATT_SELF;
+      sa.q = DQ;
+      sa.ldq = d;
+      sa.k = kc;
+      sa.v = vc;
+      sa.ldkv = d;
+      sa.heads = H;
+      sa.rows = rows_ub;
+      sa.rows_dev = d_nact;
+      sa.act = d_act;
+      sa.kv_base = d_kvb;
+      sa.step = (int)t;
+      sa.max_keys = (int)t + 1;
+      sa.q8 = DOQ;
+      sa.qa = DOA;
+      sa.err = E->err_flag;
+      MH_HIP(launch_attention(sa, s));
+      MH_HIP(dgemm(DOQ, DOA, L.self_out, EPI_STORE, store_epi(DY, d, 0)));
+      MH_HIP(launch_residual_ln(DY, DX0, L.ln1_s, L.ln1_b, rows_ub, d_nact, d, DX1, DXQ, DXA,
+                                E->err_flag, s));
+      MH_HIP(dgemm(DXQ, DXA, L.cross_q, EPI_STORE, store_epi(DQ, d, 0)));
+      AttnArgs ca;
+      ca.mode = ATT_CROSS;
+      ca.q = DQ;
+      ca.ldq = d;
+      ca.k = CKV + (size_t)l * T * 2 * d;
+      ca.v = CKV + (size_t)l * T * 2 * d + d;
+      ca.ldkv = 2 * d;
+      ca.heads = H;
+      ca.rows = rows_ub;
+      ca.rows_dev = d_nact;
+      ca.act = d_act;
+      ca.cu = d_cu;
+      ca.max_keys = (int)Lmax;
+      ca.q8 = DOQ;
+      ca.qa = DOA;
+      ca.err = E->err_flag;
+      MH_HIP(launch_attention(ca, s));
+      MH_HIP(dgemm(DOQ, DOA, L.cross_out, EPI_STORE, store_epi(DY, d, 0)));
+      MH_HIP(launch_residual_ln(DY, DX1, L.ln2_s, L.ln2_b, rows_ub, d_nact, d, DX0, DXQ, DXA,
+                                E->err_flag, s));
+      MH_HIP(dgemm(DXQ, DXA, L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
+      MH_HIP(launch_quantize_rows(DH, F, rows_ub, d_nact, F, DHQ, F, DHA, E->err_flag, s));
+      MH_HIP(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
+      MH_HIP(launch_residual_ln(DY, DX0, L.ln3_s, L.ln3_b, rows_ub, d_nact, d, DX1, DXQ, DXA,
+                                E->err_flag, s));
+      std::swap(DX0, DX1);
+    }
+    {
+      Epilogue e;
+      e.partials = PART;
+      e.partial_ld = nparts;
+      e.flags = flags;
+      const bool timed = E->kernel_timing;
+      if (timed) MH_HIP(hipEventRecord(E->vocab_ev[2 * vocab_launches], s));
+      MH_HIP(dgemm(DXQ, DXA, E->emb, EPI_ARGMAX, e));
+      if (timed) MH_HIP(hipEventRecord(E->vocab_ev[2 * vocab_launches + 1], s));
+      ++vocab_launches;
+    }
+    {
+      FinalizeArgs f;
+      f.partials = PART;
+      f.nparts = nparts;
+      f.act = d_act;
+      f.n_active = d_nact;
+      f.prev = d_prev;
+      f.limit = d_lim;
+      f.out_tok = OUT;
+      f.out_base = d_kvb;
+      f.count = COUNT;
+      f.step = (int)t;
+      f.flags = flags;
+      MH_HIP(launch_finalize(f, s));
+    }
+    ++steps;
+    if ((t + 1) % kPoll == 0) {
+      // issue a new poll, then look at the previous one if it has landed
+      MH_HIP(hipMemcpyAsync(E->pinned + poll_slot, d_nact, sizeof(int), hipMemcpyDeviceToHost, s));
+      MH_HIP(hipEventRecord(E->ev[3 + poll_slot], s));
+      const int other = poll_slot ^ 1;
+      if (t + 1 >= 2 * kPoll && hipEventQuery(E->ev[3 + other]) == hipSuccess &&
+          E->pinned[other] == 0)
+        done = true;
+      poll_slot = other;
+    }
+  }
+  MH_HIP(hipEventRecord(E->ev[2], s));
+
+  // ---- results back to the host ----
+  std::vector<uint32_t> count(B);
+  std::vector<int32_t> gen(cache_rows);
+  int err_host = 0;
+  MH_HIP(hipMemcpyAsync(count.data(), COUNT, 4 * B, hipMemcpyDeviceToHost, s));
+  MH_HIP(hipMemcpyAsync(gen.data(), OUT, 4 * cache_rows, hipMemcpyDeviceToHost, s));
+  MH_HIP(hipMemcpyAsync(&err_host, E->err_flag, sizeof(int), hipMemcpyDeviceToHost, s));
+  MH_HIP(hipStreamSynchronize(s));
+  hipEvent_t ev_end;
+  MH_HIP(hipEventCreate(&ev_end));
+  MH_HIP(hipEventRecord(ev_end, s));
+  MH_HIP(hipEventSynchronize(ev_end));
+  float ms_total = 0, ms_enc = 0, ms_dec = 0;
+  hipEventElapsedTime(&ms_total, E->ev[0], ev_end);
+  hipEventElapsedTime(&ms_enc, E->ev[0], E->ev[1]);
+  hipEventElapsedTime(&ms_dec, E->ev[1], E->ev[2]);
+  hipEventDestroy(ev_end);
+  E->stats.total_ms = ms_total;
+  E->stats.encoder_ms = ms_enc;
+  E->stats.decode_ms = ms_dec;
+  E->stats.decode_steps = steps;
+  E->stats.max_active_rows = (uint32_t)n_active0;
+  if (E->kernel_timing) {
+    double sum = 0;
+    for (uint32_t i = 0; i < vocab_launches; ++i) {
+      float ms = 0;
+      hipEventElapsedTime(&ms, E->vocab_ev[2 * i], E->vocab_ev[2 * i + 1]);
+      sum += ms;
+    }
+    E->stats.vocab_kernel_ms = sum;
+    E->stats.vocab_kernel_launches = vocab_launches;
+  }
+  if (err_host) return E->fail(MARIAN_HIP_ERR_INFERENCE, "activation is not finite");
+
+  size_t total = 0;
+  for (size_t b = 0; b < B; ++b) total += count[b];
+  E->stats.generated_tokens = total;
+  if (out_len) *out_len = total;
+  if (total > out_cap || (total && !out_tokens))
+    return E->fail(MARIAN_HIP_ERR_BUFFER, "output buffer holds %zu tokens; %zu needed", out_cap, total);
+  size_t o = 0;
+  out_offsets[0] = 0;
+  for (size_t b = 0; b < B; ++b) {
+    std::memcpy(out_tokens + o, gen.data() + kv_base[b], 4ull * count[b]);
+    o += count[b];
+    out_offsets[b + 1] = (uint32_t)o;
+  }
+  return MARIAN_HIP_OK;
+}
+
+}  // extern "C"

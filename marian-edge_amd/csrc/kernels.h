@@ -1,0 +1,135 @@
+// kernels.h — host-side launch interface of the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mh {
+
+// Quantized activations times an int8 weight matrix [N, K] (K-contiguous).
+struct GemmArgs {
+  const int8_t* A = nullptr;  // [M, lda] int8 activations
+  const float* a = nullptr;   // [M] per-row activation multipliers
+  int64_t lda = 0;
+  int M = 0;                  // row count (host) ...
+  const int* M_dev = nullptr; // ... or read on the device (decode active rows)
+  int K = 0;                  // multiple of 64
+  const int8_t* W = nullptr;
+  const float* wmult = nullptr;
+  const float* bias = nullptr;
+  int N = 0;
+};
+
+enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
+
+struct Epilogue {
+  // EPI_STORE (and the Q columns of EPI_QKV_CACHE)
+  float* out = nullptr;
+  int64_t ldo = 0;
+  int32_t* out_i32 = nullptr;
+  int64_t ldi = 0;
+  int relu = 0;
+  // EPI_QKV_CACHE: columns [d, 2d) -> kcache, [2d, 3d) -> vcache, at cache row
+  // kv_base[act[m]] + step.
+  float* kcache = nullptr;
+  float* vcache = nullptr;
+  const int* act = nullptr;
+  const int64_t* kv_base = nullptr;
+  int step = 0;
+  int d = 0;
+  // EPI_ARGMAX: per-row best key of each 64-column group -> partials[m*ld + g]
+  uint64_t* partials = nullptr;
+  int partial_ld = 0;
+  float* logits = nullptr;  // optional [M, N]
+  int64_t ldl = 0;
+  uint32_t flags = 0;  // bit 1: no generation mask
+};
+
+// Column groups of the skinny kernel (the argmax partial count per row).
+int skinny_groups(int N);
+// Skinny (M up to a few hundred, weights streamed once per 64 rows) MFMA GEMM.
+hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s);
+// LDS-tiled 128x128 MFMA GEMM for large M (EPI_STORE only).
+hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s);
+// Picks the kernel by M (host-known M only).
+hipError_t launch_gemm_store(const GemmArgs& g, const Epilogue& e, hipStream_t s);
+
+hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int* rows_dev,
+                                int cols, int8_t* q, int64_t ldq, float* a, int* err,
+                                hipStream_t s);
+
+hipError_t launch_residual_ln(const float* y, const float* r, const float* g, const float* b,
+                              int rows, const int* rows_dev, int d, float* out, int8_t* q,
+                              float* a, int* err, hipStream_t s);
+
+struct EmbedArgs {
+  const int8_t* emb = nullptr;
+  const float* emb_mult = nullptr;
+  const float* pos = nullptr;  // [kMaxPosition, d]
+  float scale = 1.0f;
+  int d = 0;
+  // encoder rows: token and position per row
+  const int32_t* tokens = nullptr;
+  const int32_t* positions = nullptr;
+  // decoder rows: token = prev[act[r]] (negative: position only), position = step
+  const int* act = nullptr;
+  const int32_t* prev = nullptr;
+  int step = 0;
+  int rows = 0;
+  const int* rows_dev = nullptr;
+  float* x = nullptr;
+  int8_t* xq = nullptr;
+  float* xa = nullptr;
+  int* err = nullptr;
+};
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
+
+enum AttnMode { ATT_SEQ = 0, ATT_CROSS = 1, ATT_SELF = 2 };
+struct AttnArgs {
+  int mode = ATT_SEQ;
+  const void* q = nullptr;
+  int64_t ldq = 0;
+  const void* k = nullptr;
+  const void* v = nullptr;
+  int64_t ldkv = 0;
+  int bf16 = 0;
+  int heads = 0;
+  int rows = 0;
+  const int* rows_dev = nullptr;
+  // ATT_SEQ: keys of row r are [cu[seq_of_row[r]], cu[seq_of_row[r]+1])
+  const int* seq_of_row = nullptr;
+  const uint32_t* cu = nullptr;
+  // ATT_CROSS: keys of row r are [cu[act[r]], cu[act[r]+1]);
+  // ATT_SELF: keys are kv_base[act[r]] + [0, step]
+  const int* act = nullptr;
+  const int64_t* kv_base = nullptr;
+  int step = 0;
+  int max_keys = 0;  // upper bound on keys per row (selects the kernel variant)
+  float* out = nullptr;
+  int64_t ldo = 0;
+  int8_t* q8 = nullptr;  // fused per-row quantization of the [heads*64] output row
+  float* qa = nullptr;
+  int* err = nullptr;
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+struct FinalizeArgs {
+  const uint64_t* partials = nullptr;
+  int nparts = 0;
+  int* act = nullptr;
+  int* n_active = nullptr;
+  int32_t* prev = nullptr;
+  const uint32_t* limit = nullptr;
+  int32_t* out_tok = nullptr;
+  const int64_t* out_base = nullptr;
+  uint32_t* count = nullptr;
+  int step = 0;
+  uint32_t flags = 0;
+};
+hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
+
+// Reduces argmax partials to token ids (op-level argmax).
+hipError_t launch_argmax_reduce(const uint64_t* partials, int nparts, int rows, int32_t* token,
+                                hipStream_t s);
+
+}  // namespace mh

@@ -1,0 +1,245 @@
+// ops.hip — op-level entry points (device pointers, caller's stream) and the
+// device-memory helpers of marian_hip_util.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/marian_hip.h"
+#include "../../include/marian_hip_util.h"
+#include "device_common.h"
+#include "kernels.h"
+
+using namespace mh;
+
+namespace {
+
+thread_local std::string g_op_error;
+
+int op_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return MARIAN_HIP_OK;
+  g_op_error = std::string(what) + ": " + hipGetErrorString(e);
+  return e == hipErrorInvalidValue ? MARIAN_HIP_ERR_INVALID_INPUT : MARIAN_HIP_ERR_DEVICE;
+}
+
+// Library scratch for the op-level entry points that need intermediate
+// buffers (quantized activations, argmax partials).  Grow-only, one set per
+// device; calls that overlap on one device race on it.
+struct OpScratch {
+  void* p[3] = {nullptr, nullptr, nullptr};
+  size_t cap[3] = {0, 0, 0};
+};
+std::mutex g_scratch_mu;
+OpScratch g_scratch[64];
+
+void* scratch(int which, size_t bytes, hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  OpScratch& S = g_scratch[dev];
+  if (S.cap[which] >= bytes && S.p[which]) return S.p[which];
+  if (S.p[which]) {
+    hipStreamSynchronize(s);
+    hipFree(S.p[which]);
+    S.p[which] = nullptr;
+    S.cap[which] = 0;
+  }
+  const size_t want = std::max<size_t>(bytes + bytes / 4, 4096);
+  if (hipMalloc(&S.p[which], want) != hipSuccess) {
+    S.p[which] = nullptr;
+    return nullptr;
+  }
+  S.cap[which] = want;
+  return S.p[which];
+}
+
+}  // namespace
+
+extern "C" {
+
+int marian_hip_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, float* a,
+                             int* err, void* stream) {
+  if (!x || !q || !a || rows < 0 || cols <= 0 || rows > INT32_MAX || cols > INT32_MAX)
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  return op_status(launch_quantize_rows(x, cols, (int)rows, nullptr, (int)cols, q, cols, a, err,
+                                        (hipStream_t)stream),
+                   "quantize_rows");
+}
+
+int marian_hip_q8_linear(const float* x, const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                         const int8_t* w, const float* w_mult, const float* bias, int64_t N,
+                         int relu, int32_t* out_i32, float* out_f32, int* err, void* stream) {
+  if (M < 0 || K <= 0 || K % 64 || N <= 0 || !w || !w_mult || !bias || M > INT32_MAX ||
+      N > INT32_MAX || K > INT32_MAX || (!x && (!xq || !xa)) || (!out_i32 && !out_f32))
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (M == 0) return MARIAN_HIP_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (x) {
+    int8_t* q = (int8_t*)scratch(0, (size_t)M * K, s);
+    float* a = (float*)scratch(1, (size_t)M * 4, s);
+    if (!q || !a) return op_status(hipErrorOutOfMemory, "q8_linear scratch");
+    int rc = op_status(launch_quantize_rows(x, K, (int)M, nullptr, (int)K, q, K, a, err, s),
+                       "q8_linear quantize");
+    if (rc) return rc;
+    xq = q;
+    xa = a;
+  }
+  GemmArgs g;
+  g.A = xq;
+  g.a = xa;
+  g.lda = K;
+  g.M = (int)M;
+  g.K = (int)K;
+  g.W = w;
+  g.wmult = w_mult;
+  g.bias = bias;
+  g.N = (int)N;
+  Epilogue e;
+  e.out = out_f32;
+  e.ldo = N;
+  e.out_i32 = out_i32;
+  e.ldi = N;
+  e.relu = relu;
+  return op_status(launch_gemm_store(g, e, s), "q8_linear gemm");
+}
+
+int marian_hip_residual_layer_norm(const float* x, const float* r, const float* scale,
+                                   const float* bias, int64_t rows, int64_t dim, float* out,
+                                   int8_t* q, float* a, int* err, void* stream) {
+  if (!x || !r || !scale || !bias || !out || rows < 0 || rows > INT32_MAX || dim % 64 ||
+      dim <= 0 || dim > 1024 || (q && !a))
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  return op_status(launch_residual_ln(x, r, scale, bias, (int)rows, nullptr, (int)dim, out, q, a,
+                                      err, (hipStream_t)stream),
+                   "residual_layer_norm");
+}
+
+int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
+                         const int32_t* seq_of_row, const uint32_t* cu_k, int64_t rows,
+                         int64_t heads, int64_t max_keys, int in_bf16, float* out, int64_t ldo,
+                         void* stream) {
+  if (!q || !k || !v || !seq_of_row || !cu_k || !out || rows < 0 || rows > INT32_MAX ||
+      heads <= 0 || heads > 16 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096)
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  AttnArgs a;
+  a.mode = ATT_SEQ;
+  a.q = q;
+  a.ldq = ldq;
+  a.k = k;
+  a.v = v;
+  a.ldkv = ldkv;
+  a.bf16 = in_bf16 ? 1 : 0;
+  a.heads = (int)heads;
+  a.rows = (int)rows;
+  a.seq_of_row = seq_of_row;
+  a.cu = cu_k;
+  a.out = out;
+  a.ldo = ldo;
+  a.max_keys = (int)max_keys;
+  return op_status(launch_attention(a, (hipStream_t)stream), "attention");
+}
+
+int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                            const int8_t* emb, const float* emb_mult, const float* bias, int64_t V,
+                            uint32_t flags, int32_t* token, float* logits, void* stream) {
+  if (!xq || !xa || !emb || !emb_mult || !bias || !token || M < 0 || K <= 0 || K % 64 ||
+      V <= 0 || M > INT32_MAX || V > INT32_MAX)
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (M == 0) return MARIAN_HIP_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int nparts = skinny_groups((int)V);
+  uint64_t* part = (uint64_t*)scratch(2, (size_t)M * nparts * 8, s);
+  if (!part) return op_status(hipErrorOutOfMemory, "vocab_argmax scratch");
+  GemmArgs g;
+  g.A = xq;
+  g.a = xa;
+  g.lda = K;
+  g.M = (int)M;
+  g.K = (int)K;
+  g.W = emb;
+  g.wmult = emb_mult;
+  g.bias = bias;
+  g.N = (int)V;
+  Epilogue e;
+  e.partials = part;
+  e.partial_ld = nparts;
+  e.logits = logits;
+  e.ldl = V;
+  e.flags = flags;
+  int rc = op_status(launch_gemm_skinny(g, EPI_ARGMAX, e, s), "vocab_argmax gemm");
+  if (rc) return rc;
+  return op_status(launch_argmax_reduce(part, nparts, (int)M, token, s), "vocab_argmax reduce");
+}
+
+// ---- util ------------------------------------------------------------------
+int marian_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int marian_hip_device_name(int device, char* buf, size_t cap) {
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, device);
+  if (e != hipSuccess) return op_status(e, "hipGetDeviceProperties");
+  snprintf(buf, cap, "%s (%s)", p.name, p.gcnArchName);
+  return MARIAN_HIP_OK;
+}
+
+int marian_hip_set_device(int device) { return op_status(hipSetDevice(device), "hipSetDevice"); }
+
+void* marian_hip_device_alloc(size_t bytes) {
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, std::max<size_t>(bytes, 1));
+  if (e != hipSuccess) {
+    op_status(e, "hipMalloc");
+    return nullptr;
+  }
+  return p;
+}
+int marian_hip_device_free(void* p) { return op_status(hipFree(p), "hipFree"); }
+int marian_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return op_status(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy h2d");
+}
+int marian_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return op_status(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy d2h");
+}
+int marian_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  return op_status(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice), "hipMemcpy d2d");
+}
+int marian_hip_memset(void* dst, int value, size_t bytes) {
+  return op_status(hipMemset(dst, value, bytes), "hipMemset");
+}
+void* marian_hip_stream_create(void) {
+  hipStream_t s = nullptr;
+  if (op_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return nullptr;
+  return s;
+}
+int marian_hip_stream_destroy(void* s) {
+  return op_status(hipStreamDestroy((hipStream_t)s), "hipStreamDestroy");
+}
+int marian_hip_stream_sync(void* s) {
+  return op_status(hipStreamSynchronize((hipStream_t)s), "hipStreamSynchronize");
+}
+int marian_hip_device_sync(void) { return op_status(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+void* marian_hip_event_create(void) {
+  hipEvent_t e = nullptr;
+  if (op_status(hipEventCreate(&e), "hipEventCreate")) return nullptr;
+  return e;
+}
+int marian_hip_event_destroy(void* e) { return op_status(hipEventDestroy((hipEvent_t)e), "hipEventDestroy"); }
+int marian_hip_event_record(void* e, void* s) {
+  return op_status(hipEventRecord((hipEvent_t)e, (hipStream_t)s), "hipEventRecord");
+}
+int marian_hip_event_sync(void* e) {
+  return op_status(hipEventSynchronize((hipEvent_t)e), "hipEventSynchronize");
+}
+int marian_hip_event_elapsed(void* a, void* b, float* ms) {
+  return op_status(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
+}
+const char* marian_hip_last_op_error(void) { return g_op_error.c_str(); }
+
+}  // extern "C"

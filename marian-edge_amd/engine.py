@@ -1,0 +1,217 @@
+"""Python mirror of the reference's token-level engine and backend interface.
+
+HipEngine.translate_token_ids mirrors CpuTokenEngine::translate_token_ids
+(crates/marian-cpu/src/backend.rs:48-57, q8_engine.rs:353-466): packed token ids
+and cu_seqlens offsets in, BatchOutput{tokens, offsets} out, errors raised with
+the reference's BackendError categories (crates/marian-core/src/types.rs:60-70).
+HipBackend carries the TranslationBackend surface that does not need a
+tokenizer: info() and is_ready() (crates/marian-core/src/backend.rs:7-38).
+Every call goes through libmarian_hip.so.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import json
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .synthetic import SeededModel, REFERENCE_LIMITS
+
+
+class BackendError(RuntimeError):
+    """Base of the reference's BackendError variants."""
+
+
+class InvalidInput(BackendError):
+    pass
+
+
+class ModelError(BackendError):
+    pass
+
+
+class InferenceError(BackendError):
+    pass
+
+
+class DeviceError(InferenceError):
+    """A HIP runtime failure; the engine is not ready afterwards."""
+
+
+class BufferTooSmall(BackendError):
+    pass
+
+
+_ERRORS = {
+    _lib.ERR_INVALID_INPUT: InvalidInput,
+    _lib.ERR_MODEL: ModelError,
+    _lib.ERR_INFERENCE: InferenceError,
+    _lib.ERR_DEVICE: DeviceError,
+    _lib.ERR_BUFFER: BufferTooSmall,
+    _lib.ERR_NOT_READY: DeviceError,
+}
+
+
+@dataclass
+class BatchOutput:
+    """crates/marian-cpu/src/engine.rs:80-85"""
+
+    tokens: np.ndarray
+    offsets: np.ndarray
+
+    def rows(self) -> list[list[int]]:
+        return [self.tokens[self.offsets[i]:self.offsets[i + 1]].tolist()
+                for i in range(len(self.offsets) - 1)]
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+class _ModelStructs:
+    """ctypes model description pointing into the SeededModel's numpy arrays."""
+
+    def __init__(self, m: SeededModel):
+        g = m.geometry
+        keep = []
+
+        def arr(a, dtype):
+            a = np.ascontiguousarray(a, dtype=dtype)
+            keep.append(a)
+            return _ptr(a)
+
+        def lin(d):
+            return _lib.Linear(arr(d["weight"], np.int8), arr(d["mult"], np.float32),
+                               arr(d["bias"], np.float32))
+
+        enc = (_lib.EncoderLayer * max(1, len(m.encoder)))()
+        for i, L in enumerate(m.encoder):
+            enc[i] = _lib.EncoderLayer(
+                lin(L["qkv"]), lin(L["out"]), arr(L["ln1"]["scale"], np.float32),
+                arr(L["ln1"]["bias"], np.float32), lin(L["ffn1"]), lin(L["ffn2"]),
+                arr(L["ln2"]["scale"], np.float32), arr(L["ln2"]["bias"], np.float32))
+        dec = (_lib.DecoderLayer * max(1, len(m.decoder)))()
+        for i, L in enumerate(m.decoder):
+            dec[i] = _lib.DecoderLayer(
+                lin(L["self_qkv"]), lin(L["self_out"]), arr(L["ln1"]["scale"], np.float32),
+                arr(L["ln1"]["bias"], np.float32), lin(L["cross_q"]), lin(L["cross_kv"]),
+                lin(L["cross_out"]), arr(L["ln2"]["scale"], np.float32),
+                arr(L["ln2"]["bias"], np.float32), lin(L["ffn1"]), lin(L["ffn2"]),
+                arr(L["ln3"]["scale"], np.float32), arr(L["ln3"]["bias"], np.float32))
+        self.model = _lib.Model(
+            g.vocab, g.dim, g.heads, g.ffn_dim, len(m.encoder), len(m.decoder),
+            arr(m.embedding, np.int8), arr(m.embedding_mult, np.float32),
+            arr(m.output_bias, np.float32), enc, dec)
+        self._keep = (keep, enc, dec)
+
+
+def make_limits(limits: dict | None) -> _lib.Limits:
+    d = dict(REFERENCE_LIMITS)
+    if limits:
+        d.update(limits)
+    return _lib.Limits(d["max_length_factor"], d["max_generation_steps"], d["max_position"],
+                       d["max_batch"], d["max_source_tokens"], d["max_padded_cells"])
+
+
+class HipEngine:
+    """Owns one marian_hip_engine (one device, one stream, one owner thread)."""
+
+    def __init__(self, model: SeededModel, limits: dict | None = None, device: int = 0):
+        self._lib = _lib.load()
+        structs = _ModelStructs(model)
+        self._limits = make_limits(limits)
+        handle = C.c_void_p()
+        rc = self._lib.marian_hip_engine_create(C.byref(structs.model), C.byref(self._limits),
+                                                device, C.byref(handle))
+        if rc != _lib.OK:
+            raise _ERRORS.get(rc, BackendError)(f"engine creation failed ({rc})")
+        self._h = handle
+        self.geometry = model.geometry
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.marian_hip_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _raise(self, rc: int):
+        msg = self._lib.marian_hip_last_error(self._h).decode(errors="replace")
+        raise _ERRORS.get(rc, BackendError)(msg)
+
+    def translate_token_ids(self, tokens, offsets, max_output_tokens, flags: int = 0) -> BatchOutput:
+        toks = np.ascontiguousarray(tokens, np.int32)
+        offs = np.ascontiguousarray(offsets, np.uint32)
+        lim = np.ascontiguousarray(max_output_tokens, np.uint32)
+        if lim.shape[0] != max(0, offs.shape[0] - 1):
+            raise InvalidInput("max_output_tokens does not match packed batch")
+        cap = int(np.minimum(lim.astype(np.int64), 4096).sum())
+        out = np.zeros(max(cap, 1), np.int32)
+        out_offs = np.zeros(max(offs.shape[0], 1), np.uint32)
+        n = C.c_size_t(0)
+        rc = self._lib.marian_hip_translate_token_ids(
+            self._h, _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+            _ptr(lim), flags, _ptr(out), out.size, _ptr(out_offs), C.byref(n))
+        if rc != _lib.OK:
+            self._raise(rc)
+        return BatchOutput(out[:n.value].copy(), out_offs.copy())
+
+    def set_kernel_timing(self, enabled: bool) -> None:
+        self._lib.marian_hip_set_kernel_timing(self._h, 1 if enabled else 0)
+
+    def last_stats(self) -> dict:
+        s = _lib.Stats()
+        self._lib.marian_hip_last_stats(self._h, C.byref(s))
+        return {f: getattr(s, f) for f, _ in _lib.Stats._fields_}
+
+    def is_ready(self) -> bool:
+        return bool(self._lib.marian_hip_is_ready(self._h))
+
+    def info(self) -> dict:
+        buf = C.create_string_buffer(1024)
+        rc = self._lib.marian_hip_info(self._h, buf, len(buf))
+        if rc != _lib.OK:
+            self._raise(rc)
+        return json.loads(buf.value.decode())
+
+
+class HipBackend:
+    """TranslationBackend surface at the token level (backend.rs:7-38)."""
+
+    def __init__(self, engine: HipEngine):
+        self.engine = engine
+
+    def info(self) -> dict:
+        return self.engine.info()
+
+    def is_ready(self) -> bool:
+        return self.engine.is_ready()
+
+    def translate_token_batch(self, sentences: list[list[int]], max_output_tokens: list[int],
+                              repetitions: list[int] | None = None, flags: int = 0):
+        """One output per logical input, like translate_batch_with_repetitions
+        (backend.rs:30-37); repetitions do not change the result."""
+        if repetitions is not None and len(repetitions) != len(sentences):
+            raise InvalidInput("repetitions do not match inputs")
+        offs = np.zeros(len(sentences) + 1, np.uint32)
+        offs[1:] = np.cumsum([len(s) for s in sentences])
+        toks = np.concatenate([np.asarray(s, np.int32) for s in sentences]) if sentences else \
+            np.zeros(0, np.int32)
+        out = self.engine.translate_token_ids(toks, offs, max_output_tokens, flags)
+        rows = out.rows()
+        if len(rows) != len(sentences):
+            raise InferenceError("backend returned a different number of outputs")
+        return rows

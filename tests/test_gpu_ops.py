@@ -1,0 +1,210 @@
+"""GPU parity of the op-level kernels against the CPU oracle, through the C ABI.
+
+Bars: i32 accumulators and int8 codes bit-exact; fp32 outputs within 1e-3
+relative (the stated tolerance), and in practice bit-identical because the
+kernels evaluate the oracle's canonical operation order — the strict tests
+assert that too.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev(pkg):
+    from importlib import import_module
+
+    d = import_module(pkg.__name__ + ".device")
+    assert d.device_count() >= 1, "no HIP device visible"
+    print(f"device: {d.device_name(0)}", flush=True)
+    return d
+
+
+def rel_err(got, want):
+    den = np.maximum(np.abs(want), 1e-6)
+    return float(np.max(np.abs(got.astype(np.float64) - want) / den)) if got.size else 0.0
+
+
+@pytest.mark.parametrize("K,N", [(512, 1536), (512, 512), (512, 2048), (2048, 512), (512, 32000)])
+@pytest.mark.parametrize("M", [1, 8, 64, 256, 4096])
+def test_q8_linear_sweep(pkg, orc, dev, M, K, N):
+    print(f"q8_linear M={M} K={K} N={N}", flush=True)
+    a, w, mult, bias = pkg.gemm_inputs(M, K, N)
+    y_ref, acc_ref, q_ref, s_ref = orc.linear_forward(a, w, mult, bias, threads=16)
+    da, dw, dm, db = (dev.DeviceArray.from_host(x) for x in (a, w, mult, bias))
+    di = dev.DeviceArray.zeros((M, N), np.int32)
+    df = dev.DeviceArray.zeros((M, N), np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.q8_linear(da, dw, dm, db, di, df, err=err)
+    dev.synchronize()
+    acc, y = di.host(), df.host()
+    assert err.host()[0] == 0
+    assert np.array_equal(acc, acc_ref), "i32 accumulators differ"
+    assert rel_err(y, y_ref) <= REL_TOL
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), "dequant not bit-identical"
+
+
+def test_quantize_rows_matches_oracle(pkg, orc, dev):
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((300, 2048)) * rng.uniform(0.01, 50, size=(300, 1))).astype(np.float32)
+    x[5] = 0.0  # all-zero row -> multiplier 1
+    x[7, :10] = [0.5, 1.5, -0.5, -1.5, 2.5, -2.5, 126.5, 3.0, 0.0, -0.0]
+    q_ref, a_ref = orc.quantize_rows(x)
+    dx = dev.DeviceArray.from_host(x)
+    dq = dev.DeviceArray.zeros(x.shape, np.int8)
+    da = dev.DeviceArray.zeros(300, np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.quantize_rows(dx, dq, da, err)
+    dev.synchronize()
+    assert np.array_equal(dq.host(), q_ref) and np.array_equal(da.host(), a_ref)
+    assert err.host()[0] == 0
+    # a non-finite activation raises the error flag (the reference rejects it)
+    x[3, 17] = np.inf
+    dx2 = dev.DeviceArray.from_host(x)
+    dev.quantize_rows(dx2, dq, da, err)
+    dev.synchronize()
+    assert err.host()[0] == 1
+
+
+def test_q8_linear_edges(pkg, orc, dev):
+    rng = np.random.default_rng(12)
+    # column tail (N not a multiple of 16/64), odd M on both kernels, ReLU,
+    # full-range weights including -128 (exact in the int8 matrix core)
+    for M, K, N in [(3, 64, 100), (77, 128, 130), (200, 192, 65), (130, 64, 1)]:
+        print(f"edge M={M} K={K} N={N}", flush=True)
+        a = rng.standard_normal((M, K)).astype(np.float32)
+        w = rng.integers(-128, 128, size=(N, K)).astype(np.int8)
+        mult = rng.uniform(50, 100, size=N).astype(np.float32)
+        bias = rng.standard_normal(N).astype(np.float32)
+        y_ref, acc_ref, _, _ = orc.linear_forward(a, w, mult, bias, relu=True)
+        dw = dev.DeviceArray.from_host(w)
+        di = dev.DeviceArray.zeros((M, N), np.int32)
+        df = dev.DeviceArray.zeros((M, N), np.float32)
+        dev.q8_linear(dev.DeviceArray.from_host(a), dw, dev.DeviceArray.from_host(mult),
+                      dev.DeviceArray.from_host(bias), di, df, relu=True)
+        dev.synchronize()
+        assert np.array_equal(di.host(), acc_ref)
+        assert np.array_equal(df.host(), y_ref)
+    # K not a multiple of 64 is rejected on the host
+    with pytest.raises(RuntimeError):
+        dev.q8_linear(dev.DeviceArray.zeros((2, 100), np.float32), dev.DeviceArray.zeros((4, 100), np.int8),
+                      dev.DeviceArray.zeros(4, np.float32), dev.DeviceArray.zeros(4, np.float32),
+                      dev.DeviceArray.zeros((2, 4), np.int32), None)
+
+
+def test_residual_layer_norm_matches_oracle(pkg, orc, dev):
+    rng = np.random.default_rng(13)
+    for d in (512, 384):
+        y = rng.standard_normal((257, d)).astype(np.float32)
+        r = (rng.standard_normal((257, d)) * 3).astype(np.float32)
+        g = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+        b = (0.1 * rng.standard_normal(d)).astype(np.float32)
+        ref = orc.residual_layer_norm(y, r, g, b)
+        q_ref, a_ref = orc.quantize_rows(ref)
+        out = dev.DeviceArray.zeros(y.shape, np.float32)
+        q = dev.DeviceArray.zeros(y.shape, np.int8)
+        a = dev.DeviceArray.zeros(257, np.float32)
+        dev.residual_layer_norm(dev.DeviceArray.from_host(y), dev.DeviceArray.from_host(r),
+                                dev.DeviceArray.from_host(g), dev.DeviceArray.from_host(b), out, q, a)
+        dev.synchronize()
+        assert np.array_equal(out.host(), ref)
+        assert np.array_equal(q.host(), q_ref) and np.array_equal(a.host(), a_ref)
+
+
+def _attention_case(pkg, orc, dev, q, k, v, cu, heads, bf16):
+    T = q.shape[0]
+    lens = np.diff(cu.astype(np.int64))
+    seq = np.repeat(np.arange(len(lens), dtype=np.int32), lens)
+    if bf16:
+        qh, kh, vh = (pkg.synthetic.bf16_round(x) for x in (q, k, v))
+        q, k, v = (pkg.synthetic.bf16_to_f32(x) for x in (qh, kh, vh))
+        dq, dk, dv = (dev.DeviceArray.from_host(x) for x in (qh, kh, vh))
+    else:
+        dq, dk, dv = (dev.DeviceArray.from_host(x) for x in (q, k, v))
+    ref = orc.attention(q, k, v, cu, cu, heads)
+    out = dev.DeviceArray.zeros((T, heads * 64), np.float32)
+    dev.attention(dq, dk, dv, dev.DeviceArray.from_host(seq), dev.DeviceArray.from_host(cu), out,
+                  heads=heads, max_keys=int(lens.max()), bf16=bf16)
+    dev.synchronize()
+    got = out.host()
+    assert rel_err(got, ref) <= REL_TOL or np.max(np.abs(got - ref)) < 1e-5
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "attention not bit-identical"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_varlen_attention_full_workload(pkg, orc, dev, bf16):
+    q, k, v, cu = pkg.attention_inputs()
+    print(f"attention T={q.shape[0]} bf16={bf16}", flush=True)
+    _attention_case(pkg, orc, dev, q, k, v, cu, 8, bf16)
+
+
+def test_attention_edges(pkg, orc, dev):
+    rng = np.random.default_rng(14)
+    # single key, 64/65 keys (chunk boundary), a 1000-key row (large variant),
+    # and the reference's masking KAT shape at head_dim 64
+    lens = np.array([1, 64, 65, 2, 1000, 3], np.int64)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    T = int(cu[-1])
+    q, k, v = (rng.standard_normal((T, 128)).astype(np.float32) for _ in range(3))
+    print("attention edges", flush=True)
+    _attention_case(pkg, orc, dev, q, k, v, cu, 2, False)
+
+
+def test_vocab_argmax_matches_oracle(pkg, orc, dev, full_model):
+    m = full_model
+    rng = np.random.default_rng(15)
+    M = 64
+    x = rng.standard_normal((M, 512)).astype(np.float32)
+    q_ref, a_ref = orc.quantize_rows(x)
+    logits_ref, _, _, _ = orc.linear_forward(x, m.embedding, m.embedding_mult, m.output_bias)
+    masked = np.zeros(m.geometry.vocab, bool)
+    masked[1] = True
+    masked[7:39] = True
+    lm = np.where(masked[None, :], -np.inf, logits_ref).astype(np.float32)
+    tok_ref = np.argmax(lm, axis=1)  # first maximum = lowest id
+    dq, da = dev.DeviceArray.from_host(q_ref), dev.DeviceArray.from_host(a_ref)
+    demb, dmult, dbias = (dev.DeviceArray.from_host(t) for t in
+                          (m.embedding, m.embedding_mult, m.output_bias))
+    tok = dev.DeviceArray.zeros(M, np.int32)
+    logits = dev.DeviceArray.zeros((M, m.geometry.vocab), np.float32)
+    dev.vocab_argmax(dq, da, demb, dmult, dbias, tok, logits)
+    dev.synchronize()
+    assert np.array_equal(tok.host(), tok_ref)
+    got = logits.host()
+    assert np.array_equal(got, lm)
+
+
+def test_vocab_argmax_ties_pick_lowest_id(pkg, dev):
+    V, K = 4096, 64
+    emb = np.zeros((V, K), np.int8)
+    emb[:, 0] = 1
+    emb[[5, 700, 3000, 4095], 0] = 9  # four equal maxima
+    mult = np.ones(V, np.float32)
+    bias = np.zeros(V, np.float32)
+    xq = np.zeros((3, K), np.int8)
+    xq[:, 0] = 127
+    xa = np.ones(3, np.float32)
+    tok = dev.DeviceArray.zeros(3, np.int32)
+    args = [dev.DeviceArray.from_host(t) for t in (xq, xa, emb, mult, bias)]
+    dev.vocab_argmax(*args, tok)
+    dev.synchronize()
+    assert tok.host().tolist() == [5, 5, 5]
+    emb[5, 0] = 1
+    emb[700, 0] = 1
+    args = [dev.DeviceArray.from_host(t) for t in (xq, xa, emb, mult, bias)]
+    dev.vocab_argmax(*args, tok)
+    dev.synchronize()
+    assert tok.host().tolist() == [3000, 3000, 3000]
+    # a masked id never wins (id 20 is in 7..38) unless the mask is off
+    emb[20, 0] = 100
+    args = [dev.DeviceArray.from_host(t) for t in (xq, xa, emb, mult, bias)]
+    dev.vocab_argmax(*args, tok)
+    dev.synchronize()
+    assert tok.host().tolist() == [3000, 3000, 3000]
+    dev.vocab_argmax(*args, tok, flags=pkg.FLAG_NO_GENERATION_MASK)
+    dev.synchronize()
+    assert tok.host().tolist() == [20, 20, 20]

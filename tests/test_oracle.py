@@ -1,0 +1,327 @@
+"""Pins the CPU oracle: the reference's own known-answer vectors, closed forms,
+brute force on small inputs, and invariants chosen so a dropped term, a wrong
+index or a transposed operand fails one of them."""
+
+import math
+
+import numpy as np
+import pytest
+
+
+def value_at(i, kats):
+    t = kats["avx2_tails"]
+    return t["activation_cycle"][i % 9], t["weight_cycle"][(i * 7 + 3) % 9]
+
+
+# ---- quantization -----------------------------------------------------------
+def test_quantize_ties_even_kat(orc, kats):
+    k = kats["quantize_ties_even"]
+    got = orc.quantize_static_u8(np.array(k["input"], np.float32), k["mult"])
+    assert got.tolist() == k["expected_u8"]
+    with pytest.raises(orc.OracleError):
+        orc.quantize_static_u8(np.array([np.nan], np.float32), 1.0)
+    with pytest.raises(orc.OracleError):
+        orc.quantize_static_u8(np.array([0.0], np.float32), 0.0)
+
+
+def test_dynamic_quantization_rule(orc):
+    # Row max 31.75 gives the multiplier 127/31.75 = 4 exactly; an all-zero
+    # row gets multiplier 1 and all-zero codes; non-finite input is rejected.
+    x = np.array([[31.75, -0.125, 0.375, -31.75], [0, 0, 0, 0]], np.float32)
+    q, a = orc.quantize_rows(x)
+    assert a.tolist() == [4.0, 1.0]
+    assert q.tolist() == [[127, 0, 2, -127], [0, 0, 0, 0]]  # -0.5 -> 0, 1.5 -> 2 (ties even)
+    with pytest.raises(orc.OracleError):
+        orc.quantize_rows(np.array([[1.0, np.inf]], np.float32))
+
+
+def test_alpha_normalization_kat(kats):
+    k = kats["alpha_normalization"]
+    mult = np.float32(127) / np.float32(k["absmax"])
+    assert abs(float(mult) - k["expected_mult"]) < k["tolerance"]
+
+
+# ---- integer GEMM -------------------------------------------------------------
+def test_linear_integer_oracle_kat(orc, kats):
+    k = kats["linear_integer_oracle"]
+    w = np.array(k["weights_out_in"], np.int8)
+    bias = np.array(k["bias"], np.float32)
+    mult = np.full(2, k["weight_mult"], np.float32)
+    for rows in k["inputs"]:
+        x = np.array(rows, np.float32)
+        # Pad each row with one element of magnitude 127/4 so the per-row
+        # dynamic multiplier equals the KAT's static multiplier 4.
+        xp = np.concatenate([x, np.full((x.shape[0], 1), 31.75, np.float32)], axis=1)
+        wp = np.concatenate([w, np.zeros((2, 1), np.int8)], axis=1)
+        y, acc, q, a = orc.linear_forward(xp, wp, mult, bias)
+        assert np.all(a == 4.0)
+        u8 = orc.quantize_static_u8(x.ravel(), 4.0).reshape(x.shape)
+        expected_acc = (u8.astype(np.int64) - 127) @ w.T.astype(np.int64)
+        assert np.array_equal(acc, expected_acc)
+        expected = expected_acc.astype(np.float32) / np.float32(32.0) + bias
+        assert np.array_equal(y, expected)
+
+
+def test_full_range_kat(orc, kats):
+    k = kats["full_range"]
+    y, acc, _, _ = orc.linear_forward(np.array([k["input"]], np.float32),
+                                      np.array([k["weights"]], np.int8),
+                                      np.ones(1, np.float32), np.zeros(1, np.float32))
+    assert acc[0, 0] == 64516 and y[0, 0] == k["expected"]
+
+
+def test_avx2_tails_match_brute_force(orc, kats):
+    for n in kats["avx2_tails"]["lengths"]:
+        pairs = [value_at(i, kats) for i in range(n)]
+        a = np.array([p[0] for p in pairs], np.uint8)
+        w = np.array([p[1] for p in pairs], np.int8)
+        want = sum((int(x) - 127) * int(y) for x, y in pairs)
+        if n:
+            assert int(orc.gemm_u8_i8_avx2(a[None, :], w[None, :])[0, 0]) == want, n
+        assert orc.dot_u8_i8(a, w) == want, n
+    s = kats["avx2_tails"]["saturation_case"]
+    a = np.full((1, s["length"]), s["activation"], np.uint8)
+    w = np.full((1, s["length"]), s["weight"], np.int8)
+    assert int(orc.gemm_u8_i8_avx2(a, w)[0, 0]) == s["expected"]
+
+
+def test_tiled_gemm_matches_brute_force(orc, kats):
+    t = kats["tiled_gemm"]
+    R, K, N = t["rows"], t["inner"], t["outputs"]
+    a = np.array([value_at(i, kats)[0] for i in range(R * K)], np.uint8).reshape(R, K)
+    w = np.array([value_at(i + t["weight_index_offset"], kats)[1] for i in range(N * K)],
+                 np.int8).reshape(N, K)
+    want = (a.astype(np.int64) - 127) @ w.T.astype(np.int64)
+    for threads in (1, 4):
+        assert np.array_equal(orc.gemm_u8_i8_avx2(a, w, threads=threads), want)
+    # signed-int8 GEMM on the same values (the activations as q = u8 - 127,
+    # clipped to the Q8 range) and both thread policies
+    q = np.clip(a.astype(np.int64) - 127, -127, 127).astype(np.int8)
+    assert np.array_equal(orc.gemm_i32(q, w, threads=1),
+                          q.astype(np.int64) @ w.T.astype(np.int64))
+
+
+def test_gemm_random_against_numpy_int64(orc):
+    rng = np.random.default_rng(0)
+    for M, K, N in [(1, 64, 5), (7, 512, 33), (65, 2048, 17)]:
+        qa = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+        qw = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+        want = qa.astype(np.int64) @ qw.T.astype(np.int64)
+        assert np.array_equal(orc.gemm_i32(qa, qw, threads=3), want)
+        u8 = (qa.astype(np.int16) + 127).astype(np.uint8)
+        assert np.array_equal(orc.gemm_u8_i8_avx2(u8, qw, threads=2), want)
+
+
+# ---- elementary fp32 ----------------------------------------------------------
+def test_canonical_exp_is_correctly_rounded_almost_always(orc):
+    xs = np.concatenate([np.linspace(-104, 0, 20001), -np.logspace(-8, 2, 2001), [0.0]])
+    xs = xs.astype(np.float32)
+    got = np.array([orc.expf(float(x)) for x in xs], np.float32)
+    want = np.exp(xs.astype(np.float64)).astype(np.float32)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1
+    assert (ulp == 0).mean() > 0.999
+    assert orc.expf(0.0) == 1.0 and orc.expf(-200.0) == 0.0
+    # the reference-order mode is libm expf: also within one ulp
+    ref = np.array([orc.expf(float(x), orc.REFERENCE) for x in xs[::50]], np.float32)
+    assert np.max(np.abs(ref.view(np.int32).astype(np.int64)
+                         - want[::50].view(np.int32).astype(np.int64))) <= 1
+
+
+def test_canonical_sum_order(orc):
+    rng = np.random.default_rng(1)
+    # integer-valued data: every partial is exact, so any order gives the sum
+    x = rng.integers(-1000, 1000, size=512).astype(np.float32)
+    assert orc.row_sum(x) == float(x.astype(np.int64).sum())
+    # the canonical order: 64 strided lane partials, then the xor butterfly
+    y = rng.standard_normal(512).astype(np.float32)
+    p = [np.float32(0)] * 64
+    for j in range(512):
+        p[j % 64] = np.float32(p[j % 64] + y[j])
+    off = 32
+    while off:
+        p = [np.float32(p[l] + p[l ^ off]) for l in range(64)]
+        off //= 2
+    assert orc.row_sum(y) == float(p[0])
+    # reference order: strictly sequential
+    s = np.float32(-0.0)
+    for v in y:
+        s = np.float32(s + v)
+    assert orc.row_sum(y, orc.REFERENCE) == float(s)
+    assert abs(orc.row_sum(y) - math.fsum(map(float, y))) < 1e-4
+
+
+def test_positions_kat(orc, kats):
+    k = kats["positions_384"]
+    p = orc.positions(k["dim"], 4).ravel()
+    for idx, val in k["exact"].items():
+        assert p[int(idx)] == val
+    assert abs(p[k["sin1_index"]] - math.sin(1.0)) < k["tolerance"]
+    assert abs(p[k["cos1_index"]] - math.cos(1.0)) < k["tolerance"]
+    with pytest.raises(orc.OracleError):
+        orc.positions(3, 1)
+    # d=512: grouped sin | cos, frequency exp(-i ln(1e4) / 255)
+    t = orc.positions(512, 64)
+    pp, i = 37, 100
+    f = math.exp(-i * math.log(10000.0) / 255)
+    assert abs(t[pp, i] - math.sin(pp * f)) < 2e-5 and abs(t[pp, 256 + i] - math.cos(pp * f)) < 2e-5
+
+
+def test_layer_norm_kat_and_closed_forms(orc, kats):
+    k = kats["layer_norm_per_row"]
+    x = np.array(k["input"], np.float32).reshape(k["rows"], k["dim"])
+    r = np.full_like(x, k["residual"])
+    out = orc.residual_layer_norm(x, r, np.ones(k["dim"], np.float32), np.zeros(k["dim"], np.float32))
+    assert abs(out[0, 0] + out[1, 0]) < k["tolerance"] and abs(out[0, 3] + out[1, 3]) < k["tolerance"]
+    assert abs(out[0].sum()) < k["tolerance"] and abs(out[1].sum()) < k["tolerance"]
+    # a constant row normalizes to beta
+    rng = np.random.default_rng(2)
+    beta = rng.standard_normal(512).astype(np.float32)
+    gamma = rng.standard_normal(512).astype(np.float32)
+    c = orc.residual_layer_norm(np.full((1, 512), 3.0, np.float32), np.zeros((1, 512), np.float32),
+                                gamma, beta)
+    assert np.array_equal(c[0], beta)
+    # float64 textbook LayerNorm within 1e-5 relative on random rows, both orders
+    y = rng.standard_normal((4, 512)).astype(np.float32)
+    z = rng.standard_normal((4, 512)).astype(np.float32)
+    s = (y.astype(np.float64) + z)
+    ref = (s - s.mean(1, keepdims=True)) / np.sqrt(s.var(1, keepdims=True) + 1e-6) * gamma + beta
+    for order in (orc.CANONICAL, orc.REFERENCE):
+        got = orc.residual_layer_norm(y, z, gamma, beta, order)
+        assert np.max(np.abs(got - ref)) < 1e-4
+
+
+def test_attention_masking_kat_and_closed_forms(orc, kats):
+    k = kats["attention_masks_padded_keys"]
+    q = np.array([k["query"]], np.float32)
+    kk = np.array(k["key"], np.float32)
+    v = np.array(k["value"], np.float32)
+    out = orc.attention(q, kk[:k["length"]], v[:k["length"]], [0, 1], [0, k["length"]], heads=1)
+    assert out[0].tolist() == k["expected"]
+    rng = np.random.default_rng(3)
+    # all-equal keys: uniform weights -> the mean of V
+    L = 37
+    q = rng.standard_normal((1, 512)).astype(np.float32)
+    keys = np.tile(rng.standard_normal((1, 512)).astype(np.float32), (L, 1))
+    vals = rng.standard_normal((L, 512)).astype(np.float32)
+    out = orc.attention(q, keys, vals, [0, 1], [0, L], heads=8)
+    assert np.max(np.abs(out[0] - vals.mean(0))) < 1e-5
+    # float64 softmax attention on random packed data, per head
+    lens = [1, 5, 64, 65, 130]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    T = int(cu[-1])
+    Q, K, V = (rng.standard_normal((T, 512)).astype(np.float32) for _ in range(3))
+    for order in (orc.CANONICAL, orc.REFERENCE):
+        got = orc.attention(Q, K, V, cu, cu, heads=8, order=order)
+        for b in range(len(lens)):
+            s, e = cu[b], cu[b + 1]
+            for h in range(8):
+                sl = slice(h * 64, (h + 1) * 64)
+                sc = Q[s:e, sl].astype(np.float64) @ K[s:e, sl].T.astype(np.float64) / 8.0
+                p = np.exp(sc - sc.max(1, keepdims=True))
+                p /= p.sum(1, keepdims=True)
+                ref = p @ V[s:e, sl].astype(np.float64)
+                assert np.max(np.abs(got[s:e, sl] - ref)) < 2e-5
+
+
+def test_weight_quantization_bound(pkg, kats):
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    q, mult = pkg.synthetic.quantize_weights(w)
+    assert q.dtype == np.int8 and q.min() >= -127
+    err = np.abs(q.astype(np.float32) / mult[:, None] - w)
+    assert np.all(err <= np.float32(0.500001) / mult[:, None])
+    assert np.all(np.abs(q).max(axis=1) == 127)
+
+
+# ---- greedy translation --------------------------------------------------------
+def _tiny_model(pkg, vocab=64, seed=3):
+    geom = pkg.Geometry(vocab=vocab, dim=128, heads=2, ffn_dim=256, encoder_layers=1,
+                        decoder_layers=1)
+    return pkg.seeded_model(seed=seed, geometry=geom)
+
+
+def test_argmax_tie_and_generation_mask(pkg, orc):
+    m = _tiny_model(pkg)
+    m.embedding[:] = 1  # every vocabulary row identical
+    m.embedding_mult[:] = 127.0
+    m.output_bias[:] = 0.0
+    om = orc.OracleModel(m)
+    toks = np.array([5, 6, 40], np.int32)
+    offs = np.array([0, 3], np.uint32)
+    lim = dict(pkg.REFERENCE_LIMITS)
+    # equal logits: the lowest candidate id (EOS 0) wins and stops the row
+    assert orc.translate(om, toks, offs, [4], lim) == [[0]]
+    assert orc.translate(om, toks, offs, [4], lim, flags=orc.FLAG_IGNORE_EOS) == [[0, 0, 0, 0]]
+    # lower id 0, then 1 and 7..38 are masked: 2 is the first candidate left
+    m.output_bias[0] = -1.0
+    om = orc.OracleModel(m)
+    assert orc.translate(om, toks, offs, [3], lim) == [[2, 2, 2]]
+    # without the mask id 1 ties with 2 and comes first
+    assert orc.translate(om, toks, offs, [3], lim, flags=orc.FLAG_NO_GENERATION_MASK) == [[1, 1, 1]]
+
+
+def test_generation_limits(pkg, orc):
+    m = _tiny_model(pkg)
+    om = orc.OracleModel(m)
+    toks = np.arange(3, 13, dtype=np.int32)
+    offs = np.array([0, 4, 10], np.uint32)
+    lim = dict(pkg.REFERENCE_LIMITS)
+    flags = orc.FLAG_IGNORE_EOS
+    out = orc.translate(om, toks, offs, [100, 100], lim, flags=flags)
+    assert [len(o) for o in out] == [8, 12]  # len * max_length_factor 2
+    lim["max_generation_steps"] = 5
+    out = orc.translate(om, toks, offs, [100, 3], lim, flags=flags)
+    assert [len(o) for o in out] == [5, 3]
+    out = orc.translate(om, toks, offs, [0, 2], lim, flags=flags)
+    assert [len(o) for o in out] == [0, 2]
+
+
+def test_validation_errors(pkg, orc):
+    m = _tiny_model(pkg)
+    om = orc.OracleModel(m)
+    lim = dict(pkg.REFERENCE_LIMITS)
+    bad = [
+        (np.array([3, 4], np.int32), np.array([0, 2, 2], np.uint32), [1, 1]),  # empty row
+        (np.array([3, 4], np.int32), np.array([1, 2], np.uint32), [1]),  # offsets[0] != 0
+        (np.array([3, 4], np.int32), np.array([0, 3], np.uint32), [1]),  # last != len
+        (np.array([3, 64], np.int32), np.array([0, 2], np.uint32), [1]),  # id >= vocab
+        (np.array([3, -1], np.int32), np.array([0, 2], np.uint32), [1]),  # negative id
+    ]
+    for toks, offs, req in bad:
+        with pytest.raises(orc.OracleError) as e:
+            orc.translate(om, toks, offs, req, lim)
+        assert e.value.code == -1
+    # padded-cell cap: 5 rows of 120 tokens = 72,000 cells > 65,536
+    toks = np.full(600, 5, np.int32)
+    offs = np.arange(0, 601, 120).astype(np.uint32)
+    with pytest.raises(orc.OracleError):
+        orc.translate(om, toks, offs, [1] * 5, lim)
+
+
+def test_batch_invariance_and_schedules_agree(pkg, orc, small_model):
+    om = orc.OracleModel(small_model)
+    b = pkg.ragged_batch(seed=5, n=6, vocab=small_model.geometry.vocab)
+    b.max_output_tokens = np.minimum(b.max_output_tokens, 12).astype(np.uint32)
+    batched = orc.translate(om, b.tokens, b.offsets, b.max_output_tokens, b.limits)
+    singles = []
+    for i in range(6):
+        s = b.subset([i])
+        singles += orc.translate(om, s.tokens, s.offsets, s.max_output_tokens, s.limits)
+    assert batched == singles
+    # the padded, all-rows reference schedule gives the same tokens
+    padded = orc.translate(om, b.tokens, b.offsets, b.max_output_tokens, b.limits,
+                           threads=4, schedule="reference")
+    assert padded == batched
+    assert [len(x) for x in batched] == [min(int(v), 12) for v in b.max_output_tokens] or \
+        any(x and x[-1] == 0 for x in batched)
+
+
+def test_encoder_output_is_batch_invariant(pkg, orc, small_model):
+    om = orc.OracleModel(small_model)
+    b = pkg.ragged_batch(seed=6, n=3, vocab=small_model.geometry.vocab)
+    full = orc.encode(om, b.tokens, b.offsets)
+    for i in range(3):
+        s = b.subset([i])
+        one = orc.encode(om, s.tokens, s.offsets)
+        assert np.array_equal(one, full[b.offsets[i]:b.offsets[i + 1]])
