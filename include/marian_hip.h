@@ -163,7 +163,8 @@ const char* marian_hip_last_error(const marian_hip_engine* engine);
 int marian_hip_info(const marian_hip_engine* engine, char* buf, size_t cap);
 
 /* Timing of the last translate call, in milliseconds (events on the engine's
- * stream): total (upload to host-visible tokens), encoder, decode loop, the
+ * stream): total (packed inputs resident in HBM to generated tokens in host
+ * memory), encoder, decode loop, the
  * summed device time of the vocabulary projection + argmax kernel and the
  * number of its launches, and the number of decode steps run. */
 typedef struct {
@@ -176,8 +177,16 @@ typedef struct {
 } marian_hip_stats;
 int marian_hip_last_stats(const marian_hip_engine* engine, marian_hip_stats* stats);
 /* When enabled, the engine records events around each vocab kernel launch so
- * marian_hip_stats.vocab_kernel_ms is filled (small overhead). */
+ * marian_hip_stats.vocab_kernel_ms is filled, and one event at the end of
+ * every decode step (small overhead). */
 int marian_hip_set_kernel_timing(marian_hip_engine* engine, int enabled);
+/* Per decode step of the last translate call: the number of active rows the
+ * step ran on and, when kernel timing was enabled, the device time at which
+ * the step's tokens were final (ms from the batch start, else 0).  Writes
+ * min(cap, steps) entries and the step count to *n_steps.  A row that
+ * produced c tokens completed at step c-1. */
+int marian_hip_last_step_trace(const marian_hip_engine* engine, uint32_t* active_rows,
+                               float* step_end_ms, size_t cap, size_t* n_steps);
 
 /* ---- op-level entry points: device pointers, `stream` is a hipStream_t or
  * NULL for the default stream.  They return MARIAN_HIP_ERR_INVALID_INPUT for
@@ -205,7 +214,7 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
 
 /* Variable-length attention, one query row per (row, head) wave:
  * query row i belongs to sequence seq_of_row[i] and attends over key rows
- * [cu_k[s], cu_k[s+1]); max_keys bounds every range (at most 4096).
+ * [cu_k[s], cu_k[s+1]); max_keys bounds every range (at most 4096); heads <= 8.
  * Row strides in elements.  in_bf16 != 0 reads q/k/v as
  * bfloat16 (converted exactly to fp32); out is fp32 [rows, heads*64]. */
 int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
@@ -215,7 +224,8 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
 
 /* Vocabulary projection + bias + generation mask + argmax per row:
  * token[m] = argmax_v (acc[m,v] * (1/(xa[m]*mult[v])) + bias[v]) with ties to
- * the lowest id; logits [M,V] optional.  xq/xa are the quantized rows. */
+ * the lowest id; logits [M,V] optional.  xq/xa are the quantized rows;
+ * K (the model width) must be a multiple of 64 and at most 512. */
 int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_t K,
                             const int8_t* emb, const float* emb_mult, const float* bias,
                             int64_t V, uint32_t flags, int32_t* token, float* logits,

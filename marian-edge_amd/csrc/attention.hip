@@ -4,11 +4,13 @@
 // Semantics of attention_into (tensor.rs:251-318): score_k = (q . k_k) * 1/8,
 // softmax as max, exp(s - max), sum, multiply by 1/sum, then
 // out = sum_k p_k v_k in key order.  Mapping onto the wave:
+//   * K and V rows arrive by coalesced 16-byte loads and pass through a
+//     per-head LDS tile;
 //   * scores: lane = key (keys lane, lane+64, ...), sequential 64-term dot
 //     with q broadcast from SGPRs;
 //   * softmax: wave max, canonical exp, lane partial sums + xor butterfly;
 //   * PV: lane = output dim, keys accumulated in order (the reference order);
-//     probabilities are broadcast from LDS.
+//     probabilities are broadcast from the score lanes through SGPRs.
 // The score row never leaves the chip.  Sequences are packed (cu_seqlens), so
 // there is no padding and no mask; keys beyond a row's count are never read.
 // The three modes differ only in where a row's keys live: its own sequence
@@ -28,46 +30,46 @@ struct Io<float> {
   static __device__ __forceinline__ float at(const void* p, int64_t i) {
     return ((const float*)p)[i];
   }
-  // 64 consecutive values starting at element i (16-byte aligned)
-  static __device__ __forceinline__ void row64(const void* p, int64_t i, float* out) {
-    const float4* v = (const float4*)((const float*)p + i);
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const float4 t = v[c];
-      out[4 * c + 0] = t.x;
-      out[4 * c + 1] = t.y;
-      out[4 * c + 2] = t.z;
-      out[4 * c + 3] = t.w;
-    }
-  }
 };
 template <>
 struct Io<uint16_t> {
   static __device__ __forceinline__ float at(const void* p, int64_t i) {
     return bf16_to_f32(((const uint16_t*)p)[i]);
   }
-  static __device__ __forceinline__ void row64(const void* p, int64_t i, float* out) {
-    const uint4* v = (const uint4*)((const uint16_t*)p + i);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const uint4 t = v[c];
-      const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        out[8 * c + 2 * u + 0] = __uint_as_float(w[u] << 16);
-        out[8 * c + 2 * u + 1] = __uint_as_float(w[u] & 0xFFFF0000u);
-      }
-    }
-  }
 };
 
+// K and V rows of one 64-key chunk move through a per-head LDS tile: 16
+// coalesced float4 loads (four 256-byte rows per instruction) into registers,
+// then stored as [key][dim].  Keys past the row's last key reload that last
+// key, so every load is in bounds and every value finite.
+constexpr int kKRow = kHeadDim + 4;  // padded LDS row (floats), 16-byte aligned
+
+template <typename T>
+__device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
+  if constexpr (sizeof(T) == 4) {
+    return *(const float4*)((const float*)p + off);
+  } else {
+    const uint2 w = *(const uint2*)((const uint16_t*)p + off);
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u));
+  }
+}
+
+// Lane l loads dims 4*(l%16)..+3 of keys first + l/16 + 4i (i < 16), clamped.
+#define MH_LOAD_CHUNK(T, P, BASE, LD, FIRST, NK, LANE, OUT)                                   \
+  _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_) {                                         \
+    const int key_ = min((FIRST) + ((LANE) >> 4) + 4 * i_, (NK)-1);                           \
+    OUT[i_] = load_row4<T>((P), (BASE) + (int64_t)key_ * (LD) + ((LANE)&15) * 4);             \
+  }
+#define MH_STORE_CHUNK(TILE, LANE, IN)                                                         \
+  _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_)                                            \
+      *(float4*)((TILE) + (((LANE) >> 4) + 4 * i_) * kKRow + ((LANE)&15) * 4) = IN[i_];
+
 template <int CH, typename T>
-__global__ __launch_bounds__(1024) void k_attention(AttnArgs a) {
-  extern __shared__ float sP[];  // [heads][CH*64] probabilities
-  __shared__ float sMax[16];
-  const int r = blockIdx.x;
-  const int n = a.rows_dev ? *a.rows_dev : a.rows;
-  if (r >= n) return;
+__global__ __launch_bounds__(512) void k_attention(AttnArgs a) {
+  extern __shared__ float sTile[];  // [heads][64][kKRow]
+  __shared__ float sMax[8];
+  const int r = blockIdx.x;  // < a.rows, the host bound
   const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int D = a.heads * kHeadDim;
 
@@ -77,79 +79,119 @@ __global__ __launch_bounds__(1024) void k_attention(AttnArgs a) {
     const int sq = a.seq_of_row[r];
     key0 = a.cu[sq];
     nk = (int)(a.cu[sq + 1] - a.cu[sq]);
-  } else if (a.mode == ATT_CROSS) {
-    const int slot = a.act[r];
-    key0 = a.cu[slot];
-    nk = (int)(a.cu[slot + 1] - a.cu[slot]);
   } else {
-    key0 = a.kv_base[a.act[r]];
-    nk = a.step + 1;
+    // Speculative: read this row's key range before the device row count.
+    key0 = a.row_key0[r];
+    nk = a.mode == ATT_CROSS ? a.row_nk[r] : a.step + 1;
+    nk = max(nk, 1);
+    key0 = min(max(key0, (int64_t)0), a.max_row - 1);
   }
   // A key range longer than this variant holds would overrun the score
-  // registers and the LDS row: flag it and attend over the first CH*64 keys.
-  if (nk > CH * 64) {
-    if (threadIdx.x == 0 && a.err) *a.err = 2;
-    nk = CH * 64;
-  }
+  // registers: attend over the first CH*64 keys (flagged below for live rows).
+  const bool too_long = nk > CH * 64;
+  if (too_long) nk = CH * 64;
+  const int nch = (nk + 63) >> 6;
+  const int64_t kbase = key0 * a.ldkv + h * kHeadDim;
+  float* tile = sTile + h * 64 * kKRow;
 
-  // q of this head, one element per lane, broadcast through SGPRs.
-  const float qv = Io<T>::at(a.q, (int64_t)r * a.ldq + h * kHeadDim + lane);
-  float qs[kHeadDim];
-#pragma unroll
-  for (int i = 0; i < kHeadDim; ++i)
-    qs[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qv), i));
+  // Keys of a stale row may run past the buffer: its last readable key.
+  const int nk_ld = a.mode == ATT_SEQ ? nk : (int)min((int64_t)nk, a.max_row - key0);
 
+  // Chunk 0's V rows are loaded now (used after the softmax), then K.
+  float4 vreg[16], kreg[16];
+  MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 0, nk_ld, lane, vreg)
+  MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, 0, nk_ld, lane, kreg)
+  // q of this head, one element per lane; broadcast 16 values at a time.
+  const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * kHeadDim + lane));
+  const int n = a.rows_dev ? *a.rows_dev : a.rows;
+  if (r >= n) return;
+  if (too_long && threadIdx.x == 0 && a.err) *a.err = 2;
+
+  // Scores: lane = key within the chunk, 64-term dot in dimension order.  The
+  // next chunk's K rows are loaded while this chunk's dot runs.
   const float scale = 1.0f / sqrtf((float)kHeadDim);
   float s[CH];
-  float mloc = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     s[c] = -INFINITY;
-    const int j = c * 64 + lane;
-    if (c * 64 < nk && j < nk) {
-      float kr[kHeadDim];
-      Io<T>::row64(a.k, (key0 + j) * a.ldkv + h * kHeadDim, kr);
+    if (c < nch) {
+      if (c > 0) __syncthreads();  // the previous chunk's rows have been read
+      MH_STORE_CHUNK(tile, lane, kreg)
+      if (c + 1 < nch) {
+        MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, (c + 1) * 64, nk_ld, lane, kreg)
+      }
+      __syncthreads();
       float dot = -0.0f;
 #pragma unroll
-      for (int i = 0; i < kHeadDim; ++i) dot = dot + qs[i] * kr[i];
-      s[c] = dot * scale;
-      mloc = fmaxf(mloc, s[c]);
+      for (int i0 = 0; i0 < kHeadDim; i0 += 16) {
+        float kr[16], qs[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+          const float4 v = *(const float4*)(tile + lane * kKRow + i0 + i);
+          kr[i] = v.x;
+          kr[i + 1] = v.y;
+          kr[i + 2] = v.z;
+          kr[i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          qs[i] = __int_as_float(__builtin_amdgcn_readlane(qv, i0 + i));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dot = dot + qs[i] * kr[i];
+      }
+      if (c * 64 + lane < nk) s[c] = dot * scale;
     }
   }
+  // V rows of chunk 1 go into the now free K registers (chunk c uses vreg
+  // for even c, kreg for odd c).
+  if (nch > 1) {
+    MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 64, nk_ld, lane, kreg)
+  }
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) mloc = fmaxf(mloc, s[c]);
   const float mx = wave_max(mloc);
+  // exp and the canonical sum: lane partials over its keys in chunk order.
   float part = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int j = c * 64 + lane;
-    if (j < nk) {
+    if (c < nch && c * 64 + lane < nk) {
       s[c] = canon_expf(s[c] - mx);
       part = part + s[c];
+    } else {
+      s[c] = 0.0f;
     }
   }
   const float inv = 1.0f / wave_sum_canon(part);
-  float* ph = sP + h * (CH * 64);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) s[c] = s[c] * inv;
+
+  // out_d = sum_j v[j][d] * p_j in key order; p_j is broadcast from lane
+  // j%64 of chunk j/64 through an SGPR; keys past the last have p = 0, and
+  // adding v * 0 = +-0 leaves the sum bit-identical to skipping them.
+  float o = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int j = c * 64 + lane;
-    if (j < nk) ph[j] = s[c] * inv;
+    if (c < nch) {
+      __syncthreads();  // the tile's previous contents have been read
+      if (c & 1) {
+        MH_STORE_CHUNK(tile, lane, kreg)
+        if (c + 2 < nch) {
+          MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, (c + 2) * 64, nk_ld, lane, kreg)
+        }
+      } else {
+        MH_STORE_CHUNK(tile, lane, vreg)
+        if (c + 2 < nch) {
+          MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, (c + 2) * 64, nk_ld, lane, vreg)
+        }
+      }
+      __syncthreads();
+      const int pc = __float_as_int(s[c]);
+#pragma unroll
+      for (int u = 0; u < 64; ++u)
+        o = o + tile[u * kKRow + lane] * __int_as_float(__builtin_amdgcn_readlane(pc, u));
+    }
   }
-  __syncthreads();
-
-  // out_d = sum_j v[j][d] * p_j, keys in order.
-  const int64_t vbase = key0 * a.ldkv + h * kHeadDim + lane;
-  float o = 0.0f;
-  int j = 0;
-  for (; j + 4 <= nk; j += 4) {
-    const float v0 = Io<T>::at(a.v, vbase + (int64_t)(j + 0) * a.ldkv);
-    const float v1 = Io<T>::at(a.v, vbase + (int64_t)(j + 1) * a.ldkv);
-    const float v2 = Io<T>::at(a.v, vbase + (int64_t)(j + 2) * a.ldkv);
-    const float v3 = Io<T>::at(a.v, vbase + (int64_t)(j + 3) * a.ldkv);
-    o = o + v0 * ph[j + 0];
-    o = o + v1 * ph[j + 1];
-    o = o + v2 * ph[j + 2];
-    o = o + v3 * ph[j + 3];
-  }
-  for (; j < nk; ++j) o = o + Io<T>::at(a.v, vbase + (int64_t)j * a.ldkv) * ph[j];
 
   if (a.out) a.out[(int64_t)r * a.ldo + h * kHeadDim + lane] = o;
   if (a.q8) {
@@ -166,37 +208,35 @@ __global__ __launch_bounds__(1024) void k_attention(AttnArgs a) {
   }
 }
 
+template <int CH, typename T>
+hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
+  const size_t lds = (size_t)a.heads * 64 * kKRow * sizeof(float);
+  static bool attr_set = false;  // the attribute is per kernel, set once
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)k_attention<CH, T>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       8 * 64 * kKRow * (int)sizeof(float));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_attention<CH, T>), dim3(a.rows), dim3(a.heads * 64), lds, s, a);
+  return hipGetLastError();
+}
+
 template <int CH>
 hipError_t launch_ch(const AttnArgs& a, hipStream_t s) {
-  const size_t lds = (size_t)a.heads * CH * 64 * sizeof(float);
-  const dim3 grid(a.rows), block(a.heads * 64);
-  if (a.bf16) {
-    if (lds > 64 * 1024) {
-      hipError_t e = hipFuncSetAttribute((const void*)k_attention<CH, uint16_t>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL((k_attention<CH, uint16_t>), grid, block, lds, s, a);
-  } else {
-    if (lds > 64 * 1024) {
-      hipError_t e = hipFuncSetAttribute((const void*)k_attention<CH, float>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL((k_attention<CH, float>), grid, block, lds, s, a);
-  }
-  return hipGetLastError();
+  return a.bf16 ? launch_t<CH, uint16_t>(a, s) : launch_t<CH, float>(a, s);
 }
 
 }  // namespace
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
-  if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0) return hipErrorInvalidValue;
+  if (a.heads <= 0 || a.heads > 8 || a.max_keys <= 0) return hipErrorInvalidValue;
   if (a.max_keys <= 128) return launch_ch<2>(a, s);
   if (a.max_keys <= 512) return launch_ch<8>(a, s);
   if (a.max_keys <= 1024) return launch_ch<16>(a, s);
-  if (a.max_keys <= 4096 && a.heads <= 8) return launch_ch<64>(a, s);
+  if (a.max_keys <= 4096) return launch_ch<64>(a, s);
   return hipErrorInvalidValue;
 }
 

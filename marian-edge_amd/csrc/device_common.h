@@ -23,31 +23,67 @@ constexpr int kMaxRowsPerCall = 4096;  // engine batch ceiling (LDS scan size)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// Value of lane (l ^ off) for lane l, for off = 1, 2 (DPP quad permutes),
+// 4, 8, 16 (ds_swizzle lane swaps within 32) and 32 (v_permlane32_swap).
+// Exactly the xor pairing of __shfl_xor, without the LDS crossbar.
+template <int OFF>
+__device__ __forceinline__ int xor_lane(int v) {
+  if constexpr (OFF == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (OFF == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (OFF == 4 || OFF == 8 || OFF == 16) {
+    return __builtin_amdgcn_ds_swizzle(v, (OFF << 10) | 0x1F);  // swizzle(SWAP, OFF)
+  } else {
+    static_assert(OFF == 32, "xor_lane offset");
+    const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (__lane_id() < 32) ? (int)sw[1] : (int)sw[0];
+  }
+}
+
+template <int OFF>
+__device__ __forceinline__ float xor_lane_f(float v) {
+  return __int_as_float(xor_lane<OFF>(__float_as_int(v)));
+}
+
+template <int OFF>
+__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)xor_lane<OFF>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)xor_lane<OFF>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Canonical sum of the 64 lane partials: p = p + p[l ^ off] for off = 32,
+// 16, 8, 4, 2, 1 (every lane ends with the same value).
 __device__ __forceinline__ float wave_sum_canon(float p) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) p = p + __shfl_xor(p, off, kWave);
+  p = p + xor_lane_f<32>(p);
+  p = p + xor_lane_f<16>(p);
+  p = p + xor_lane_f<8>(p);
+  p = p + xor_lane_f<4>(p);
+  p = p + xor_lane_f<2>(p);
+  p = p + xor_lane_f<1>(p);
   return p;
 }
 
 __device__ __forceinline__ float wave_max(float p) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) p = fmaxf(p, __shfl_xor(p, off, kWave));
+  p = fmaxf(p, xor_lane_f<32>(p));
+  p = fmaxf(p, xor_lane_f<16>(p));
+  p = fmaxf(p, xor_lane_f<8>(p));
+  p = fmaxf(p, xor_lane_f<4>(p));
+  p = fmaxf(p, xor_lane_f<2>(p));
+  p = fmaxf(p, xor_lane_f<1>(p));
   return p;
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
-  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  const uint32_t l2 = (uint32_t)__shfl_xor((int)lo, off, kWave);
-  const uint32_t h2 = (uint32_t)__shfl_xor((int)hi, off, kWave);
-  return ((uint64_t)h2 << 32) | l2;
-}
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint64_t o = shfl_xor_u64(v, off);
-    v = o > v ? o : v;
-  }
+  v = umax64(v, xor_lane_u64<32>(v));
+  v = umax64(v, xor_lane_u64<16>(v));
+  v = umax64(v, xor_lane_u64<8>(v));
+  v = umax64(v, xor_lane_u64<4>(v));
+  v = umax64(v, xor_lane_u64<2>(v));
+  v = umax64(v, xor_lane_u64<1>(v));
   return v;
 }
 

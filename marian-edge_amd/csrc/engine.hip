@@ -46,7 +46,7 @@ struct DecLayer {
 enum Buf {
   B_META, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
   B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DOQ, B_DOA, B_DY, B_DH, B_DHQ, B_DHA,
-  B_PART, B_OUT, B_COUNT, B_COUNT_
+  B_PART, B_OUT, B_COUNT, B_HIST, B_COUNT_
 };
 
 uint32_t host_positions(uint32_t dim, uint32_t count, float* out) {
@@ -89,6 +89,9 @@ struct marian_hip_engine {
   int* pinned = nullptr;  // host-visible n_active polls
   hipEvent_t ev[5] = {};  // start, encoder end, decode end, two poll slots
   std::vector<hipEvent_t> vocab_ev;
+  std::vector<hipEvent_t> step_ev;
+  std::vector<uint32_t> step_rows;
+  std::vector<float> step_ms;
   marian_hip_stats stats{};
 
   int fail(int code, const char* fmt, ...) {
@@ -142,9 +145,10 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
   if (!m || !out_engine) return MARIAN_HIP_ERR_INVALID_INPUT;
   *out_engine = nullptr;
   if (!m->embedding || !m->embedding_mult || !m->output_bias || !m->vocab || !m->heads ||
-      m->dim != m->heads * kHeadDim || m->dim % 64 || m->dim > 1024 || m->ffn_dim % 64 ||
+      m->dim != m->heads * kHeadDim || m->dim % 64 || m->dim > 512 || m->ffn_dim % 64 ||
+      m->ffn_dim > 2048 ||
       (m->encoder_layers && !m->encoder) || (m->decoder_layers && !m->decoder) ||
-      m->heads > 16)
+      m->heads > 8)
     return MARIAN_HIP_ERR_MODEL;
   auto* E = new marian_hip_engine();
   E->device = device;
@@ -169,8 +173,12 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
   };
   if (hipSetDevice(device) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
   hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) == hipSuccess)
-    E->device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+    char name[256] = {0};
+    if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
+      std::snprintf(name, sizeof name, "%s", prop.name);
+    E->device_name = std::string(name) + " (" + prop.gcnArchName + ")";
+  }
   if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
     return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
 
@@ -268,6 +276,7 @@ void marian_hip_engine_destroy(marian_hip_engine* E) {
   for (auto& ev : E->ev)
     if (ev) hipEventDestroy(ev);
   for (auto& ev : E->vocab_ev) hipEventDestroy(ev);
+  for (auto& ev : E->step_ev) hipEventDestroy(ev);
   if (E->stream) hipStreamDestroy(E->stream);
   delete E;
 }
@@ -291,6 +300,18 @@ int marian_hip_info(const marian_hip_engine* E, char* buf, size_t cap) {
 int marian_hip_last_stats(const marian_hip_engine* E, marian_hip_stats* s) {
   if (!E || !s) return MARIAN_HIP_ERR_INVALID_INPUT;
   *s = E->stats;
+  return MARIAN_HIP_OK;
+}
+
+int marian_hip_last_step_trace(const marian_hip_engine* E, uint32_t* active_rows,
+                               float* step_end_ms, size_t cap, size_t* n_steps) {
+  if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
+  const size_t n = E->step_rows.size();
+  if (n_steps) *n_steps = n;
+  for (size_t i = 0; i < std::min(cap, n); ++i) {
+    if (active_rows) active_rows[i] = E->step_rows[i];
+    if (step_end_ms) step_end_ms[i] = i < E->step_ms.size() ? E->step_ms[i] : 0.0f;
+  }
   return MARIAN_HIP_OK;
 }
 
@@ -364,8 +385,15 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   E->stats = marian_hip_stats{};
 
   // ---- host metadata -> one upload ----
-  std::vector<int32_t> positions(T), seq_of_row(T), act0;
+  // Per token: id, position in its sentence, sentence index; the cu offsets.
+  // Per active row (initially every sequence with a non-zero limit, in
+  // order): its sequence, first KV-cache/output row, source range, previous
+  // token and generation limit.
+  std::vector<int32_t> positions(T), seq_of_row(T);
   std::vector<int64_t> kv_base(B);
+  std::vector<int32_t> r_slot, r_srcn, r_prev;
+  std::vector<uint32_t> r_lim;
+  std::vector<int64_t> r_kv0, r_src0;
   int64_t run = 0;
   for (size_t b = 0; b < B; ++b) {
     for (uint32_t i = offsets[b]; i < offsets[b + 1]; ++i) {
@@ -374,27 +402,46 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     }
     kv_base[b] = run;
     run += limit[b];
-    if (limit[b] > 0) act0.push_back((int32_t)b);
+    if (limit[b] > 0) {
+      r_slot.push_back((int32_t)b);
+      r_kv0.push_back(kv_base[b]);
+      r_src0.push_back(offsets[b]);
+      r_srcn.push_back((int32_t)(offsets[b + 1] - offsets[b]));
+      r_prev.push_back(-1);
+      r_lim.push_back(limit[b]);
+    }
   }
-  const int n_active0 = (int)act0.size();
-  act0.resize(B, 0);
-  // layout: tokens | positions | seq_of_row | cu | limit | act | n_active | kv_base
+  const int n_active0 = (int)r_slot.size();
+  r_slot.resize(B, 0);
+  r_kv0.resize(B, 0);
+  r_src0.resize(B, 0);
+  r_srcn.resize(B, 1);
+  r_prev.resize(B, -1);
+  r_lim.resize(B, 0);
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
-  size_t o_tok = 0, o_pos = align(o_tok + 4 * (size_t)T), o_seq = align(o_pos + 4 * (size_t)T),
-         o_cu = align(o_seq + 4 * (size_t)T), o_lim = align(o_cu + 4 * (B + 1)),
-         o_act = align(o_lim + 4 * B), o_nact = align(o_act + 4 * B),
-         o_kvb = align(o_nact + 4), o_prev = align(o_kvb + 8 * B), meta_bytes = align(o_prev + 4 * B);
+  size_t cur = 0;
+  auto place = [&](size_t bytes) {
+    const size_t o = cur;
+    cur = align(cur + bytes);
+    return o;
+  };
+  const size_t o_tok = place(4ull * T), o_pos = place(4ull * T), o_seq = place(4ull * T),
+               o_cu = place(4 * (B + 1)), o_nact = place(4), o_rslot = place(4 * B), o_rkv0 = place(8 * B),
+               o_rsrc0 = place(8 * B), o_rsrcn = place(4 * B), o_rprev = place(4 * B),
+               o_rlim = place(4 * B);
+  const size_t meta_bytes = cur;
   std::vector<char> meta(meta_bytes, 0);
   std::memcpy(meta.data() + o_tok, tokens, 4 * (size_t)T);
   std::memcpy(meta.data() + o_pos, positions.data(), 4 * (size_t)T);
   std::memcpy(meta.data() + o_seq, seq_of_row.data(), 4 * (size_t)T);
   std::memcpy(meta.data() + o_cu, offsets, 4 * (B + 1));
-  std::memcpy(meta.data() + o_lim, limit.data(), 4 * B);
-  std::memcpy(meta.data() + o_act, act0.data(), 4 * B);
   std::memcpy(meta.data() + o_nact, &n_active0, 4);
-  std::memcpy(meta.data() + o_kvb, kv_base.data(), 8 * B);
-  std::vector<int32_t> prev0(B, -1);
-  std::memcpy(meta.data() + o_prev, prev0.data(), 4 * B);
+  std::memcpy(meta.data() + o_rslot, r_slot.data(), 4 * B);
+  std::memcpy(meta.data() + o_rkv0, r_kv0.data(), 8 * B);
+  std::memcpy(meta.data() + o_rsrc0, r_src0.data(), 8 * B);
+  std::memcpy(meta.data() + o_rsrcn, r_srcn.data(), 4 * B);
+  std::memcpy(meta.data() + o_rprev, r_prev.data(), 4 * B);
+  std::memcpy(meta.data() + o_rlim, r_lim.data(), 4 * B);
 
   const size_t cache_rows = std::max<uint64_t>(total_cap, 1);
   char* dmeta = (char*)E->get(B_META, meta_bytes);
@@ -423,10 +470,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   float* DH = (float*)E->get(B_DH, 4ull * B * F);
   int8_t* DHQ = (int8_t*)E->get(B_DHQ, B * F);
   float* DHA = (float*)E->get(B_DHA, 4ull * B);
-  const int nparts = skinny_groups((int)E->V);
+  const int nparts = argmax_groups((int)E->V, (int)E->d);
   uint64_t* PART = (uint64_t*)E->get(B_PART, 8ull * B * nparts);
   int32_t* OUT = (int32_t*)E->get(B_OUT, 4ull * cache_rows);
   uint32_t* COUNT = (uint32_t*)E->get(B_COUNT, 4ull * B);
+  uint32_t* HIST = (uint32_t*)E->get(B_HIST, 4ull * (gen_limit + 1));
   for (int b = 0; b < B_COUNT_; ++b)
     if (!E->buf[b]) return E->fail(MARIAN_HIP_ERR_DEVICE, "device allocation failed");
 
@@ -434,16 +482,20 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   int32_t* d_pos = (int32_t*)(dmeta + o_pos);
   int32_t* d_seq = (int32_t*)(dmeta + o_seq);
   uint32_t* d_cu = (uint32_t*)(dmeta + o_cu);
-  uint32_t* d_lim = (uint32_t*)(dmeta + o_lim);
-  int* d_act = (int*)(dmeta + o_act);
   int* d_nact = (int*)(dmeta + o_nact);
-  int64_t* d_kvb = (int64_t*)(dmeta + o_kvb);
-  int32_t* d_prev = (int32_t*)(dmeta + o_prev);
+  RowMeta rm;
+  rm.slot = (int*)(dmeta + o_rslot);
+  rm.kv0 = (int64_t*)(dmeta + o_rkv0);
+  rm.src0 = (int64_t*)(dmeta + o_rsrc0);
+  rm.srcn = (int32_t*)(dmeta + o_rsrcn);
+  rm.prev = (int32_t*)(dmeta + o_rprev);
+  rm.limit = (uint32_t*)(dmeta + o_rlim);
 
-  MH_HIP(hipEventRecord(E->ev[0], s));
   MH_HIP(hipMemcpyAsync(dmeta, meta.data(), meta_bytes, hipMemcpyHostToDevice, s));
   MH_HIP(hipMemsetAsync(E->err_flag, 0, sizeof(int), s));
   MH_HIP(hipMemsetAsync(COUNT, 0, 4 * B, s));
+  // The timed region starts with the packed inputs resident in HBM.
+  MH_HIP(hipEventRecord(E->ev[0], s));
 
   // ---- encoder over packed rows ----
   {
@@ -516,6 +568,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       MH_HIP(hipEventCreate(&ev));
       E->vocab_ev.push_back(ev);
     }
+    while (E->step_ev.size() < gen_limit) {
+      hipEvent_t ev;
+      MH_HIP(hipEventCreate(&ev));
+      E->step_ev.push_back(ev);
+    }
   }
   std::vector<uint32_t> remaining(gen_limit + 1, 0);  // rows with limit > t
   for (size_t b = 0; b < B; ++b) remaining[0] += limit[b] > 0;
@@ -524,12 +581,13 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     for (size_t b = 0; b < B; ++b) ends[limit[b]]++;
     for (uint32_t t = 1; t <= gen_limit; ++t) remaining[t] = remaining[t - 1] - ends[t];
   }
+  int rows_ub = 0;  // host bound on this step's active rows
   auto dgemm = [&](const int8_t* A, const float* a, const Lin& L, int mode, const Epilogue& e) {
     GemmArgs g;
     g.A = A;
     g.a = a;
     g.lda = L.K;
-    g.M = Bi;
+    g.M = rows_ub;
     g.M_dev = d_nact;
     g.K = L.K;
     g.W = L.w;
@@ -553,7 +611,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   uint32_t vocab_launches = 0;
   bool done = n_active0 == 0;
   for (uint32_t t = 0; t < gen_limit && !done; ++t) {
-    const int rows_ub = (int)remaining[t];
+    rows_ub = (int)remaining[t];
     if (rows_ub == 0) break;
     {
       EmbedArgs ea;
@@ -562,8 +620,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ea.pos = E->pos;
       ea.scale = E->emb_scale;
       ea.d = d;
-      ea.act = d_act;
-      ea.prev = d_prev;
+      ea.row_prev = rm.prev;
       ea.step = (int)t;
       ea.rows = rows_ub;
       ea.rows_dev = d_nact;
@@ -583,8 +640,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         e.ldo = d;
         e.kcache = kc;
         e.vcache = vc;
-        e.act = d_act;
-        e.kv_base = d_kvb;
+        e.row_kv0 = rm.kv0;
         e.step = (int)t;
         e.d = d;
         MH_HIP(dgemm(DXQ, DXA, L.self_qkv, EPI_QKV_CACHE, e));
@@ -599,8 +655,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       sa.heads = H;
       sa.rows = rows_ub;
       sa.rows_dev = d_nact;
-      sa.act = d_act;
-      sa.kv_base = d_kvb;
+      sa.row_key0 = rm.kv0;
+      sa.max_row = (int64_t)cache_rows;
       sa.step = (int)t;
       sa.max_keys = (int)t + 1;
       sa.q8 = DOQ;
@@ -621,8 +677,9 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ca.heads = H;
       ca.rows = rows_ub;
       ca.rows_dev = d_nact;
-      ca.act = d_act;
-      ca.cu = d_cu;
+      ca.row_key0 = rm.src0;
+      ca.row_nk = rm.srcn;
+      ca.max_row = T;
       ca.max_keys = (int)Lmax;
       ca.q8 = DOQ;
       ca.qa = DOA;
@@ -653,16 +710,15 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       FinalizeArgs f;
       f.partials = PART;
       f.nparts = nparts;
-      f.act = d_act;
+      f.rows = rm;
       f.n_active = d_nact;
-      f.prev = d_prev;
-      f.limit = d_lim;
       f.out_tok = OUT;
-      f.out_base = d_kvb;
       f.count = COUNT;
       f.step = (int)t;
       f.flags = flags;
+      f.active_hist = HIST;
       MH_HIP(launch_finalize(f, s));
+      if (E->kernel_timing) MH_HIP(hipEventRecord(E->step_ev[t], s));
     }
     ++steps;
     if ((t + 1) % kPoll == 0) {
@@ -682,6 +738,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   std::vector<uint32_t> count(B);
   std::vector<int32_t> gen(cache_rows);
   int err_host = 0;
+  E->step_rows.assign(steps, 0);
+  if (steps) MH_HIP(hipMemcpyAsync(E->step_rows.data(), HIST, 4ull * steps, hipMemcpyDeviceToHost, s));
   MH_HIP(hipMemcpyAsync(count.data(), COUNT, 4 * B, hipMemcpyDeviceToHost, s));
   MH_HIP(hipMemcpyAsync(gen.data(), OUT, 4 * cache_rows, hipMemcpyDeviceToHost, s));
   MH_HIP(hipMemcpyAsync(&err_host, E->err_flag, sizeof(int), hipMemcpyDeviceToHost, s));
@@ -710,6 +768,9 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     E->stats.vocab_kernel_ms = sum;
     E->stats.vocab_kernel_launches = vocab_launches;
   }
+  E->step_ms.assign(steps, 0.0f);
+  if (E->kernel_timing)
+    for (uint32_t i = 0; i < steps; ++i) hipEventElapsedTime(&E->step_ms[i], E->ev[0], E->step_ev[i]);
   if (err_host) return E->fail(MARIAN_HIP_ERR_INFERENCE, "activation is not finite");
 
   size_t total = 0;

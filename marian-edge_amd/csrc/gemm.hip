@@ -15,10 +15,8 @@
 namespace mh {
 namespace {
 
-constexpr int kSkinnyRows = 64;     // rows per pass (A chunk in LDS)
-constexpr int kSkinnyKChunk = 512;  // K per pass
-constexpr int kSkinnyLds = kSkinnyKChunk + 16;  // padded LDS row (bytes)
-constexpr int kSkinnyCols = 64;     // columns per workgroup (4 waves x 16)
+constexpr int kSkinnyRows = 64;    // rows per pass of the skinny kernel
+constexpr int kSkinnyMaxK = 2048;  // 8 waves x 4 k-steps x 64
 
 constexpr int kTile = 128;
 constexpr int kTileK = 64;
@@ -27,118 +25,254 @@ constexpr int kTileLds = kTileK + 16;  // padded LDS row (bytes)
 __device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM: one workgroup = 4 waves = 64 output columns.  The 16 columns of
-// a wave are held as MFMA B fragments in registers for a whole K chunk, A
-// streams through LDS 64 rows at a time, so each weight byte is read once per
-// 64 rows (once per decode step for the usual M <= 64).
+// Skinny GEMM (decode and small M).  One workgroup owns CT*16 output columns
+// for every row; its NW waves split K (wave w takes k-steps w, w+NW, ...),
+// load their A and B fragments straight from memory (A is small and L2
+// resident, B = the weights, streamed once per 64 rows), and add their exact
+// i32 partial tiles into LDS with integer atomics, so the reduction order is
+// irrelevant.  The epilogue then walks the LDS tile row-major: consecutive
+// threads write consecutive columns.
 // ---------------------------------------------------------------------------
-template <int MODE>
-__global__ __launch_bounds__(256) void k_gemm_skinny(GemmArgs g, Epilogue e) {
-  __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kSkinnyLds];
-  __shared__ uint64_t sKey[4][kSkinnyRows];
-  const int M = g.M_dev ? *g.M_dev : g.M;
-  if (M <= 0) return;
+template <int MODE, int CT, int NW, int KSW>
+__global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
+  constexpr int NT = NW * 64;
+  constexpr int COLS = CT * 16;
+  constexpr int LDC = COLS + 1;          // padded LDS row (i32)
+  constexpr int ROWS_PER_THREAD = kSkinnyRows * COLS / NT;
+  __shared__ int32_t sAcc[kSkinnyRows * LDC];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int ncol = blockIdx.x * kSkinnyCols + wave * 16 + (lane & 15);
-  const bool col_ok = ncol < g.N;
+  const int n0 = blockIdx.x * COLS;
   const int kq = (lane >> 4) * 16;
+  const int ksteps = g.K >> 6;
+  // g.M bounds the rows on the host side; every row below it is allocated,
+  // so the first row chunk's activations are loaded before the device row
+  // count (g.M_dev) is known.
+  const int Mh = g.M;
+
+  // Every weight fragment of this wave (k-steps wave, wave+NW, ...).
+  v4i bf[KSW][CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int n = min(n0 + ct * 16 + (lane & 15), g.N - 1);
+    const int8_t* wr = g.W + (int64_t)n * g.K + kq;
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int s = wave + NW * i;
+      bf[i][ct] = s < ksteps ? *(const v4i*)(wr + s * 64) : zero4();
+    }
+  }
+  // First chunk's activation fragments.
+  v4i af[KSW][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int m = mt * 16 + (lane & 15);
+    const int8_t* ar = g.A + (int64_t)min(m, Mh - 1) * g.lda + kq;
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      const int s = wave + NW * i;
+      af[i][mt] = (s < ksteps && mt * 16 < Mh) ? *(const v4i*)(ar + s * 64) : zero4();
+    }
+  }
+  // Epilogue operands: each thread always handles the same column.
+  const int ec = tid % COLS;
+  const int en = min(n0 + ec, g.N - 1);
+  const float ewm = g.wmult[en], ebias = g.bias[en];
+  float am[ROWS_PER_THREAD];
+#pragma unroll
+  for (int k = 0; k < ROWS_PER_THREAD; ++k)
+    am[k] = g.a[min(tid / COLS + k * (NT / COLS), Mh - 1)];
+  const int M = g.M_dev ? *g.M_dev : g.M;
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
-    v4i acc[4] = {zero4(), zero4(), zero4(), zero4()};
-    for (int k0 = 0; k0 < g.K; k0 += kSkinnyKChunk) {
-      const int kc = min(kSkinnyKChunk, g.K - k0);
-      const int ksteps = kc >> 6;
-      v4i bf[8];
-      const int8_t* wrow = g.W + (int64_t)(col_ok ? ncol : 0) * g.K + k0 + kq;
+    if (m0 > 0) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
-        bf[s] = (s < ksteps && col_ok) ? *(const v4i*)(wrow + s * 64) : zero4();
-      __syncthreads();  // previous chunk's LDS reads are done
-      const int cpr = kc >> 4;  // 16-byte chunks per row
-      for (int c = tid; c < kSkinnyRows * cpr; c += 256) {
-        const int row = c / cpr, cc = c - row * cpr;
-        const int m = m0 + row;
-        v4i v = zero4();
-        if (m < M) v = *(const v4i*)(g.A + (int64_t)m * g.lda + k0 + cc * 16);
-        *(v4i*)(sA + row * kSkinnyLds + cc * 16) = v;
-      }
-      __syncthreads();
+      for (int mt = 0; mt < 4; ++mt) {
+        const int m = m0 + mt * 16 + (lane & 15);
+        const int8_t* ar = g.A + (int64_t)min(m, M - 1) * g.lda + kq;
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
-        if (m0 + ms * 16 < M) {
-          const int8_t* arow = sA + (ms * 16 + (lane & 15)) * kSkinnyLds + kq;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            if (s < ksteps) {
-              const v4i af = *(const v4i*)(arow + s * 64);
-              acc[ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[s], acc[ms], 0, 0, 0);
-            }
-          }
+        for (int i = 0; i < KSW; ++i) {
+          const int s = wave + NW * i;
+          af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? *(const v4i*)(ar + s * 64) : zero4();
         }
+      }
+#pragma unroll
+      for (int k = 0; k < ROWS_PER_THREAD; ++k)
+        am[k] = g.a[min(m0 + tid / COLS + k * (NT / COLS), M - 1)];
+    }
+    for (int i = tid; i < kSkinnyRows * LDC; i += NT) sAcc[i] = 0;
+    __syncthreads();
+    const int mt_n = min(4, (M - m0 + 15) >> 4);  // live 16-row tiles (uniform)
+    v4i acc[4][CT];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[mt][ct] = zero4();
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      if (wave + NW * i < ksteps) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          if (mt < mt_n)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+              acc[mt][ct] =
+                  __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i][mt], bf[i][ct], acc[mt][ct], 0, 0, 0);
       }
     }
+    // Lane l holds rows 4*(l/16)+r of column l%16 of each 16x16 tile.  Rows
+    // at or past M carry garbage and are never stored.
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+      if (mt < mt_n)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            atomicAdd(&sAcc[(mt * 16 + (lane >> 4) * 4 + r) * LDC + ct * 16 + (lane & 15)],
+                      acc[mt][ct][r]);
+    __syncthreads();
 
-    // Epilogue.  Lane l holds rows 4*(l/16)+r (r = 0..3) of column l%16.
-    if (MODE == EPI_ARGMAX) {
+    const int n = n0 + ec;
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
-        if (m0 + ms * 16 < M) {
+    for (int k = 0; k < ROWS_PER_THREAD; ++k) {
+      const int row = tid / COLS + k * (NT / COLS);
+      const int m = m0 + row;
+      if (m >= M || n >= g.N) continue;
+      const int32_t iv = sAcc[row * LDC + ec];
+      float y = dequant(iv, am[k], ewm, ebias);
+      if (e.relu) y = y > 0.0f ? y : 0.0f;
+      if (MODE == EPI_QKV_CACHE) {
+        if (n < e.d) {
+          e.out[(int64_t)m * e.ldo + n] = y;
+        } else {
+          const int64_t crow = e.row_kv0[m] + e.step;
+          if (n < 2 * e.d)
+            e.kcache[crow * e.d + (n - e.d)] = y;
+          else
+            e.vcache[crow * e.d + (n - 2 * e.d)] = y;
+        }
+      } else {
+        if (e.out) e.out[(int64_t)m * e.ldo + n] = y;
+        if (e.out_i32) e.out_i32[(int64_t)m * e.ldi + n] = iv;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Vocabulary projection + bias + generation mask + argmax (the tied output
+// embedding, N = vocab).  One workgroup = 4 waves = 128 columns; every wave
+// owns two 16-column tiles for the whole K, so its weight fragments (all of
+// them, issued at once) stay in registers across row chunks and no cross-wave
+// reduction of accumulators is needed.  The activation rows are staged once
+// per workgroup in LDS.  Each row's best (logit, id) key over the workgroup's
+// columns is written as one partial; the step finalizer reduces the partials.
+// ---------------------------------------------------------------------------
+constexpr int kVocabCT = 2;                       // column tiles per wave
+constexpr int kVocabCols = 4 * 16 * kVocabCT;     // 128 columns per workgroup
+constexpr int kVocabMaxK = 512;                   // K held in registers
+constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
+
+__global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
+  constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
+  __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
+  __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int kq = (lane >> 4) * 16;
+  const int ksteps = g.K >> 6;
+  const int nbase = blockIdx.x * kVocabCols + wave * 16 * kVocabCT;
+
+  // Weight fragments for the wave's columns over all of K, issued first.
+  v4i bf[kVocabCT][kVocabMaxK / 64];
+  int ncol[kVocabCT];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + ms * 16 + (lane >> 4) * 4 + r;
-            uint64_t key = 0;
-            if (m < M && col_ok) {
-              const float y = dequant(acc[ms][r], g.a[m], g.wmult[ncol], g.bias[ncol]);
-              const bool masked = !(e.flags & 2u) && generation_masked((uint32_t)ncol);
-              if (e.logits) e.logits[(int64_t)m * e.ldl + ncol] = masked ? -INFINITY : y;
-              if (!masked && y == y) key = argmax_key(y, (uint32_t)ncol);
-            }
+  for (int ct = 0; ct < kVocabCT; ++ct) {
+    ncol[ct] = nbase + ct * 16 + (lane & 15);
+    const int8_t* wr = g.W + (int64_t)min(ncol[ct], g.N - 1) * g.K + kq;
 #pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-              const uint64_t o = shfl_xor_u64(key, off);
-              key = o > key ? o : key;
-            }
-            if ((lane & 15) == 0) sKey[wave][ms * 16 + (lane >> 4) * 4 + r] = key;
+    for (int s = 0; s < kVocabMaxK / 64; ++s)
+      bf[ct][s] = s < ksteps ? *(const v4i*)(wr + s * 64) : zero4();
+  }
+  // Epilogue operands of this lane's columns.
+  float wm[kVocabCT], bi[kVocabCT];
+  bool live[kVocabCT];
+#pragma unroll
+  for (int ct = 0; ct < kVocabCT; ++ct) {
+    const int n = min(ncol[ct], g.N - 1);
+    wm[ct] = g.wmult[n];
+    bi[ct] = g.bias[n];
+    live[ct] = ncol[ct] < g.N && ((e.flags & 2u) || !generation_masked((uint32_t)ncol[ct]));
+  }
+  const int M = g.M_dev ? *g.M_dev : g.M;
+  const int cpr = g.K >> 4;  // 16-byte chunks per activation row
+
+  for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
+    const int rows = min(kSkinnyRows, M - m0);
+    for (int c = tid; c < rows * cpr; c += 256) {
+      const int row = c / cpr, cc = c - row * cpr;
+      *(v4i*)(sA + row * kVocabLds + cc * 16) =
+          *(const v4i*)(g.A + (int64_t)(m0 + row) * g.lda + cc * 16);
+    }
+    __syncthreads();
+    const int mt_n = (rows + 15) >> 4;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt < mt_n) {
+        v4i acc[kVocabCT] = {zero4(), zero4()};
+        const int8_t* arow = sA + (mt * 16 + (lane & 15)) * kVocabLds + kq;
+#pragma unroll
+        for (int s = 0; s < kVocabMaxK / 64; ++s) {
+          if (s < ksteps) {
+            const v4i af = *(const v4i*)(arow + s * 64);
+#pragma unroll
+            for (int ct = 0; ct < kVocabCT; ++ct)
+              acc[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[ct][s], acc[ct], 0, 0, 0);
           }
         }
-      }
-      __syncthreads();
-      if (tid < kSkinnyRows && m0 + tid < M) {
-        uint64_t best = sKey[0][tid];
+        // Lane holds rows 4*(lane/16)+r of this tile and column lane%16 of
+        // each of its column tiles: dequantize in registers, keep the best of
+        // its columns per row, and park it in LDS.
 #pragma unroll
-        for (int w = 1; w < 4; ++w) best = sKey[w][tid] > best ? sKey[w][tid] : best;
-        e.partials[(int64_t)(m0 + tid) * e.partial_ld + blockIdx.x] = best;
-      }
-    } else {
+        for (int r = 0; r < 4; ++r) {
+          const int lr = mt * 16 + (lane >> 4) * 4 + r;
+          uint64_t key = 0;
+          if (lr < rows) {
+            const int m = m0 + lr;
+            const float am = g.a[m];
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
-        if (m0 + ms * 16 < M) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + ms * 16 + (lane >> 4) * 4 + r;
-            if (m < M && col_ok) {
-              const int32_t iv = acc[ms][r];
-              float y = dequant(iv, g.a[m], g.wmult[ncol], g.bias[ncol]);
-              if (e.relu) y = y > 0.0f ? y : 0.0f;
-              if (MODE == EPI_QKV_CACHE) {
-                if (ncol < e.d) {
-                  e.out[(int64_t)m * e.ldo + ncol] = y;
-                } else {
-                  const int64_t crow = e.kv_base[e.act[m]] + e.step;
-                  if (ncol < 2 * e.d)
-                    e.kcache[crow * e.d + (ncol - e.d)] = y;
-                  else
-                    e.vcache[crow * e.d + (ncol - 2 * e.d)] = y;
-                }
-              } else {
-                if (e.out) e.out[(int64_t)m * e.ldo + ncol] = y;
-                if (e.out_i32) e.out_i32[(int64_t)m * e.ldi + ncol] = iv;
+            for (int ct = 0; ct < kVocabCT; ++ct) {
+              const float y = dequant(acc[ct][r], am, wm[ct], bi[ct]);
+              if (e.logits && ncol[ct] < g.N)
+                e.logits[(int64_t)m * e.ldl + ncol[ct]] = live[ct] ? y : -INFINITY;
+              if (live[ct] && y == y) {
+                const uint64_t k = argmax_key(y, (uint32_t)ncol[ct]);
+                key = k > key ? k : key;
               }
             }
           }
+          sK[lr * (KEYS + 1) + wave * 16 + (lane & 15)] = key;
         }
       }
     }
+    __syncthreads();
+    // 4 threads per row reduce its 64 parked keys.
+    {
+      const int row = tid >> 2, part = tid & 3;
+      uint64_t best = 0;
+      if (row < rows) {
+#pragma unroll
+        for (int j = 0; j < KEYS / 4; ++j) {
+          const uint64_t k = sK[row * (KEYS + 1) + part * (KEYS / 4) + j];
+          best = k > best ? k : best;
+        }
+      }
+      best = umax64(best, xor_lane_u64<1>(best));
+      best = umax64(best, xor_lane_u64<2>(best));
+      if (row < rows && part == 0)
+        e.partials[(int64_t)(m0 + row) * e.partial_ld + blockIdx.x] = best;
+    }
+    __syncthreads();
   }
 }
 
@@ -231,26 +365,47 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e) {
 
 }  // namespace
 
-int skinny_groups(int N) { return (N + kSkinnyCols - 1) / kSkinnyCols; }
+// Columns per skinny workgroup: wide enough that the vocabulary projection
+// does not re-read the activations too often, narrow enough that the small
+// decode GEMMs still spread over many CUs.
+int skinny_cols(int N) { return N >= 8192 ? 64 : (N >= 1024 ? 32 : 16); }
+int skinny_groups(int N) { return (N + skinny_cols(N) - 1) / skinny_cols(N); }
+int argmax_groups(int N, int /*K*/) { return (N + kVocabCols - 1) / kVocabCols; }
 
-hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s) {
-  if (g.K <= 0 || g.K % 64 || g.N <= 0) return hipErrorInvalidValue;
-  if (!g.M_dev && g.M <= 0) return hipSuccess;
-  const dim3 grid(skinny_groups(g.N)), block(256);
-  switch (mode) {
-    case EPI_STORE:
-      hipLaunchKernelGGL(k_gemm_skinny<EPI_STORE>, grid, block, 0, s, g, e);
-      break;
-    case EPI_QKV_CACHE:
-      hipLaunchKernelGGL(k_gemm_skinny<EPI_QKV_CACHE>, grid, block, 0, s, g, e);
-      break;
-    case EPI_ARGMAX:
-      hipLaunchKernelGGL(k_gemm_skinny<EPI_ARGMAX>, grid, block, 0, s, g, e);
-      break;
-    default:
-      return hipErrorInvalidValue;
+template <int MODE, int NW, int KSW>
+static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
+  const dim3 grid(skinny_groups(g.N)), block(NW * 64);
+  switch (skinny_cols(g.N)) {
+    case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW>), grid, block, 0, s, g, e); break;
+    case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW>), grid, block, 0, s, g, e); break;
+    default: hipLaunchKernelGGL((k_gemm_skinny<MODE, 1, NW, KSW>), grid, block, 0, s, g, e); break;
   }
   return hipGetLastError();
+}
+
+// Waves and per-wave k-steps by K: long K (the FFN down-projection) spreads
+// over 8 waves; each wave holds its k-steps' fragments in registers.
+template <int MODE>
+static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
+  const int ksteps = g.K >> 6;
+  if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1>(g, e, s);
+  if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2>(g, e, s);
+  if (ksteps <= 16) return launch_skinny_k<MODE, 4, 4>(g, e, s);
+  return launch_skinny_k<MODE, 8, 4>(g, e, s);
+}
+
+hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s) {
+  if (g.K <= 0 || g.K % 64 || g.K > kSkinnyMaxK || g.N <= 0 || g.M <= 0) return hipErrorInvalidValue;
+    switch (mode) {
+    case EPI_STORE: return launch_skinny_mode<EPI_STORE>(g, e, s);
+    case EPI_QKV_CACHE: return launch_skinny_mode<EPI_QKV_CACHE>(g, e, s);
+    case EPI_ARGMAX:
+      if (g.K > kVocabMaxK) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(k_vocab_argmax, dim3((g.N + kVocabCols - 1) / kVocabCols), dim3(256), 0,
+                         s, g, e);
+      return hipGetLastError();
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
@@ -262,7 +417,8 @@ hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s)
 }
 
 hipError_t launch_gemm_store(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
-  if (g.M_dev || g.M <= kSkinnyRows) return launch_gemm_skinny(g, EPI_STORE, e, s);
+  if (g.M_dev || (g.M <= kSkinnyRows && g.K <= kSkinnyMaxK))
+    return launch_gemm_skinny(g, EPI_STORE, e, s);
   return launch_gemm_tile(g, e, s);
 }
 

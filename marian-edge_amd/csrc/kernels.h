@@ -30,11 +30,10 @@ struct Epilogue {
   int64_t ldi = 0;
   int relu = 0;
   // EPI_QKV_CACHE: columns [d, 2d) -> kcache, [2d, 3d) -> vcache, at cache row
-  // kv_base[act[m]] + step.
+  // row_kv0[m] + step (the row's sequence's first cache row).
   float* kcache = nullptr;
   float* vcache = nullptr;
-  const int* act = nullptr;
-  const int64_t* kv_base = nullptr;
+  const int64_t* row_kv0 = nullptr;
   int step = 0;
   int d = 0;
   // EPI_ARGMAX: per-row best key of each 64-column group -> partials[m*ld + g]
@@ -45,8 +44,9 @@ struct Epilogue {
   uint32_t flags = 0;  // bit 1: no generation mask
 };
 
-// Column groups of the skinny kernel (the argmax partial count per row).
+// Column groups of the skinny kernel, and the argmax partial count per row.
 int skinny_groups(int N);
+int argmax_groups(int N, int K);
 // Skinny (M up to a few hundred, weights streamed once per 64 rows) MFMA GEMM.
 hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s);
 // LDS-tiled 128x128 MFMA GEMM for large M (EPI_STORE only).
@@ -71,9 +71,8 @@ struct EmbedArgs {
   // encoder rows: token and position per row
   const int32_t* tokens = nullptr;
   const int32_t* positions = nullptr;
-  // decoder rows: token = prev[act[r]] (negative: position only), position = step
-  const int* act = nullptr;
-  const int32_t* prev = nullptr;
+  // decoder rows: token = row_prev[r] (negative: position only), position = step
+  const int32_t* row_prev = nullptr;
   int step = 0;
   int rows = 0;
   const int* rows_dev = nullptr;
@@ -99,11 +98,15 @@ struct AttnArgs {
   // ATT_SEQ: keys of row r are [cu[seq_of_row[r]], cu[seq_of_row[r]+1])
   const int* seq_of_row = nullptr;
   const uint32_t* cu = nullptr;
-  // ATT_CROSS: keys of row r are [cu[act[r]], cu[act[r]+1]);
-  // ATT_SELF: keys are kv_base[act[r]] + [0, step]
-  const int* act = nullptr;
-  const int64_t* kv_base = nullptr;
+  // ATT_CROSS: keys of row r are row_key0[r] + [0, row_nk[r]);
+  // ATT_SELF: keys are row_key0[r] + [0, step]
+  const int64_t* row_key0 = nullptr;
+  const int32_t* row_nk = nullptr;
   int step = 0;
+  // ATT_CROSS / ATT_SELF: key rows of the K/V buffers are < max_row.  Rows at
+  // or past the device row count read their (stale) ranges clamped to this
+  // bound before the count is known, and are then discarded.
+  int64_t max_row = 0;
   int max_keys = 0;  // upper bound on keys per row (selects the kernel variant)
   float* out = nullptr;
   int64_t ldo = 0;
@@ -113,18 +116,26 @@ struct AttnArgs {
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
+// Per-row decode metadata, rebuilt in active-row order by the finalizer.
+struct RowMeta {
+  int* slot = nullptr;        // sequence of each active row
+  int64_t* kv0 = nullptr;     // first KV-cache (and output) row of that sequence
+  int64_t* src0 = nullptr;    // first encoder row of that sequence
+  int32_t* srcn = nullptr;    // its source length
+  int32_t* prev = nullptr;    // its last emitted token (-1 before the first step)
+  uint32_t* limit = nullptr;  // its generation limit
+};
+
 struct FinalizeArgs {
   const uint64_t* partials = nullptr;
   int nparts = 0;
-  int* act = nullptr;
+  RowMeta rows;
   int* n_active = nullptr;
-  int32_t* prev = nullptr;
-  const uint32_t* limit = nullptr;
-  int32_t* out_tok = nullptr;
-  const int64_t* out_base = nullptr;
+  int32_t* out_tok = nullptr;        // row kv0 + step
   uint32_t* count = nullptr;
   int step = 0;
   uint32_t flags = 0;
+  uint32_t* active_hist = nullptr;  // optional: active_hist[step] = rows this step ran on
 };
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 

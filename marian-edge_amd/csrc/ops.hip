@@ -122,7 +122,7 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
                          int64_t heads, int64_t max_keys, int in_bf16, float* out, int64_t ldo,
                          void* stream) {
   if (!q || !k || !v || !seq_of_row || !cu_k || !out || rows < 0 || rows > INT32_MAX ||
-      heads <= 0 || heads > 16 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096)
+      heads <= 0 || heads > 8 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096)
     return MARIAN_HIP_ERR_INVALID_INPUT;
   AttnArgs a;
   a.mode = ATT_SEQ;
@@ -146,11 +146,11 @@ int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_
                             const int8_t* emb, const float* emb_mult, const float* bias, int64_t V,
                             uint32_t flags, int32_t* token, float* logits, void* stream) {
   if (!xq || !xa || !emb || !emb_mult || !bias || !token || M < 0 || K <= 0 || K % 64 ||
-      V <= 0 || M > INT32_MAX || V > INT32_MAX)
+      K > 512 || V <= 0 || M > INT32_MAX || V > INT32_MAX)
     return MARIAN_HIP_ERR_INVALID_INPUT;
   if (M == 0) return MARIAN_HIP_OK;
   hipStream_t s = (hipStream_t)stream;
-  const int nparts = skinny_groups((int)V);
+  const int nparts = argmax_groups((int)V, (int)K);
   uint64_t* part = (uint64_t*)scratch(2, (size_t)M * nparts * 8, s);
   if (!part) return op_status(hipErrorOutOfMemory, "vocab_argmax scratch");
   GemmArgs g;
@@ -185,7 +185,10 @@ int marian_hip_device_name(int device, char* buf, size_t cap) {
   hipDeviceProp_t p;
   hipError_t e = hipGetDeviceProperties(&p, device);
   if (e != hipSuccess) return op_status(e, "hipGetDeviceProperties");
-  snprintf(buf, cap, "%s (%s)", p.name, p.gcnArchName);
+  char name[256] = {0};
+  if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
+    snprintf(name, sizeof name, "%s", p.name);
+  snprintf(buf, cap, "%s (%s)", name, p.gcnArchName);
   return MARIAN_HIP_OK;
 }
 

@@ -33,6 +33,42 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float* x, int64_t l
   if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
+// Same, for rows of V4*256 values held in registers: one 16-byte load and one
+// 4-byte store per lane per 256 columns.
+template <int V4>
+__global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_t ldx, int rows,
+                                                          const int* rows_dev, int8_t* q,
+                                                          int64_t ldq, float* a, int* err) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;  // host bound: rows below it are allocated
+  const float4* xr = (const float4*)(x + (int64_t)row * ldx);
+  float4 v[V4];
+#pragma unroll
+  for (int j = 0; j < V4; ++j) v[j] = xr[lane + 64 * j];
+  const int n = rows_dev ? *rows_dev : rows;
+  if (row >= n) return;
+  float m = 0.0f;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    bad |= !isfinite(v[j].x) || !isfinite(v[j].y) || !isfinite(v[j].z) || !isfinite(v[j].w);
+    m = fmaxf(fmaxf(m, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+  }
+  m = wave_max(m);
+  const float sc = row_multiplier(m);
+  uint32_t* qr = (uint32_t*)(q + (int64_t)row * ldq);
+#pragma unroll
+  for (int j = 0; j < V4; ++j) {
+    const uint32_t b0 = (uint32_t)(quantize_one(v[j].x, sc) & 0xFF);
+    const uint32_t b1 = (uint32_t)(quantize_one(v[j].y, sc) & 0xFF);
+    const uint32_t b2 = (uint32_t)(quantize_one(v[j].z, sc) & 0xFF);
+    const uint32_t b3 = (uint32_t)(quantize_one(v[j].w, sc) & 0xFF);
+    qr[lane + 64 * j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+  }
+  if (lane == 0) a[row] = sc;
+  if (__any(bad) && lane == 0 && err) *err = 1;
+}
+
 // out = LN(y + r) with canonical sums; optional quantization of out.
 template <int PER>
 __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float* r,
@@ -41,15 +77,26 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
                                                      int8_t* q, float* a, int* err) {
   constexpr int D = PER * 64;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int n = rows_dev ? *rows_dev : rows;
-  if (row >= n) return;
+  if (row >= rows) return;
+  // Rows below the host bound are always backed by memory, so every load is
+  // issued before the device row count arrives.
   const float* yr = y + (int64_t)row * D;
   const float* rr = r + (int64_t)row * D;
+  float yv[PER], rv[PER], gv[PER], bv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    yv[j] = yr[lane + 64 * j];
+    rv[j] = rr[lane + 64 * j];
+    gv[j] = gamma[lane + 64 * j];
+    bv[j] = beta[lane + 64 * j];
+  }
+  const int n = rows_dev ? *rows_dev : rows;
+  if (row >= n) return;
   float z[PER];
   float p = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    z[j] = yr[lane + 64 * j] + rr[lane + 64 * j];
+    z[j] = yv[j] + rv[j];
     p = p + z[j];
   }
   const float mean = wave_sum_canon(p) / (float)D;
@@ -67,7 +114,7 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = lane + 64 * j;
-    o[j] = ((z[j] - mean) * inv) * gamma[i] + beta[i];
+    o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];
     bad |= !isfinite(o[j]);
     m = fmaxf(m, fabsf(o[j]));
     out[(int64_t)row * D + i] = o[j];
@@ -88,30 +135,38 @@ template <int PER>
 __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
   constexpr int D = PER * 64;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int n = a.rows_dev ? *a.rows_dev : a.rows;
-  if (row >= n) return;
+  if (row >= a.rows) return;  // host bound: rows below it are allocated
   int token, p;
   if (a.tokens) {
     token = a.tokens[row];
     p = a.positions[row];
   } else {
-    token = a.prev[a.act[row]];
+    token = a.row_prev[row];  // read before the device row count is known
     p = a.step;
   }
   const float* pr = a.pos + (int64_t)p * D;
+  float pv[PER], ev[PER];
+  const int tk = token < 0 ? 0 : token;
+  const int8_t* er = a.emb + (int64_t)tk * D;
+  const float mult = a.emb_mult[tk];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    pv[j] = pr[lane + 64 * j];
+    ev[j] = (float)er[lane + 64 * j];
+  }
+  const int n = a.rows_dev ? *a.rows_dev : a.rows;
+  if (row >= n) return;
   float o[PER];
   float m = 0.0f;
   bool bad = false;
   if (token < 0) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) o[j] = pr[lane + 64 * j];
+    for (int j = 0; j < PER; ++j) o[j] = pv[j];
   } else {
-    const int8_t* er = a.emb + (int64_t)token * D;
-    const float mult = a.emb_mult[token];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const float v = (float)er[lane + 64 * j] / mult;
-      o[j] = v * a.scale + pr[lane + 64 * j];
+      const float v = ev[j] / mult;
+      o[j] = v * a.scale + pv[j];
     }
   }
 #pragma unroll
@@ -133,26 +188,48 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
 // compact the active list in order.  One workgroup; rows <= kMaxRowsPerCall.
 __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
   __shared__ int s_slot[kMaxRowsPerCall];
+  __shared__ int s_tok[kMaxRowsPerCall];
+  __shared__ int64_t s_kv0[kMaxRowsPerCall];
+  __shared__ int64_t s_src0[kMaxRowsPerCall];
+  __shared__ int s_srcn[kMaxRowsPerCall];
+  __shared__ uint32_t s_lim[kMaxRowsPerCall];
   __shared__ unsigned char s_keep[kMaxRowsPerCall];
   __shared__ int s_wsum[16];
   __shared__ int s_total;
   const int n = *f.n_active;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (tid == 0 && f.active_hist) f.active_hist[f.step] = (uint32_t)n;
   for (int r = wave; r < n; r += 16) {
+    // row state (independent of the partials, loaded alongside them)
+    int slot = 0, srcn = 0;
+    int64_t kv0 = 0, src0 = 0;
+    uint32_t lim = 0;
+    if (lane == 0) {
+      slot = f.rows.slot[r];
+      kv0 = f.rows.kv0[r];
+      src0 = f.rows.src0[r];
+      srcn = f.rows.srcn[r];
+      lim = f.rows.limit[r];
+    }
     uint64_t best = 0;
+    const uint64_t* pr = f.partials + (int64_t)r * f.nparts;
+#pragma unroll 4
     for (int p = lane; p < f.nparts; p += 64) {
-      const uint64_t k = f.partials[(int64_t)r * f.nparts + p];
+      const uint64_t k = pr[p];
       best = k > best ? k : best;
     }
     best = wave_max_u64(best);
     if (lane == 0) {
-      const int slot = f.act[r];
       const int32_t tok = argmax_key_id(best);
-      f.out_tok[f.out_base[slot] + f.step] = tok;
+      f.out_tok[kv0 + f.step] = tok;
       f.count[slot] = (uint32_t)f.step + 1u;
-      f.prev[slot] = tok;
-      const bool fin = (tok == 0 && !(f.flags & 1u)) || (uint32_t)f.step + 1u >= f.limit[slot];
+      const bool fin = (tok == 0 && !(f.flags & 1u)) || (uint32_t)f.step + 1u >= lim;
       s_slot[r] = slot;
+      s_tok[r] = tok;
+      s_kv0[r] = kv0;
+      s_src0[r] = src0;
+      s_srcn[r] = srcn;
+      s_lim[r] = lim;
       s_keep[r] = fin ? 0 : 1;
     }
   }
@@ -185,7 +262,15 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * tid + i;
-    if (r < n && s_keep[r]) f.act[pos++] = s_slot[r];
+    if (r < n && s_keep[r]) {
+      f.rows.slot[pos] = s_slot[r];
+      f.rows.kv0[pos] = s_kv0[r];
+      f.rows.src0[pos] = s_src0[r];
+      f.rows.srcn[pos] = s_srcn[r];
+      f.rows.limit[pos] = s_lim[r];
+      f.rows.prev[pos] = s_tok[r];
+      ++pos;
+    }
   }
   if (tid == 0) *f.n_active = s_total;
 }
@@ -209,8 +294,17 @@ hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int
                                 int cols, int8_t* q, int64_t ldq, float* a, int* err,
                                 hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quantize_rows, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, rows,
-                     rows_dev, cols, q, ldq, a, err);
+  const dim3 grid((rows + 3) / 4), block(256);
+  const bool vec = cols % 256 == 0 && ldx % 4 == 0 && ldq % 4 == 0 &&
+                   ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 4) == 0;
+  if (vec && cols == 2048)
+    hipLaunchKernelGGL(k_quantize_rows_v4<8>, grid, block, 0, s, x, ldx, rows, rows_dev, q, ldq, a, err);
+  else if (vec && cols == 512)
+    hipLaunchKernelGGL(k_quantize_rows_v4<2>, grid, block, 0, s, x, ldx, rows, rows_dev, q, ldq, a, err);
+  else if (vec && cols == 1536)
+    hipLaunchKernelGGL(k_quantize_rows_v4<6>, grid, block, 0, s, x, ldx, rows, rows_dev, q, ldq, a, err);
+  else
+    hipLaunchKernelGGL(k_quantize_rows, grid, block, 0, s, x, ldx, rows, rows_dev, cols, q, ldq, a, err);
   return hipGetLastError();
 }
 

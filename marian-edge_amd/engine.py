@@ -177,6 +177,15 @@ class HipEngine:
         self._lib.marian_hip_last_stats(self._h, C.byref(s))
         return {f: getattr(s, f) for f, _ in _lib.Stats._fields_}
 
+    def last_step_trace(self) -> tuple[np.ndarray, np.ndarray]:
+        """(active rows per decode step, device ms at each step's end)."""
+        n = C.c_size_t(0)
+        self._lib.marian_hip_last_step_trace(self._h, None, None, 0, C.byref(n))
+        rows = np.zeros(max(n.value, 1), np.uint32)
+        ms = np.zeros(max(n.value, 1), np.float32)
+        self._lib.marian_hip_last_step_trace(self._h, _ptr(rows), _ptr(ms), n.value, C.byref(n))
+        return rows[:n.value], ms[:n.value]
+
     def is_ready(self) -> bool:
         return bool(self._lib.marian_hip_is_ready(self._h))
 
