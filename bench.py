@@ -119,8 +119,8 @@ def cpu_baseline(pkg, model, batch, cores: int, threads: int = 4):
 def vocab_bytes(V, K, rows):
     """Algorithmic bytes of one vocabulary launch over `rows` active rows:
     int8 weights + fp32 multipliers + fp32 bias + int8 activations + fp32 row
-    multipliers + the 8-byte argmax partial per row and 64-column group."""
-    groups = (V + 63) // 64
+    multipliers + the 8-byte argmax partial per row and 128-column workgroup."""
+    groups = (V + 127) // 128
     return V * K + 8 * V + rows * (K + 4 + 8 * groups)
 
 
@@ -218,7 +218,7 @@ def main(argv=None):
         "decode_ms": round(statistics.mean(r["dec_ms"]), 4),
         "pcie_inclusive_tokens_per_s": round(r["ntok"] / (wall / 1000.0), 1),
         "roofline": {
-            "kernel": "k_gemm_skinny<EPI_ARGMAX> (vocab projection + bias + mask + argmax)",
+            "kernel": "k_vocab_argmax (vocab projection + bias + mask + argmax partials)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -214,7 +214,7 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
 
 /* Variable-length attention, one query row per (row, head) wave:
  * query row i belongs to sequence seq_of_row[i] and attends over key rows
- * [cu_k[s], cu_k[s+1]); max_keys bounds every range (at most 4096); heads <= 8.
+ * [cu_k[s], cu_k[s+1]); max_keys bounds every range (at most 4096); heads <= 16.
  * Row strides in elements.  in_bf16 != 0 reads q/k/v as
  * bfloat16 (converted exactly to fp32); out is fp32 [rows, heads*64]. */
 int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,

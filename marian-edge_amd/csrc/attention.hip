@@ -1,5 +1,5 @@
-// attention.hip — variable-length multi-head attention, one query row per
-// workgroup and one 64-wide wavefront per head (head_dim = 64).
+// attention.hip — variable-length multi-head attention: one single-wave
+// workgroup per (query row, head), head_dim = 64.
 //
 // Semantics of attention_into (tensor.rs:251-318): score_k = (q . k_k) * 1/8,
 // softmax as max, exp(s - max), sum, multiply by 1/sum, then
@@ -66,12 +66,10 @@ __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
       *(float4*)((TILE) + (((LANE) >> 4) + 4 * i_) * kKRow + ((LANE)&15) * 4) = IN[i_];
 
 template <int CH, typename T>
-__global__ __launch_bounds__(512) void k_attention(AttnArgs a) {
-  extern __shared__ float sTile[];  // [heads][64][kKRow]
-  __shared__ float sMax[8];
-  const int r = blockIdx.x;  // < a.rows, the host bound
-  const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int D = a.heads * kHeadDim;
+__global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float tile[64 * kKRow];
+  const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
+  const int lane = threadIdx.x;
 
   int64_t key0;
   int nk;
@@ -92,7 +90,6 @@ __global__ __launch_bounds__(512) void k_attention(AttnArgs a) {
   if (too_long) nk = CH * 64;
   const int nch = (nk + 63) >> 6;
   const int64_t kbase = key0 * a.ldkv + h * kHeadDim;
-  float* tile = sTile + h * 64 * kKRow;
 
   // Keys of a stale row may run past the buffer: its last readable key.
   const int nk_ld = a.mode == ATT_SEQ ? nk : (int)min((int64_t)nk, a.max_row - key0);
@@ -193,33 +190,18 @@ __global__ __launch_bounds__(512) void k_attention(AttnArgs a) {
     }
   }
 
-  if (a.out) a.out[(int64_t)r * a.ldo + h * kHeadDim + lane] = o;
-  if (a.q8) {
-    const bool bad = !isfinite(o);
-    const float m = wave_max(fabsf(o));
-    if (lane == 0) sMax[h] = m;
-    __syncthreads();
-    float absmax = 0.0f;
-    for (int w = 0; w < a.heads; ++w) absmax = fmaxf(absmax, sMax[w]);
-    const float sc = row_multiplier(absmax);
-    a.q8[(int64_t)r * D + h * kHeadDim + lane] = (int8_t)quantize_one(o, sc);
-    if (threadIdx.x == 0) a.qa[r] = sc;
-    if (__any(bad) && lane == 0 && a.err) *a.err = 1;
-  }
+  a.out[(int64_t)r * a.ldo + h * kHeadDim + lane] = o;
+  // |max| of this head's slice: the consumer derives the row's quantization
+  // multiplier from the maxima of all heads.
+  const bool bad = !isfinite(o);
+  const float m = wave_max(fabsf(o));
+  if (lane == 0 && a.amax) a.amax[(int64_t)r * a.heads + h] = m;
+  if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
 template <int CH, typename T>
 hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
-  const size_t lds = (size_t)a.heads * 64 * kKRow * sizeof(float);
-  static bool attr_set = false;  // the attribute is per kernel, set once
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)k_attention<CH, T>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       8 * 64 * kKRow * (int)sizeof(float));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL((k_attention<CH, T>), dim3(a.rows), dim3(a.heads * 64), lds, s, a);
+  hipLaunchKernelGGL((k_attention<CH, T>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 
@@ -232,7 +214,9 @@ hipError_t launch_ch(const AttnArgs& a, hipStream_t s) {
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
-  if (a.heads <= 0 || a.heads > 8 || a.max_keys <= 0) return hipErrorInvalidValue;
+  if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out ||
+      (int64_t)a.rows * a.heads > 0x7fffffff)
+    return hipErrorInvalidValue;
   if (a.max_keys <= 128) return launch_ch<2>(a, s);
   if (a.max_keys <= 512) return launch_ch<8>(a, s);
   if (a.max_keys <= 1024) return launch_ch<16>(a, s);

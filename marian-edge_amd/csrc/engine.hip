@@ -44,8 +44,8 @@ struct DecLayer {
 // Grow-only device buffers reused across calls (the reference pools its
 // scratch too, q8_engine.rs:733-747).
 enum Buf {
-  B_META, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
-  B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DOQ, B_DOA, B_DY, B_DH, B_DHQ, B_DHA,
+  B_META, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_ATT, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
+  B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DATT, B_DAMAX, B_DY, B_DH, B_DHQ, B_DHA,
   B_PART, B_OUT, B_COUNT, B_HIST, B_COUNT_
 };
 
@@ -450,6 +450,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   int8_t* XQ = (int8_t*)E->get(B_XQ, (size_t)T * d);
   float* XA = (float*)E->get(B_XA, 4ull * T);
   float* QKV = (float*)E->get(B_QKV, 12ull * T * d);
+  float* ATT = (float*)E->get(B_ATT, 4ull * T * d);
   int8_t* OQ = (int8_t*)E->get(B_OQ, (size_t)T * d);
   float* OA = (float*)E->get(B_OA, 4ull * T);
   float* Y = (float*)E->get(B_Y, 4ull * T * d);
@@ -464,8 +465,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   int8_t* DXQ = (int8_t*)E->get(B_DXQ, B * d);
   float* DXA = (float*)E->get(B_DXA, 4ull * B);
   float* DQ = (float*)E->get(B_DQ, 4ull * B * d);
-  int8_t* DOQ = (int8_t*)E->get(B_DOQ, B * d);
-  float* DOA = (float*)E->get(B_DOA, 4ull * B);
+  float* DATT = (float*)E->get(B_DATT, 4ull * B * d);
+  float* DAMAX = (float*)E->get(B_DAMAX, 4ull * B * H);
   float* DY = (float*)E->get(B_DY, 4ull * B * d);
   float* DH = (float*)E->get(B_DH, 4ull * B * F);
   int8_t* DHQ = (int8_t*)E->get(B_DHQ, B * F);
@@ -546,10 +547,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     aa.seq_of_row = d_seq;
     aa.cu = d_cu;
     aa.max_keys = (int)Lmax;
-    aa.q8 = OQ;
-    aa.qa = OA;
+    aa.out = ATT;
+    aa.ldo = d;
     aa.err = E->err_flag;
     MH_HIP(launch_attention(aa, s));
+    MH_HIP(launch_quantize_rows(ATT, d, T, nullptr, d, OQ, d, OA, E->err_flag, s));
     MH_HIP(gemm(OQ, OA, T, L.out, Y, 0));
     MH_HIP(launch_residual_ln(Y, X0, L.ln1_s, L.ln1_b, T, nullptr, d, X1, XQ, XA, E->err_flag, s));
     MH_HIP(gemm(XQ, XA, T, L.ffn1, Hb, 1));
@@ -595,6 +597,23 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     g.bias = L.bias;
     g.N = L.N;
     return launch_gemm_skinny(g, mode, e, s);
+  };
+  // Attention-output projection: A is the fp32 attention output, quantized
+  // while loading with the per-head maxima.
+  auto agemm = [&](const Lin& L, const Epilogue& e) {
+    GemmArgs g;
+    g.Af = DATT;
+    g.ldaf = d;
+    g.Aamax = DAMAX;
+    g.amax_parts = H;
+    g.M = rows_ub;
+    g.M_dev = d_nact;
+    g.K = L.K;
+    g.W = L.w;
+    g.wmult = L.mult;
+    g.bias = L.bias;
+    g.N = L.N;
+    return launch_gemm_skinny(g, EPI_STORE, e, s);
   };
   auto store_epi = [&](float* out, int ldo, int relu) {
     Epilogue e;
@@ -659,11 +678,12 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       sa.max_row = (int64_t)cache_rows;
       sa.step = (int)t;
       sa.max_keys = (int)t + 1;
-      sa.q8 = DOQ;
-      sa.qa = DOA;
+      sa.out = DATT;
+      sa.ldo = d;
+      sa.amax = DAMAX;
       sa.err = E->err_flag;
       MH_HIP(launch_attention(sa, s));
-      MH_HIP(dgemm(DOQ, DOA, L.self_out, EPI_STORE, store_epi(DY, d, 0)));
+      MH_HIP(agemm(L.self_out, store_epi(DY, d, 0)));
       MH_HIP(launch_residual_ln(DY, DX0, L.ln1_s, L.ln1_b, rows_ub, d_nact, d, DX1, DXQ, DXA,
                                 E->err_flag, s));
       MH_HIP(dgemm(DXQ, DXA, L.cross_q, EPI_STORE, store_epi(DQ, d, 0)));
@@ -681,11 +701,12 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ca.row_nk = rm.srcn;
       ca.max_row = T;
       ca.max_keys = (int)Lmax;
-      ca.q8 = DOQ;
-      ca.qa = DOA;
+      ca.out = DATT;
+      ca.ldo = d;
+      ca.amax = DAMAX;
       ca.err = E->err_flag;
       MH_HIP(launch_attention(ca, s));
-      MH_HIP(dgemm(DOQ, DOA, L.cross_out, EPI_STORE, store_epi(DY, d, 0)));
+      MH_HIP(agemm(L.cross_out, store_epi(DY, d, 0)));
       MH_HIP(launch_residual_ln(DY, DX1, L.ln2_s, L.ln2_b, rows_ub, d_nact, d, DX0, DXQ, DXA,
                                 E->err_flag, s));
       MH_HIP(dgemm(DXQ, DXA, L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
@@ -700,10 +721,23 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       e.partials = PART;
       e.partial_ld = nparts;
       e.flags = flags;
-      const bool timed = E->kernel_timing;
-      if (timed) MH_HIP(hipEventRecord(E->vocab_ev[2 * vocab_launches], s));
-      MH_HIP(dgemm(DXQ, DXA, E->emb, EPI_ARGMAX, e));
-      if (timed) MH_HIP(hipEventRecord(E->vocab_ev[2 * vocab_launches + 1], s));
+      GemmArgs g;
+      g.A = DXQ;
+      g.a = DXA;
+      g.lda = d;
+      g.M = rows_ub;
+      g.M_dev = d_nact;
+      g.K = d;
+      g.W = E->emb.w;
+      g.wmult = E->emb.mult;
+      g.bias = E->emb.bias;
+      g.N = (int)E->V;
+      // With kernel timing on, the kernel's own dispatch records the events.
+      if (E->kernel_timing)
+        MH_HIP(launch_vocab_argmax(g, e, s, E->vocab_ev[2 * vocab_launches],
+                                   E->vocab_ev[2 * vocab_launches + 1]));
+      else
+        MH_HIP(launch_vocab_argmax(g, e, s));
       ++vocab_launches;
     }
     {

@@ -11,6 +11,7 @@
 // ReLU (tensor.rs:114-116), optional raw i32 store.
 #include "device_common.h"
 #include "kernels.h"
+#include <hip/hip_ext.h>
 
 namespace mh {
 namespace {
@@ -33,7 +34,31 @@ __device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
 // irrelevant.  The epilogue then walks the LDS tile row-major: consecutive
 // threads write consecutive columns.
 // ---------------------------------------------------------------------------
-template <int MODE, int CT, int NW, int KSW>
+// Row multiplier of row m of an fp32 A source from its producer's partial
+// maxima (amax_parts = 8 per row, read as two 16-byte vectors so the loads
+// issue together).
+constexpr int kAfParts = 8;
+__device__ __forceinline__ float af_row_mult(const GemmArgs& g, int m) {
+  const float4* p = (const float4*)(g.Aamax + (int64_t)m * kAfParts);
+  const float4 u = p[0], v = p[1];
+  const float mx = fmaxf(fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)), fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+  return row_multiplier(fmaxf(mx, 0.0f));
+}
+
+// 16 consecutive fp32 values quantized with multiplier a, packed as the
+// 16 int8 bytes of an MFMA operand fragment (byte j = element j).
+__device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
+  v4i r;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4 f = *(const float4*)(x + 4 * w);
+    r[w] = (quantize_one(f.x, a) & 0xFF) | ((quantize_one(f.y, a) & 0xFF) << 8) |
+           ((quantize_one(f.z, a) & 0xFF) << 16) | ((quantize_one(f.w, a) & 0xFF) << 24);
+  }
+  return r;
+}
+
+template <int MODE, int CT, int NW, int KSW, bool AF>
 __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
   constexpr int NT = NW * 64;
   constexpr int COLS = CT * 16;
@@ -65,12 +90,22 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   v4i af[KSW][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
-    const int m = mt * 16 + (lane & 15);
-    const int8_t* ar = g.A + (int64_t)min(m, Mh - 1) * g.lda + kq;
+    const int m = min(mt * 16 + (lane & 15), Mh - 1);
+    if constexpr (AF) {
+      const float a_m = af_row_mult(g, m);
+      const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
 #pragma unroll
-    for (int i = 0; i < KSW; ++i) {
-      const int s = wave + NW * i;
-      af[i][mt] = (s < ksteps && mt * 16 < Mh) ? *(const v4i*)(ar + s * 64) : zero4();
+      for (int i = 0; i < KSW; ++i) {
+        const int s = wave + NW * i;
+        af[i][mt] = (s < ksteps && mt * 16 < Mh) ? quantize_frag16(ar + s * 64, a_m) : zero4();
+      }
+    } else {
+      const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
+#pragma unroll
+      for (int i = 0; i < KSW; ++i) {
+        const int s = wave + NW * i;
+        af[i][mt] = (s < ksteps && mt * 16 < Mh) ? *(const v4i*)(ar + s * 64) : zero4();
+      }
     }
   }
   // Epilogue operands: each thread always handles the same column.
@@ -79,25 +114,39 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   const float ewm = g.wmult[en], ebias = g.bias[en];
   float am[ROWS_PER_THREAD];
 #pragma unroll
-  for (int k = 0; k < ROWS_PER_THREAD; ++k)
-    am[k] = g.a[min(tid / COLS + k * (NT / COLS), Mh - 1)];
+  for (int k = 0; k < ROWS_PER_THREAD; ++k) {
+    const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
+    am[k] = AF ? af_row_mult(g, m) : g.a[m];
+  }
   const int M = g.M_dev ? *g.M_dev : g.M;
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     if (m0 > 0) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const int m = m0 + mt * 16 + (lane & 15);
-        const int8_t* ar = g.A + (int64_t)min(m, M - 1) * g.lda + kq;
+        const int m = min(m0 + mt * 16 + (lane & 15), M - 1);
+        if constexpr (AF) {
+          const float a_m = af_row_mult(g, m);
+          const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
 #pragma unroll
-        for (int i = 0; i < KSW; ++i) {
-          const int s = wave + NW * i;
-          af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? *(const v4i*)(ar + s * 64) : zero4();
+          for (int i = 0; i < KSW; ++i) {
+            const int s = wave + NW * i;
+            af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? quantize_frag16(ar + s * 64, a_m) : zero4();
+          }
+        } else {
+          const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
+#pragma unroll
+          for (int i = 0; i < KSW; ++i) {
+            const int s = wave + NW * i;
+            af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? *(const v4i*)(ar + s * 64) : zero4();
+          }
         }
       }
 #pragma unroll
-      for (int k = 0; k < ROWS_PER_THREAD; ++k)
-        am[k] = g.a[min(m0 + tid / COLS + k * (NT / COLS), M - 1)];
+      for (int k = 0; k < ROWS_PER_THREAD; ++k) {
+        const int m = min(m0 + tid / COLS + k * (NT / COLS), M - 1);
+        am[k] = AF ? af_row_mult(g, m) : g.a[m];
+      }
     }
     for (int i = tid; i < kSkinnyRows * LDC; i += NT) sAcc[i] = 0;
     __syncthreads();
@@ -372,26 +421,31 @@ int skinny_cols(int N) { return N >= 8192 ? 64 : (N >= 1024 ? 32 : 16); }
 int skinny_groups(int N) { return (N + skinny_cols(N) - 1) / skinny_cols(N); }
 int argmax_groups(int N, int /*K*/) { return (N + kVocabCols - 1) / kVocabCols; }
 
-template <int MODE, int NW, int KSW>
+template <int MODE, int NW, int KSW, bool AF>
 static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const dim3 grid(skinny_groups(g.N)), block(NW * 64);
   switch (skinny_cols(g.N)) {
-    case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW>), grid, block, 0, s, g, e); break;
-    case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW>), grid, block, 0, s, g, e); break;
-    default: hipLaunchKernelGGL((k_gemm_skinny<MODE, 1, NW, KSW>), grid, block, 0, s, g, e); break;
+    case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW, AF>), grid, block, 0, s, g, e); break;
+    case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW, AF>), grid, block, 0, s, g, e); break;
+    default: hipLaunchKernelGGL((k_gemm_skinny<MODE, 1, NW, KSW, AF>), grid, block, 0, s, g, e); break;
   }
   return hipGetLastError();
 }
 
 // Waves and per-wave k-steps by K: long K (the FFN down-projection) spreads
-// over 8 waves; each wave holds its k-steps' fragments in registers.
+// over 8 waves; each wave holds its k-steps' fragments in registers.  An
+// fp32 A source is supported for K <= 512 (the attention-output projections).
 template <int MODE>
 static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const int ksteps = g.K >> 6;
-  if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1>(g, e, s);
-  if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2>(g, e, s);
-  if (ksteps <= 16) return launch_skinny_k<MODE, 4, 4>(g, e, s);
-  return launch_skinny_k<MODE, 8, 4>(g, e, s);
+  if (g.Af) {
+    if (ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4) return hipErrorInvalidValue;
+    return launch_skinny_k<MODE, 4, 2, true>(g, e, s);
+  }
+  if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1, false>(g, e, s);
+  if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2, false>(g, e, s);
+  if (ksteps <= 16) return launch_skinny_k<MODE, 4, 4, false>(g, e, s);
+  return launch_skinny_k<MODE, 8, 4, false>(g, e, s);
 }
 
 hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s) {
@@ -400,12 +454,20 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hi
     case EPI_STORE: return launch_skinny_mode<EPI_STORE>(g, e, s);
     case EPI_QKV_CACHE: return launch_skinny_mode<EPI_QKV_CACHE>(g, e, s);
     case EPI_ARGMAX:
-      if (g.K > kVocabMaxK) return hipErrorInvalidValue;
-      hipLaunchKernelGGL(k_vocab_argmax, dim3((g.N + kVocabCols - 1) / kVocabCols), dim3(256), 0,
-                         s, g, e);
-      return hipGetLastError();
+      return launch_vocab_argmax(g, e, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
+                               hipEvent_t ev_start, hipEvent_t ev_stop) {
+  if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
+  const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
+  if (ev_start || ev_stop)
+    hipExtLaunchKernelGGL(k_vocab_argmax, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
+  else
+    hipLaunchKernelGGL(k_vocab_argmax, grid, block, 0, s, g, e);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s) {

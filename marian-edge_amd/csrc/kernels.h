@@ -18,6 +18,14 @@ struct GemmArgs {
   const float* wmult = nullptr;
   const float* bias = nullptr;
   int N = 0;
+  // Alternative A source (skinny kernel only): fp32 rows Af[M, ldaf] that are
+  // quantized while loading, with row multiplier 127 / max_p Aamax[m*parts+p]
+  // (the per-part |max| written by the producer: one per attention head;
+  // parts must be 8).
+  const float* Af = nullptr;
+  int64_t ldaf = 0;
+  const float* Aamax = nullptr;
+  int amax_parts = 0;
 };
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
@@ -49,6 +57,10 @@ int skinny_groups(int N);
 int argmax_groups(int N, int K);
 // Skinny (M up to a few hundred, weights streamed once per 64 rows) MFMA GEMM.
 hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s);
+// The vocabulary kernel (EPI_ARGMAX); when ev_start/ev_stop are given they are
+// recorded by the kernel's own dispatch (start and end of the kernel).
+hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
+                               hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 // LDS-tiled 128x128 MFMA GEMM for large M (EPI_STORE only).
 hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s);
 // Picks the kernel by M (host-known M only).
@@ -108,10 +120,9 @@ struct AttnArgs {
   // bound before the count is known, and are then discarded.
   int64_t max_row = 0;
   int max_keys = 0;  // upper bound on keys per row (selects the kernel variant)
-  float* out = nullptr;
+  float* out = nullptr;   // fp32 [rows, ldo], head h at columns [64h, 64h+64)
   int64_t ldo = 0;
-  int8_t* q8 = nullptr;  // fused per-row quantization of the [heads*64] output row
-  float* qa = nullptr;
+  float* amax = nullptr;  // optional [rows, heads]: max |out| of each head's slice
   int* err = nullptr;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);

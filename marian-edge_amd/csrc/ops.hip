@@ -122,7 +122,7 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
                          int64_t heads, int64_t max_keys, int in_bf16, float* out, int64_t ldo,
                          void* stream) {
   if (!q || !k || !v || !seq_of_row || !cu_k || !out || rows < 0 || rows > INT32_MAX ||
-      heads <= 0 || heads > 8 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096)
+      heads <= 0 || heads > 16 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096)
     return MARIAN_HIP_ERR_INVALID_INPUT;
   AttnArgs a;
   a.mode = ATT_SEQ;
