@@ -8,7 +8,8 @@
 //     per-head LDS tile;
 //   * scores: lane = key (keys lane, lane+64, ...), sequential 64-term dot
 //     with q broadcast from SGPRs;
-//   * softmax: wave max, canonical exp, lane partial sums + xor butterfly;
+//   * softmax: wave max, the C library's expf (ref_expf.h) per key, then the
+//     denominator summed over the keys in order through LDS;
 //   * PV: lane = output dim, keys accumulated in order (the reference order);
 //     probabilities are broadcast from the score lanes through SGPRs.
 // The score row never leaves the chip.  Sequences are packed (cu_seqlens), so
@@ -44,6 +45,9 @@ struct Io<uint16_t> {
 // key, so every load is in bounds and every value finite.
 constexpr int kKRow = kHeadDim + 4;  // padded LDS row (floats), 16-byte aligned
 
+// 2^(i/32) table of ref_expf, staged into LDS by each workgroup.
+__constant__ uint64_t kExp2Tab[32] = {MH_EXP2_TABLE_32};
+
 template <typename T>
 __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
   if constexpr (sizeof(T) == 4) {
@@ -65,11 +69,17 @@ __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
   _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_)                                            \
       *(float4*)((TILE) + (((LANE) >> 4) + 4 * i_) * kKRow + ((LANE)&15) * 4) = IN[i_];
 
-template <int CH, typename T>
+// PRE (two chunks only): all four K/V chunks are requested up front, so a
+// decode row waits for one memory round trip after its key range is known.
+template <int CH, typename T, bool PRE>
 __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
+  static_assert(!PRE || CH == 2, "up-front loads hold two chunks");
+  static_assert(CH * 64 <= 64 * kKRow, "the tile holds every probability of a row");
   __shared__ __attribute__((aligned(16))) float tile[64 * kKRow];
+  __shared__ uint64_t sTab[32];
   const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
   const int lane = threadIdx.x;
+  const uint64_t tab_v = kExp2Tab[lane & 31];
 
   int64_t key0;
   int nk;
@@ -95,9 +105,15 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   const int nk_ld = a.mode == ATT_SEQ ? nk : (int)min((int64_t)nk, a.max_row - key0);
 
   // Chunk 0's V rows are loaded now (used after the softmax), then K.
-  float4 vreg[16], kreg[16];
+  float4 vreg[16], kreg[16], kreg1[PRE ? 16 : 1], vreg1[PRE ? 16 : 1];
   MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 0, nk_ld, lane, vreg)
   MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, 0, nk_ld, lane, kreg)
+  if constexpr (PRE) {
+    if (nch > 1) {
+      MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, 64, nk_ld, lane, kreg1)
+      MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 64, nk_ld, lane, vreg1)
+    }
+  }
   // q of this head, one element per lane; broadcast 16 values at a time.
   const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * kHeadDim + lane));
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
@@ -107,15 +123,24 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   // Scores: lane = key within the chunk, 64-term dot in dimension order.  The
   // next chunk's K rows are loaded while this chunk's dot runs.
   const float scale = 1.0f / sqrtf((float)kHeadDim);
+  if (lane < 32) sTab[lane] = tab_v;  // published by the first barrier below
   float s[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     s[c] = -INFINITY;
     if (c < nch) {
       if (c > 0) __syncthreads();  // the previous chunk's rows have been read
-      MH_STORE_CHUNK(tile, lane, kreg)
-      if (c + 1 < nch) {
-        MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, (c + 1) * 64, nk_ld, lane, kreg)
+      if constexpr (PRE) {
+        if (c == 0) {
+          MH_STORE_CHUNK(tile, lane, kreg)
+        } else {
+          MH_STORE_CHUNK(tile, lane, kreg1)
+        }
+      } else {
+        MH_STORE_CHUNK(tile, lane, kreg)
+        if (c + 1 < nch) {
+          MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, (c + 1) * 64, nk_ld, lane, kreg)
+        }
       }
       __syncthreads();
       float dot = -0.0f;
@@ -141,25 +166,34 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   }
   // V rows of chunk 1 go into the now free K registers (chunk c uses vreg
   // for even c, kreg for odd c).
-  if (nch > 1) {
+  if (!PRE && nch > 1) {
     MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 64, nk_ld, lane, kreg)
   }
   float mloc = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CH; ++c) mloc = fmaxf(mloc, s[c]);
   const float mx = wave_max(mloc);
-  // exp and the canonical sum: lane partials over its keys in chunk order.
-  float part = 0.0f;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    if (c < nch && c * 64 + lane < nk) {
-      s[c] = canon_expf(s[c] - mx);
-      part = part + s[c];
-    } else {
-      s[c] = 0.0f;
-    }
+  for (int c = 0; c < CH; ++c)
+    s[c] = (c < nch && c * 64 + lane < nk) ? ref_expf(s[c] - mx, sTab) : 0.0f;
+  // Denominator in key order from 0.0 (softmax_in_place): the probabilities
+  // pass through the tile and every lane folds them sequentially.  Keys past
+  // the last hold +0.0, which leaves the (non-negative) sum unchanged.
+  __syncthreads();  // the last K chunk has been read
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+    if (c < nch) tile[c * 64 + lane] = s[c];
+  __syncthreads();
+  float sum = 0.0f;
+#pragma unroll 4
+  for (int j = 0; j < nch * 64; j += 4) {
+    const float4 v = *(const float4*)(tile + j);
+    sum = sum + v.x;
+    sum = sum + v.y;
+    sum = sum + v.z;
+    sum = sum + v.w;
   }
-  const float inv = 1.0f / wave_sum_canon(part);
+  const float inv = 1.0f / sum;
 #pragma unroll
   for (int c = 0; c < CH; ++c) s[c] = s[c] * inv;
 
@@ -171,7 +205,13 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   for (int c = 0; c < CH; ++c) {
     if (c < nch) {
       __syncthreads();  // the tile's previous contents have been read
-      if (c & 1) {
+      if constexpr (PRE) {
+        if (c == 0) {
+          MH_STORE_CHUNK(tile, lane, vreg)
+        } else {
+          MH_STORE_CHUNK(tile, lane, vreg1)
+        }
+      } else if (c & 1) {
         MH_STORE_CHUNK(tile, lane, kreg)
         if (c + 2 < nch) {
           MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, (c + 2) * 64, nk_ld, lane, kreg)
@@ -199,15 +239,15 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
-template <int CH, typename T>
+template <int CH, typename T, bool PRE>
 hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((k_attention<CH, T>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
+  hipLaunchKernelGGL((k_attention<CH, T, PRE>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 
-template <int CH>
+template <int CH, bool PRE = false>
 hipError_t launch_ch(const AttnArgs& a, hipStream_t s) {
-  return a.bf16 ? launch_t<CH, uint16_t>(a, s) : launch_t<CH, float>(a, s);
+  return a.bf16 ? launch_t<CH, uint16_t, PRE>(a, s) : launch_t<CH, float, PRE>(a, s);
 }
 
 }  // namespace
@@ -217,7 +257,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out ||
       (int64_t)a.rows * a.heads > 0x7fffffff)
     return hipErrorInvalidValue;
-  if (a.max_keys <= 128) return launch_ch<2>(a, s);
+  // Decode launches cover few rows: one round trip per row matters more
+  // than occupancy.  Encoder launches keep the lighter register budget.
+  if (a.max_keys <= 128) return a.mode == ATT_SEQ ? launch_ch<2>(a, s) : launch_ch<2, true>(a, s);
   if (a.max_keys <= 512) return launch_ch<8>(a, s);
   if (a.max_keys <= 1024) return launch_ch<16>(a, s);
   if (a.max_keys <= 4096) return launch_ch<64>(a, s);

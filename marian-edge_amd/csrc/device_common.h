@@ -1,18 +1,23 @@
 // device_common.h — device helpers shared by the gfx950 kernels.
 //
-// Arithmetic contract (identical in the CPU oracle, bit for bit):
-//  * fp32 sums over a row are "canonical": lane l of a 64-wide wavefront sums
-//    elements l, l+64, l+128, ... in that order starting from 0.0f, then the
-//    wave combines lane partials with an xor butterfly 32,16,8,4,2,1.
-//  * exp is evaluated by canon_expf below (double precision Cody-Waite
-//    reduction + degree-11 Taylor polynomial, rounded once to fp32).
-//  * every other fp32 expression is evaluated in the reference's sequential
-//    order with separate multiply and add (the library is built with
-//    -ffp-contract=off, IEEE division and square root).
+// Arithmetic contract: every fp32 value is produced by the same sequence of
+// IEEE operations as the reference's x86 Q8 path, so results are identical
+// bit for bit:
+//  * sums follow the reference's order: LayerNorm's mean and variance and
+//    attention's dot products are strictly sequential folds starting from
+//    -0.0 (Rust's f32 Sum), the softmax denominator a sequential sum from 0.0;
+//  * exp is the C library's expf (restated in ref_expf.h);
+//  * every other expression is evaluated in the reference's order with
+//    separate multiplies and adds (the library is built with
+//    -ffp-contract=off, IEEE division and square root, fp32 denormals kept).
+// Maxima (absmax, softmax max, argmax) are order independent and use wave
+// reductions.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "ref_expf.h"
 
 namespace mh {
 
@@ -53,18 +58,6 @@ __device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Canonical sum of the 64 lane partials: p = p + p[l ^ off] for off = 32,
-// 16, 8, 4, 2, 1 (every lane ends with the same value).
-__device__ __forceinline__ float wave_sum_canon(float p) {
-  p = p + xor_lane_f<32>(p);
-  p = p + xor_lane_f<16>(p);
-  p = p + xor_lane_f<8>(p);
-  p = p + xor_lane_f<4>(p);
-  p = p + xor_lane_f<2>(p);
-  p = p + xor_lane_f<1>(p);
-  return p;
-}
-
 __device__ __forceinline__ float wave_max(float p) {
   p = fmaxf(p, xor_lane_f<32>(p));
   p = fmaxf(p, xor_lane_f<16>(p));
@@ -85,31 +78,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   v = umax64(v, xor_lane_u64<2>(v));
   v = umax64(v, xor_lane_u64<1>(v));
   return v;
-}
-
-// exp(x) evaluated as: n = rint(x/ln2), r = x - n*ln2 (double), Horner
-// polynomial sum_{k<=11} r^k/k! with separate multiplies and adds, scaled by
-// 2^n and rounded once to fp32.  Matches the oracle's canon_expf exactly.
-__device__ __forceinline__ float canon_expf(float xf) {
-  if (!(xf == xf)) return xf;
-  if (xf < -104.0f) return 0.0f;
-  if (xf > 89.0f) return __int_as_float(0x7f800000);
-  const double x = (double)xf;
-  const double n = rint(x * 0x1.71547652b82fep+0);
-  const double r = x - n * 0x1.62e42fefa39efp-1;
-  double p = 0x1.ae64567f544e4p-26;
-  p = p * r + 0x1.27e4fb7789f5cp-22;
-  p = p * r + 0x1.71de3a556c734p-19;
-  p = p * r + 0x1.a01a01a01a01ap-16;
-  p = p * r + 0x1.a01a01a01a01ap-13;
-  p = p * r + 0x1.6c16c16c16c17p-10;
-  p = p * r + 0x1.1111111111111p-7;
-  p = p * r + 0x1.5555555555555p-5;
-  p = p * r + 0x1.5555555555555p-3;
-  p = p * r + 0x1.0000000000000p-1;
-  p = p * r + 1.0;
-  p = p * r + 1.0;
-  return (float)ldexp(p, (int)n);
 }
 
 // q = clamp(round_half_even(x * a), -127, 127)  (q8_gemm.rs:584-587)
@@ -133,7 +101,11 @@ __device__ __forceinline__ float dequant(int32_t acc, float a, float w, float b)
 
 // Orderable 64-bit key: larger logit wins, equal logits prefer the lower id
 // (the reference's strict '>' scan in ascending id order).  0 = no candidate.
+// The scan starts from -inf at the first candidate and never takes a NaN, so
+// NaN ranks with -inf (a row of only -inf/NaN logits yields its first
+// candidate); -0.0 equals +0.0 under '>', so it is folded into +0.0.
 __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t id) {
+  v = (v != v) ? -INFINITY : v + 0.0f;
   const uint32_t b = __float_as_uint(v);
   const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
   return ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - id);

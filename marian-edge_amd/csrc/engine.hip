@@ -584,6 +584,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     for (uint32_t t = 1; t <= gen_limit; ++t) remaining[t] = remaining[t - 1] - ends[t];
   }
   int rows_ub = 0;  // host bound on this step's active rows
+  constexpr int kAfMaxRows = 16;
   auto dgemm = [&](const int8_t* A, const float* a, const Lin& L, int mode, const Epilogue& e) {
     GemmArgs g;
     g.A = A;
@@ -598,9 +599,16 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     g.N = L.N;
     return launch_gemm_skinny(g, mode, e, s);
   };
-  // Attention-output projection: A is the fp32 attention output, quantized
-  // while loading with the per-head maxima.
-  auto agemm = [&](const Lin& L, const Epilogue& e) {
+  // Attention-output projection.  Up to kAfMaxRows rows, A is the fp32
+  // attention output, quantized while loading with the per-head maxima the
+  // attention kernel wrote; above that every workgroup would repeat the
+  // quantization of many rows, so a row-quantization pass runs first.
+  auto agemm = [&](const Lin& L, const Epilogue& e) -> hipError_t {
+    if (rows_ub > kAfMaxRows) {
+      hipError_t rc = launch_quantize_rows(DATT, d, rows_ub, d_nact, d, DHQ, d, DHA, E->err_flag, s);
+      if (rc != hipSuccess) return rc;
+      return dgemm(DHQ, DHA, L, EPI_STORE, e);
+    }
     GemmArgs g;
     g.Af = DATT;
     g.ldaf = d;
@@ -680,7 +688,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       sa.max_keys = (int)t + 1;
       sa.out = DATT;
       sa.ldo = d;
-      sa.amax = DAMAX;
+      sa.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
       sa.err = E->err_flag;
       MH_HIP(launch_attention(sa, s));
       MH_HIP(agemm(L.self_out, store_epi(DY, d, 0)));
@@ -703,7 +711,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ca.max_keys = (int)Lmax;
       ca.out = DATT;
       ca.ldo = d;
-      ca.amax = DAMAX;
+      ca.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
       ca.err = E->err_flag;
       MH_HIP(launch_attention(ca, s));
       MH_HIP(agemm(L.cross_out, store_epi(DY, d, 0)));
@@ -746,6 +754,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       f.nparts = nparts;
       f.rows = rm;
       f.n_active = d_nact;
+      f.rows_ub = rows_ub;
+      f.err = E->err_flag;
       f.out_tok = OUT;
       f.count = COUNT;
       f.step = (int)t;
@@ -805,6 +815,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   E->step_ms.assign(steps, 0.0f);
   if (E->kernel_timing)
     for (uint32_t i = 0; i < steps; ++i) hipEventElapsedTime(&E->step_ms[i], E->ev[0], E->step_ev[i]);
+  if (err_host == 2) return E->fail(MARIAN_HIP_ERR_INFERENCE, "key range exceeds the attention kernel");
+  if (err_host == 3) return E->fail(MARIAN_HIP_ERR_INFERENCE, "active rows exceed the step bound");
   if (err_host) return E->fail(MARIAN_HIP_ERR_INFERENCE, "activation is not finite");
 
   size_t total = 0;

@@ -113,12 +113,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   const int en = min(n0 + ec, g.N - 1);
   const float ewm = g.wmult[en], ebias = g.bias[en];
   float am[ROWS_PER_THREAD];
+  int64_t crow[MODE == EPI_QKV_CACHE ? ROWS_PER_THREAD : 1];
 #pragma unroll
   for (int k = 0; k < ROWS_PER_THREAD; ++k) {
     const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
     am[k] = AF ? af_row_mult(g, m) : g.a[m];
+    if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
-  const int M = g.M_dev ? *g.M_dev : g.M;
+  const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     if (m0 > 0) {
@@ -146,6 +148,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       for (int k = 0; k < ROWS_PER_THREAD; ++k) {
         const int m = min(m0 + tid / COLS + k * (NT / COLS), M - 1);
         am[k] = AF ? af_row_mult(g, m) : g.a[m];
+        if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
       }
     }
     for (int i = tid; i < kSkinnyRows * LDC; i += NT) sAcc[i] = 0;
@@ -194,11 +197,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
         if (n < e.d) {
           e.out[(int64_t)m * e.ldo + n] = y;
         } else {
-          const int64_t crow = e.row_kv0[m] + e.step;
           if (n < 2 * e.d)
-            e.kcache[crow * e.d + (n - e.d)] = y;
+            e.kcache[crow[k] * e.d + (n - e.d)] = y;
           else
-            e.vcache[crow * e.d + (n - 2 * e.d)] = y;
+            e.vcache[crow[k] * e.d + (n - 2 * e.d)] = y;
         }
       } else {
         if (e.out) e.out[(int64_t)m * e.ldo + n] = y;
@@ -227,6 +229,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
   __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
+  __shared__ float sAm[kSkinnyRows];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kq = (lane >> 4) * 16;
   const int ksteps = g.K >> 6;
@@ -253,16 +256,44 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     bi[ct] = g.bias[n];
     live[ct] = ncol[ct] < g.N && ((e.flags & 2u) || !generation_masked((uint32_t)ncol[ct]));
   }
-  const int M = g.M_dev ? *g.M_dev : g.M;
-  const int cpr = g.K >> 4;  // 16-byte chunks per activation row
+  // Activation rows of a 64-row chunk: thread t holds 16-byte pieces
+  // t + 256 j (row = piece / 32, piece % 32 < K / 16), all requested at once.
+  // The first chunk is requested for the rows below the host bound g.M (all
+  // allocated) before the device row count arrives.
+  constexpr int kStage = kSkinnyRows * (kVocabMaxK / 16) / 256;
+  const int cpr = g.K >> 4;
+  v4i st[kStage];
+  float sa = 0.0f;
+  {
+    const int rows_h = min(kSkinnyRows, g.M);
+#pragma unroll
+    for (int j = 0; j < kStage; ++j) {
+      const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
+      st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
+                                         : zero4();
+    }
+    if (tid < rows_h) sa = g.a[tid];
+  }
+  const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
-    for (int c = tid; c < rows * cpr; c += 256) {
-      const int row = c / cpr, cc = c - row * cpr;
-      *(v4i*)(sA + row * kVocabLds + cc * 16) =
-          *(const v4i*)(g.A + (int64_t)(m0 + row) * g.lda + cc * 16);
+    if (m0 > 0) {
+#pragma unroll
+      for (int j = 0; j < kStage; ++j) {
+        const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
+        st[j] = (row < rows && cc < cpr)
+                    ? *(const v4i*)(g.A + (int64_t)(m0 + row) * g.lda + cc * 16)
+                    : zero4();
+      }
+      sa = tid < rows ? g.a[m0 + tid] : 0.0f;
     }
+#pragma unroll
+    for (int j = 0; j < kStage; ++j) {
+      const int c = tid + 256 * j;
+      *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
+    }
+    if (tid < kSkinnyRows) sAm[tid] = sa;
     __syncthreads();
     const int mt_n = (rows + 15) >> 4;
 #pragma unroll
@@ -288,13 +319,13 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
           uint64_t key = 0;
           if (lr < rows) {
             const int m = m0 + lr;
-            const float am = g.a[m];
+            const float am = sAm[lr];
 #pragma unroll
             for (int ct = 0; ct < kVocabCT; ++ct) {
               const float y = dequant(acc[ct][r], am, wm[ct], bi[ct]);
               if (e.logits && ncol[ct] < g.N)
                 e.logits[(int64_t)m * e.ldl + ncol[ct]] = live[ct] ? y : -INFINITY;
-              if (live[ct] && y == y) {
+              if (live[ct]) {
                 const uint64_t k = argmax_key(y, (uint32_t)ncol[ct]);
                 key = k > key ? k : key;
               }

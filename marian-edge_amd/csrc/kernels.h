@@ -142,6 +142,8 @@ struct FinalizeArgs {
   int nparts = 0;
   RowMeta rows;
   int* n_active = nullptr;
+  int rows_ub = 0;                   // host bound on *n_active; rows below it are allocated
+  int* err = nullptr;                // set to 3 if *n_active exceeds rows_ub
   int32_t* out_tok = nullptr;        // row kv0 + step
   uint32_t* count = nullptr;
   int step = 0;

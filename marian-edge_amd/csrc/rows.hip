@@ -69,15 +69,52 @@ __global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_
   if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
-// out = LN(y + r) with canonical sums; optional quantization of out.
+// Strictly sequential fp32 fold init + p[0] + p[1] + ... over N4 float4 in
+// LDS (same address for every lane: broadcast reads).  The reads run a batch
+// of NB float4 ahead of the dependent adds so the chain never waits on LDS.
+template <int N4>
+__device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
+  constexpr int NB = 8;
+  static_assert(N4 % NB == 0, "whole batches");
+  float4 cur[NB], nxt[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) cur[b] = p[b];
+  float s = init;
+#pragma unroll
+  for (int k = 0; k < N4 / NB; ++k) {
+    if (k + 1 < N4 / NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) nxt[b] = p[(k + 1) * NB + b];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      s = s + cur[b].x;
+      s = s + cur[b].y;
+      s = s + cur[b].z;
+      s = s + cur[b].w;
+    }
+    if (k + 1 < N4 / NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) cur[b] = nxt[b];
+    }
+  }
+  return s;
+}
+
+// out = LN(y + r), optionally quantized for the next GEMM.  One wave per row.
+// normalize_row (tensor.rs:372-385) sums the row strictly left to right, so
+// the wave parks z = y + r in LDS and every lane folds the row sequentially;
+// the centred squares are formed lane-parallel and parked the same way.
 template <int PER>
 __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float* r,
                                                      const float* gamma, const float* beta,
                                                      int rows, const int* rows_dev, float* out,
                                                      int8_t* q, float* a, int* err) {
   constexpr int D = PER * 64;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= rows) return;
+  __shared__ __attribute__((aligned(16))) float sZ[4][D];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= rows) return;  // uniform per wave; the waves share no barrier
   // Rows below the host bound are always backed by memory, so every load is
   // issued before the device row count arrives.
   const float* yr = y + (int64_t)row * D;
@@ -92,21 +129,26 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
   }
   const int n = rows_dev ? *rows_dev : rows;
   if (row >= n) return;
+  float* zr = sZ[wave];
   float z[PER];
-  float p = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     z[j] = yv[j] + rv[j];
-    p = p + z[j];
+    zr[lane + 64 * j] = z[j];
   }
-  const float mean = wave_sum_canon(p) / (float)D;
-  float p2 = 0.0f;
+  // The wave's LDS writes complete before its reads below.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  const float mean = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const float c = z[j] - mean;
-    p2 = p2 + c * c;
+    zr[lane + 64 * j] = c * c;
   }
-  const float var = wave_sum_canon(p2) / (float)D;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const float var = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
   const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
   float o[PER];
   float m = 0.0f;
@@ -125,8 +167,8 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
 #pragma unroll
     for (int j = 0; j < PER; ++j) q[(int64_t)row * D + lane + 64 * j] = (int8_t)quantize_one(o[j], sc);
     if (lane == 0) a[row] = sc;
-    if (__any(bad) && lane == 0 && err) *err = 1;
   }
+  if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
 // x = (q/mult)*sqrt(d) + pos[p] (q8_engine.rs:53-74, 586-630); token < 0 gives
@@ -196,30 +238,48 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
   __shared__ unsigned char s_keep[kMaxRowsPerCall];
   __shared__ int s_wsum[16];
   __shared__ int s_total;
-  const int n = *f.n_active;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // Rows below the host bound are allocated, so their partials and state are
+  // loaded together with the device row count (one memory round trip); rows
+  // at or past the count are dropped afterwards.
+  const int ub = min(f.rows_ub, kMaxRowsPerCall);
+  const int n_dev = *f.n_active;
+  const int n = min(n_dev, ub);
+  if (tid == 0 && n_dev > ub && f.err) *f.err = 3;
   if (tid == 0 && f.active_hist) f.active_hist[f.step] = (uint32_t)n;
-  for (int r = wave; r < n; r += 16) {
-    // row state (independent of the partials, loaded alongside them)
+  const int np = f.nparts;
+  // Wave w takes rows 4w..4w+3 of each 64-row pass; lane i < 4 owns row r0 + i.
+  for (int r0 = 4 * wave; r0 < ub; r0 += 64) {
+    const int rl = min(r0 + (lane & 3), ub - 1);
     int slot = 0, srcn = 0;
     int64_t kv0 = 0, src0 = 0;
     uint32_t lim = 0;
-    if (lane == 0) {
-      slot = f.rows.slot[r];
-      kv0 = f.rows.kv0[r];
-      src0 = f.rows.src0[r];
-      srcn = f.rows.srcn[r];
-      lim = f.rows.limit[r];
+    if (lane < 4) {
+      slot = f.rows.slot[rl];
+      kv0 = f.rows.kv0[rl];
+      src0 = f.rows.src0[rl];
+      srcn = f.rows.srcn[rl];
+      lim = f.rows.limit[rl];
     }
-    uint64_t best = 0;
-    const uint64_t* pr = f.partials + (int64_t)r * f.nparts;
+    const uint64_t* p0 = f.partials + (int64_t)r0 * np;
+    const uint64_t* p1 = f.partials + (int64_t)min(r0 + 1, ub - 1) * np;
+    const uint64_t* p2 = f.partials + (int64_t)min(r0 + 2, ub - 1) * np;
+    const uint64_t* p3 = f.partials + (int64_t)min(r0 + 3, ub - 1) * np;
+    uint64_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
 #pragma unroll 4
-    for (int p = lane; p < f.nparts; p += 64) {
-      const uint64_t k = pr[p];
-      best = k > best ? k : best;
+    for (int p = lane; p < np; p += 64) {
+      b0 = umax64(b0, p0[p]);
+      b1 = umax64(b1, p1[p]);
+      b2 = umax64(b2, p2[p]);
+      b3 = umax64(b3, p3[p]);
     }
-    best = wave_max_u64(best);
-    if (lane == 0) {
+    b0 = wave_max_u64(b0);
+    b1 = wave_max_u64(b1);
+    b2 = wave_max_u64(b2);
+    b3 = wave_max_u64(b3);
+    const uint64_t best = lane == 0 ? b0 : lane == 1 ? b1 : lane == 2 ? b2 : b3;
+    const int r = r0 + lane;
+    if (lane < 4 && r < n) {
       const int32_t tok = argmax_key_id(best);
       f.out_tok[kv0 + f.step] = tok;
       f.count[slot] = (uint32_t)f.step + 1u;
@@ -342,6 +402,7 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
+  if (f.rows_ub <= 0 || f.rows_ub > kMaxRowsPerCall || f.nparts <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_finalize, dim3(1), dim3(1024), 0, s, f);
   return hipGetLastError();
 }

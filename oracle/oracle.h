@@ -24,13 +24,13 @@
  *   generation mask     crates/marian-model/src/shortlist.rs:169-176
  *
  * Reduction order.  `order` selects how fp32 sums are rounded:
- *   ORACLE_ORDER_CANONICAL (0): the order the HIP kernels use (LayerNorm and
- *     softmax sums as 64 strided lane partials + xor butterfly; exp via the
- *     double-precision Cody-Waite/Taylor routine below).  This is the mode the
- *     GPU is checked against bit-for-bit.
  *   ORACLE_ORDER_REFERENCE (1): the x86 reference order (strictly sequential
- *     sums, libm expf).  Used to measure how far the canonical order moves
- *     results away from the reference's own rounding.
+ *     LayerNorm and softmax sums, the C library's expf).  This is the mode
+ *     the HIP kernels reproduce bit for bit.
+ *   ORACLE_ORDER_CANONICAL (0): an alternative (64 strided lane partials +
+ *     xor butterfly, exp via a double-precision Cody-Waite/Taylor routine),
+ *     kept to measure how sensitive greedy outputs are to the fp32 summation
+ *     order.
  * Everything else (dot products, PV accumulation, dequant, LN affine, embedding)
  * uses the reference's sequential op order in both modes.
  */

@@ -208,3 +208,40 @@ def test_vocab_argmax_ties_pick_lowest_id(pkg, dev):
     dev.vocab_argmax(*args, tok, flags=pkg.FLAG_NO_GENERATION_MASK)
     dev.synchronize()
     assert tok.host().tolist() == [20, 20, 20]
+
+
+@pytest.mark.gpu
+def test_vocab_argmax_nonfinite_logits_follow_strict_scan(pkg, dev):
+    """The reference scores with a strict '>' scan from -inf that starts at the
+    first unmasked id (q8_engine.rs:749-790): NaN never wins, a row whose
+    logits are all -inf or NaN yields its first candidate, and -0.0 ties with
+    +0.0.  Zero activations make every logit equal to its bias."""
+    V, K = 4096, 64
+    emb = np.zeros((V, K), np.int8)
+    mult = np.ones(V, np.float32)
+    xq = np.zeros((2, K), np.int8)
+    xa = np.ones(2, np.float32)
+
+    def run(bias):
+        tok = dev.DeviceArray.zeros(2, np.int32)
+        args = [dev.DeviceArray.from_host(t) for t in (xq, xa, emb, mult, bias)]
+        dev.vocab_argmax(*args, tok)
+        dev.synchronize()
+        return tok.host().tolist()
+
+    b = np.full(V, -np.inf, np.float32)
+    b[[0, 2, 900]] = np.nan
+    assert run(b) == [0, 0]          # only -inf / NaN: first candidate (id 0)
+    b[0] = -np.inf
+    b[[3, 4]] = np.nan
+    assert run(b) == [0, 0]
+    b[3000] = -5.0
+    b[3001] = np.nan
+    assert run(b) == [3000, 3000]    # the one finite logit wins over NaN
+    b = np.full(V, -1.0, np.float32)
+    b[50] = -0.0
+    b[100] = 0.0
+    assert run(b) == [50, 50]        # -0.0 == +0.0: the lower id
+    b[50] = 0.0
+    b[100] = -0.0
+    assert run(b) == [50, 50]

@@ -113,28 +113,32 @@ def test_gemm_random_against_numpy_int64(orc):
 
 
 # ---- elementary fp32 ----------------------------------------------------------
-def test_canonical_exp_is_correctly_rounded_almost_always(orc):
+def test_exp_modes_are_correctly_rounded_almost_always(orc):
     xs = np.concatenate([np.linspace(-104, 0, 20001), -np.logspace(-8, 2, 2001), [0.0]])
     xs = xs.astype(np.float32)
-    got = np.array([orc.expf(float(x)) for x in xs], np.float32)
     want = np.exp(xs.astype(np.float64)).astype(np.float32)
-    ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
-    assert ulp.max() <= 1
-    assert (ulp == 0).mean() > 0.999
-    assert orc.expf(0.0) == 1.0 and orc.expf(-200.0) == 0.0
-    # the reference-order mode is libm expf: also within one ulp
-    ref = np.array([orc.expf(float(x), orc.REFERENCE) for x in xs[::50]], np.float32)
-    assert np.max(np.abs(ref.view(np.int32).astype(np.int64)
-                         - want[::50].view(np.int32).astype(np.int64))) <= 1
+    for order in (orc.REFERENCE, orc.CANONICAL):
+        got = np.array([orc.expf(float(x), order) for x in xs], np.float32)
+        ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+        assert ulp.max() <= 1
+        assert (ulp == 0).mean() > 0.999
+        assert orc.expf(0.0, order) == 1.0 and orc.expf(-200.0, order) == 0.0
 
 
-def test_canonical_sum_order(orc):
+def test_sum_orders(orc):
     rng = np.random.default_rng(1)
     # integer-valued data: every partial is exact, so any order gives the sum
     x = rng.integers(-1000, 1000, size=512).astype(np.float32)
     assert orc.row_sum(x) == float(x.astype(np.int64).sum())
-    # the canonical order: 64 strided lane partials, then the xor butterfly
+    assert orc.row_sum(x, orc.CANONICAL) == float(x.astype(np.int64).sum())
+    # reference order (the default): strictly sequential from -0.0
     y = rng.standard_normal(512).astype(np.float32)
+    s = np.float32(-0.0)
+    for v in y:
+        s = np.float32(s + v)
+    assert orc.row_sum(y) == float(s)
+    assert math.copysign(1.0, orc.row_sum(np.full(4, -0.0, np.float32))) == -1.0
+    # the canonical alternative: 64 strided lane partials, then the xor butterfly
     p = [np.float32(0)] * 64
     for j in range(512):
         p[j % 64] = np.float32(p[j % 64] + y[j])
@@ -142,12 +146,7 @@ def test_canonical_sum_order(orc):
     while off:
         p = [np.float32(p[l] + p[l ^ off]) for l in range(64)]
         off //= 2
-    assert orc.row_sum(y) == float(p[0])
-    # reference order: strictly sequential
-    s = np.float32(-0.0)
-    for v in y:
-        s = np.float32(s + v)
-    assert orc.row_sum(y, orc.REFERENCE) == float(s)
+    assert orc.row_sum(y, orc.CANONICAL) == float(p[0])
     assert abs(orc.row_sum(y) - math.fsum(map(float, y))) < 1e-4
 
 
@@ -325,3 +324,30 @@ def test_encoder_output_is_batch_invariant(pkg, orc, small_model):
         s = b.subset([i])
         one = orc.encode(om, s.tokens, s.offsets)
         assert np.array_equal(one, full[b.offsets[i]:b.offsets[i + 1]])
+
+
+def test_summation_order_sensitivity(pkg, orc, full_model):
+    """Why the kernels follow the reference's summation order: on identical
+    inputs the two orders agree per op to ~1e-6 relative (well inside 1e-3),
+    but over 6 encoder layers the last-bit differences flip int8 rounding
+    decisions and grow to percent level, so greedy outputs can change."""
+    rng = np.random.default_rng(8)
+    y, z = (rng.standard_normal((64, 512)).astype(np.float32) for _ in range(2))
+    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    ln_r = orc.residual_layer_norm(y, z, g, b)
+    ln_c = orc.residual_layer_norm(y, z, g, b, orc.CANONICAL)
+    assert float(np.max(np.abs(ln_c - ln_r) / np.maximum(np.abs(ln_r), 1.0))) <= 1e-5
+    lens = [3, 40, 128]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    Q, K, V = (rng.standard_normal((int(cu[-1]), 512)).astype(np.float32) for _ in range(3))
+    at_r = orc.attention(Q, K, V, cu, cu, heads=8)
+    at_c = orc.attention(Q, K, V, cu, cu, heads=8, order=orc.CANONICAL)
+    assert float(np.max(np.abs(at_c - at_r) / np.maximum(np.abs(at_r), 1.0))) <= 1e-5
+    om = orc.OracleModel(full_model)
+    b = pkg.ragged_batch(n=8)
+    enc_r = orc.encode(om, b.tokens, b.offsets)
+    enc_c = orc.encode(om, b.tokens, b.offsets, order=orc.CANONICAL)
+    drift = float(np.max(np.abs(enc_c - enc_r) / np.maximum(np.abs(enc_r), 1.0)))
+    print(f"encoder output drift between summation orders: {drift:.3g}")
+    assert 0 < drift < 0.1
