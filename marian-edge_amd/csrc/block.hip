@@ -1,0 +1,304 @@
+// block.hip — decode attention block for steps with few active rows: one
+// 256-thread workgroup per (row, head) builds the row's input (the residual
+// LayerNorm of the previous sublayer, or the decoder input embedding),
+// projects it onto this head's query (self-attention: query, key and value)
+// with int8 MFMA, and attends over the row's keys.  One launch replaces the
+// LayerNorm, projection and attention kernels; the weight and K/V loads are
+// issued first, so they overlap the LayerNorm's sequential folds.
+//
+// Every value is produced by the same operations, in the same order, as the
+// separate kernels (and the reference):
+//   LayerNorm       normalize_row, tensor.rs:372-385 (sequential folds)
+//   quantization    q8_gemm.rs:569-590 (per-row multiplier)
+//   projection      exact i32 MFMA, dequant q8_gemm.rs:438-446
+//   attention       attention_into, tensor.rs:251-318 (sequential dot, max,
+//                   C-library expf, sequential sum from 0.0, PV in key order)
+#include "device_common.h"
+#include "kernels.h"
+
+namespace mh {
+namespace {
+
+constexpr int kBlkThreads = 256;
+constexpr int kBlkD = 512;             // model width handled (8 heads x 64)
+constexpr int kBlkMaxKeys = 128;       // keys staged in LDS
+constexpr int kBlkRow = kHeadDim + 4;  // padded LDS key row (floats)
+constexpr int kBlkKeyPer = kBlkMaxKeys * (kHeadDim / 4) / kBlkThreads;  // float4 per thread (8)
+
+__constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
+
+__device__ __forceinline__ v4i zero4b() { return v4i{0, 0, 0, 0}; }
+
+// Native 4 x fp32 vector (HIP's float4 is a struct whose copies become memcpy,
+// which keeps an array of them out of registers).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Work split: wave 0 builds the input row (its LayerNorm folds are a single
+// dependent chain, so it runs with nothing else live); waves 1-3 meanwhile
+// load this head's weight rows and stage the row's keys and values in LDS,
+// then run the projection; wave 0 attends.
+constexpr int kBlkLoaders = kBlkThreads - 64;  // threads of waves 1-3
+constexpr int kBlkStage = (kBlkMaxKeys * (kHeadDim / 4) + kBlkLoaders - 1) / kBlkLoaders;  // 11
+
+template <int MODE, int PK>
+__global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
+  constexpr bool SELF = MODE == ATT_SELF;
+  constexpr int NT = SELF ? 12 : 4;        // 16-column projection tiles: Q (+ K, V)
+  constexpr int TPW = (NT + 2) / 3;        // tiles per loader wave
+  __shared__ __attribute__((aligned(16))) float sK[kBlkMaxKeys * kBlkRow];
+  __shared__ __attribute__((aligned(16))) float sV[kBlkMaxKeys * kBlkRow];
+  __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
+  __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
+  __shared__ __attribute__((aligned(16))) float sQ[kHeadDim];
+  __shared__ __attribute__((aligned(16))) float sP[kBlkMaxKeys];
+  __shared__ uint64_t sTab[32];
+  __shared__ float sA;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = blockIdx.x % b.heads, r = blockIdx.x / b.heads;  // r < b.rows (host bound)
+  const int n = b.rows_dev ? *b.rows_dev : b.rows;
+  // Key range of this row (read before the device row count is known; rows
+  // past it read clamped stale ranges and are discarded below).
+  int64_t key0 = b.row_key0[r];
+  const int nk_row = SELF ? b.step : b.row_nk[r];
+  key0 = min(max(key0, (int64_t)0), b.max_row - 1);
+  const int nkm = max(min(nk_row, kBlkMaxKeys - (SELF ? 1 : 0)), SELF ? 0 : 1);  // keys from memory
+  const int nk_ld = (int)min((int64_t)nkm, b.max_row - key0);                   // readable rows
+  const int nkey = SELF ? nkm + 1 : nkm;                                       // keys attended
+
+  if (wave == 0) {
+    // ---- the input row: lane l holds elements 4l..4l+3 and 256+4l..+3 -------
+    const uint64_t tab_v = kBlkExp2Tab[lane & 31];
+    f4v o[2];
+    if constexpr (PK == PRO_LN) {
+      f4v y[2], x[2], g[2], bb[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int e = 4 * lane + 256 * j;
+        y[j] = *(const f4v*)(b.pro.y + (int64_t)r * kBlkD + e);
+        x[j] = *(const f4v*)(b.pro.r + (int64_t)r * kBlkD + e);
+        g[j] = *(const f4v*)(b.pro.gamma + e);
+        bb[j] = *(const f4v*)(b.pro.beta + e);
+      }
+      if (r >= n) return;
+      f4v z[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        z[j] = y[j] + x[j];  // add_slices
+        *(f4v*)(sZ + 4 * lane + 256 * j) = z[j];
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+      __builtin_amdgcn_wave_barrier();
+      const float mean = seq_fold_lds<kBlkD / 4>((const float4*)sZ, -0.0f) / (float)kBlkD;
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f4v c = z[j] - mean;
+        *(f4v*)(sZ + 4 * lane + 256 * j) = c * c;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      const float var = seq_fold_lds<kBlkD / 4>((const float4*)sZ, -0.0f) / (float)kBlkD;
+      const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) o[j] = ((z[j] - mean) * inv) * g[j] + bb[j];
+    } else {
+      const int tok = b.pro.row_prev[r];
+      const int tk = max(tok, 0);
+      f4v pos[2];
+      uint32_t e4[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int e = 4 * lane + 256 * j;
+        pos[j] = *(const f4v*)(b.pro.pos + (int64_t)b.pro.step * kBlkD + e);
+        e4[j] = *(const uint32_t*)(b.pro.emb + (int64_t)tk * kBlkD + e);
+      }
+      const float mu = b.pro.emb_mult[tk];
+      if (r >= n) return;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (tok < 0) {
+          o[j] = pos[j];
+        } else {
+          f4v v;
+          v.x = (float)(int8_t)(e4[j] & 0xFF) / mu;
+          v.y = (float)(int8_t)((e4[j] >> 8) & 0xFF) / mu;
+          v.z = (float)(int8_t)((e4[j] >> 16) & 0xFF) / mu;
+          v.w = (float)(int8_t)(e4[j] >> 24) / mu;
+          o[j] = v * b.pro.scale + pos[j];
+        }
+      }
+    }
+    bool bad = false;
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bad |= !isfinite(o[j].x) || !isfinite(o[j].y) || !isfinite(o[j].z) || !isfinite(o[j].w);
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
+    }
+    const float a_row = row_multiplier(wave_max(m));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = 4 * lane + 256 * j;
+      *(uint32_t*)(sX + e) = (uint32_t)(quantize_one(o[j].x, a_row) & 0xFF) |
+                             ((uint32_t)(quantize_one(o[j].y, a_row) & 0xFF) << 8) |
+                             ((uint32_t)(quantize_one(o[j].z, a_row) & 0xFF) << 16) |
+                             ((uint32_t)(quantize_one(o[j].w, a_row) & 0xFF) << 24);
+      if (h == 0 && b.pro.out) *(f4v*)(b.pro.out + (int64_t)r * kBlkD + e) = o[j];
+    }
+    if (lane == 0) sA = a_row;
+    if (lane < 32) sTab[lane] = tab_v;
+    if (__any(bad) && lane == 0 && b.err) *b.err = 1;
+    if (lane == 0 && nk_row > nkm && b.err) *b.err = 2;  // more keys than the LDS stages
+  } else {
+    // ---- waves 1-3: weights, then the keys and values into LDS -----------------
+    const int kq = (lane >> 4) * 16;
+    v4i bf[TPW][kBlkD / 64];
+    float wm[TPW], bi[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = min((wave - 1) + 3 * i, NT - 1);  // 16 columns of Q, K or V
+      const int n_w = (tile / 4) * kBlkD + h * kHeadDim + (tile % 4) * 16 + (lane & 15);
+      const int8_t* wr = b.W + (int64_t)n_w * kBlkD + kq;
+#pragma unroll
+      for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = *(const v4i*)(wr + s * 64);
+      wm[i] = b.wmult[n_w];
+      bi[i] = b.bias[n_w];
+    }
+    // Key rows: loader thread u stages float4 (u + 192 j) % 16 of key (u + 192 j) / 16.
+    // Past the readable keys the last readable row is reloaded (all in bounds)
+    // and not stored.
+    const int u = tid - 64;
+    const int last = max(nk_ld - 1, 0);
+    const int64_t base = key0 * b.ldkv + h * kHeadDim;
+    f4v kv[kBlkStage], vv[kBlkStage];
+#pragma unroll
+    for (int j = 0; j < kBlkStage; ++j) {
+      const int idx = u + kBlkLoaders * j;
+      const int key = min(idx >> 4, last);
+      const int64_t off = base + (int64_t)key * b.ldkv + (idx & 15) * 4;
+      kv[j] = *(const f4v*)(b.k + off);
+      vv[j] = *(const f4v*)(b.v + off);
+    }
+    if (r >= n) return;
+#pragma unroll
+    for (int j = 0; j < kBlkStage; ++j) {
+      const int idx = u + kBlkLoaders * j;
+      if ((idx >> 4) < nk_ld) {  // a live row's keys are all readable (nk_ld == nkm)
+        *(f4v*)(sK + (idx >> 4) * kBlkRow + (idx & 15) * 4) = kv[j];
+        *(f4v*)(sV + (idx >> 4) * kBlkRow + (idx & 15) * 4) = vv[j];
+      }
+    }
+    __syncthreads();  // the input row (wave 0) is in LDS
+    // ---- projection: row 0 of a 16-row MFMA tile ----------------------------------
+    const float a_row = sA;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int tile = (wave - 1) + 3 * i;
+      if (tile >= NT) break;
+      v4i acc = zero4b();
+#pragma unroll
+      for (int s = 0; s < kBlkD / 64; ++s) {
+        const v4i af = (lane & 15) == 0 ? *(const v4i*)(sX + s * 64 + kq) : zero4b();
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[i][s], acc, 0, 0, 0);
+      }
+      if (lane < 16) {  // lanes 0..15 hold row 0 of the tile's 16 columns
+        const int c = (tile % 4) * 16 + lane;
+        const float yv = dequant(acc[0], a_row, wm[i], bi[i]);
+        if (tile < 4) {
+          sQ[c] = yv;
+        } else if (tile < 8) {
+          // This step's key: attended now and cached for later steps.
+          sK[nkm * kBlkRow + c] = yv;
+          b.kc_out[(key0 + b.step) * b.ldkv + h * kHeadDim + c] = yv;
+        } else {
+          sV[nkm * kBlkRow + c] = yv;
+          b.vc_out[(key0 + b.step) * b.ldkv + h * kHeadDim + c] = yv;
+        }
+      }
+    }
+    __syncthreads();  // query and keys are in LDS
+    return;
+  }
+  __syncthreads();  // input row published; keys staged
+  __syncthreads();  // projection done
+
+  // ---- attention (wave 0) ---------------------------------------------------------
+  // Scores: lane = key of chunk c, 64-term dot in dimension order.
+  const float scale = 1.0f / sqrtf((float)kHeadDim);
+  float sc[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int key = c * 64 + lane;
+    sc[c] = -INFINITY;
+    if (c * 64 < nkey) {
+      const float* kr = sK + min(key, nkey - 1) * kBlkRow;
+      float dot = -0.0f;
+#pragma unroll
+      for (int i = 0; i < kHeadDim; i += 4) {
+        const float4 kk = *(const float4*)(kr + i);
+        const float4 qq = *(const float4*)(sQ + i);
+        dot = dot + qq.x * kk.x;
+        dot = dot + qq.y * kk.y;
+        dot = dot + qq.z * kk.z;
+        dot = dot + qq.w * kk.w;
+      }
+      if (key < nkey) sc[c] = dot * scale;
+    }
+  }
+  const float mx = wave_max(fmaxf(sc[0], sc[1]));
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int key = c * 64 + lane;
+    sP[key] = key < nkey ? ref_expf(sc[c] - mx, sTab) : 0.0f;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+  __builtin_amdgcn_wave_barrier();
+  // Denominator: keys in order from 0.0 (softmax_in_place).
+  float sum = 0.0f;
+#pragma unroll 8
+  for (int k = 0; k < nkey; ++k) sum = sum + sP[k];
+  const float inv = 1.0f / sum;
+  // out_d = sum_k v_k[d] * (e_k * inv), keys in order.
+  float o = 0.0f;
+#pragma unroll 8
+  for (int k = 0; k < nkey; ++k) o = o + sV[k * kBlkRow + lane] * (sP[k] * inv);
+  b.out[(int64_t)r * b.ldo + h * kHeadDim + lane] = o;
+  const bool bad = !isfinite(o);
+  const float am = wave_max(fabsf(o));
+  if (lane == 0 && b.amax) b.amax[(int64_t)r * b.heads + h] = am;
+  if (__any(bad) && lane == 0 && b.err) *b.err = 1;
+}
+
+}  // namespace
+
+bool attn_block_supported(int d, int heads, int max_keys) {
+  return d == kBlkD && heads * kHeadDim == kBlkD && max_keys >= 1 && max_keys <= kBlkMaxKeys;
+}
+
+hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s) {
+  if (b.rows <= 0) return hipSuccess;
+  if (!attn_block_supported(kBlkD, b.heads, b.max_keys) || !b.W || !b.wmult || !b.bias ||
+      !b.k || !b.v || !b.out || !b.row_key0 || b.max_row <= 0 ||
+      (b.mode == ATT_CROSS && !b.row_nk) ||
+      (b.mode == ATT_SELF && (!b.kc_out || !b.vc_out || b.step < 0 || b.step + 1 > kBlkMaxKeys)))
+    return hipErrorInvalidValue;
+  const RowPrologue& p = b.pro;
+  if (p.kind == PRO_LN ? !(p.y && p.r && p.gamma && p.beta)
+                       : !(p.kind == PRO_EMB && p.emb && p.emb_mult && p.pos && p.row_prev &&
+                           p.step >= 0 && p.step < kMaxPosition))
+    return hipErrorInvalidValue;
+  const dim3 grid(b.rows * b.heads), block(kBlkThreads);
+  if (b.mode == ATT_SELF) {
+    if (p.kind == PRO_LN)
+      hipLaunchKernelGGL((k_attn_block<ATT_SELF, PRO_LN>), grid, block, 0, s, b);
+    else
+      hipLaunchKernelGGL((k_attn_block<ATT_SELF, PRO_EMB>), grid, block, 0, s, b);
+  } else {
+    if (p.kind != PRO_LN) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_attn_block<ATT_CROSS, PRO_LN>), grid, block, 0, s, b);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mh

@@ -25,6 +25,7 @@ constexpr int kWave = 64;
 constexpr int kHeadDim = 64;           // per-head width supported by the kernels
 constexpr int kMaxPosition = 4096;     // marian-model manifest.rs:13
 constexpr int kMaxRowsPerCall = 4096;  // engine batch ceiling (LDS scan size)
+constexpr float kLayerNormEpsilon = 1.0e-6f;  // tensor.rs:3
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -58,26 +59,81 @@ __device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Maximum over the wave; max is exact in any order, so the reduction uses
+// VALU-only lane moves: DPP within each 16-lane row (quad swaps, rotations by
+// 4 and 8), then the four row maxima are read out as scalars.  Every lane
+// returns the same value.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
 __device__ __forceinline__ float wave_max(float p) {
-  p = fmaxf(p, xor_lane_f<32>(p));
-  p = fmaxf(p, xor_lane_f<16>(p));
-  p = fmaxf(p, xor_lane_f<8>(p));
-  p = fmaxf(p, xor_lane_f<4>(p));
-  p = fmaxf(p, xor_lane_f<2>(p));
-  p = fmaxf(p, xor_lane_f<1>(p));
-  return p;
+  p = fmaxf(p, __int_as_float(dpp_mov<0xB1>(__float_as_int(p))));   // quad_perm [1,0,3,2]
+  p = fmaxf(p, __int_as_float(dpp_mov<0x4E>(__float_as_int(p))));   // quad_perm [2,3,0,1]
+  p = fmaxf(p, __int_as_float(dpp_mov<0x124>(__float_as_int(p))));  // row_ror:4
+  p = fmaxf(p, __int_as_float(dpp_mov<0x128>(__float_as_int(p))));  // row_ror:8
+  const int b = __float_as_int(p);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_mov_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)dpp_mov<CTRL>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)dpp_mov<CTRL>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = umax64(v, xor_lane_u64<32>(v));
-  v = umax64(v, xor_lane_u64<16>(v));
-  v = umax64(v, xor_lane_u64<8>(v));
-  v = umax64(v, xor_lane_u64<4>(v));
-  v = umax64(v, xor_lane_u64<2>(v));
-  v = umax64(v, xor_lane_u64<1>(v));
-  return v;
+  v = umax64(v, dpp_mov_u64<0xB1>(v));
+  v = umax64(v, dpp_mov_u64<0x4E>(v));
+  v = umax64(v, dpp_mov_u64<0x124>(v));
+  v = umax64(v, dpp_mov_u64<0x128>(v));
+  uint64_t best = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * r);
+    best = umax64(best, (hi << 32) | lo);
+  }
+  return best;
+}
+
+// Strictly sequential fp32 fold init + p[0] + p[1] + ... over N4 float4 in
+// LDS (each lane its own p, or one shared p read as a broadcast).  The reads
+// run a batch of NB float4 ahead of the dependent adds so the chain never
+// waits on LDS.
+template <int N4>
+__device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
+  constexpr int NB = 8;
+  static_assert(N4 % NB == 0, "whole batches");
+  float4 cur[NB], nxt[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) cur[b] = p[b];
+  float s = init;
+#pragma unroll
+  for (int k = 0; k < N4 / NB; ++k) {
+    if (k + 1 < N4 / NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) nxt[b] = p[(k + 1) * NB + b];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      s = s + cur[b].x;
+      s = s + cur[b].y;
+      s = s + cur[b].z;
+      s = s + cur[b].w;
+    }
+    if (k + 1 < N4 / NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) cur[b] = nxt[b];
+    }
+  }
+  return s;
 }
 
 // q = clamp(round_half_even(x * a), -127, 127)  (q8_gemm.rs:584-587)

@@ -637,10 +637,100 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   uint32_t steps = 0;
   uint32_t vocab_launches = 0;
   bool done = n_active0 == 0;
+  // Steps with few rows let the GEMM that consumes a LayerNorm (or the decoder
+  // input embedding) build its rows in its own prologue: no separate kernel,
+  // and the LayerNorm's sequential folds overlap that GEMM's weight loads.
+  // `pend` is the not yet materialised layer input; kind PRO_NONE means it
+  // is in DXQ / DXA.
+  RowPrologue pend;
+  auto xgemm = [&](const Lin& L, int mode, const Epilogue& e) -> hipError_t {
+    GemmArgs g;
+    g.A = DXQ;
+    g.a = DXA;
+    g.lda = L.K;
+    g.M = rows_ub;
+    g.M_dev = d_nact;
+    g.K = L.K;
+    g.W = L.w;
+    g.wmult = L.mult;
+    g.bias = L.bias;
+    g.N = L.N;
+    g.pro = pend;
+    pend.kind = PRO_NONE;
+    return launch_gemm_skinny(g, mode, e, s);
+  };
   for (uint32_t t = 0; t < gen_limit && !done; ++t) {
     rows_ub = (int)remaining[t];
     if (rows_ub == 0) break;
-    {
+    // Few rows: LayerNorms and the input embedding run inside the kernel that
+    // consumes them, and each attention sublayer is one block kernel
+    // (LayerNorm + projection + attention) when its key ranges fit.
+    const bool fused = rows_ub <= kProRows && d == (uint32_t)kProK;
+    const bool blk_self = fused && attn_block_supported((int)d, (int)H, (int)t + 1);
+    const bool blk_cross = fused && attn_block_supported((int)d, (int)H, (int)Lmax);
+    float* xres = DX0;  // the residual stream
+    float* xalt = DX1;  // where the next LayerNorm writes it
+    // A LayerNorm of y + xres: run now, or left pending for its consumer.  The
+    // last layer's pending LayerNorm feeds only the vocabulary projection and
+    // need not store its rows.
+    auto layer_norm = [&](const float* y, const float* gm, const float* bt, bool last) -> hipError_t {
+      hipError_t rc = hipSuccess;
+      if (!fused) {
+        rc = launch_residual_ln(y, xres, gm, bt, rows_ub, d_nact, d, xalt, DXQ, DXA, E->err_flag, s);
+      } else {
+        pend = RowPrologue();
+        pend.kind = PRO_LN;
+        pend.y = y;
+        pend.r = xres;
+        pend.gamma = gm;
+        pend.beta = bt;
+        pend.out = last ? nullptr : xalt;
+        pend.err = E->err_flag;
+      }
+      std::swap(xres, xalt);
+      return rc;
+    };
+    auto block = [&](int mode, const Lin& L, const float* k, const float* v, int64_t ldkv,
+                     float* kc_out, float* vc_out, const int64_t* key0, const int32_t* nk,
+                     int64_t max_row, int max_keys) -> hipError_t {
+      BlockArgs ba;
+      ba.mode = mode;
+      ba.pro = pend;
+      pend.kind = PRO_NONE;
+      ba.rows = rows_ub;
+      ba.rows_dev = d_nact;
+      ba.heads = (int)H;
+      ba.W = L.w;
+      ba.wmult = L.mult;
+      ba.bias = L.bias;
+      ba.k = k;
+      ba.v = v;
+      ba.kc_out = kc_out;
+      ba.vc_out = vc_out;
+      ba.ldkv = ldkv;
+      ba.row_key0 = key0;
+      ba.row_nk = nk;
+      ba.step = (int)t;
+      ba.max_row = max_row;
+      ba.max_keys = max_keys;
+      ba.out = DATT;
+      ba.ldo = d;
+      ba.amax = DAMAX;
+      ba.err = E->err_flag;
+      return launch_attn_block(ba, s);
+    };
+    if (fused) {
+      pend = RowPrologue();
+      pend.kind = PRO_EMB;
+      pend.emb = E->emb.w;
+      pend.emb_mult = E->emb.mult;
+      pend.pos = E->pos;
+      pend.scale = E->emb_scale;
+      pend.row_prev = rm.prev;
+      pend.step = (int)t;
+      pend.out = xres;
+      pend.err = E->err_flag;
+    } else {
       EmbedArgs ea;
       ea.emb = E->emb.w;
       ea.emb_mult = E->emb.mult;
@@ -651,7 +741,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ea.step = (int)t;
       ea.rows = rows_ub;
       ea.rows_dev = d_nact;
-      ea.x = DX0;
+      ea.x = xres;
       ea.xq = DXQ;
       ea.xa = DXA;
       ea.err = E->err_flag;
@@ -661,7 +751,12 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       const DecLayer& L = E->dec[l];
       float* kc = KC + (size_t)l * cache_rows * d;
       float* vc = VC + (size_t)l * cache_rows * d;
-      {
+      const float* ckv = CKV + (size_t)l * T * 2 * d;
+      // ---- self-attention over the row's cache ----
+      if (blk_self) {
+        MH_HIP(block(ATT_SELF, L.self_qkv, kc, vc, d, kc, vc, rm.kv0, nullptr, (int64_t)cache_rows,
+                     (int)t + 1));
+      } else {
         Epilogue e;
         e.out = DQ;
         e.ldo = d;
@@ -670,59 +765,62 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         e.row_kv0 = rm.kv0;
         e.step = (int)t;
         e.d = d;
-        MH_HIP(dgemm(DXQ, DXA, L.self_qkv, EPI_QKV_CACHE, e));
+        MH_HIP(xgemm(L.self_qkv, EPI_QKV_CACHE, e));
+        AttnArgs sa;
+        sa.mode = ATT_SELF;
+        sa.q = DQ;
+        sa.ldq = d;
+        sa.k = kc;
+        sa.v = vc;
+        sa.ldkv = d;
+        sa.heads = H;
+        sa.rows = rows_ub;
+        sa.rows_dev = d_nact;
+        sa.row_key0 = rm.kv0;
+        sa.max_row = (int64_t)cache_rows;
+        sa.step = (int)t;
+        sa.max_keys = (int)t + 1;
+        sa.out = DATT;
+        sa.ldo = d;
+        sa.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
+        sa.err = E->err_flag;
+        MH_HIP(launch_attention(sa, s));
       }
-      AttnArgs sa;
-      sa.mode = ATT_SELF;
-      sa.q = DQ;
-      sa.ldq = d;
-      sa.k = kc;
-      sa.v = vc;
-      sa.ldkv = d;
-      sa.heads = H;
-      sa.rows = rows_ub;
-      sa.rows_dev = d_nact;
-      sa.row_key0 = rm.kv0;
-      sa.max_row = (int64_t)cache_rows;
-      sa.step = (int)t;
-      sa.max_keys = (int)t + 1;
-      sa.out = DATT;
-      sa.ldo = d;
-      sa.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
-      sa.err = E->err_flag;
-      MH_HIP(launch_attention(sa, s));
       MH_HIP(agemm(L.self_out, store_epi(DY, d, 0)));
-      MH_HIP(launch_residual_ln(DY, DX0, L.ln1_s, L.ln1_b, rows_ub, d_nact, d, DX1, DXQ, DXA,
-                                E->err_flag, s));
-      MH_HIP(dgemm(DXQ, DXA, L.cross_q, EPI_STORE, store_epi(DQ, d, 0)));
-      AttnArgs ca;
-      ca.mode = ATT_CROSS;
-      ca.q = DQ;
-      ca.ldq = d;
-      ca.k = CKV + (size_t)l * T * 2 * d;
-      ca.v = CKV + (size_t)l * T * 2 * d + d;
-      ca.ldkv = 2 * d;
-      ca.heads = H;
-      ca.rows = rows_ub;
-      ca.rows_dev = d_nact;
-      ca.row_key0 = rm.src0;
-      ca.row_nk = rm.srcn;
-      ca.max_row = T;
-      ca.max_keys = (int)Lmax;
-      ca.out = DATT;
-      ca.ldo = d;
-      ca.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
-      ca.err = E->err_flag;
-      MH_HIP(launch_attention(ca, s));
+      MH_HIP(layer_norm(DY, L.ln1_s, L.ln1_b, false));
+      // ---- cross-attention over the encoder output of the row's sentence ----
+      if (blk_cross) {
+        MH_HIP(block(ATT_CROSS, L.cross_q, ckv, ckv + d, 2 * (int64_t)d, nullptr, nullptr, rm.src0,
+                     rm.srcn, (int64_t)T, (int)Lmax));
+      } else {
+        MH_HIP(xgemm(L.cross_q, EPI_STORE, store_epi(DQ, d, 0)));
+        AttnArgs ca;
+        ca.mode = ATT_CROSS;
+        ca.q = DQ;
+        ca.ldq = d;
+        ca.k = ckv;
+        ca.v = ckv + d;
+        ca.ldkv = 2 * d;
+        ca.heads = H;
+        ca.rows = rows_ub;
+        ca.rows_dev = d_nact;
+        ca.row_key0 = rm.src0;
+        ca.row_nk = rm.srcn;
+        ca.max_row = T;
+        ca.max_keys = (int)Lmax;
+        ca.out = DATT;
+        ca.ldo = d;
+        ca.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
+        ca.err = E->err_flag;
+        MH_HIP(launch_attention(ca, s));
+      }
       MH_HIP(agemm(L.cross_out, store_epi(DY, d, 0)));
-      MH_HIP(launch_residual_ln(DY, DX1, L.ln2_s, L.ln2_b, rows_ub, d_nact, d, DX0, DXQ, DXA,
-                                E->err_flag, s));
-      MH_HIP(dgemm(DXQ, DXA, L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
+      MH_HIP(layer_norm(DY, L.ln2_s, L.ln2_b, false));
+      // ---- feed-forward ----
+      MH_HIP(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
       MH_HIP(launch_quantize_rows(DH, F, rows_ub, d_nact, F, DHQ, F, DHA, E->err_flag, s));
       MH_HIP(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
-      MH_HIP(launch_residual_ln(DY, DX0, L.ln3_s, L.ln3_b, rows_ub, d_nact, d, DX1, DXQ, DXA,
-                                E->err_flag, s));
-      std::swap(DX0, DX1);
+      MH_HIP(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 == E->Ld));
     }
     {
       Epilogue e;
@@ -740,6 +838,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.wmult = E->emb.mult;
       g.bias = E->emb.bias;
       g.N = (int)E->V;
+      g.pro = pend;
+      pend.kind = PRO_NONE;
       // With kernel timing on, the kernel's own dispatch records the events.
       if (E->kernel_timing)
         MH_HIP(launch_vocab_argmax(g, e, s, E->vocab_ev[2 * vocab_launches],

@@ -6,6 +6,34 @@
 
 namespace mh {
 
+// A-operand prologue of the small-M decode kernels: the workgroup builds the
+// quantized activation rows itself instead of reading A / a, so the producer
+// of those rows needs no kernel of its own.
+//   PRO_LN:  rows = LayerNorm(y + r) with gamma/beta (the post-norm residual
+//            LayerNorm of a sublayer's output),
+//   PRO_EMB: rows = emb[prev]/mult * scale + pos[step] (the decoder input; a
+//            negative prev gives pos[step] alone).
+// Workgroup 0 also stores the fp32 rows to `out` (the next residual).  The
+// prologue handles K = kProK and at most kProRows rows (host bound g.M).
+enum ProKind { PRO_NONE = 0, PRO_LN = 1, PRO_EMB = 2 };
+constexpr int kProRows = 16;
+constexpr int kProK = 512;
+struct RowPrologue {
+  int kind = PRO_NONE;
+  const float* y = nullptr;
+  const float* r = nullptr;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  const int8_t* emb = nullptr;
+  const float* emb_mult = nullptr;
+  const float* pos = nullptr;  // [kMaxPosition, K]
+  float scale = 1.0f;
+  const int32_t* row_prev = nullptr;
+  int step = 0;
+  float* out = nullptr;  // fp32 [M, K], or nullptr when nothing reads the rows again
+  int* err = nullptr;    // set to 1 on a non-finite row value
+};
+
 // Quantized activations times an int8 weight matrix [N, K] (K-contiguous).
 struct GemmArgs {
   const int8_t* A = nullptr;  // [M, lda] int8 activations
@@ -26,6 +54,9 @@ struct GemmArgs {
   int64_t ldaf = 0;
   const float* Aamax = nullptr;
   int amax_parts = 0;
+  // Or rows built by the kernel's prologue (skinny kernel with N <= 2048 and
+  // the vocabulary kernel; K = kProK, M <= kProRows).
+  RowPrologue pro;
 };
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
@@ -126,6 +157,41 @@ struct AttnArgs {
   int* err = nullptr;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+// Decode attention block (one launch per attention sublayer on steps with few
+// rows): per (row, head) it builds the row's input with `pro` (PRO_LN, or
+// PRO_EMB for the first self-attention), projects it onto the head's query
+// (ATT_SELF: query, key and value rows h*64.., d + h*64.., 2d + h*64.. of W),
+// and attends.  ATT_SELF attends over cache rows row_key0[r] + [0, step) plus
+// this step's key and value, which it also writes to kc_out / vc_out at row
+// row_key0[r] + step; ATT_CROSS attends over row_key0[r] + [0, row_nk[r]).
+// d = 512, head_dim 64, at most 128 keys per row (max_keys).
+struct BlockArgs {
+  int mode = ATT_SELF;
+  RowPrologue pro;
+  int rows = 0;
+  const int* rows_dev = nullptr;
+  int heads = 0;
+  const int8_t* W = nullptr;  // [3d or d, d]
+  const float* wmult = nullptr;
+  const float* bias = nullptr;
+  const float* k = nullptr;  // key rows (ATT_SELF: the cache), stride ldkv
+  const float* v = nullptr;
+  float* kc_out = nullptr;  // ATT_SELF: this step's key / value rows
+  float* vc_out = nullptr;
+  int64_t ldkv = 0;
+  const int64_t* row_key0 = nullptr;
+  const int32_t* row_nk = nullptr;
+  int step = 0;
+  int64_t max_row = 0;  // key rows of k / v are < max_row
+  int max_keys = 0;     // upper bound on keys attended per row
+  float* out = nullptr;  // [rows, ldo], head h at columns [64h, 64h+64)
+  int64_t ldo = 0;
+  float* amax = nullptr;  // [rows, heads]
+  int* err = nullptr;
+};
+bool attn_block_supported(int d, int heads, int max_keys);
+hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s);
 
 // Per-row decode metadata, rebuilt in active-row order by the finalizer.
 struct RowMeta {

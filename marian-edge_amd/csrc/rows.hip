@@ -7,7 +7,6 @@
 namespace mh {
 namespace {
 
-constexpr float kLayerNormEpsilon = 1.0e-6f;  // tensor.rs:3
 
 // Row quantization for the next GEMM: absmax -> multiplier -> int8
 // (q8_gemm.rs:569-590 with a per-row multiplier).  Non-finite input sets *err.
@@ -67,38 +66,6 @@ __global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_
   }
   if (lane == 0) a[row] = sc;
   if (__any(bad) && lane == 0 && err) *err = 1;
-}
-
-// Strictly sequential fp32 fold init + p[0] + p[1] + ... over N4 float4 in
-// LDS (same address for every lane: broadcast reads).  The reads run a batch
-// of NB float4 ahead of the dependent adds so the chain never waits on LDS.
-template <int N4>
-__device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
-  constexpr int NB = 8;
-  static_assert(N4 % NB == 0, "whole batches");
-  float4 cur[NB], nxt[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) cur[b] = p[b];
-  float s = init;
-#pragma unroll
-  for (int k = 0; k < N4 / NB; ++k) {
-    if (k + 1 < N4 / NB) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) nxt[b] = p[(k + 1) * NB + b];
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      s = s + cur[b].x;
-      s = s + cur[b].y;
-      s = s + cur[b].z;
-      s = s + cur[b].w;
-    }
-    if (k + 1 < N4 / NB) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) cur[b] = nxt[b];
-    }
-  }
-  return s;
 }
 
 // out = LN(y + r), optionally quantized for the next GEMM.  One wave per row.
