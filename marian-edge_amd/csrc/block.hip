@@ -247,22 +247,49 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     }
   }
   const float mx = wave_max(fmaxf(sc[0], sc[1]));
+  float e[2];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int key = c * 64 + lane;
-    sP[key] = key < nkey ? ref_expf(sc[c] - mx, sTab) : 0.0f;
+    e[c] = key < nkey ? ref_expf(sc[c] - mx, sTab) : 0.0f;
+    sP[key] = e[c];
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
   __builtin_amdgcn_wave_barrier();
-  // Denominator: keys in order from 0.0 (softmax_in_place).
-  float sum = 0.0f;
-#pragma unroll 8
-  for (int k = 0; k < nkey; ++k) sum = sum + sP[k];
-  const float inv = 1.0f / sum;
-  // out_d = sum_k v_k[d] * (e_k * inv), keys in order.
+  // Denominator: keys in order from 0.0 (softmax_in_place).  The fold runs
+  // over all kBlkMaxKeys entries: past the last key they hold +0.0, which
+  // leaves the (non-negative) sum unchanged.
+  const float inv = 1.0f / seq_fold_lds<kBlkMaxKeys / 4>((const float4*)sP, 0.0f);
+  __builtin_amdgcn_wave_barrier();
+  // p_k = e_k * inv (scale_in_place), then out_d = sum_k v_k[d] * p_k in key
+  // order.  Keys are taken in batches of 8 whose V values and p are read one
+  // batch ahead; past the last key p is 0 and the row read is a valid key's,
+  // so the added products are +-0 and leave the sum unchanged.
+#pragma unroll
+  for (int c = 0; c < 2; ++c) sP[c * 64 + lane] = e[c] * inv;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const int nbat = (nkey + 7) >> 3;
+  float va[8], pa[8], vb[8], pb[8];
+  auto load8 = [&](int k0, float (&v)[8], float (&pp)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[i] = sV[min(k0 + i, nkey - 1) * kBlkRow + lane];
+      pp[i] = sP[k0 + i];
+    }
+  };
   float o = 0.0f;
-#pragma unroll 8
-  for (int k = 0; k < nkey; ++k) o = o + sV[k * kBlkRow + lane] * (sP[k] * inv);
+  load8(0, va, pa);
+#pragma unroll 1
+  for (int bt = 0; bt < nbat; bt += 2) {
+    if (bt + 1 < nbat) load8((bt + 1) * 8, vb, pb);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o = o + va[i] * pa[i];
+    if (bt + 1 >= nbat) break;
+    if (bt + 2 < nbat) load8((bt + 2) * 8, va, pa);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o = o + vb[i] * pb[i];
+  }
   b.out[(int64_t)r * b.ldo + h * kHeadDim + lane] = o;
   const bool bad = !isfinite(o);
   const float am = wave_max(fabsf(o));

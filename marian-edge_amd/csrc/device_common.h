@@ -104,34 +104,55 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 // Strictly sequential fp32 fold init + p[0] + p[1] + ... over N4 float4 in
-// LDS (each lane its own p, or one shared p read as a broadcast).  The reads
-// run a batch of NB float4 ahead of the dependent adds so the chain never
-// waits on LDS.
+// LDS (each lane its own p, or one shared p read as a broadcast).  Two
+// buffers of NB float4 alternate: the next batch is read while the current
+// one is added, so the dependent chain never waits on LDS.  The batch loop is
+// kept rolled, which bounds the live registers (a fully unrolled fold lets
+// the scheduler hoist every read and spill) and the code size.
 template <int N4>
 __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
-  constexpr int NB = 8;
-  static_assert(N4 % NB == 0, "whole batches");
-  float4 cur[NB], nxt[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) cur[b] = p[b];
+  constexpr int NB = 8, NBATCH = N4 / NB;
+  static_assert(N4 % (2 * NB) == 0, "pairs of batches");
+  float4 A[NB], B[NB];
   float s = init;
 #pragma unroll
-  for (int k = 0; k < N4 / NB; ++k) {
-    if (k + 1 < N4 / NB) {
+  for (int b = 0; b < NB; ++b) A[b] = p[b];
+#pragma unroll 1
+  for (int k = 0; k < NBATCH - 2; k += 2) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) nxt[b] = p[(k + 1) * NB + b];
-    }
+    for (int b = 0; b < NB; ++b) B[b] = p[(k + 1) * NB + b];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      s = s + cur[b].x;
-      s = s + cur[b].y;
-      s = s + cur[b].z;
-      s = s + cur[b].w;
+      s = s + A[b].x;
+      s = s + A[b].y;
+      s = s + A[b].z;
+      s = s + A[b].w;
     }
-    if (k + 1 < N4 / NB) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) cur[b] = nxt[b];
+    for (int b = 0; b < NB; ++b) A[b] = p[(k + 2) * NB + b];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      s = s + B[b].x;
+      s = s + B[b].y;
+      s = s + B[b].z;
+      s = s + B[b].w;
     }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) B[b] = p[(NBATCH - 1) * NB + b];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    s = s + A[b].x;
+    s = s + A[b].y;
+    s = s + A[b].z;
+    s = s + A[b].w;
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    s = s + B[b].x;
+    s = s + B[b].y;
+    s = s + B[b].z;
+    s = s + B[b].w;
   }
   return s;
 }

@@ -585,6 +585,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   }
   int rows_ub = 0;  // host bound on this step's active rows
   constexpr int kAfMaxRows = 16;
+  constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
   auto dgemm = [&](const int8_t* A, const float* a, const Lin& L, int mode, const Epilogue& e) {
     GemmArgs g;
     g.A = A;
@@ -662,20 +663,22 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   for (uint32_t t = 0; t < gen_limit && !done; ++t) {
     rows_ub = (int)remaining[t];
     if (rows_ub == 0) break;
-    // Few rows: LayerNorms and the input embedding run inside the kernel that
-    // consumes them, and each attention sublayer is one block kernel
-    // (LayerNorm + projection + attention) when its key ranges fit.
-    const bool fused = rows_ub <= kProRows && d == (uint32_t)kProK;
-    const bool blk_self = fused && attn_block_supported((int)d, (int)H, (int)t + 1);
-    const bool blk_cross = fused && attn_block_supported((int)d, (int)H, (int)Lmax);
+    // Each attention sublayer is one block kernel (LayerNorm or embedding +
+    // projection + attention) when its key ranges fit; with few rows the
+    // skinny GEMMs also build their input rows in a prologue.  A LayerNorm
+    // (or the embedding) runs inside the kernel that consumes it whenever
+    // that kernel can.
+    const bool pro = rows_ub <= kProRows && d == (uint32_t)kProK;
+    const bool blk_self = rows_ub <= kBlkMaxRows && attn_block_supported((int)d, (int)H, (int)t + 1);
+    const bool blk_cross = rows_ub <= kBlkMaxRows && attn_block_supported((int)d, (int)H, (int)Lmax);
     float* xres = DX0;  // the residual stream
     float* xalt = DX1;  // where the next LayerNorm writes it
-    // A LayerNorm of y + xres: run now, or left pending for its consumer.  The
-    // last layer's pending LayerNorm feeds only the vocabulary projection and
-    // need not store its rows.
-    auto layer_norm = [&](const float* y, const float* gm, const float* bt, bool last) -> hipError_t {
+    // A LayerNorm of y + xres: run now, or (defer) left pending for its
+    // consumer.  The vocabulary kernel is a pure projection + argmax, so the
+    // last layer's LayerNorm always runs on its own.
+    auto layer_norm = [&](const float* y, const float* gm, const float* bt, bool defer) -> hipError_t {
       hipError_t rc = hipSuccess;
-      if (!fused) {
+      if (!defer) {
         rc = launch_residual_ln(y, xres, gm, bt, rows_ub, d_nact, d, xalt, DXQ, DXA, E->err_flag, s);
       } else {
         pend = RowPrologue();
@@ -684,7 +687,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         pend.r = xres;
         pend.gamma = gm;
         pend.beta = bt;
-        pend.out = last ? nullptr : xalt;
+        pend.out = xalt;
         pend.err = E->err_flag;
       }
       std::swap(xres, xalt);
@@ -719,7 +722,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ba.err = E->err_flag;
       return launch_attn_block(ba, s);
     };
-    if (fused) {
+    if (blk_self || pro) {
       pend = RowPrologue();
       pend.kind = PRO_EMB;
       pend.emb = E->emb.w;
@@ -787,7 +790,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         MH_HIP(launch_attention(sa, s));
       }
       MH_HIP(agemm(L.self_out, store_epi(DY, d, 0)));
-      MH_HIP(layer_norm(DY, L.ln1_s, L.ln1_b, false));
+      MH_HIP(layer_norm(DY, L.ln1_s, L.ln1_b, blk_cross || pro));
       // ---- cross-attention over the encoder output of the row's sentence ----
       if (blk_cross) {
         MH_HIP(block(ATT_CROSS, L.cross_q, ckv, ckv + d, 2 * (int64_t)d, nullptr, nullptr, rm.src0,
@@ -815,12 +818,12 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         MH_HIP(launch_attention(ca, s));
       }
       MH_HIP(agemm(L.cross_out, store_epi(DY, d, 0)));
-      MH_HIP(layer_norm(DY, L.ln2_s, L.ln2_b, false));
+      MH_HIP(layer_norm(DY, L.ln2_s, L.ln2_b, pro));
       // ---- feed-forward ----
       MH_HIP(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
       MH_HIP(launch_quantize_rows(DH, F, rows_ub, d_nact, F, DHQ, F, DHA, E->err_flag, s));
       MH_HIP(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
-      MH_HIP(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 == E->Ld));
+      MH_HIP(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && (blk_self || pro)));
     }
     {
       Epilogue e;
@@ -838,8 +841,6 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.wmult = E->emb.mult;
       g.bias = E->emb.bias;
       g.N = (int)E->V;
-      g.pro = pend;
-      pend.kind = PRO_NONE;
       // With kernel timing on, the kernel's own dispatch records the events.
       if (E->kernel_timing)
         MH_HIP(launch_vocab_argmax(g, e, s, E->vocab_ev[2 * vocab_launches],

@@ -434,21 +434,16 @@ constexpr int kVocabCols = 4 * 16 * kVocabCT;     // 128 columns per workgroup
 constexpr int kVocabMaxK = 512;                   // K held in registers
 constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 
-static_assert(kVocabLds == kProLdA, "the prologue writes the vocabulary kernel's A rows");
-template <int PK>  // PRO_NONE: A / a from memory; PRO_LN: built by the row prologue
 __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
   __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
   __shared__ float sAm[kSkinnyRows];
-  __shared__ __attribute__((aligned(16))) SkinnyLds<PK == PRO_NONE ? A_I8 : A_LN> sp;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kq = (lane >> 4) * 16;
   const int ksteps = g.K >> 6;
   const int nbase = blockIdx.x * kVocabCols + wave * 16 * kVocabCT;
 
-  ProRegs pr;
-  if constexpr (PK != PRO_NONE) pro_load<PK>(g.pro, g.M, pr);
   // Weight fragments for the wave's columns over all of K, issued first.
   v4i bf[kVocabCT][kVocabMaxK / 64];
   int ncol[kVocabCT];
@@ -478,7 +473,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   const int cpr = g.K >> 4;
   v4i st[kStage];
   float sa = 0.0f;
-  if constexpr (PK == PRO_NONE) {
+  {
     const int rows_h = min(kSkinnyRows, g.M);
 #pragma unroll
     for (int j = 0; j < kStage; ++j) {
@@ -489,11 +484,10 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     if (tid < rows_h) sa = g.a[tid];
   }
   const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
-  if constexpr (PK != PRO_NONE) pro_build<PK>(g.pro, g.M, M, pr, sp.pro, sA, sAm);
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
-    if (PK == PRO_NONE && m0 > 0) {
+    if (m0 > 0) {
 #pragma unroll
       for (int j = 0; j < kStage; ++j) {
         const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
@@ -503,33 +497,41 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
       }
       sa = tid < rows ? g.a[m0 + tid] : 0.0f;
     }
-    if constexpr (PK == PRO_NONE) {
 #pragma unroll
-      for (int j = 0; j < kStage; ++j) {
-        const int c = tid + 256 * j;
-        *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
-      }
-      if (tid < kSkinnyRows) sAm[tid] = sa;
-      __syncthreads();
+    for (int j = 0; j < kStage; ++j) {
+      const int c = tid + 256 * j;
+      *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
     }
+    if (tid < kSkinnyRows) sAm[tid] = sa;
+    __syncthreads();
     const int mt_n = (rows + 15) >> 4;
+    // All live row tiles advance together over K: up to 4 x kVocabCT
+    // independent accumulation chains keep the matrix core busy.
+    v4i acc[4][kVocabCT];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int ct = 0; ct < kVocabCT; ++ct) acc[mt][ct] = zero4();
+#pragma unroll
+    for (int s = 0; s < kVocabMaxK / 64; ++s) {
+      if (s < ksteps) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          if (mt < mt_n) {
+            const v4i af = *(const v4i*)(sA + (mt * 16 + (lane & 15)) * kVocabLds + kq + s * 64);
+#pragma unroll
+            for (int ct = 0; ct < kVocabCT; ++ct)
+              acc[mt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[ct][s], acc[mt][ct], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // Lane holds rows 4*(lane/16)+r of each tile and column lane%16 of each of
+    // its column tiles: dequantize in registers, keep the best of its columns
+    // per row, and park it in LDS.
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       if (mt < mt_n) {
-        v4i acc[kVocabCT] = {zero4(), zero4()};
-        const int8_t* arow = sA + (mt * 16 + (lane & 15)) * kVocabLds + kq;
-#pragma unroll
-        for (int s = 0; s < kVocabMaxK / 64; ++s) {
-          if (s < ksteps) {
-            const v4i af = *(const v4i*)(arow + s * 64);
-#pragma unroll
-            for (int ct = 0; ct < kVocabCT; ++ct)
-              acc[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[ct][s], acc[ct], 0, 0, 0);
-          }
-        }
-        // Lane holds rows 4*(lane/16)+r of this tile and column lane%16 of
-        // each of its column tiles: dequantize in registers, keep the best of
-        // its columns per row, and park it in LDS.
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int lr = mt * 16 + (lane >> 4) * 4 + r;
@@ -539,7 +541,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
             const float am = sAm[lr];
 #pragma unroll
             for (int ct = 0; ct < kVocabCT; ++ct) {
-              const float y = dequant(acc[ct][r], am, wm[ct], bi[ct]);
+              const float y = dequant(acc[mt][ct][r], am, wm[ct], bi[ct]);
               if (e.logits && ncol[ct] < g.N)
                 e.logits[(int64_t)m * e.ldl + ncol[ct]] = live[ct] ? y : -INFINITY;
               if (live[ct]) {
@@ -726,19 +728,12 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hi
 hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
-  if (g.pro.kind != PRO_NONE && (g.pro.kind != PRO_LN || !prologue_ok(g))) return hipErrorInvalidValue;
+  if (g.pro.kind != PRO_NONE) return hipErrorInvalidValue;
   const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
-  if (g.pro.kind == PRO_LN) {
-    if (ev_start || ev_stop)
-      hipExtLaunchKernelGGL(k_vocab_argmax<PRO_LN>, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
-    else
-      hipLaunchKernelGGL(k_vocab_argmax<PRO_LN>, grid, block, 0, s, g, e);
-  } else {
-    if (ev_start || ev_stop)
-      hipExtLaunchKernelGGL(k_vocab_argmax<PRO_NONE>, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
-    else
-      hipLaunchKernelGGL(k_vocab_argmax<PRO_NONE>, grid, block, 0, s, g, e);
-  }
+  if (ev_start || ev_stop)
+    hipExtLaunchKernelGGL(k_vocab_argmax, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
+  else
+    hipLaunchKernelGGL(k_vocab_argmax, grid, block, 0, s, g, e);
   return hipGetLastError();
 }
 

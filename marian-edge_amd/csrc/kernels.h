@@ -54,8 +54,8 @@ struct GemmArgs {
   int64_t ldaf = 0;
   const float* Aamax = nullptr;
   int amax_parts = 0;
-  // Or rows built by the kernel's prologue (skinny kernel with N <= 2048 and
-  // the vocabulary kernel; K = kProK, M <= kProRows).
+  // Or rows built by the kernel's prologue (skinny kernel only; K = kProK,
+  // M <= kProRows).
   RowPrologue pro;
 };
 
