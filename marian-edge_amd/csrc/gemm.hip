@@ -580,18 +580,21 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
 // owning 64x64 (4x4 MFMA tiles), K in steps of 64 double-buffered through LDS
 // (global -> registers -> LDS, next step's loads in flight during the MFMAs).
 // ---------------------------------------------------------------------------
+template <int TM>  // square tile edge: 128 or 64
 __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e) {
-  __shared__ __attribute__((aligned(16))) int8_t sA[2][kTile * kTileLds];
-  __shared__ __attribute__((aligned(16))) int8_t sB[2][kTile * kTileLds];
+  constexpr int F = TM / 32;            // 16x16 fragments per wave and dimension
+  constexpr int CH = TM * 4 / 256;      // 16-byte chunks per thread per operand and k-step
+  __shared__ __attribute__((aligned(16))) int8_t sA[2][TM * kTileLds];
+  __shared__ __attribute__((aligned(16))) int8_t sB[2][TM * kTileLds];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TM;
   const int M = g.M, N = g.N, K = g.K;
 
-  v4i ra[2], rb[2];
+  v4i ra[CH], rb[CH];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < CH; ++i) {
       const int c = tid + i * 256, row = c >> 2, col = (c & 3) * 16;
       const int m = m0 + row, n = n0 + row;
       ra[i] = m < M ? *(const v4i*)(g.A + (int64_t)m * g.lda + k0 + col) : zero4();
@@ -600,18 +603,18 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e) {
   };
   auto lstore = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < CH; ++i) {
       const int c = tid + i * 256, row = c >> 2, col = (c & 3) * 16;
       *(v4i*)(sA[buf] + row * kTileLds + col) = ra[i];
       *(v4i*)(sB[buf] + row * kTileLds + col) = rb[i];
     }
   };
 
-  v4i acc[4][4];
+  v4i acc[F][F];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < F; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
+    for (int j = 0; j < F; ++j) acc[i][j] = zero4();
 
   gload(0);
   lstore(0);
@@ -621,17 +624,17 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e) {
   for (int k0 = 0; k0 < K; k0 += kTileK) {
     const bool more = k0 + kTileK < K;
     if (more) gload(k0 + kTileK);
-    v4i af[4], bfr[4];
+    v4i af[F], bfr[F];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[i] = *(const v4i*)(sA[cur] + (wm * 64 + i * 16 + (lane & 15)) * kTileLds + kq);
+    for (int i = 0; i < F; ++i)
+      af[i] = *(const v4i*)(sA[cur] + (wm * (TM / 2) + i * 16 + (lane & 15)) * kTileLds + kq);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bfr[j] = *(const v4i*)(sB[cur] + (wn * 64 + j * 16 + (lane & 15)) * kTileLds + kq);
+    for (int j = 0; j < F; ++j)
+      bfr[j] = *(const v4i*)(sB[cur] + (wn * (TM / 2) + j * 16 + (lane & 15)) * kTileLds + kq);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < F; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < F; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bfr[j], acc[i][j], 0, 0, 0);
     if (more) {
       lstore(cur ^ 1);
@@ -641,15 +644,15 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e) {
   }
 
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + j * 16 + (lane & 15);
+  for (int j = 0; j < F; ++j) {
+    const int n = n0 + wn * (TM / 2) + j * 16 + (lane & 15);
     if (n >= N) continue;
     const float wmul = g.wmult[n], bias = g.bias[n];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < F; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
+        const int m = m0 + wm * (TM / 2) + i * 16 + (lane >> 4) * 4 + r;
         if (m < M) {
           const int32_t iv = acc[i][j][r];
           float y = dequant(iv, g.a[m], wmul, bias);
@@ -740,8 +743,16 @@ hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t
 hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   if (g.K <= 0 || g.K % 64 || g.N <= 0 || g.M_dev) return hipErrorInvalidValue;
   if (g.M <= 0) return hipSuccess;
-  const dim3 grid((g.N + kTile - 1) / kTile, (g.M + kTile - 1) / kTile), block(256);
-  hipLaunchKernelGGL(k_gemm_tile, grid, block, 0, s, g, e);
+  // 128x128 tiles only when they already give every CU two workgroups;
+  // otherwise 64x64 tiles (four times as many workgroups).
+  const int64_t big = (int64_t)((g.N + kTile - 1) / kTile) * ((g.M + kTile - 1) / kTile);
+  if (big >= 512) {
+    const dim3 grid((g.N + kTile - 1) / kTile, (g.M + kTile - 1) / kTile), block(256);
+    hipLaunchKernelGGL(k_gemm_tile<kTile>, grid, block, 0, s, g, e);
+  } else {
+    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64), block(256);
+    hipLaunchKernelGGL(k_gemm_tile<64>, grid, block, 0, s, g, e);
+  }
   return hipGetLastError();
 }
 
