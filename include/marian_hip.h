@@ -176,12 +176,28 @@ typedef struct {
   uint64_t generated_tokens;
 } marian_hip_stats;
 int marian_hip_last_stats(const marian_hip_engine* engine, marian_hip_stats* stats);
-/* When enabled, the engine records events around each vocab kernel launch so
- * marian_hip_stats.vocab_kernel_ms is filled, and one event at the end of
- * every decode step (small overhead). */
-int marian_hip_set_kernel_timing(marian_hip_engine* engine, int enabled);
+/* Timing of later translate calls (default 0: none).
+ * MARIAN_HIP_TIME_STEPS: one event at the end of every decode step
+ *   (marian_hip_last_step_trace reports the times); cheap.
+ * MARIAN_HIP_TIME_KERNELS: the vocabulary and attention-block launches record
+ *   events from their own dispatches (marian_hip_stats.vocab_kernel_ms and
+ *   marian_hip_last_kernel_trace are filled); this adds several microseconds
+ *   of device time per timed launch, so throughput is measured without it. */
+#define MARIAN_HIP_TIME_STEPS 1u
+#define MARIAN_HIP_TIME_KERNELS 2u
+int marian_hip_set_timing(marian_hip_engine* engine, uint32_t flags);
+/* Kernel kinds of marian_hip_last_kernel_trace. */
+#define MARIAN_HIP_KERNEL_VOCAB 0       /* vocabulary projection + argmax partials */
+#define MARIAN_HIP_KERNEL_SELF_BLOCK 1  /* decoder self-attention block */
+#define MARIAN_HIP_KERNEL_CROSS_BLOCK 2 /* decoder cross-attention block */
+/* With MARIAN_HIP_TIME_KERNELS: one record per timed decode launch of the last
+ * translate call, in launch order: its kind, decode step, decoder layer and
+ * device duration in microseconds (from events its own dispatch recorded).
+ * Writes min(cap, launches) entries and the launch count to *n. */
+int marian_hip_last_kernel_trace(const marian_hip_engine* engine, uint32_t* kind, uint32_t* step,
+                                 uint32_t* layer, float* us, size_t cap, size_t* n);
 /* Per decode step of the last translate call: the number of active rows the
- * step ran on and, when kernel timing was enabled, the device time at which
+ * step ran on and, with MARIAN_HIP_TIME_STEPS, the device time at which
  * the step's tokens were final (ms from the batch start, else 0).  Writes
  * min(cap, steps) entries and the step count to *n_steps.  A row that
  * produced c tokens completed at step c-1. */

@@ -87,8 +87,9 @@ SIGNATURES = {
     "marian_hip_last_error": (C.c_char_p, [_P]),
     "marian_hip_info": (C.c_int, [_P, C.c_char_p, _SZ]),
     "marian_hip_last_stats": (C.c_int, [_P, C.POINTER(Stats)]),
-    "marian_hip_set_kernel_timing": (C.c_int, [_P, C.c_int]),
+    "marian_hip_set_timing": (C.c_int, [_P, C.c_uint32]),
     "marian_hip_last_step_trace": (C.c_int, [_P, _P, _P, _SZ, C.POINTER(_SZ)]),
+    "marian_hip_last_kernel_trace": (C.c_int, [_P, _P, _P, _P, _P, _SZ, C.POINTER(_SZ)]),
     "marian_hip_quantize_rows": (C.c_int, [_P, _I64, _I64, _P, _P, _P, _P]),
     "marian_hip_q8_linear": (C.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _P, _I64, C.c_int, _P, _P, _P, _P]),
     "marian_hip_residual_layer_norm": (C.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),

@@ -15,6 +15,7 @@
 //                   C-library expf, sequential sum from 0.0, PV in key order)
 #include "device_common.h"
 #include "kernels.h"
+#include <hip/hip_ext.h>
 
 namespace mh {
 namespace {
@@ -57,10 +58,11 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x % b.heads, r = blockIdx.x / b.heads;  // r < b.rows (host bound)
   const int n = b.rows_dev ? *b.rows_dev : b.rows;
+  const int step = b.step;
   // Key range of this row (read before the device row count is known; rows
   // past it read clamped stale ranges and are discarded below).
   int64_t key0 = b.row_key0[r];
-  const int nk_row = SELF ? b.step : b.row_nk[r];
+  const int nk_row = SELF ? step : b.row_nk[r];
   key0 = min(max(key0, (int64_t)0), b.max_row - 1);
   const int nkm = max(min(nk_row, kBlkMaxKeys - (SELF ? 1 : 0)), SELF ? 0 : 1);  // keys from memory
   const int nk_ld = (int)min((int64_t)nkm, b.max_row - key0);                   // readable rows
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int e = 4 * lane + 256 * j;
-        pos[j] = *(const f4v*)(b.pro.pos + (int64_t)b.pro.step * kBlkD + e);
+        pos[j] = *(const f4v*)(b.pro.pos + (int64_t)step * kBlkD + e);
         e4[j] = *(const uint32_t*)(b.pro.emb + (int64_t)tk * kBlkD + e);
       }
       const float mu = b.pro.emb_mult[tk];
@@ -210,10 +212,10 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
         } else if (tile < 8) {
           // This step's key: attended now and cached for later steps.
           sK[nkm * kBlkRow + c] = yv;
-          b.kc_out[(key0 + b.step) * b.ldkv + h * kHeadDim + c] = yv;
+          b.kc_out[(key0 + step) * b.ldkv + h * kHeadDim + c] = yv;
         } else {
           sV[nkm * kBlkRow + c] = yv;
-          b.vc_out[(key0 + b.step) * b.ldkv + h * kHeadDim + c] = yv;
+          b.vc_out[(key0 + step) * b.ldkv + h * kHeadDim + c] = yv;
         }
       }
     }
@@ -303,7 +305,8 @@ bool attn_block_supported(int d, int heads, int max_keys) {
   return d == kBlkD && heads * kHeadDim == kBlkD && max_keys >= 1 && max_keys <= kBlkMaxKeys;
 }
 
-hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s) {
+hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s, hipEvent_t ev_start,
+                             hipEvent_t ev_stop) {
   if (b.rows <= 0) return hipSuccess;
   if (!attn_block_supported(kBlkD, b.heads, b.max_keys) || !b.W || !b.wmult || !b.bias ||
       !b.k || !b.v || !b.out || !b.row_key0 || b.max_row <= 0 ||
@@ -313,18 +316,18 @@ hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s) {
   const RowPrologue& p = b.pro;
   if (p.kind == PRO_LN ? !(p.y && p.r && p.gamma && p.beta)
                        : !(p.kind == PRO_EMB && p.emb && p.emb_mult && p.pos && p.row_prev &&
-                           p.step >= 0 && p.step < kMaxPosition))
+                           b.step >= 0 && b.step < kMaxPosition))
     return hipErrorInvalidValue;
+  if (b.mode == ATT_CROSS && p.kind != PRO_LN) return hipErrorInvalidValue;
   const dim3 grid(b.rows * b.heads), block(kBlkThreads);
-  if (b.mode == ATT_SELF) {
-    if (p.kind == PRO_LN)
-      hipLaunchKernelGGL((k_attn_block<ATT_SELF, PRO_LN>), grid, block, 0, s, b);
-    else
-      hipLaunchKernelGGL((k_attn_block<ATT_SELF, PRO_EMB>), grid, block, 0, s, b);
-  } else {
-    if (p.kind != PRO_LN) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_attn_block<ATT_CROSS, PRO_LN>), grid, block, 0, s, b);
-  }
+  auto kern = b.mode == ATT_CROSS ? k_attn_block<ATT_CROSS, PRO_LN>
+               : p.kind == PRO_LN  ? k_attn_block<ATT_SELF, PRO_LN>
+                                   : k_attn_block<ATT_SELF, PRO_EMB>;
+  // With events the dispatch itself records them at its start and end.
+  if (ev_start || ev_stop)
+    hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev_start, ev_stop, 0, b);
+  else
+    hipLaunchKernelGGL(kern, grid, block, 0, s, b);
   return hipGetLastError();
 }
 

@@ -44,7 +44,7 @@ struct DecLayer {
 // Grow-only device buffers reused across calls (the reference pools its
 // scratch too, q8_engine.rs:733-747).
 enum Buf {
-  B_META, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_ATT, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
+  B_META, B_DMETA, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_ATT, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
   B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DATT, B_DAMAX, B_DY, B_DH, B_DHQ, B_DHA,
   B_PART, B_OUT, B_COUNT, B_HIST, B_COUNT_
 };
@@ -73,7 +73,7 @@ struct marian_hip_engine {
   float emb_scale = 1.0f;
   marian_hip_limits limits{};
   bool ready = true;
-  bool kernel_timing = false;
+  uint32_t timing = 0;  // MARIAN_HIP_TIME_* flags
   std::string error;
   std::string device_name;
 
@@ -88,11 +88,19 @@ struct marian_hip_engine {
   int* err_flag = nullptr;
   int* pinned = nullptr;  // host-visible n_active polls
   hipEvent_t ev[5] = {};  // start, encoder end, decode end, two poll slots
-  std::vector<hipEvent_t> vocab_ev;
+  // Kernel timing: start/stop event pairs of the timed launches and, per
+  // launch, its kind (MARIAN_HIP_KERNEL_*), decode step and decoder layer.
+  std::vector<hipEvent_t> kev;
+  std::vector<uint32_t> kev_kind, kev_step, kev_layer;
+  std::vector<float> kev_us;
   std::vector<hipEvent_t> step_ev;
   std::vector<uint32_t> step_rows;
   std::vector<float> step_ms;
   marian_hip_stats stats{};
+
+  // Row capacities of the decode buffers (grow-only, with headroom): active
+  // rows, KV-cache rows, encoder rows of the cross K/V, decode steps.
+  size_t rcap = 0, ccap = 0, tcap = 0, hcap = 0;
 
   int fail(int code, const char* fmt, ...) {
     char msg[512];
@@ -177,6 +185,7 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     char name[256] = {0};
     if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
       std::snprintf(name, sizeof name, "%s", prop.name);
+    if (!name[0]) std::snprintf(name, sizeof name, "AMD GPU");  // no marketing name visible
     E->device_name = std::string(name) + " (" + prop.gcnArchName + ")";
   }
   if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
@@ -275,7 +284,7 @@ void marian_hip_engine_destroy(marian_hip_engine* E) {
   if (E->pinned) hipHostFree(E->pinned);
   for (auto& ev : E->ev)
     if (ev) hipEventDestroy(ev);
-  for (auto& ev : E->vocab_ev) hipEventDestroy(ev);
+  for (auto& ev : E->kev) hipEventDestroy(ev);
   for (auto& ev : E->step_ev) hipEventDestroy(ev);
   if (E->stream) hipStreamDestroy(E->stream);
   delete E;
@@ -315,9 +324,24 @@ int marian_hip_last_step_trace(const marian_hip_engine* E, uint32_t* active_rows
   return MARIAN_HIP_OK;
 }
 
-int marian_hip_set_kernel_timing(marian_hip_engine* E, int enabled) {
+int marian_hip_last_kernel_trace(const marian_hip_engine* E, uint32_t* kind, uint32_t* step,
+                                 uint32_t* layer, float* us, size_t cap, size_t* n) {
   if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
-  E->kernel_timing = enabled != 0;
+  const size_t m = E->kev_us.size();
+  if (n) *n = m;
+  for (size_t i = 0; i < std::min(cap, m); ++i) {
+    if (kind) kind[i] = E->kev_kind[i];
+    if (step) step[i] = E->kev_step[i];
+    if (layer) layer[i] = E->kev_layer[i];
+    if (us) us[i] = E->kev_us[i];
+  }
+  return MARIAN_HIP_OK;
+}
+
+int marian_hip_set_timing(marian_hip_engine* E, uint32_t flags) {
+  if (!E || (flags & ~(uint32_t)(MARIAN_HIP_TIME_STEPS | MARIAN_HIP_TIME_KERNELS)))
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  E->timing = flags;
   return MARIAN_HIP_OK;
 }
 
@@ -384,17 +408,32 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   const int T = (int)n_tokens, Bi = (int)B;
   E->stats = marian_hip_stats{};
 
-  // ---- host metadata -> one upload ----
-  // Per token: id, position in its sentence, sentence index; the cu offsets.
-  // Per active row (initially every sequence with a non-zero limit, in
-  // order): its sequence, first KV-cache/output row, source range, previous
-  // token and generation limit.
+  // ---- decode-buffer capacities (grow-only) ----
+  const size_t cache_rows = std::max<uint64_t>(total_cap, 1);
+  {
+    auto grow = [](size_t need, size_t cur) { return need <= cur ? cur : std::max(need, cur + cur / 2); };
+    const size_t rc = grow(B, E->rcap), cc = grow(cache_rows, E->ccap),
+                 tc = grow((size_t)std::max(T, 1), E->tcap), hc = grow((size_t)gen_limit + 1, E->hcap);
+    E->rcap = rc;
+    E->ccap = cc;
+    E->tcap = tc;
+    E->hcap = hc;
+  }
+  const size_t R = E->rcap, CR = E->ccap, TR = E->tcap;
+
+  // ---- host metadata -> two uploads ----
+  // Encoder, per token: id, position in its sentence, sentence index; the cu
+  // offsets.  Decoder, per active row (initially every sequence with a
+  // non-zero limit, in order; the rest of the R rows padded with valid
+  // values): its sequence, first KV-cache/output row, source range, previous
+  // token and generation limit; plus the device row count and step.
   std::vector<int32_t> positions(T), seq_of_row(T);
   std::vector<int64_t> kv_base(B);
-  std::vector<int32_t> r_slot, r_srcn, r_prev;
-  std::vector<uint32_t> r_lim;
-  std::vector<int64_t> r_kv0, r_src0;
+  std::vector<int32_t> r_slot(R, 0), r_srcn(R, 1), r_prev(R, -1);
+  std::vector<uint32_t> r_lim(R, 0);
+  std::vector<int64_t> r_kv0(R, 0), r_src0(R, 0);
   int64_t run = 0;
+  int n_active0 = 0;
   for (size_t b = 0; b < B; ++b) {
     for (uint32_t i = offsets[b]; i < offsets[b + 1]; ++i) {
       positions[i] = (int32_t)(i - offsets[b]);
@@ -403,21 +442,14 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     kv_base[b] = run;
     run += limit[b];
     if (limit[b] > 0) {
-      r_slot.push_back((int32_t)b);
-      r_kv0.push_back(kv_base[b]);
-      r_src0.push_back(offsets[b]);
-      r_srcn.push_back((int32_t)(offsets[b + 1] - offsets[b]));
-      r_prev.push_back(-1);
-      r_lim.push_back(limit[b]);
+      r_slot[n_active0] = (int32_t)b;
+      r_kv0[n_active0] = kv_base[b];
+      r_src0[n_active0] = offsets[b];
+      r_srcn[n_active0] = (int32_t)(offsets[b + 1] - offsets[b]);
+      r_lim[n_active0] = limit[b];
+      ++n_active0;
     }
   }
-  const int n_active0 = (int)r_slot.size();
-  r_slot.resize(B, 0);
-  r_kv0.resize(B, 0);
-  r_src0.resize(B, 0);
-  r_srcn.resize(B, 1);
-  r_prev.resize(B, -1);
-  r_lim.resize(B, 0);
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   size_t cur = 0;
   auto place = [&](size_t bytes) {
@@ -426,25 +458,30 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     return o;
   };
   const size_t o_tok = place(4ull * T), o_pos = place(4ull * T), o_seq = place(4ull * T),
-               o_cu = place(4 * (B + 1)), o_nact = place(4), o_rslot = place(4 * B), o_rkv0 = place(8 * B),
-               o_rsrc0 = place(8 * B), o_rsrcn = place(4 * B), o_rprev = place(4 * B),
-               o_rlim = place(4 * B);
+               o_cu = place(4 * (B + 1));
   const size_t meta_bytes = cur;
-  std::vector<char> meta(meta_bytes, 0);
+  cur = 0;
+  const size_t o_state = place(8), o_rslot = place(4 * R), o_rkv0 = place(8 * R),
+               o_rsrc0 = place(8 * R), o_rsrcn = place(4 * R), o_rprev = place(4 * R),
+               o_rlim = place(4 * R);
+  const size_t dmeta_bytes = cur;
+  std::vector<char> meta(meta_bytes, 0), dmeta_h(dmeta_bytes, 0);
   std::memcpy(meta.data() + o_tok, tokens, 4 * (size_t)T);
   std::memcpy(meta.data() + o_pos, positions.data(), 4 * (size_t)T);
   std::memcpy(meta.data() + o_seq, seq_of_row.data(), 4 * (size_t)T);
   std::memcpy(meta.data() + o_cu, offsets, 4 * (B + 1));
-  std::memcpy(meta.data() + o_nact, &n_active0, 4);
-  std::memcpy(meta.data() + o_rslot, r_slot.data(), 4 * B);
-  std::memcpy(meta.data() + o_rkv0, r_kv0.data(), 8 * B);
-  std::memcpy(meta.data() + o_rsrc0, r_src0.data(), 8 * B);
-  std::memcpy(meta.data() + o_rsrcn, r_srcn.data(), 4 * B);
-  std::memcpy(meta.data() + o_rprev, r_prev.data(), 4 * B);
-  std::memcpy(meta.data() + o_rlim, r_lim.data(), 4 * B);
+  const int state0[2] = {n_active0, 0};  // device row count, decode step
+  std::memcpy(dmeta_h.data() + o_state, state0, 8);
+  std::memcpy(dmeta_h.data() + o_rslot, r_slot.data(), 4 * R);
+  std::memcpy(dmeta_h.data() + o_rkv0, r_kv0.data(), 8 * R);
+  std::memcpy(dmeta_h.data() + o_rsrc0, r_src0.data(), 8 * R);
+  std::memcpy(dmeta_h.data() + o_rsrcn, r_srcn.data(), 4 * R);
+  std::memcpy(dmeta_h.data() + o_rprev, r_prev.data(), 4 * R);
+  std::memcpy(dmeta_h.data() + o_rlim, r_lim.data(), 4 * R);
 
-  const size_t cache_rows = std::max<uint64_t>(total_cap, 1);
+  const uint32_t LdA = std::max<uint32_t>(E->Ld, 1);
   char* dmeta = (char*)E->get(B_META, meta_bytes);
+  char* ddec = (char*)E->get(B_DMETA, dmeta_bytes);
   float* X0 = (float*)E->get(B_X0, 4ull * T * d);
   float* X1 = (float*)E->get(B_X1, 4ull * T * d);
   int8_t* XQ = (int8_t*)E->get(B_XQ, (size_t)T * d);
@@ -457,25 +494,25 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   float* Hb = (float*)E->get(B_H, 4ull * T * F);
   int8_t* HQ = (int8_t*)E->get(B_HQ, (size_t)T * F);
   float* HA = (float*)E->get(B_HA, 4ull * T);
-  float* CKV = (float*)E->get(B_CKV, 8ull * T * d * std::max<uint32_t>(E->Ld, 1));
-  float* KC = (float*)E->get(B_KC, 4ull * cache_rows * d * std::max<uint32_t>(E->Ld, 1));
-  float* VC = (float*)E->get(B_VC, 4ull * cache_rows * d * std::max<uint32_t>(E->Ld, 1));
-  float* DX0 = (float*)E->get(B_DX0, 4ull * B * d);
-  float* DX1 = (float*)E->get(B_DX1, 4ull * B * d);
-  int8_t* DXQ = (int8_t*)E->get(B_DXQ, B * d);
-  float* DXA = (float*)E->get(B_DXA, 4ull * B);
-  float* DQ = (float*)E->get(B_DQ, 4ull * B * d);
-  float* DATT = (float*)E->get(B_DATT, 4ull * B * d);
-  float* DAMAX = (float*)E->get(B_DAMAX, 4ull * B * H);
-  float* DY = (float*)E->get(B_DY, 4ull * B * d);
-  float* DH = (float*)E->get(B_DH, 4ull * B * F);
-  int8_t* DHQ = (int8_t*)E->get(B_DHQ, B * F);
-  float* DHA = (float*)E->get(B_DHA, 4ull * B);
+  float* CKV = (float*)E->get(B_CKV, 8ull * TR * d * LdA);
+  float* KC = (float*)E->get(B_KC, 4ull * CR * d * LdA);
+  float* VC = (float*)E->get(B_VC, 4ull * CR * d * LdA);
+  float* DX0 = (float*)E->get(B_DX0, 4ull * R * d);
+  float* DX1 = (float*)E->get(B_DX1, 4ull * R * d);
+  int8_t* DXQ = (int8_t*)E->get(B_DXQ, R * d);
+  float* DXA = (float*)E->get(B_DXA, 4ull * R);
+  float* DQ = (float*)E->get(B_DQ, 4ull * R * d);
+  float* DATT = (float*)E->get(B_DATT, 4ull * R * d);
+  float* DAMAX = (float*)E->get(B_DAMAX, 4ull * R * H);
+  float* DY = (float*)E->get(B_DY, 4ull * R * d);
+  float* DH = (float*)E->get(B_DH, 4ull * R * F);
+  int8_t* DHQ = (int8_t*)E->get(B_DHQ, R * F);
+  float* DHA = (float*)E->get(B_DHA, 4ull * R);
   const int nparts = argmax_groups((int)E->V, (int)E->d);
-  uint64_t* PART = (uint64_t*)E->get(B_PART, 8ull * B * nparts);
-  int32_t* OUT = (int32_t*)E->get(B_OUT, 4ull * cache_rows);
-  uint32_t* COUNT = (uint32_t*)E->get(B_COUNT, 4ull * B);
-  uint32_t* HIST = (uint32_t*)E->get(B_HIST, 4ull * (gen_limit + 1));
+  uint64_t* PART = (uint64_t*)E->get(B_PART, 8ull * R * nparts);
+  int32_t* OUT = (int32_t*)E->get(B_OUT, 4ull * CR);
+  uint32_t* COUNT = (uint32_t*)E->get(B_COUNT, 4ull * R);
+  uint32_t* HIST = (uint32_t*)E->get(B_HIST, 4ull * E->hcap);
   for (int b = 0; b < B_COUNT_; ++b)
     if (!E->buf[b]) return E->fail(MARIAN_HIP_ERR_DEVICE, "device allocation failed");
 
@@ -483,16 +520,18 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   int32_t* d_pos = (int32_t*)(dmeta + o_pos);
   int32_t* d_seq = (int32_t*)(dmeta + o_seq);
   uint32_t* d_cu = (uint32_t*)(dmeta + o_cu);
-  int* d_nact = (int*)(dmeta + o_nact);
+  int* d_nact = (int*)(ddec + o_state);
+  int* d_step = d_nact + 1;
   RowMeta rm;
-  rm.slot = (int*)(dmeta + o_rslot);
-  rm.kv0 = (int64_t*)(dmeta + o_rkv0);
-  rm.src0 = (int64_t*)(dmeta + o_rsrc0);
-  rm.srcn = (int32_t*)(dmeta + o_rsrcn);
-  rm.prev = (int32_t*)(dmeta + o_rprev);
-  rm.limit = (uint32_t*)(dmeta + o_rlim);
+  rm.slot = (int*)(ddec + o_rslot);
+  rm.kv0 = (int64_t*)(ddec + o_rkv0);
+  rm.src0 = (int64_t*)(ddec + o_rsrc0);
+  rm.srcn = (int32_t*)(ddec + o_rsrcn);
+  rm.prev = (int32_t*)(ddec + o_rprev);
+  rm.limit = (uint32_t*)(ddec + o_rlim);
 
   MH_HIP(hipMemcpyAsync(dmeta, meta.data(), meta_bytes, hipMemcpyHostToDevice, s));
+  MH_HIP(hipMemcpyAsync(ddec, dmeta_h.data(), dmeta_bytes, hipMemcpyHostToDevice, s));
   MH_HIP(hipMemsetAsync(E->err_flag, 0, sizeof(int), s));
   MH_HIP(hipMemsetAsync(COUNT, 0, 4 * B, s));
   // The timed region starts with the packed inputs resident in HBM.
@@ -560,22 +599,44 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, XQ, XA, E->err_flag, s));
   }
   for (uint32_t l = 0; l < E->Ld; ++l)
-    MH_HIP(gemm(XQ, XA, T, E->dec[l].cross_kv, CKV + (size_t)l * T * 2 * d, 0));
+    MH_HIP(gemm(XQ, XA, T, E->dec[l].cross_kv, CKV + (size_t)l * TR * 2 * d, 0));
   MH_HIP(hipEventRecord(E->ev[1], s));
 
   // ---- greedy decode with device-side active set ----
-  if (E->kernel_timing) {
-    while (E->vocab_ev.size() < 2ull * gen_limit) {
-      hipEvent_t ev;
-      MH_HIP(hipEventCreate(&ev));
-      E->vocab_ev.push_back(ev);
-    }
+  E->kev_kind.clear();
+  E->kev_step.clear();
+  E->kev_layer.clear();
+  E->kev_us.clear();
+  const bool time_steps = E->timing & MARIAN_HIP_TIME_STEPS;
+  const bool time_kernels = E->timing & MARIAN_HIP_TIME_KERNELS;
+  if (time_steps) {
     while (E->step_ev.size() < gen_limit) {
       hipEvent_t ev;
       MH_HIP(hipEventCreate(&ev));
       E->step_ev.push_back(ev);
     }
   }
+  // With kernel timing on, a timed launch's own dispatch records a start and
+  // a stop event (ev[0], ev[1]); otherwise both stay null.  Each such launch
+  // costs several microseconds of extra device time.
+  size_t n_timed = 0;
+  auto timer = [&](uint32_t kind, uint32_t step, uint32_t layer, hipEvent_t* ev) -> hipError_t {
+    ev[0] = ev[1] = nullptr;
+    if (!time_kernels) return hipSuccess;
+    while (E->kev.size() < 2 * (n_timed + 1)) {
+      hipEvent_t x;
+      const hipError_t rc = hipEventCreate(&x);
+      if (rc != hipSuccess) return rc;
+      E->kev.push_back(x);
+    }
+    ev[0] = E->kev[2 * n_timed];
+    ev[1] = E->kev[2 * n_timed + 1];
+    E->kev_kind.push_back(kind);
+    E->kev_step.push_back(step);
+    E->kev_layer.push_back(layer);
+    ++n_timed;
+    return hipSuccess;
+  };
   std::vector<uint32_t> remaining(gen_limit + 1, 0);  // rows with limit > t
   for (size_t b = 0; b < B; ++b) remaining[0] += limit[b] > 0;
   {
@@ -583,103 +644,98 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     for (size_t b = 0; b < B; ++b) ends[limit[b]]++;
     for (uint32_t t = 1; t <= gen_limit; ++t) remaining[t] = remaining[t - 1] - ends[t];
   }
-  int rows_ub = 0;  // host bound on this step's active rows
   constexpr int kAfMaxRows = 16;
   constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
-  auto dgemm = [&](const int8_t* A, const float* a, const Lin& L, int mode, const Epilogue& e) {
-    GemmArgs g;
-    g.A = A;
-    g.a = a;
-    g.lda = L.K;
-    g.M = rows_ub;
-    g.M_dev = d_nact;
-    g.K = L.K;
-    g.W = L.w;
-    g.wmult = L.mult;
-    g.bias = L.bias;
-    g.N = L.N;
-    return launch_gemm_skinny(g, mode, e, s);
+
+  // What one decode step launches is decided on the host: the row bound
+  // (grid sizes; rows at or past the device row count exit early), the path
+  // of each attention sublayer and the key bounds that pick kernel variants.
+  struct StepPlan {
+    int rows, self_keys, cross_keys;
+    bool blk_self, blk_cross, af;
   };
-  // Attention-output projection.  Up to kAfMaxRows rows, A is the fp32
-  // attention output, quantized while loading with the per-head maxima the
-  // attention kernel wrote; above that every workgroup would repeat the
-  // quantization of many rows, so a row-quantization pass runs first.
-  auto agemm = [&](const Lin& L, const Epilogue& e) -> hipError_t {
-    if (rows_ub > kAfMaxRows) {
-      hipError_t rc = launch_quantize_rows(DATT, d, rows_ub, d_nact, d, DHQ, d, DHA, E->err_flag, s);
-      if (rc != hipSuccess) return rc;
-      return dgemm(DHQ, DHA, L, EPI_STORE, e);
-    }
-    GemmArgs g;
-    g.Af = DATT;
-    g.ldaf = d;
-    g.Aamax = DAMAX;
-    g.amax_parts = H;
-    g.M = rows_ub;
-    g.M_dev = d_nact;
-    g.K = L.K;
-    g.W = L.w;
-    g.wmult = L.mult;
-    g.bias = L.bias;
-    g.N = L.N;
-    return launch_gemm_skinny(g, EPI_STORE, e, s);
+  auto make_plan = [&](int rows, int self_keys, int cross_keys) {
+    StepPlan P;
+    P.rows = rows;
+    P.self_keys = self_keys;
+    P.cross_keys = cross_keys;
+    P.blk_self = rows <= kBlkMaxRows && attn_block_supported(d, H, self_keys);
+    P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
+    P.af = rows <= kAfMaxRows;
+    return P;
   };
-  auto store_epi = [&](float* out, int ldo, int relu) {
-    Epilogue e;
-    e.out = out;
-    e.ldo = ldo;
-    e.relu = relu;
-    return e;
-  };
-  // Poll the active count every kPoll steps without blocking; stop launching
-  // once it has reached zero (rows can end early on EOS).
-  constexpr uint32_t kPoll = 8;
-  int poll_slot = 0;
-  uint32_t steps = 0;
-  uint32_t vocab_launches = 0;
-  bool done = n_active0 == 0;
-  // Steps with few rows let the GEMM that consumes a LayerNorm (or the decoder
-  // input embedding) build its rows in its own prologue: no separate kernel,
-  // and the LayerNorm's sequential folds overlap that GEMM's weight loads.
-  // `pend` is the not yet materialised layer input; kind PRO_NONE means it
-  // is in DXQ / DXA.
-  RowPrologue pend;
-  auto xgemm = [&](const Lin& L, int mode, const Epilogue& e) -> hipError_t {
-    GemmArgs g;
-    g.A = DXQ;
-    g.a = DXA;
-    g.lda = L.K;
-    g.M = rows_ub;
-    g.M_dev = d_nact;
-    g.K = L.K;
-    g.W = L.w;
-    g.wmult = L.mult;
-    g.bias = L.bias;
-    g.N = L.N;
-    g.pro = pend;
-    pend.kind = PRO_NONE;
-    return launch_gemm_skinny(g, mode, e, s);
-  };
-  for (uint32_t t = 0; t < gen_limit && !done; ++t) {
-    rows_ub = (int)remaining[t];
-    if (rows_ub == 0) break;
-    // Each attention sublayer is one block kernel (LayerNorm or embedding +
-    // projection + attention) when its key ranges fit; with few rows the
-    // skinny GEMMs also build their input rows in a prologue.  A LayerNorm
-    // (or the embedding) runs inside the kernel that consumes it whenever
-    // that kernel can.
-    const bool pro = rows_ub <= kProRows && d == (uint32_t)kProK;
-    const bool blk_self = rows_ub <= kBlkMaxRows && attn_block_supported((int)d, (int)H, (int)t + 1);
-    const bool blk_cross = rows_ub <= kBlkMaxRows && attn_block_supported((int)d, (int)H, (int)Lmax);
+
+#define MH_TRY(expr)                            \
+  do {                                          \
+    const hipError_t e_ = (expr);               \
+    if (e_ != hipSuccess) return e_;            \
+  } while (0)
+
+  // The launches of decode step t.
+  auto emit_step = [&](const StepPlan& P, uint32_t t) -> hipError_t {
+    const int rows = P.rows;
+    // When an attention block consumes a LayerNorm (or the decoder input
+    // embedding), it builds its rows in its own prologue: no separate kernel,
+    // and the LayerNorm's sequential folds overlap the block's weight and key
+    // loads.  `pend` is the not yet materialised layer input; kind PRO_NONE
+    // means it is in DXQ / DXA.
+    RowPrologue pend;
     float* xres = DX0;  // the residual stream
     float* xalt = DX1;  // where the next LayerNorm writes it
+    auto dgemm = [&](const int8_t* A, const float* a, const Lin& L, int mode, const Epilogue& e) {
+      GemmArgs g;
+      g.A = A;
+      g.a = a;
+      g.lda = L.K;
+      g.M = rows;
+      g.M_dev = d_nact;
+      g.K = L.K;
+      g.W = L.w;
+      g.wmult = L.mult;
+      g.bias = L.bias;
+      g.N = L.N;
+      return launch_gemm_skinny(g, mode, e, s);
+    };
+    // Attention-output projection.  Up to kAfMaxRows rows, A is the fp32
+    // attention output, quantized while loading with the per-head maxima the
+    // attention kernel wrote; above that every workgroup would repeat the
+    // quantization of many rows, so a row-quantization pass runs first.
+    auto agemm = [&](const Lin& L, const Epilogue& e) -> hipError_t {
+      if (!P.af) {
+        MH_TRY(launch_quantize_rows(DATT, d, rows, d_nact, d, DHQ, d, DHA, E->err_flag, s));
+        return dgemm(DHQ, DHA, L, EPI_STORE, e);
+      }
+      GemmArgs g;
+      g.Af = DATT;
+      g.ldaf = d;
+      g.Aamax = DAMAX;
+      g.amax_parts = H;
+      g.M = rows;
+      g.M_dev = d_nact;
+      g.K = L.K;
+      g.W = L.w;
+      g.wmult = L.mult;
+      g.bias = L.bias;
+      g.N = L.N;
+      return launch_gemm_skinny(g, EPI_STORE, e, s);
+    };
+    auto store_epi = [&](float* out, int ldo, int relu) {
+      Epilogue e;
+      e.out = out;
+      e.ldo = ldo;
+      e.relu = relu;
+      return e;
+    };
+    auto xgemm = [&](const Lin& L, int mode, const Epilogue& e) -> hipError_t {
+      return dgemm(DXQ, DXA, L, mode, e);
+    };
     // A LayerNorm of y + xres: run now, or (defer) left pending for its
     // consumer.  The vocabulary kernel is a pure projection + argmax, so the
     // last layer's LayerNorm always runs on its own.
     auto layer_norm = [&](const float* y, const float* gm, const float* bt, bool defer) -> hipError_t {
       hipError_t rc = hipSuccess;
       if (!defer) {
-        rc = launch_residual_ln(y, xres, gm, bt, rows_ub, d_nact, d, xalt, DXQ, DXA, E->err_flag, s);
+        rc = launch_residual_ln(y, xres, gm, bt, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag, s);
       } else {
         pend = RowPrologue();
         pend.kind = PRO_LN;
@@ -693,14 +749,17 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       std::swap(xres, xalt);
       return rc;
     };
-    auto block = [&](int mode, const Lin& L, const float* k, const float* v, int64_t ldkv,
-                     float* kc_out, float* vc_out, const int64_t* key0, const int32_t* nk,
-                     int64_t max_row, int max_keys) -> hipError_t {
+    auto block = [&](int mode, uint32_t layer, const Lin& L, const float* k, const float* v,
+                     int64_t ldkv, float* kc_out, float* vc_out, const int64_t* key0,
+                     const int32_t* nk, int64_t max_row, int max_keys) -> hipError_t {
+      hipEvent_t ev[2];
+      MH_TRY(timer(mode == ATT_SELF ? MARIAN_HIP_KERNEL_SELF_BLOCK : MARIAN_HIP_KERNEL_CROSS_BLOCK, t,
+                   layer, ev));
       BlockArgs ba;
       ba.mode = mode;
       ba.pro = pend;
       pend.kind = PRO_NONE;
-      ba.rows = rows_ub;
+      ba.rows = rows;
       ba.rows_dev = d_nact;
       ba.heads = (int)H;
       ba.W = L.w;
@@ -720,9 +779,9 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ba.ldo = d;
       ba.amax = DAMAX;
       ba.err = E->err_flag;
-      return launch_attn_block(ba, s);
+      return launch_attn_block(ba, s, ev[0], ev[1]);
     };
-    if (blk_self || pro) {
+    if (P.blk_self) {
       pend = RowPrologue();
       pend.kind = PRO_EMB;
       pend.emb = E->emb.w;
@@ -730,7 +789,6 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       pend.pos = E->pos;
       pend.scale = E->emb_scale;
       pend.row_prev = rm.prev;
-      pend.step = (int)t;
       pend.out = xres;
       pend.err = E->err_flag;
     } else {
@@ -742,23 +800,23 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ea.d = d;
       ea.row_prev = rm.prev;
       ea.step = (int)t;
-      ea.rows = rows_ub;
+      ea.rows = rows;
       ea.rows_dev = d_nact;
       ea.x = xres;
       ea.xq = DXQ;
       ea.xa = DXA;
       ea.err = E->err_flag;
-      MH_HIP(launch_embed(ea, s));
+      MH_TRY(launch_embed(ea, s));
     }
     for (uint32_t l = 0; l < E->Ld; ++l) {
       const DecLayer& L = E->dec[l];
-      float* kc = KC + (size_t)l * cache_rows * d;
-      float* vc = VC + (size_t)l * cache_rows * d;
-      const float* ckv = CKV + (size_t)l * T * 2 * d;
+      float* kc = KC + (size_t)l * CR * d;
+      float* vc = VC + (size_t)l * CR * d;
+      const float* ckv = CKV + (size_t)l * TR * 2 * d;
       // ---- self-attention over the row's cache ----
-      if (blk_self) {
-        MH_HIP(block(ATT_SELF, L.self_qkv, kc, vc, d, kc, vc, rm.kv0, nullptr, (int64_t)cache_rows,
-                     (int)t + 1));
+      if (P.blk_self) {
+        MH_TRY(block(ATT_SELF, l, L.self_qkv, kc, vc, d, kc, vc, rm.kv0, nullptr, (int64_t)CR,
+                     P.self_keys));
       } else {
         Epilogue e;
         e.out = DQ;
@@ -768,7 +826,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         e.row_kv0 = rm.kv0;
         e.step = (int)t;
         e.d = d;
-        MH_HIP(xgemm(L.self_qkv, EPI_QKV_CACHE, e));
+        MH_TRY(xgemm(L.self_qkv, EPI_QKV_CACHE, e));
         AttnArgs sa;
         sa.mode = ATT_SELF;
         sa.q = DQ;
@@ -777,26 +835,26 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         sa.v = vc;
         sa.ldkv = d;
         sa.heads = H;
-        sa.rows = rows_ub;
+        sa.rows = rows;
         sa.rows_dev = d_nact;
         sa.row_key0 = rm.kv0;
-        sa.max_row = (int64_t)cache_rows;
+        sa.max_row = (int64_t)CR;
         sa.step = (int)t;
-        sa.max_keys = (int)t + 1;
+        sa.max_keys = P.self_keys;
         sa.out = DATT;
         sa.ldo = d;
-        sa.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
+        sa.amax = P.af ? DAMAX : nullptr;
         sa.err = E->err_flag;
-        MH_HIP(launch_attention(sa, s));
+        MH_TRY(launch_attention(sa, s));
       }
-      MH_HIP(agemm(L.self_out, store_epi(DY, d, 0)));
-      MH_HIP(layer_norm(DY, L.ln1_s, L.ln1_b, blk_cross || pro));
+      MH_TRY(agemm(L.self_out, store_epi(DY, d, 0)));
+      MH_TRY(layer_norm(DY, L.ln1_s, L.ln1_b, P.blk_cross));
       // ---- cross-attention over the encoder output of the row's sentence ----
-      if (blk_cross) {
-        MH_HIP(block(ATT_CROSS, L.cross_q, ckv, ckv + d, 2 * (int64_t)d, nullptr, nullptr, rm.src0,
-                     rm.srcn, (int64_t)T, (int)Lmax));
+      if (P.blk_cross) {
+        MH_TRY(block(ATT_CROSS, l, L.cross_q, ckv, ckv + d, 2 * (int64_t)d, nullptr, nullptr, rm.src0,
+                     rm.srcn, (int64_t)TR, P.cross_keys));
       } else {
-        MH_HIP(xgemm(L.cross_q, EPI_STORE, store_epi(DQ, d, 0)));
+        MH_TRY(xgemm(L.cross_q, EPI_STORE, store_epi(DQ, d, 0)));
         AttnArgs ca;
         ca.mode = ATT_CROSS;
         ca.q = DQ;
@@ -805,25 +863,25 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         ca.v = ckv + d;
         ca.ldkv = 2 * d;
         ca.heads = H;
-        ca.rows = rows_ub;
+        ca.rows = rows;
         ca.rows_dev = d_nact;
         ca.row_key0 = rm.src0;
         ca.row_nk = rm.srcn;
-        ca.max_row = T;
-        ca.max_keys = (int)Lmax;
+        ca.max_row = (int64_t)TR;
+        ca.max_keys = P.cross_keys;
         ca.out = DATT;
         ca.ldo = d;
-        ca.amax = rows_ub > kAfMaxRows ? nullptr : DAMAX;
+        ca.amax = P.af ? DAMAX : nullptr;
         ca.err = E->err_flag;
-        MH_HIP(launch_attention(ca, s));
+        MH_TRY(launch_attention(ca, s));
       }
-      MH_HIP(agemm(L.cross_out, store_epi(DY, d, 0)));
-      MH_HIP(layer_norm(DY, L.ln2_s, L.ln2_b, pro));
+      MH_TRY(agemm(L.cross_out, store_epi(DY, d, 0)));
+      MH_TRY(layer_norm(DY, L.ln2_s, L.ln2_b, false));
       // ---- feed-forward ----
-      MH_HIP(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
-      MH_HIP(launch_quantize_rows(DH, F, rows_ub, d_nact, F, DHQ, F, DHA, E->err_flag, s));
-      MH_HIP(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
-      MH_HIP(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && (blk_self || pro)));
+      MH_TRY(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
+      MH_TRY(launch_quantize_rows(DH, F, rows, d_nact, F, DHQ, F, DHA, E->err_flag, s));
+      MH_TRY(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
+      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && P.blk_self));
     }
     {
       Epilogue e;
@@ -834,49 +892,58 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.A = DXQ;
       g.a = DXA;
       g.lda = d;
-      g.M = rows_ub;
+      g.M = rows;
       g.M_dev = d_nact;
       g.K = d;
       g.W = E->emb.w;
       g.wmult = E->emb.mult;
       g.bias = E->emb.bias;
       g.N = (int)E->V;
-      // With kernel timing on, the kernel's own dispatch records the events.
-      if (E->kernel_timing)
-        MH_HIP(launch_vocab_argmax(g, e, s, E->vocab_ev[2 * vocab_launches],
-                                   E->vocab_ev[2 * vocab_launches + 1]));
-      else
-        MH_HIP(launch_vocab_argmax(g, e, s));
-      ++vocab_launches;
+      hipEvent_t ev[2];
+      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
+      MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));
     }
-    {
-      FinalizeArgs f;
-      f.partials = PART;
-      f.nparts = nparts;
-      f.rows = rm;
-      f.n_active = d_nact;
-      f.rows_ub = rows_ub;
-      f.err = E->err_flag;
-      f.out_tok = OUT;
-      f.count = COUNT;
-      f.step = (int)t;
-      f.flags = flags;
-      f.active_hist = HIST;
-      MH_HIP(launch_finalize(f, s));
-      if (E->kernel_timing) MH_HIP(hipEventRecord(E->step_ev[t], s));
-    }
+    FinalizeArgs f;
+    f.partials = PART;
+    f.nparts = nparts;
+    f.rows = rm;
+    f.n_active = d_nact;
+    f.rows_ub = rows;
+    f.err = E->err_flag;
+    f.out_tok = OUT;
+    f.count = COUNT;
+    f.step = (int)t;
+    f.flags = flags;
+    f.active_hist = HIST;
+    return launch_finalize(f, s);
+  };
+
+  // Poll the active count without blocking; stop launching once it has
+  // reached zero (rows can end early on EOS).
+  constexpr uint32_t kPoll = 8;
+  int poll_slot = 0;
+  uint32_t polls = 0;
+  bool done = n_active0 == 0;
+  auto poll = [&]() -> hipError_t {
+    // issue a new poll, then look at the previous one if it has landed
+    MH_TRY(hipMemcpyAsync(E->pinned + poll_slot, d_nact, sizeof(int), hipMemcpyDeviceToHost, s));
+    MH_TRY(hipEventRecord(E->ev[3 + poll_slot], s));
+    const int other = poll_slot ^ 1;
+    if (polls > 0 && hipEventQuery(E->ev[3 + other]) == hipSuccess && E->pinned[other] == 0) done = true;
+    poll_slot = other;
+    ++polls;
+    return hipSuccess;
+  };
+  uint32_t steps = 0;
+  for (uint32_t t = 0; t < gen_limit && !done; ++t) {
+    const int rows = (int)remaining[t];
+    if (rows == 0) break;
+    MH_HIP(emit_step(make_plan(rows, (int)t + 1, (int)Lmax), t));
+    if (time_steps) MH_HIP(hipEventRecord(E->step_ev[t], s));
     ++steps;
-    if ((t + 1) % kPoll == 0) {
-      // issue a new poll, then look at the previous one if it has landed
-      MH_HIP(hipMemcpyAsync(E->pinned + poll_slot, d_nact, sizeof(int), hipMemcpyDeviceToHost, s));
-      MH_HIP(hipEventRecord(E->ev[3 + poll_slot], s));
-      const int other = poll_slot ^ 1;
-      if (t + 1 >= 2 * kPoll && hipEventQuery(E->ev[3 + other]) == hipSuccess &&
-          E->pinned[other] == 0)
-        done = true;
-      poll_slot = other;
-    }
+    if ((t + 1) % kPoll == 0) MH_HIP(poll());
   }
+#undef MH_TRY
   MH_HIP(hipEventRecord(E->ev[2], s));
 
   // ---- results back to the host ----
@@ -889,6 +956,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   MH_HIP(hipMemcpyAsync(gen.data(), OUT, 4 * cache_rows, hipMemcpyDeviceToHost, s));
   MH_HIP(hipMemcpyAsync(&err_host, E->err_flag, sizeof(int), hipMemcpyDeviceToHost, s));
   MH_HIP(hipStreamSynchronize(s));
+  // Steps launched after every row had finished (before the poll saw the
+  // count reach zero) ran on no rows.
+  const uint32_t launched = steps;
+  while (steps > 0 && E->step_rows[steps - 1] == 0) --steps;
+  E->step_rows.resize(steps);
   hipEvent_t ev_end;
   MH_HIP(hipEventCreate(&ev_end));
   MH_HIP(hipEventRecord(ev_end, s));
@@ -903,19 +975,22 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   E->stats.decode_ms = ms_dec;
   E->stats.decode_steps = steps;
   E->stats.max_active_rows = (uint32_t)n_active0;
-  if (E->kernel_timing) {
-    double sum = 0;
-    for (uint32_t i = 0; i < vocab_launches; ++i) {
-      float ms = 0;
-      hipEventElapsedTime(&ms, E->vocab_ev[2 * i], E->vocab_ev[2 * i + 1]);
-      sum += ms;
+  E->stats.vocab_kernel_ms = 0;
+  E->stats.vocab_kernel_launches = 0;
+  E->kev_us.assign(n_timed, 0.0f);
+  for (size_t i = 0; i < n_timed; ++i) {
+    float ms = 0;
+    MH_HIP(hipEventElapsedTime(&ms, E->kev[2 * i], E->kev[2 * i + 1]));
+    E->kev_us[i] = ms * 1000.0f;
+    if (E->kev_kind[i] == MARIAN_HIP_KERNEL_VOCAB) {
+      E->stats.vocab_kernel_ms += ms;
+      ++E->stats.vocab_kernel_launches;
     }
-    E->stats.vocab_kernel_ms = sum;
-    E->stats.vocab_kernel_launches = vocab_launches;
   }
   E->step_ms.assign(steps, 0.0f);
-  if (E->kernel_timing)
-    for (uint32_t i = 0; i < steps; ++i) hipEventElapsedTime(&E->step_ms[i], E->ev[0], E->step_ev[i]);
+  if (time_steps)
+    for (uint32_t i = 0; i < std::min(steps, launched); ++i)
+      hipEventElapsedTime(&E->step_ms[i], E->ev[0], E->step_ev[i]);
   if (err_host == 2) return E->fail(MARIAN_HIP_ERR_INFERENCE, "key range exceeds the attention kernel");
   if (err_host == 3) return E->fail(MARIAN_HIP_ERR_INFERENCE, "active rows exceed the step bound");
   if (err_host) return E->fail(MARIAN_HIP_ERR_INFERENCE, "activation is not finite");

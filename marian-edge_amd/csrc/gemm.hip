@@ -58,201 +58,18 @@ __device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
   return r;
 }
 
-// ---------------------------------------------------------------------------
-// Row prologue (RowPrologue in kernels.h): a 256-thread workgroup builds up to
-// kProRows quantized rows of width kProK = 512 in LDS.  Thread t owns float4
-// column c4 = t % 128 of rows t / 128 + 2j (j < 8), so each 64-lane wave holds
-// one row per j and row maxima reduce within a wave.  The LayerNorm's two
-// sequential folds (mean, then variance; see k_residual_ln) run in lane =
-// row layout in wave 0 over a padded LDS copy of the rows.  The prologue's
-// loads are issued before the weight loads, so those folds overlap the weight
-// traffic.
-// ---------------------------------------------------------------------------
-constexpr int kProThreads = 256;
-constexpr int kProRpt = kProRows / 2;  // rows per thread
-constexpr int kProLdz = kProK + 4;     // padded fp32 LDS row (floats)
-constexpr int kProLdA = kProK + 16;    // padded int8 LDS row (bytes)
-
-struct ProLds {
-  float z[kProRows * kProLdz];
-  float mean[kProRows], inv[kProRows];
-  int amax[kProRows];
-};
-
-struct ProRegs {
-  float4 v[kProRpt];  // y, then z, then the finished row values
-  float4 w[kProRpt];  // r
-  float4 g, b;        // gamma / beta of this column (LN), the position row (embed)
-  int tok[kProRpt];
-  uint32_t e4[kProRpt];
-  float mult[kProRpt];
-};
-
-// First loads: LN rows and parameters, or the embedding rows' tokens.  Rows at
-// or past the host bound Mh are never touched by any prologue step (the test
-// is uniform per wave); their LDS rows hold stale values whose products are
-// never stored.
-template <int PK>
-__device__ __forceinline__ void pro_load(const RowPrologue& p, int Mh, ProRegs& pr) {
-  const int tid = threadIdx.x, c4 = tid & 127, rb = tid >> 7;
-  if constexpr (PK == PRO_LN) {
-    pr.g = *(const float4*)(p.gamma + 4 * c4);
-    pr.b = *(const float4*)(p.beta + 4 * c4);
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j) {
-      const int row = rb + 2 * j;
-      if (row < Mh) {
-        const int64_t off = (int64_t)row * kProK + 4 * c4;
-        pr.v[j] = *(const float4*)(p.y + off);
-        pr.w[j] = *(const float4*)(p.r + off);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j)
-      if (rb + 2 * j < Mh) pr.tok[j] = p.row_prev[rb + 2 * j];
-  }
-}
-
-// Second loads (embedding only): the token rows, their multipliers and the
-// position row of this step.
-template <int PK>
-__device__ __forceinline__ void pro_load2(const RowPrologue& p, int Mh, ProRegs& pr) {
-  if constexpr (PK == PRO_EMB) {
-    const int c4 = threadIdx.x & 127, rb = threadIdx.x >> 7;
-    pr.g = *(const float4*)(p.pos + (int64_t)p.step * kProK + 4 * c4);
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j) {
-      if (rb + 2 * j < Mh) {
-        const int tk = max(pr.tok[j], 0);
-        pr.e4[j] = *(const uint32_t*)(p.emb + (int64_t)tk * kProK + 4 * c4);
-        pr.mult[j] = p.emb_mult[tk];
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
-  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
-__device__ __forceinline__ float byte_f(uint32_t w, int i) {
-  return (float)(int8_t)(uint8_t)(w >> (8 * i));
-}
-
-// Builds the rows: quantized int8 into sA (row stride kProLdA), multipliers
-// into sAm, fp32 rows to p.out by workgroup 0 (rows below the device count M).
-template <int PK>
-__device__ __forceinline__ void pro_build(const RowPrologue& p, int Mh, int M, ProRegs& pr,
-                                          ProLds& L, int8_t* sA, float* sAm) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c4 = tid & 127, rb = tid >> 7;
-  if (tid < kProRows) L.amax[tid] = 0;
-  if constexpr (PK == PRO_LN) {
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j) {
-      if (rb + 2 * j < Mh) {
-        pr.v[j] = f4_add(pr.v[j], pr.w[j]);  // z = y + r (add_slices)
-        *(float4*)(L.z + (rb + 2 * j) * kProLdz + 4 * c4) = pr.v[j];
-      }
-    }
-    __syncthreads();
-    if (wave == 0 && lane < Mh)
-      L.mean[lane] = seq_fold_lds<kProK / 4>((const float4*)(L.z + lane * kProLdz), -0.0f) / (float)kProK;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j) {
-      const int row = rb + 2 * j;
-      if (row < Mh) {
-        const float m = L.mean[row];
-        const float4 z = pr.v[j];
-        const float cx = z.x - m, cy = z.y - m, cz = z.z - m, cw = z.w - m;
-        *(float4*)(L.z + row * kProLdz + 4 * c4) = make_float4(cx * cx, cy * cy, cz * cz, cw * cw);
-      }
-    }
-    __syncthreads();
-    if (wave == 0 && lane < Mh) {
-      const float var =
-          seq_fold_lds<kProK / 4>((const float4*)(L.z + lane * kProLdz), -0.0f) / (float)kProK;
-      L.inv[lane] = 1.0f / sqrtf(var + kLayerNormEpsilon);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j) {
-      const int row = rb + 2 * j;
-      if (row >= Mh) continue;
-      const float m = L.mean[row], iv = L.inv[row];
-      const float4 z = pr.v[j];
-      pr.v[j] = make_float4(((z.x - m) * iv) * pr.g.x + pr.b.x, ((z.y - m) * iv) * pr.g.y + pr.b.y,
-                            ((z.z - m) * iv) * pr.g.z + pr.b.z, ((z.w - m) * iv) * pr.g.w + pr.b.w);
-    }
-  } else {
-    __syncthreads();  // the row maxima are zeroed before any wave merges into them
-#pragma unroll
-    for (int j = 0; j < kProRpt; ++j) {
-      if (rb + 2 * j >= Mh) continue;
-      if (pr.tok[j] < 0) {
-        pr.v[j] = pr.g;
-      } else {
-        const float mu = pr.mult[j];
-        const float ex = byte_f(pr.e4[j], 0) / mu, ey = byte_f(pr.e4[j], 1) / mu;
-        const float ez = byte_f(pr.e4[j], 2) / mu, ew = byte_f(pr.e4[j], 3) / mu;
-        pr.v[j] = make_float4(ex * p.scale + pr.g.x, ey * p.scale + pr.g.y, ez * p.scale + pr.g.z,
-                              ew * p.scale + pr.g.w);
-      }
-    }
-  }
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < kProRpt; ++j) {
-    const int row = rb + 2 * j;
-    if (row >= Mh) continue;
-    const float4 o = pr.v[j];
-    float mx = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-    if (row < M) bad |= !isfinite(o.x) || !isfinite(o.y) || !isfinite(o.z) || !isfinite(o.w);
-    mx = wave_max(mx);
-    if (lane == 0) atomicMax(&L.amax[row], __float_as_int(mx));  // |values| >= 0: int order
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kProRpt; ++j) {
-    const int row = rb + 2 * j;
-    if (row >= Mh) continue;
-    const float a = row_multiplier(__int_as_float(L.amax[row]));
-    const float4 o = pr.v[j];
-    *(uint32_t*)(sA + row * kProLdA + 4 * c4) =
-        (uint32_t)(quantize_one(o.x, a) & 0xFF) | ((uint32_t)(quantize_one(o.y, a) & 0xFF) << 8) |
-        ((uint32_t)(quantize_one(o.z, a) & 0xFF) << 16) | ((uint32_t)(quantize_one(o.w, a) & 0xFF) << 24);
-    if (c4 == 0) sAm[row] = a;
-    if (p.out && blockIdx.x == 0 && row < M) *(float4*)(p.out + (int64_t)row * kProK + 4 * c4) = o;
-  }
-  if (__any(bad) && lane == 0 && p.err) *p.err = 1;
-  __syncthreads();
-}
-
-// A sources of the skinny kernel.
-enum ASrc { A_I8 = 0, A_F32 = 1, A_LN = 2, A_EMB = 3 };
-template <int ASRC>
-struct SkinnyLds {  // prologue rows (A_LN / A_EMB only)
-  ProLds pro;
-  int8_t a[kProRows * kProLdA];
-  float am[kProRows];
-};
-template <>
-struct SkinnyLds<A_I8> {};
-template <>
-struct SkinnyLds<A_F32> {};
+// A sources of the skinny kernel: int8 rows with their multipliers, or fp32
+// rows quantized while loading.
+enum ASrc { A_I8 = 0, A_F32 = 1 };
 
 template <int MODE, int CT, int NW, int KSW, int ASRC>
 __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
   constexpr bool AF = ASRC == A_F32;
-  constexpr bool PRO = ASRC == A_LN || ASRC == A_EMB;
-  constexpr int PK = ASRC == A_LN ? PRO_LN : PRO_EMB;
-  static_assert(!PRO || NW * 64 == kProThreads, "the prologue runs on 256 threads");
   constexpr int NT = NW * 64;
   constexpr int COLS = CT * 16;
   constexpr int LDC = COLS + 1;          // padded LDS row (i32)
   constexpr int ROWS_PER_THREAD = kSkinnyRows * COLS / NT;
   __shared__ int32_t sAcc[kSkinnyRows * LDC];
-  __shared__ __attribute__((aligned(16))) SkinnyLds<ASRC> sp;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n0 = blockIdx.x * COLS;
   const int kq = (lane >> 4) * 16;
@@ -262,8 +79,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   // count (g.M_dev) is known.
   const int Mh = g.M;
 
-  ProRegs pr;
-  if constexpr (PRO) pro_load<PK>(g.pro, Mh, pr);
   // Every weight fragment of this wave (k-steps wave, wave+NW, ...).
   v4i bf[KSW][CT];
 #pragma unroll
@@ -276,28 +91,25 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       bf[i][ct] = s < ksteps ? *(const v4i*)(wr + s * 64) : zero4();
     }
   }
-  if constexpr (PRO) pro_load2<PK>(g.pro, Mh, pr);
   // First chunk's activation fragments.
   v4i af[KSW][4];
-  if constexpr (!PRO) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int m = min(mt * 16 + (lane & 15), Mh - 1);
-      if constexpr (AF) {
-        const float a_m = af_row_mult(g, m);
-        const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
+  for (int mt = 0; mt < 4; ++mt) {
+    const int m = min(mt * 16 + (lane & 15), Mh - 1);
+    if constexpr (AF) {
+      const float a_m = af_row_mult(g, m);
+      const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
 #pragma unroll
-        for (int i = 0; i < KSW; ++i) {
-          const int s = wave + NW * i;
-          af[i][mt] = (s < ksteps && mt * 16 < Mh) ? quantize_frag16(ar + s * 64, a_m) : zero4();
-        }
-      } else {
-        const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
+      for (int i = 0; i < KSW; ++i) {
+        const int s = wave + NW * i;
+        af[i][mt] = (s < ksteps && mt * 16 < Mh) ? quantize_frag16(ar + s * 64, a_m) : zero4();
+      }
+    } else {
+      const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
 #pragma unroll
-        for (int i = 0; i < KSW; ++i) {
-          const int s = wave + NW * i;
-          af[i][mt] = (s < ksteps && mt * 16 < Mh) ? *(const v4i*)(ar + s * 64) : zero4();
-        }
+      for (int i = 0; i < KSW; ++i) {
+        const int s = wave + NW * i;
+        af[i][mt] = (s < ksteps && mt * 16 < Mh) ? *(const v4i*)(ar + s * 64) : zero4();
       }
     }
   }
@@ -310,29 +122,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
   for (int k = 0; k < ROWS_PER_THREAD; ++k) {
     const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
-    if constexpr (!PRO) am[k] = AF ? af_row_mult(g, m) : g.a[m];
+    am[k] = AF ? af_row_mult(g, m) : g.a[m];
     if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
   const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
 
-  if constexpr (PRO) {
-    pro_build<PK>(g.pro, Mh, M, pr, sp.pro, sp.a, sp.am);
-#pragma unroll
-    for (int i = 0; i < KSW; ++i) {
-      const int s = wave + NW * i;
-      af[i][0] = s < ksteps ? *(const v4i*)(sp.a + (lane & 15) * kProLdA + kq + s * 64) : zero4();
-#pragma unroll
-      for (int mt = 1; mt < 4; ++mt) af[i][mt] = zero4();
-    }
-#pragma unroll
-    for (int k = 0; k < ROWS_PER_THREAD; ++k) {
-      const int row = tid / COLS + k * (NT / COLS);
-      am[k] = row < kProRows ? sp.am[row] : 1.0f;
-    }
-  }
-
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
-    if (!PRO && m0 > 0) {
+    if (m0 > 0) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int m = min(m0 + mt * 16 + (lane & 15), M - 1);
@@ -685,28 +481,12 @@ static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStrea
   return hipGetLastError();
 }
 
-// A row prologue is usable for K = kProK, at most kProRows host rows and with
-// every operand it reads present.
-static bool prologue_ok(const GemmArgs& g) {
-  const RowPrologue& p = g.pro;
-  if (g.K != kProK || g.M > kProRows || g.Af) return false;
-  if (p.kind == PRO_LN) return p.y && p.r && p.gamma && p.beta;
-  if (p.kind == PRO_EMB)
-    return p.emb && p.emb_mult && p.pos && p.row_prev && p.step >= 0 && p.step < kMaxPosition;
-  return false;
-}
-
 // Waves and per-wave k-steps by K: long K (the FFN down-projection) spreads
 // over 8 waves; each wave holds its k-steps' fragments in registers.  An
 // fp32 A source is supported for K <= 512 (the attention-output projections).
 template <int MODE>
 static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const int ksteps = g.K >> 6;
-  if (g.pro.kind != PRO_NONE) {
-    if (!prologue_ok(g)) return hipErrorInvalidValue;
-    return g.pro.kind == PRO_LN ? launch_skinny_k<MODE, 4, 2, A_LN>(g, e, s)
-                                : launch_skinny_k<MODE, 4, 2, A_EMB>(g, e, s);
-  }
   if (g.Af) {
     if (ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4) return hipErrorInvalidValue;
     return launch_skinny_k<MODE, 4, 2, A_F32>(g, e, s);
@@ -719,7 +499,7 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
 
 hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s) {
   if (g.K <= 0 || g.K % 64 || g.K > kSkinnyMaxK || g.N <= 0 || g.M <= 0) return hipErrorInvalidValue;
-    switch (mode) {
+  switch (mode) {
     case EPI_STORE: return launch_skinny_mode<EPI_STORE>(g, e, s);
     case EPI_QKV_CACHE: return launch_skinny_mode<EPI_QKV_CACHE>(g, e, s);
     case EPI_ARGMAX:
@@ -731,7 +511,6 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hi
 hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
-  if (g.pro.kind != PRO_NONE) return hipErrorInvalidValue;
   const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
   if (ev_start || ev_stop)
     hipExtLaunchKernelGGL(k_vocab_argmax, grid, block, 0, s, ev_start, ev_stop, 0, g, e);

@@ -6,18 +6,16 @@
 
 namespace mh {
 
-// A-operand prologue of the small-M decode kernels: the workgroup builds the
-// quantized activation rows itself instead of reading A / a, so the producer
-// of those rows needs no kernel of its own.
-//   PRO_LN:  rows = LayerNorm(y + r) with gamma/beta (the post-norm residual
+// Input-row prologue of the decode attention block: the workgroup builds its
+// row itself instead of reading a quantized row, so the producer of that row
+// needs no kernel of its own.
+//   PRO_LN:  row = LayerNorm(y + r) with gamma/beta (the post-norm residual
 //            LayerNorm of a sublayer's output),
-//   PRO_EMB: rows = emb[prev]/mult * scale + pos[step] (the decoder input; a
+//   PRO_EMB: row = emb[prev]/mult * scale + pos[step] (the decoder input; a
 //            negative prev gives pos[step] alone).
-// Workgroup 0 also stores the fp32 rows to `out` (the next residual).  The
-// prologue handles K = kProK and at most kProRows rows (host bound g.M).
+// The head-0 workgroup of each row also stores the fp32 row to `out` (the
+// next residual).
 enum ProKind { PRO_NONE = 0, PRO_LN = 1, PRO_EMB = 2 };
-constexpr int kProRows = 16;
-constexpr int kProK = 512;
 struct RowPrologue {
   int kind = PRO_NONE;
   const float* y = nullptr;
@@ -28,8 +26,7 @@ struct RowPrologue {
   const float* emb_mult = nullptr;
   const float* pos = nullptr;  // [kMaxPosition, K]
   float scale = 1.0f;
-  const int32_t* row_prev = nullptr;
-  int step = 0;
+  const int32_t* row_prev = nullptr;  // position row: the consumer's step
   float* out = nullptr;  // fp32 [M, K], or nullptr when nothing reads the rows again
   int* err = nullptr;    // set to 1 on a non-finite row value
 };
@@ -54,9 +51,6 @@ struct GemmArgs {
   int64_t ldaf = 0;
   const float* Aamax = nullptr;
   int amax_parts = 0;
-  // Or rows built by the kernel's prologue (skinny kernel only; K = kProK,
-  // M <= kProRows).
-  RowPrologue pro;
 };
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
@@ -191,7 +185,9 @@ struct BlockArgs {
   int* err = nullptr;
 };
 bool attn_block_supported(int d, int heads, int max_keys);
-hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s);
+// ev_start / ev_stop as in launch_vocab_argmax.
+hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s, hipEvent_t ev_start = nullptr,
+                             hipEvent_t ev_stop = nullptr);
 
 // Per-row decode metadata, rebuilt in active-row order by the finalizer.
 struct RowMeta {

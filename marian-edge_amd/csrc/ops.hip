@@ -188,6 +188,7 @@ int marian_hip_device_name(int device, char* buf, size_t cap) {
   char name[256] = {0};
   if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
     snprintf(name, sizeof name, "%s", p.name);
+  if (!name[0]) snprintf(name, sizeof name, "AMD GPU");  // no marketing name visible
   snprintf(buf, cap, "%s (%s)", name, p.gcnArchName);
   return MARIAN_HIP_OK;
 }

@@ -169,8 +169,15 @@ class HipEngine:
             self._raise(rc)
         return BatchOutput(out[:n.value].copy(), out_offs.copy())
 
-    def set_kernel_timing(self, enabled: bool) -> None:
-        self._lib.marian_hip_set_kernel_timing(self._h, 1 if enabled else 0)
+    TIME_STEPS, TIME_KERNELS = 1, 2
+
+    def set_timing(self, flags: int) -> None:
+        """TIME_STEPS: per-step end times (last_step_trace); TIME_KERNELS: per
+        launch durations of the vocabulary and attention-block kernels
+        (last_kernel_trace), at several microseconds of device time each."""
+        rc = self._lib.marian_hip_set_timing(self._h, int(flags))
+        if rc != _lib.OK:
+            self._raise(rc)
 
     def last_stats(self) -> dict:
         s = _lib.Stats()
@@ -185,6 +192,21 @@ class HipEngine:
         ms = np.zeros(max(n.value, 1), np.float32)
         self._lib.marian_hip_last_step_trace(self._h, _ptr(rows), _ptr(ms), n.value, C.byref(n))
         return rows[:n.value], ms[:n.value]
+
+    KERNEL_VOCAB, KERNEL_SELF_BLOCK, KERNEL_CROSS_BLOCK = 0, 1, 2
+
+    def last_kernel_trace(self) -> dict:
+        """Per timed decode launch of the last call (kernel timing on):
+        kind (KERNEL_*), decode step, decoder layer, device microseconds."""
+        n = C.c_size_t(0)
+        self._lib.marian_hip_last_kernel_trace(self._h, None, None, None, None, 0, C.byref(n))
+        m = max(n.value, 1)
+        kind, step, layer = (np.zeros(m, np.uint32) for _ in range(3))
+        us = np.zeros(m, np.float32)
+        self._lib.marian_hip_last_kernel_trace(self._h, _ptr(kind), _ptr(step), _ptr(layer), _ptr(us),
+                                               n.value, C.byref(n))
+        k = n.value
+        return dict(kind=kind[:k], step=step[:k], layer=layer[:k], us=us[:k])
 
     def is_ready(self) -> bool:
         return bool(self._lib.marian_hip_is_ready(self._h))
