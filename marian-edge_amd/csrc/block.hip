@@ -191,6 +191,11 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
         *(f4v*)(sV + (idx >> 4) * kBlkRow + (idx & 15) * 4) = vv[j];
       }
     }
+    // Value rows from the last key up to the next multiple of 8 are zero, so
+    // the PV loop's batches of 8 keys read no stale LDS.
+    const int zrows = min((nkey + 7) & ~7, kBlkMaxKeys) - nkey;
+    for (int idx = u; idx < zrows * 16; idx += kBlkLoaders)
+      *(f4v*)(sV + (nkey + (idx >> 4)) * kBlkRow + (idx & 15) * 4) = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();  // the input row (wave 0) is in LDS
     // ---- projection: row 0 of a 16-row MFMA tile ----------------------------------
     const float a_row = sA;
@@ -198,12 +203,18 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     for (int i = 0; i < TPW; ++i) {
       const int tile = (wave - 1) + 3 * i;
       if (tile >= NT) break;
-      v4i acc = zero4b();
+      // Two independent accumulation chains over the two halves of K (exact
+      // integers: their sum does not depend on the split).
+      v4i acc = zero4b(), acc2 = zero4b();
 #pragma unroll
-      for (int s = 0; s < kBlkD / 64; ++s) {
+      for (int s = 0; s < kBlkD / 128; ++s) {
+        const int s2 = s + kBlkD / 128;
         const v4i af = (lane & 15) == 0 ? *(const v4i*)(sX + s * 64 + kq) : zero4b();
+        const v4i af2 = (lane & 15) == 0 ? *(const v4i*)(sX + s2 * 64 + kq) : zero4b();
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[i][s], acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af2, bf[i][s2], acc2, 0, 0, 0);
       }
+      acc += acc2;
       if (lane < 16) {  // lanes 0..15 hold row 0 of the tile's 16 columns
         const int c = (tile % 4) * 16 + lane;
         const float yv = dequant(acc[0], a_row, wm[i], bi[i]);
@@ -258,27 +269,26 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
   __builtin_amdgcn_wave_barrier();
-  // Denominator: keys in order from 0.0 (softmax_in_place).  The fold runs
-  // over all kBlkMaxKeys entries: past the last key they hold +0.0, which
-  // leaves the (non-negative) sum unchanged.
-  const float inv = 1.0f / seq_fold_lds<kBlkMaxKeys / 4>((const float4*)sP, 0.0f);
+  // Denominator: keys in order from 0.0 (softmax_in_place), folded over whole
+  // batches of 32 entries: past the last key they hold +0.0, which leaves the
+  // (non-negative) sum unchanged.
+  const float inv = 1.0f / seq_fold_lds_batches((const float4*)sP, (nkey + 31) >> 5, 0.0f);
   __builtin_amdgcn_wave_barrier();
   // p_k = e_k * inv (scale_in_place), then out_d = sum_k v_k[d] * p_k in key
   // order.  Keys are taken in batches of 8 whose V values and p are read one
-  // batch ahead; past the last key p is 0 and the row read is a valid key's,
-  // so the added products are +-0 and leave the sum unchanged.
+  // batch ahead; past the last key p is +0 and the value rows are zero, so
+  // the added products are +0 and leave the sum (never -0) unchanged.
 #pragma unroll
   for (int c = 0; c < 2; ++c) sP[c * 64 + lane] = e[c] * inv;
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
   const int nbat = (nkey + 7) >> 3;
-  float va[8], pa[8], vb[8], pb[8];
-  auto load8 = [&](int k0, float (&v)[8], float (&pp)[8]) {
+  f4v va[2], pa[2], vb[2], pb[2];
+  auto load8 = [&](int k0, f4v (&v)[2], f4v (&pp)[2]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      v[i] = sV[min(k0 + i, nkey - 1) * kBlkRow + lane];
-      pp[i] = sP[k0 + i];
-    }
+    for (int i = 0; i < 8; ++i) v[i >> 2][i & 3] = sV[(k0 + i) * kBlkRow + lane];
+    pp[0] = *(const f4v*)(sP + k0);
+    pp[1] = *(const f4v*)(sP + k0 + 4);
   };
   float o = 0.0f;
   load8(0, va, pa);
@@ -286,11 +296,11 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   for (int bt = 0; bt < nbat; bt += 2) {
     if (bt + 1 < nbat) load8((bt + 1) * 8, vb, pb);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o = o + va[i] * pa[i];
+    for (int i = 0; i < 8; ++i) o = o + va[i >> 2][i & 3] * pa[i >> 2][i & 3];
     if (bt + 1 >= nbat) break;
     if (bt + 2 < nbat) load8((bt + 2) * 8, va, pa);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o = o + vb[i] * pb[i];
+    for (int i = 0; i < 8; ++i) o = o + vb[i >> 2][i & 3] * pb[i >> 2][i & 3];
   }
   b.out[(int64_t)r * b.ldo + h * kHeadDim + lane] = o;
   const bool bad = !isfinite(o);

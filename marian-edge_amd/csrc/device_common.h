@@ -157,6 +157,43 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
   return s;
 }
 
+// The same fold over the first nb batches of 8 float4 (nb >= 1, a value known
+// only at run time), with the same two-buffer read-ahead.
+__device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, float init) {
+  constexpr int NB = 8;
+  float4 A[NB], B[NB];
+  float s = init;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) A[b] = p[b];
+#pragma unroll 1
+  for (int k = 0; k < nb; k += 2) {
+    if (k + 1 < nb) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) B[b] = p[(k + 1) * NB + b];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      s = s + A[b].x;
+      s = s + A[b].y;
+      s = s + A[b].z;
+      s = s + A[b].w;
+    }
+    if (k + 1 >= nb) break;
+    if (k + 2 < nb) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) A[b] = p[(k + 2) * NB + b];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      s = s + B[b].x;
+      s = s + B[b].y;
+      s = s + B[b].z;
+      s = s + B[b].w;
+    }
+  }
+  return s;
+}
+
 // q = clamp(round_half_even(x * a), -127, 127)  (q8_gemm.rs:584-587)
 __device__ __forceinline__ int quantize_one(float x, float a) {
   float v = rintf(x * a);
