@@ -34,6 +34,105 @@ __device__ __forceinline__ v4i zero4b() { return v4i{0, 0, 0, 0}; }
 // which keeps an array of them out of registers).
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// ---- the input row, built by one wave: lane l holds elements 4l..4l+3 and
+// 256+4l..256+4l+3 of the kBlkD-wide row ---------------------------------------
+template <int PK>
+struct RowLoads {
+  f4v a[2], b[2], g[2], bb[2];  // LN: y, r, gamma, beta; embedding: pos in a
+  uint32_t e4[2];               // embedding: four int8 entries
+  float mu = 1.0f;              // embedding: the token's multiplier
+  int tok = -1;
+};
+
+// Loads of row r (issued before the device row count is known).
+template <int PK>
+__device__ __forceinline__ void row_load(const RowPrologue& p, int r, int step, int lane, RowLoads<PK>& L) {
+  if constexpr (PK == PRO_LN) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = 4 * lane + 256 * j;
+      L.a[j] = *(const f4v*)(p.y + (int64_t)r * kBlkD + e);
+      L.b[j] = *(const f4v*)(p.r + (int64_t)r * kBlkD + e);
+      L.g[j] = *(const f4v*)(p.gamma + e);
+      L.bb[j] = *(const f4v*)(p.beta + e);
+    }
+  } else {
+    L.tok = p.row_prev[r];
+    const int tk = max(L.tok, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = 4 * lane + 256 * j;
+      L.a[j] = *(const f4v*)(p.pos + (int64_t)step * kBlkD + e);
+      L.e4[j] = *(const uint32_t*)(p.emb + (int64_t)tk * kBlkD + e);
+    }
+    L.mu = p.emb_mult[tk];
+  }
+}
+
+// The row's values: LayerNorm(y + r) with its two sequential folds over an
+// LDS copy (sZ), or the scaled embedding plus the position row.
+template <int PK>
+__device__ __forceinline__ void row_build(const RowPrologue& p, const RowLoads<PK>& L, float* sZ,
+                                          int lane, f4v (&o)[2]) {
+  if constexpr (PK == PRO_LN) {
+    f4v z[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      z[j] = L.a[j] + L.b[j];  // add_slices
+      *(f4v*)(sZ + 4 * lane + 256 * j) = z[j];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+    __builtin_amdgcn_wave_barrier();
+    const float mean = seq_fold_lds<kBlkD / 4>((const float4*)sZ, -0.0f) / (float)kBlkD;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const f4v c = z[j] - mean;
+      *(f4v*)(sZ + 4 * lane + 256 * j) = c * c;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const float var = seq_fold_lds<kBlkD / 4>((const float4*)sZ, -0.0f) / (float)kBlkD;
+    const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) o[j] = ((z[j] - mean) * inv) * L.g[j] + L.bb[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (L.tok < 0) {
+        o[j] = L.a[j];
+      } else {
+        f4v v;
+        v.x = (float)(int8_t)(L.e4[j] & 0xFF) / L.mu;
+        v.y = (float)(int8_t)((L.e4[j] >> 8) & 0xFF) / L.mu;
+        v.z = (float)(int8_t)((L.e4[j] >> 16) & 0xFF) / L.mu;
+        v.w = (float)(int8_t)(L.e4[j] >> 24) / L.mu;
+        o[j] = v * p.scale + L.a[j];
+      }
+    }
+  }
+}
+
+// Quantizes the row into sX with its row multiplier (returned); `bad` tells
+// whether any value is not finite.
+__device__ __forceinline__ float row_quantize(const f4v (&o)[2], int8_t* sX, int lane, bool& bad) {
+  bad = false;
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    bad |= !isfinite(o[j].x) || !isfinite(o[j].y) || !isfinite(o[j].z) || !isfinite(o[j].w);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
+  }
+  const float a_row = row_multiplier(wave_max(m));
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    *(uint32_t*)(sX + 4 * lane + 256 * j) = (uint32_t)(quantize_one(o[j].x, a_row) & 0xFF) |
+                                            ((uint32_t)(quantize_one(o[j].y, a_row) & 0xFF) << 8) |
+                                            ((uint32_t)(quantize_one(o[j].z, a_row) & 0xFF) << 16) |
+                                            ((uint32_t)(quantize_one(o[j].w, a_row) & 0xFF) << 24);
+  return a_row;
+}
+
 // Work split: wave 0 builds the input row (its LayerNorm folds are a single
 // dependent chain, so it runs with nothing else live); waves 1-3 meanwhile
 // load this head's weight rows and stage the row's keys and values in LDS,
@@ -69,84 +168,18 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   const int nkey = SELF ? nkm + 1 : nkm;                                       // keys attended
 
   if (wave == 0) {
-    // ---- the input row: lane l holds elements 4l..4l+3 and 256+4l..+3 -------
+    // ---- the input row ----------------------------------------------------------
     const uint64_t tab_v = kBlkExp2Tab[lane & 31];
+    RowLoads<PK> in;
+    row_load<PK>(b.pro, r, step, lane, in);
+    if (r >= n) return;
     f4v o[2];
-    if constexpr (PK == PRO_LN) {
-      f4v y[2], x[2], g[2], bb[2];
+    row_build<PK>(b.pro, in, sZ, lane, o);
+    bool bad;
+    const float a_row = row_quantize(o, sX, lane, bad);
+    if (h == 0 && b.pro.out) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int e = 4 * lane + 256 * j;
-        y[j] = *(const f4v*)(b.pro.y + (int64_t)r * kBlkD + e);
-        x[j] = *(const f4v*)(b.pro.r + (int64_t)r * kBlkD + e);
-        g[j] = *(const f4v*)(b.pro.gamma + e);
-        bb[j] = *(const f4v*)(b.pro.beta + e);
-      }
-      if (r >= n) return;
-      f4v z[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        z[j] = y[j] + x[j];  // add_slices
-        *(f4v*)(sZ + 4 * lane + 256 * j) = z[j];
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
-      __builtin_amdgcn_wave_barrier();
-      const float mean = seq_fold_lds<kBlkD / 4>((const float4*)sZ, -0.0f) / (float)kBlkD;
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const f4v c = z[j] - mean;
-        *(f4v*)(sZ + 4 * lane + 256 * j) = c * c;
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();
-      const float var = seq_fold_lds<kBlkD / 4>((const float4*)sZ, -0.0f) / (float)kBlkD;
-      const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) o[j] = ((z[j] - mean) * inv) * g[j] + bb[j];
-    } else {
-      const int tok = b.pro.row_prev[r];
-      const int tk = max(tok, 0);
-      f4v pos[2];
-      uint32_t e4[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int e = 4 * lane + 256 * j;
-        pos[j] = *(const f4v*)(b.pro.pos + (int64_t)step * kBlkD + e);
-        e4[j] = *(const uint32_t*)(b.pro.emb + (int64_t)tk * kBlkD + e);
-      }
-      const float mu = b.pro.emb_mult[tk];
-      if (r >= n) return;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (tok < 0) {
-          o[j] = pos[j];
-        } else {
-          f4v v;
-          v.x = (float)(int8_t)(e4[j] & 0xFF) / mu;
-          v.y = (float)(int8_t)((e4[j] >> 8) & 0xFF) / mu;
-          v.z = (float)(int8_t)((e4[j] >> 16) & 0xFF) / mu;
-          v.w = (float)(int8_t)(e4[j] >> 24) / mu;
-          o[j] = v * b.pro.scale + pos[j];
-        }
-      }
-    }
-    bool bad = false;
-    float m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bad |= !isfinite(o[j].x) || !isfinite(o[j].y) || !isfinite(o[j].z) || !isfinite(o[j].w);
-      m = fmaxf(m, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
-    }
-    const float a_row = row_multiplier(wave_max(m));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int e = 4 * lane + 256 * j;
-      *(uint32_t*)(sX + e) = (uint32_t)(quantize_one(o[j].x, a_row) & 0xFF) |
-                             ((uint32_t)(quantize_one(o[j].y, a_row) & 0xFF) << 8) |
-                             ((uint32_t)(quantize_one(o[j].z, a_row) & 0xFF) << 16) |
-                             ((uint32_t)(quantize_one(o[j].w, a_row) & 0xFF) << 24);
-      if (h == 0 && b.pro.out) *(f4v*)(b.pro.out + (int64_t)r * kBlkD + e) = o[j];
+      for (int j = 0; j < 2; ++j) *(f4v*)(b.pro.out + (int64_t)r * kBlkD + 4 * lane + 256 * j) = o[j];
     }
     if (lane == 0) sA = a_row;
     if (lane < 32) sTab[lane] = tab_v;
@@ -309,6 +342,81 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   if (__any(bad) && lane == 0 && b.err) *b.err = 1;
 }
 
+
+// ---------------------------------------------------------------------------
+// LayerNorm + up-projection block (the FFN's first layer on steps with few
+// rows): one 256-thread workgroup per (row, 128-column slice).  Wave 0 builds
+// the row's residual LayerNorm and quantizes it, as in the attention block;
+// waves 1-3 meanwhile load the slice's weight rows into registers, then run
+// the projection on MFMA (row 0 of a 16-row tile), dequantize, apply ReLU and
+// store.  Replaces the LayerNorm kernel and the skinny GEMM that followed it.
+// ---------------------------------------------------------------------------
+constexpr int kLgCols = 128;                 // output columns per workgroup
+constexpr int kLgTiles = kLgCols / 16;       // MFMA column tiles per workgroup
+constexpr int kLgTpw = (kLgTiles + 2) / 3;   // tiles per loader wave
+
+__global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
+  __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
+  __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
+  __shared__ float sA;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int slices = a.N / kLgCols;
+  const int slice = blockIdx.x % slices, r = blockIdx.x / slices;  // r < a.rows (host bound)
+  const int n = a.rows_dev ? *a.rows_dev : a.rows;
+  if (wave == 0) {
+    RowLoads<PRO_LN> in;
+    row_load<PRO_LN>(a.pro, r, 0, lane, in);
+    if (r >= n) return;
+    f4v o[2];
+    row_build<PRO_LN>(a.pro, in, sZ, lane, o);
+    bool bad;
+    const float a_row = row_quantize(o, sX, lane, bad);
+    if (slice == 0 && a.pro.out) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) *(f4v*)(a.pro.out + (int64_t)r * kBlkD + 4 * lane + 256 * j) = o[j];
+    }
+    if (lane == 0) sA = a_row;
+    if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+    __syncthreads();  // the quantized row is in LDS
+    return;
+  }
+  const int kq = (lane >> 4) * 16;
+  v4i bf[kLgTpw][kBlkD / 64];
+  float wm[kLgTpw], bi[kLgTpw];
+#pragma unroll
+  for (int i = 0; i < kLgTpw; ++i) {
+    const int tile = min((wave - 1) + 3 * i, kLgTiles - 1);
+    const int col = slice * kLgCols + tile * 16 + (lane & 15);
+    const int8_t* wr = a.W + (int64_t)col * kBlkD + kq;
+#pragma unroll
+    for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = *(const v4i*)(wr + s * 64);
+    wm[i] = a.wmult[col];
+    bi[i] = a.bias[col];
+  }
+  if (r >= n) return;
+  __syncthreads();  // the quantized row is in LDS
+  const float a_row = sA;
+#pragma unroll
+  for (int i = 0; i < kLgTpw; ++i) {
+    const int tile = (wave - 1) + 3 * i;
+    if (tile >= kLgTiles) break;
+    v4i acc = zero4b(), acc2 = zero4b();
+#pragma unroll
+    for (int s = 0; s < kBlkD / 128; ++s) {
+      const int s2 = s + kBlkD / 128;
+      const v4i af = (lane & 15) == 0 ? *(const v4i*)(sX + s * 64 + kq) : zero4b();
+      const v4i af2 = (lane & 15) == 0 ? *(const v4i*)(sX + s2 * 64 + kq) : zero4b();
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[i][s], acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af2, bf[i][s2], acc2, 0, 0, 0);
+    }
+    acc += acc2;
+    if (lane < 16) {  // lanes 0..15 hold row 0 of the tile's 16 columns
+      float y = dequant(acc[0], a_row, wm[i], bi[i]);
+      if (a.relu) y = y > 0.0f ? y : 0.0f;
+      a.out[(int64_t)r * a.ldo + slice * kLgCols + tile * 16 + lane] = y;
+    }
+  }
+}
 }  // namespace
 
 bool attn_block_supported(int d, int heads, int max_keys) {
@@ -338,6 +446,18 @@ hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s, hipEvent_t ev_st
     hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev_start, ev_stop, 0, b);
   else
     hipLaunchKernelGGL(kern, grid, block, 0, s, b);
+  return hipGetLastError();
+}
+
+bool ln_gemm_block_supported(int K, int N) { return K == kBlkD && N > 0 && N % kLgCols == 0; }
+
+hipError_t launch_ln_gemm_block(const LnGemmArgs& a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  const RowPrologue& p = a.pro;
+  if (!ln_gemm_block_supported(a.K, a.N) || p.kind != PRO_LN || !p.y || !p.r || !p.gamma ||
+      !p.beta || !a.W || !a.wmult || !a.bias || !a.out || a.ldo < a.N)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_ln_gemm_block, dim3(a.rows * (a.N / kLgCols)), dim3(kBlkThreads), 0, s, a);
   return hipGetLastError();
 }
 

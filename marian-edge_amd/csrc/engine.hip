@@ -646,13 +646,14 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   }
   constexpr int kAfMaxRows = 16;
   constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
+  constexpr int kLnFfnMaxRows = 16;  // ... and the LayerNorm + FFN up-projection block
 
   // What one decode step launches is decided on the host: the row bound
   // (grid sizes; rows at or past the device row count exit early), the path
   // of each attention sublayer and the key bounds that pick kernel variants.
   struct StepPlan {
     int rows, self_keys, cross_keys;
-    bool blk_self, blk_cross, af;
+    bool blk_self, blk_cross, af, ln_ffn;
   };
   auto make_plan = [&](int rows, int self_keys, int cross_keys) {
     StepPlan P;
@@ -662,6 +663,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     P.blk_self = rows <= kBlkMaxRows && attn_block_supported(d, H, self_keys);
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
     P.af = rows <= kAfMaxRows;
+    P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
     return P;
   };
 
@@ -876,9 +878,27 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         MH_TRY(launch_attention(ca, s));
       }
       MH_TRY(agemm(L.cross_out, store_epi(DY, d, 0)));
-      MH_TRY(layer_norm(DY, L.ln2_s, L.ln2_b, false));
-      // ---- feed-forward ----
-      MH_TRY(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
+      // ---- feed-forward; its LayerNorm inside the up-projection block ----
+      MH_TRY(layer_norm(DY, L.ln2_s, L.ln2_b, P.ln_ffn));
+      if (P.ln_ffn) {
+        LnGemmArgs lg;
+        lg.pro = pend;
+        pend.kind = PRO_NONE;
+        lg.rows = rows;
+        lg.rows_dev = d_nact;
+        lg.W = L.ffn1.w;
+        lg.wmult = L.ffn1.mult;
+        lg.bias = L.ffn1.bias;
+        lg.K = L.ffn1.K;
+        lg.N = L.ffn1.N;
+        lg.relu = 1;
+        lg.out = DH;
+        lg.ldo = F;
+        lg.err = E->err_flag;
+        MH_TRY(launch_ln_gemm_block(lg, s));
+      } else {
+        MH_TRY(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
+      }
       MH_TRY(launch_quantize_rows(DH, F, rows, d_nact, F, DHQ, F, DHA, E->err_flag, s));
       MH_TRY(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
       MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && P.blk_self));

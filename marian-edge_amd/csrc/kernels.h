@@ -185,6 +185,26 @@ struct BlockArgs {
   int* err = nullptr;
 };
 bool attn_block_supported(int d, int heads, int max_keys);
+
+// LayerNorm + up-projection block: out[r, :] = (relu of) the Q8 linear of the
+// row `pro` builds (PRO_LN), one workgroup per (row, 128 output columns); the
+// column-slice-0 workgroup also stores the LayerNorm row to pro.out.
+// K = 512, N a multiple of 128.
+struct LnGemmArgs {
+  RowPrologue pro;
+  int rows = 0;
+  const int* rows_dev = nullptr;
+  const int8_t* W = nullptr;  // [N, K]
+  const float* wmult = nullptr;
+  const float* bias = nullptr;
+  int K = 0, N = 0;
+  int relu = 0;
+  float* out = nullptr;  // [rows, ldo]
+  int64_t ldo = 0;
+  int* err = nullptr;
+};
+bool ln_gemm_block_supported(int K, int N);
+hipError_t launch_ln_gemm_block(const LnGemmArgs& a, hipStream_t s);
 // ev_start / ev_stop as in launch_vocab_argmax.
 hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s, hipEvent_t ev_start = nullptr,
                              hipEvent_t ev_stop = nullptr);
