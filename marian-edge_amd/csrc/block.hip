@@ -270,26 +270,43 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   __syncthreads();  // projection done
 
   // ---- attention (wave 0) ---------------------------------------------------------
-  // Scores: lane = key of chunk c, 64-term dot in dimension order.
+  // Scores: lane = key of chunk c (keys c*64 + lane), 64-term dot in
+  // dimension order.  The query and the key rows are read into registers
+  // first; with more than 64 keys the two chunks' chains run interleaved.
   const float scale = 1.0f / sqrtf((float)kHeadDim);
-  float sc[2];
+  float sc[2] = {-INFINITY, -INFINITY};
+  {
+    f4v q[kHeadDim / 4], ka[kHeadDim / 4];
+    const float* kra = sK + min(lane, nkey - 1) * kBlkRow;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int key = c * 64 + lane;
-    sc[c] = -INFINITY;
-    if (c * 64 < nkey) {
-      const float* kr = sK + min(key, nkey - 1) * kBlkRow;
-      float dot = -0.0f;
+    for (int i = 0; i < kHeadDim / 4; ++i) {
+      q[i] = *(const f4v*)(sQ + 4 * i);
+      ka[i] = *(const f4v*)(kra + 4 * i);
+    }
+    if (nkey > 64) {
+      f4v kb[kHeadDim / 4];
+      const float* krb = sK + min(64 + lane, nkey - 1) * kBlkRow;
 #pragma unroll
-      for (int i = 0; i < kHeadDim; i += 4) {
-        const float4 kk = *(const float4*)(kr + i);
-        const float4 qq = *(const float4*)(sQ + i);
-        dot = dot + qq.x * kk.x;
-        dot = dot + qq.y * kk.y;
-        dot = dot + qq.z * kk.z;
-        dot = dot + qq.w * kk.w;
-      }
-      if (key < nkey) sc[c] = dot * scale;
+      for (int i = 0; i < kHeadDim / 4; ++i) kb[i] = *(const f4v*)(krb + 4 * i);
+      __builtin_amdgcn_sched_barrier(0);
+      float da = -0.0f, db = -0.0f;
+#pragma unroll
+      for (int i = 0; i < kHeadDim / 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          da = da + q[i][j] * ka[i][j];
+          db = db + q[i][j] * kb[i][j];
+        }
+      sc[0] = da * scale;
+      if (64 + lane < nkey) sc[1] = db * scale;
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
+      float da = -0.0f;
+#pragma unroll
+      for (int i = 0; i < kHeadDim / 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) da = da + q[i][j] * ka[i][j];
+      if (lane < nkey) sc[0] = da * scale;
     }
   }
   const float mx = wave_max(fmaxf(sc[0], sc[1]));
@@ -323,17 +340,22 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     pp[0] = *(const f4v*)(sP + k0);
     pp[1] = *(const f4v*)(sP + k0 + 4);
   };
+  // The read-ahead is unconditional (clamped inside the staged rows; past the
+  // last batch its values are unused), so each wait is for the batch in use.
   float o = 0.0f;
   load8(0, va, pa);
 #pragma unroll 1
-  for (int bt = 0; bt < nbat; bt += 2) {
-    if (bt + 1 < nbat) load8((bt + 1) * 8, vb, pb);
+  for (int bt = 0;;) {
+    load8(min((bt + 1) * 8, kBlkMaxKeys - 8), vb, pb);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o = o + va[i >> 2][i & 3] * pa[i >> 2][i & 3];
-    if (bt + 1 >= nbat) break;
-    if (bt + 2 < nbat) load8((bt + 2) * 8, va, pa);
+    if (++bt >= nbat) break;
+    load8(min((bt + 1) * 8, kBlkMaxKeys - 8), va, pa);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o = o + vb[i >> 2][i & 3] * pb[i >> 2][i & 3];
+    if (++bt >= nbat) break;
   }
   b.out[(int64_t)r * b.ldo + h * kHeadDim + lane] = o;
   const bool bad = !isfinite(o);

@@ -121,6 +121,7 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
   for (int k = 0; k < NBATCH - 2; k += 2) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) B[b] = p[(k + 1) * NB + b];
+    __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the adds
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       s = s + A[b].x;
@@ -130,6 +131,7 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) A[b] = p[(k + 2) * NB + b];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       s = s + B[b].x;
@@ -140,6 +142,7 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) B[b] = p[(NBATCH - 1) * NB + b];
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     s = s + A[b].x;
@@ -158,7 +161,8 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
 }
 
 // The same fold over the first nb batches of 8 float4 (nb >= 1, a value known
-// only at run time), with the same two-buffer read-ahead.
+// only at run time).  The read-ahead is unconditional (past the last batch it
+// re-reads that batch, unused), so every wait is for the batch being added.
 __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, float init) {
   constexpr int NB = 8;
   float4 A[NB], B[NB];
@@ -166,11 +170,11 @@ __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, f
 #pragma unroll
   for (int b = 0; b < NB; ++b) A[b] = p[b];
 #pragma unroll 1
-  for (int k = 0; k < nb; k += 2) {
-    if (k + 1 < nb) {
+  for (int k = 0;;) {
+    const int kb = min(k + 1, nb - 1);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) B[b] = p[(k + 1) * NB + b];
-    }
+    for (int b = 0; b < NB; ++b) B[b] = p[kb * NB + b];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       s = s + A[b].x;
@@ -178,11 +182,11 @@ __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, f
       s = s + A[b].z;
       s = s + A[b].w;
     }
-    if (k + 1 >= nb) break;
-    if (k + 2 < nb) {
+    if (++k >= nb) break;
+    const int ka = min(k + 1, nb - 1);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) A[b] = p[(k + 2) * NB + b];
-    }
+    for (int b = 0; b < NB; ++b) A[b] = p[ka * NB + b];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       s = s + B[b].x;
@@ -190,6 +194,7 @@ __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, f
       s = s + B[b].z;
       s = s + B[b].w;
     }
+    if (++k >= nb) break;
   }
   return s;
 }
