@@ -228,15 +228,19 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
                                    const float* bias, int64_t rows, int64_t dim, float* out,
                                    int8_t* q, float* a, int* err, void* stream);
 
-/* Variable-length attention, one query row per (row, head) wave:
- * query row i belongs to sequence seq_of_row[i] and attends over key rows
- * [cu_k[s], cu_k[s+1]); max_keys bounds every range (at most 4096); heads <= 16.
- * Row strides in elements.  in_bf16 != 0 reads q/k/v as
- * bfloat16 (converted exactly to fp32); out is fp32 [rows, heads*64]. */
+/* Variable-length attention: query row i belongs to sequence seq_of_row[i]
+ * and attends over key rows [cu_k[s], cu_k[s+1]); max_keys bounds every range
+ * (at most 4096); heads <= 16.  Row strides in elements.  in_bf16 != 0 reads
+ * q/k/v as bfloat16 (converted exactly to fp32); out is fp32 [rows, heads*64].
+ * n_seqs > 0 declares packed self-attention: the query rows are the key rows
+ * (row i lies in [cu_k[s], cu_k[s+1]) for s = seq_of_row[i]), cu_k has
+ * n_seqs + 1 entries, rows = cu_k[n_seqs]; then ranges of at most 256 keys
+ * run on the kernel that stages each sequence's keys once per 16 queries.
+ * n_seqs = 0: one (row, head) wave each, for any query/key pairing. */
 int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
-                         const int32_t* seq_of_row, const uint32_t* cu_k, int64_t rows,
-                         int64_t heads, int64_t max_keys, int in_bf16, float* out, int64_t ldo,
-                         void* stream);
+                         const int32_t* seq_of_row, const uint32_t* cu_k, int64_t n_seqs,
+                         int64_t rows, int64_t heads, int64_t max_keys, int in_bf16, float* out,
+                         int64_t ldo, void* stream);
 
 /* Vocabulary projection + bias + generation mask + argmax per row:
  * token[m] = argmax_v (acc[m,v] * (1/(xa[m]*mult[v])) + bias[v]) with ties to

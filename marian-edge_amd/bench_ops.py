@@ -21,8 +21,10 @@ Cases:
     256, 4096.  Algorithmic bytes 4MK + KN + 4N + 8MN (fp32 A, int8 W, one
     per-column scale, i32 + fp32 out); bias reads are 4N more and counted.
   * Varlen attention: 256 packed sentences with lengths ~ lognormal(3.2, 0.6)
-    clipped to [4, 256], 8 heads x 64, Q/K/V fp32 and bf16.  Algorithmic bytes
-    4 * T * d * b (Q, K, V in, O out).
+    clipped to [4, 256], 8 heads x 64, Q/K/V fp32 and bf16, as packed
+    self-attention (the query-tile list, then the key-staging kernel).
+    Algorithmic bytes 3 * T * d * b + 4 * T * d (Q, K, V in their type, fp32
+    O out).
 """
 
 from __future__ import annotations
@@ -88,8 +90,9 @@ def run(out_path: str, reps: int) -> None:
             dev.attention(dq, dk, dv, dseq, dcu, do, heads=d // 64, max_keys=lmax, bf16=bf16)
         dev.synchronize()
         # Q, K, V read in their type, O written in fp32.
+        # Two kernels per call: the query-tile list, then the attention.
         cases.append(dict(label=f"attention {'bf16' if bf16 else 'fp32'} T={T}", kind="attention",
-                          T=T, calls=reps, kernels_per_call=1,
+                          T=T, calls=reps, kernels_per_call=2,
                           bytes=3 * T * d * b + 4 * T * d, flops=4 * d * int((np.diff(cu.astype(np.int64)) ** 2).sum())))
         for t in (dq, dk, dv, dseq, dcu, do):
             t.free()
@@ -119,7 +122,7 @@ def summarize(run_path: str, trace_path: str) -> str:
             ks = rows[i:i + c["kernels_per_call"]]
             i += c["kernels_per_call"]
             per_call.append(sum(e - s for s, e, _ in ks) / 1000.0)
-            names.update(n.split("(")[0].replace("mh::(anonymous namespace)::", "").replace("void ", "")
+            names.update(n.replace("mh::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
                          for _, _, n in ks)
         us = statistics.median(per_call[1:] if len(per_call) > 1 else per_call)
         gbs = c["bytes"] / (us * 1e-6) / 1e9

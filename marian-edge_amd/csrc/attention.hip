@@ -239,6 +239,194 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
+
+// ---------------------------------------------------------------------------
+// Self-attention of packed sequences (ATT_SEQ) with keys shared by the queries
+// of a tile: one workgroup of kTileQ waves per (query tile, head), a tile
+// being up to kTileQ consecutive query rows of one sequence.  The sequence's
+// K rows of this head are staged in LDS once and read by every wave (one
+// query per wave); then its V rows replace them.  Per query the arithmetic is
+// k_attention's: lane = key for the sequential 64-term dots, wave max, the
+// restated expf, the denominator folded in key order from 0.0 through LDS,
+// PV in key order with lane = dimension.  Sequences of up to kTileMaxKeys.
+// ---------------------------------------------------------------------------
+constexpr int kTileQ = 16;          // queries (waves) per workgroup
+constexpr int kTileMaxKeys = 256;   // keys staged in LDS
+
+__global__ __launch_bounds__(1024) void k_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles,
+                                                    int cap) {
+  // tiles[0] = count; tiles[1 + 2i] = sequence, tiles[2 + 2i] = first query.
+  __shared__ int s_wsum[16];
+  __shared__ int s_base;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int per = (nseq + 1023) / 1024;
+  const int s0 = tid * per, s1 = min(s0 + per, nseq);
+  int cnt = 0;
+  for (int q = s0; q < s1; ++q) cnt += (int)((cu[q + 1] - cu[q] + kTileQ - 1) / kTileQ);
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < 16; ++w) {
+      const int t = s_wsum[w];
+      s_wsum[w] = run;
+      run += t;
+    }
+    s_base = run;
+  }
+  __syncthreads();
+  int pos = s_wsum[wave] + incl - cnt;
+  for (int q = s0; q < s1; ++q) {
+    const int L = (int)(cu[q + 1] - cu[q]);
+    for (int q0 = 0; q0 < L; q0 += kTileQ, ++pos) {
+      if (pos < cap) {
+        tiles[1 + 2 * pos] = (uint32_t)q;
+        tiles[2 + 2 * pos] = (uint32_t)q0;
+      }
+    }
+  }
+  if (tid == 0) tiles[0] = (uint32_t)min(s_base, cap);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kTileQ * 64) void k_attn_tiles(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float dyn[];
+  __shared__ uint64_t sTab[32];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int h = blockIdx.x % a.heads, ti = blockIdx.x / a.heads;
+  if (ti >= (int)a.tiles[0]) return;  // uniform: the list is shorter than its bound
+  const int sq = (int)a.tiles[1 + 2 * ti], q0 = (int)a.tiles[2 + 2 * ti];
+  const int64_t key0 = a.cu[sq];
+  const int L = (int)(a.cu[sq + 1] - key0);
+  const int nq = min(kTileQ, L - q0);
+  // A range past the launch's key bound is cut to it (and flagged).
+  const int Lc = min(L, min(a.tile_keys_pad, kTileMaxKeys));
+  const int nch = (Lc + 63) >> 6;
+  const int lpad = (Lc + 7) & ~7;
+  float* stage = dyn;                                        // [lpad][kKRow]
+  float* sP = dyn + (size_t)a.tile_keys_pad * kKRow + w * a.tile_keys_pad;  // this wave's probabilities
+  const int64_t base = key0 * a.ldkv + h * kHeadDim;
+  if (tid < 32) sTab[tid] = kExp2Tab[tid];
+  if (L > Lc && tid == 0 && a.err) *a.err = 2;
+
+  // K rows: thread t stages float4 (t + 1024 j) % 16 of key (t + 1024 j) / 16.
+  for (int idx = tid; idx < Lc * 16; idx += kTileQ * 64)
+    *(float4*)(stage + (idx >> 4) * kKRow + (idx & 15) * 4) =
+        load_row4<T>(a.k, base + (int64_t)(idx >> 4) * a.ldkv + (idx & 15) * 4);
+  const bool live = w < nq;
+  const int row = (int)key0 + q0 + w;
+  const int qv = live ? __float_as_int(Io<T>::at(a.q, (int64_t)row * a.ldq + h * kHeadDim + lane)) : 0;
+  __syncthreads();
+
+  float sc[kTileMaxKeys / 64];
+  if (live) {
+    const float scale = 1.0f / sqrtf((float)kHeadDim);
+#pragma unroll
+    for (int c = 0; c < kTileMaxKeys / 64; ++c) {
+      sc[c] = -INFINITY;
+      if (c < nch) {
+        const float* kr = stage + min(c * 64 + lane, Lc - 1) * kKRow;
+        float dot = -0.0f;
+#pragma unroll
+        for (int i0 = 0; i0 < kHeadDim; i0 += 16) {
+          float kk[16], qs[16];
+#pragma unroll
+          for (int i = 0; i < 16; i += 4) {
+            const float4 v = *(const float4*)(kr + i0 + i);
+            kk[i] = v.x;
+            kk[i + 1] = v.y;
+            kk[i + 2] = v.z;
+            kk[i + 3] = v.w;
+          }
+#pragma unroll
+          for (int i = 0; i < 16; ++i) qs[i] = __int_as_float(__builtin_amdgcn_readlane(qv, i0 + i));
+#pragma unroll
+          for (int i = 0; i < 16; ++i) dot = dot + qs[i] * kk[i];
+        }
+        if (c * 64 + lane < Lc) sc[c] = dot * scale;
+      }
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kTileMaxKeys / 64; ++c) mloc = fmaxf(mloc, sc[c]);
+    const float mx = wave_max(mloc);
+#pragma unroll
+    for (int c = 0; c < kTileMaxKeys / 64; ++c) {
+      if (c < nch) {
+        sc[c] = c * 64 + lane < Lc ? ref_expf(sc[c] - mx, sTab) : 0.0f;
+        sP[c * 64 + lane] = sc[c];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+    __builtin_amdgcn_wave_barrier();
+    // Denominator in key order from 0.0; entries past the last key are +0.0.
+    const float inv = 1.0f / seq_fold_lds_batches((const float4*)sP, (Lc + 31) >> 5, 0.0f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < kTileMaxKeys / 64; ++c)
+      if (c < nch) sP[c * 64 + lane] = sc[c] * inv;
+  }
+  __syncthreads();  // every wave is done with the K rows
+
+  // V rows replace them; rows [Lc, lpad) are zero so PV runs whole batches.
+  for (int idx = tid; idx < lpad * 16; idx += kTileQ * 64) {
+    const int key = idx >> 4;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (key < Lc) v = load_row4<T>(a.v, base + (int64_t)key * a.ldkv + (idx & 15) * 4);
+    *(float4*)(stage + key * kKRow + (idx & 15) * 4) = v;
+  }
+  __syncthreads();
+  if (!live) return;
+  // out_d = sum_k v_k[d] * p_k in key order, in batches of 8 keys whose
+  // values and probabilities are read one batch ahead (clamped inside the
+  // staged rows; past the last key p is +0 and the rows are zero).
+  const int nbat = lpad >> 3;
+  float va[8], vb[8];
+  float4 pa0, pa1, pb0, pb1;
+  auto load8 = [&](int k0, float (&v)[8], float4& p0, float4& p1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = stage[(k0 + i) * kKRow + lane];
+    p0 = *(const float4*)(sP + k0);
+    p1 = *(const float4*)(sP + k0 + 4);
+  };
+  float o = 0.0f;
+  load8(0, va, pa0, pa1);
+#pragma unroll 1
+  for (int bt = 0;;) {
+    load8(min((bt + 1) * 8, lpad - 8), vb, pb0, pb1);
+    __builtin_amdgcn_sched_barrier(0);
+    o = o + va[0] * pa0.x;
+    o = o + va[1] * pa0.y;
+    o = o + va[2] * pa0.z;
+    o = o + va[3] * pa0.w;
+    o = o + va[4] * pa1.x;
+    o = o + va[5] * pa1.y;
+    o = o + va[6] * pa1.z;
+    o = o + va[7] * pa1.w;
+    if (++bt >= nbat) break;
+    load8(min((bt + 1) * 8, lpad - 8), va, pa0, pa1);
+    __builtin_amdgcn_sched_barrier(0);
+    o = o + vb[0] * pb0.x;
+    o = o + vb[1] * pb0.y;
+    o = o + vb[2] * pb0.z;
+    o = o + vb[3] * pb0.w;
+    o = o + vb[4] * pb1.x;
+    o = o + vb[5] * pb1.y;
+    o = o + vb[6] * pb1.z;
+    o = o + vb[7] * pb1.w;
+    if (++bt >= nbat) break;
+  }
+  a.out[(int64_t)row * a.ldo + h * kHeadDim + lane] = o;
+  const bool bad = !isfinite(o);
+  if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+}
+
 template <int CH, typename T, bool PRE>
 hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((k_attention<CH, T, PRE>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
@@ -252,11 +440,35 @@ hipError_t launch_ch(const AttnArgs& a, hipStream_t s) {
 
 }  // namespace
 
+int seq_tiles_bound(int rows, int nseq) { return (rows + kTileQ - 1) / kTileQ + nseq; }
+
+hipError_t launch_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles, int cap, hipStream_t s) {
+  if (nseq <= 0 || nseq > 16 * 1024 || cap <= 0 || !cu || !tiles) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_seq_tiles, dim3(1), dim3(1024), 0, s, cu, nseq, tiles, cap);
+  return hipGetLastError();
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
   if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out ||
       (int64_t)a.rows * a.heads > 0x7fffffff)
     return hipErrorInvalidValue;
+  // Packed self-attention with a tile list: keys staged once per tile.
+  if (a.mode == ATT_SEQ && a.tiles && a.tiles_cap > 0 && a.max_keys <= kTileMaxKeys) {
+    if ((int64_t)a.tiles_cap * a.heads > 0x7fffffff) return hipErrorInvalidValue;
+    AttnArgs t = a;
+    t.tile_keys_pad = (a.max_keys + 63) & ~63;  // probability stride; also >= every lpad
+    const size_t lds = ((size_t)t.tile_keys_pad * kKRow + (size_t)kTileQ * t.tile_keys_pad) * 4;
+    const dim3 grid(a.tiles_cap * a.heads), block(kTileQ * 64);
+    auto kern = a.bf16 ? k_attn_tiles<uint16_t> : k_attn_tiles<float>;
+    if (lds > 64 * 1024) {
+      const hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kern, grid, block, lds, s, t);
+    return hipGetLastError();
+  }
   // Decode launches cover few rows: one round trip per row matters more
   // than occupancy.  Encoder launches keep the lighter register budget.
   if (a.max_keys <= 128) return a.mode == ATT_SEQ ? launch_ch<2>(a, s) : launch_ch<2, true>(a, s);

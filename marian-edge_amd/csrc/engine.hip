@@ -46,7 +46,7 @@ struct DecLayer {
 enum Buf {
   B_META, B_DMETA, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_ATT, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
   B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DATT, B_DAMAX, B_DY, B_DH, B_DHQ, B_DHA,
-  B_PART, B_OUT, B_COUNT, B_HIST, B_COUNT_
+  B_PART, B_OUT, B_COUNT, B_HIST, B_TILES, B_COUNT_
 };
 
 uint32_t host_positions(uint32_t dim, uint32_t count, float* out) {
@@ -513,6 +513,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   int32_t* OUT = (int32_t*)E->get(B_OUT, 4ull * CR);
   uint32_t* COUNT = (uint32_t*)E->get(B_COUNT, 4ull * R);
   uint32_t* HIST = (uint32_t*)E->get(B_HIST, 4ull * E->hcap);
+  const int tiles_cap = seq_tiles_bound(T, Bi);
+  uint32_t* TILES = (uint32_t*)E->get(B_TILES, 4ull * (1 + 2 * (size_t)tiles_cap));
   for (int b = 0; b < B_COUNT_; ++b)
     if (!E->buf[b]) return E->fail(MARIAN_HIP_ERR_DEVICE, "device allocation failed");
 
@@ -554,6 +556,9 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     ea.err = E->err_flag;
     MH_HIP(launch_embed(ea, s));
   }
+  // Query tiles of the packed sentences for the encoder's self-attention.
+  const bool tiled = Lmax <= 256;
+  if (tiled) MH_HIP(launch_seq_tiles(d_cu, Bi, TILES, tiles_cap, s));
   auto gemm = [&](const int8_t* A, const float* a, int M, const Lin& L, float* out, int relu) {
     GemmArgs g;
     g.A = A;
@@ -586,6 +591,10 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     aa.seq_of_row = d_seq;
     aa.cu = d_cu;
     aa.max_keys = (int)Lmax;
+    if (tiled) {
+      aa.tiles = TILES;
+      aa.tiles_cap = tiles_cap;
+    }
     aa.out = ATT;
     aa.ldo = d;
     aa.err = E->err_flag;

@@ -149,8 +149,17 @@ struct AttnArgs {
   int64_t ldo = 0;
   float* amax = nullptr;  // optional [rows, heads]: max |out| of each head's slice
   int* err = nullptr;
+  // ATT_SEQ with max_keys <= 256: the query-tile list written by
+  // launch_seq_tiles (tiles_cap = its bound) selects the tiled kernel (no amax).
+  const uint32_t* tiles = nullptr;
+  int tiles_cap = 0;
+  int tile_keys_pad = 0;  // set by the launcher
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+// Query tiles of packed sequences cu[0..nseq] for the tiled ATT_SEQ kernel:
+// at most seq_tiles_bound(rows, nseq) entries; tiles needs 1 + 2 * cap words.
+int seq_tiles_bound(int rows, int nseq);
+hipError_t launch_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles, int cap, hipStream_t s);
 
 // Decode attention block (one launch per attention sublayer on steps with few
 // rows): per (row, head) it builds the row's input with `pro` (PRO_LN, or

@@ -29,8 +29,8 @@ int op_status(hipError_t e, const char* what) {
 // buffers (quantized activations, argmax partials).  Grow-only, one set per
 // device; calls that overlap on one device race on it.
 struct OpScratch {
-  void* p[3] = {nullptr, nullptr, nullptr};
-  size_t cap[3] = {0, 0, 0};
+  void* p[4] = {nullptr, nullptr, nullptr, nullptr};
+  size_t cap[4] = {0, 0, 0, 0};
 };
 std::mutex g_scratch_mu;
 OpScratch g_scratch[64];
@@ -118,11 +118,12 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
 }
 
 int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
-                         const int32_t* seq_of_row, const uint32_t* cu_k, int64_t rows,
-                         int64_t heads, int64_t max_keys, int in_bf16, float* out, int64_t ldo,
-                         void* stream) {
+                         const int32_t* seq_of_row, const uint32_t* cu_k, int64_t n_seqs,
+                         int64_t rows, int64_t heads, int64_t max_keys, int in_bf16, float* out,
+                         int64_t ldo, void* stream) {
   if (!q || !k || !v || !seq_of_row || !cu_k || !out || rows < 0 || rows > INT32_MAX ||
-      heads <= 0 || heads > 16 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096)
+      heads <= 0 || heads > 16 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096 ||
+      n_seqs < 0 || n_seqs > 16 * 1024)
     return MARIAN_HIP_ERR_INVALID_INPUT;
   AttnArgs a;
   a.mode = ATT_SEQ;
@@ -139,6 +140,17 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
   a.out = out;
   a.ldo = ldo;
   a.max_keys = (int)max_keys;
+  if (n_seqs > 0 && rows > 0 && max_keys <= 256) {
+    // Packed self-attention: the query-tile list first (library scratch).
+    const int cap = seq_tiles_bound((int)rows, (int)n_seqs);
+    uint32_t* tiles = (uint32_t*)scratch(3, (1 + 2 * (size_t)cap) * 4, (hipStream_t)stream);
+    if (!tiles) return op_status(hipErrorOutOfMemory, "attention scratch");
+    const int rc = op_status(launch_seq_tiles(cu_k, (int)n_seqs, tiles, cap, (hipStream_t)stream),
+                             "attention tiles");
+    if (rc != MARIAN_HIP_OK) return rc;
+    a.tiles = tiles;
+    a.tiles_cap = cap;
+  }
   return op_status(launch_attention(a, (hipStream_t)stream), "attention");
 }
 

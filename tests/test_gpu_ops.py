@@ -126,13 +126,18 @@ def _attention_case(pkg, orc, dev, q, k, v, cu, heads, bf16):
     else:
         dq, dk, dv = (dev.DeviceArray.from_host(x) for x in (q, k, v))
     ref = orc.attention(q, k, v, cu, cu, heads)
-    out = dev.DeviceArray.zeros((T, heads * 64), np.float32)
-    dev.attention(dq, dk, dv, dev.DeviceArray.from_host(seq), dev.DeviceArray.from_host(cu), out,
-                  heads=heads, max_keys=int(lens.max()), bf16=bf16)
-    dev.synchronize()
-    got = out.host()
-    assert rel_err(got, ref) <= REL_TOL or np.max(np.abs(got - ref)) < 1e-5
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "attention not bit-identical"
+    dseq, dcu = dev.DeviceArray.from_host(seq), dev.DeviceArray.from_host(cu)
+    # packed_self: the key-staging kernel (ranges up to 256 keys); otherwise
+    # one wave per (row, head).
+    for packed in (True, False):
+        out = dev.DeviceArray.zeros((T, heads * 64), np.float32)
+        dev.attention(dq, dk, dv, dseq, dcu, out, heads=heads, max_keys=int(lens.max()), bf16=bf16,
+                      packed_self=packed)
+        dev.synchronize()
+        got = out.host()
+        assert rel_err(got, ref) <= REL_TOL or np.max(np.abs(got - ref)) < 1e-5
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+            f"attention not bit-identical (packed_self={packed})"
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -152,6 +157,14 @@ def test_attention_edges(pkg, orc, dev):
     q, k, v = (rng.standard_normal((T, 128)).astype(np.float32) for _ in range(3))
     print("attention edges", flush=True)
     _attention_case(pkg, orc, dev, q, k, v, cu, 2, False)
+    # ranges of 1..256 keys around the staging kernel's batch and chunk edges
+    lens = np.array([1, 7, 8, 9, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 2],
+                    np.int64)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    T = int(cu[-1])
+    q, k, v = (rng.standard_normal((T, 512)).astype(np.float32) for _ in range(3))
+    print("attention edges up to 256 keys", flush=True)
+    _attention_case(pkg, orc, dev, q, k, v, cu, 8, False)
 
 
 def test_vocab_argmax_matches_oracle(pkg, orc, dev, full_model):
