@@ -245,7 +245,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // of a tile: one workgroup of kTileQ waves per (query tile, head), a tile
 // being up to kTileQ consecutive query rows of one sequence.  The sequence's
 // K rows of this head are staged in LDS once and read by every wave (one
-// query per wave); then its V rows replace them.  Per query the arithmetic is
+// query per wave), 64 keys at a time; then its V rows, likewise.  Per query the arithmetic is
 // k_attention's: lane = key for the sequential 64-term dots, wave max, the
 // restated expf, the denominator folded in key order from 0.0 through LDS,
 // PV in key order with lane = dimension.  Sequences of up to kTileMaxKeys.
@@ -294,9 +294,12 @@ __global__ __launch_bounds__(1024) void k_seq_tiles(const uint32_t* cu, int nseq
   if (tid == 0) tiles[0] = (uint32_t)min(s_base, cap);
 }
 
+// Two workgroups per CU: at most 64 VGPRs (eight waves per SIMD).
 template <typename T>
-__global__ __launch_bounds__(kTileQ * 64) void k_attn_tiles(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float dyn[];
+__global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_attn_tiles(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float stage[64 * kKRow];            // one 64-key chunk
+  __shared__ __attribute__((aligned(16))) float sPall[kTileQ * kTileMaxKeys];  // per-wave probabilities
+  __shared__ __attribute__((aligned(16))) float sQall[kTileQ * kHeadDim];     // per-wave query
   __shared__ uint64_t sTab[32];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x % a.heads, ti = blockIdx.x / a.heads;
@@ -305,53 +308,60 @@ __global__ __launch_bounds__(kTileQ * 64) void k_attn_tiles(AttnArgs a) {
   const int64_t key0 = a.cu[sq];
   const int L = (int)(a.cu[sq + 1] - key0);
   const int nq = min(kTileQ, L - q0);
-  // A range past the launch's key bound is cut to it (and flagged).
-  const int Lc = min(L, min(a.tile_keys_pad, kTileMaxKeys));
+  // A range past kTileMaxKeys is cut to it (and flagged).
+  const int Lc = min(L, kTileMaxKeys);
   const int nch = (Lc + 63) >> 6;
   const int lpad = (Lc + 7) & ~7;
-  float* stage = dyn;                                        // [lpad][kKRow]
-  float* sP = dyn + (size_t)a.tile_keys_pad * kKRow + w * a.tile_keys_pad;  // this wave's probabilities
+  float* sP = sPall + w * kTileMaxKeys;
   const int64_t base = key0 * a.ldkv + h * kHeadDim;
   if (tid < 32) sTab[tid] = kExp2Tab[tid];
   if (L > Lc && tid == 0 && a.err) *a.err = 2;
 
-  // K rows: thread t stages float4 (t + 1024 j) % 16 of key (t + 1024 j) / 16.
-  for (int idx = tid; idx < Lc * 16; idx += kTileQ * 64)
-    *(float4*)(stage + (idx >> 4) * kKRow + (idx & 15) * 4) =
-        load_row4<T>(a.k, base + (int64_t)(idx >> 4) * a.ldkv + (idx & 15) * 4);
+  // Chunk rows: thread t moves float4 t % 16 of key t / 16 of the chunk; keys
+  // past the last are zero.  The next chunk is requested while this one is used.
+  auto ld = [&](const void* src, int c) {
+    const int key = c * 64 + (tid >> 4);
+    return key < Lc ? load_row4<T>(src, base + (int64_t)key * a.ldkv + (tid & 15) * 4)
+                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  };
+  float4 pre = ld(a.k, 0);
   const bool live = w < nq;
   const int row = (int)key0 + q0 + w;
-  const int qv = live ? __float_as_int(Io<T>::at(a.q, (int64_t)row * a.ldq + h * kHeadDim + lane)) : 0;
-  __syncthreads();
+  const float* sQ = sQall + w * kHeadDim;
+  if (live) sQall[w * kHeadDim + lane] = Io<T>::at(a.q, (int64_t)row * a.ldq + h * kHeadDim + lane);
+  float* srow = stage + (tid >> 4) * kKRow + (tid & 15) * 4;
 
+  // Scores: lane = key of the chunk, 64-term dot in dimension order.
+  const float scale = 1.0f / sqrtf((float)kHeadDim);
   float sc[kTileMaxKeys / 64];
-  if (live) {
-    const float scale = 1.0f / sqrtf((float)kHeadDim);
 #pragma unroll
-    for (int c = 0; c < kTileMaxKeys / 64; ++c) {
-      sc[c] = -INFINITY;
-      if (c < nch) {
-        const float* kr = stage + min(c * 64 + lane, Lc - 1) * kKRow;
+  for (int c = 0; c < kTileMaxKeys / 64; ++c) {
+    sc[c] = -INFINITY;
+    if (c < nch) {
+      if (c > 0) __syncthreads();  // every wave has read the previous chunk
+      *(float4*)srow = pre;
+      __syncthreads();
+      pre = c + 1 < nch ? ld(a.k, c + 1) : ld(a.v, 0);
+      if (live) {
+        const float* kr = stage + min(lane, Lc - 1 - c * 64) * kKRow;
+        // The query is read from LDS as broadcasts (published by the barrier above).
         float dot = -0.0f;
 #pragma unroll
-        for (int i0 = 0; i0 < kHeadDim; i0 += 16) {
-          float kk[16], qs[16];
-#pragma unroll
-          for (int i = 0; i < 16; i += 4) {
-            const float4 v = *(const float4*)(kr + i0 + i);
-            kk[i] = v.x;
-            kk[i + 1] = v.y;
-            kk[i + 2] = v.z;
-            kk[i + 3] = v.w;
-          }
-#pragma unroll
-          for (int i = 0; i < 16; ++i) qs[i] = __int_as_float(__builtin_amdgcn_readlane(qv, i0 + i));
-#pragma unroll
-          for (int i = 0; i < 16; ++i) dot = dot + qs[i] * kk[i];
+        for (int i = 0; i < kHeadDim; i += 4) {
+          const float4 kk = *(const float4*)(kr + i);
+          const float4 qq = *(const float4*)(sQ + i);
+          dot = dot + qq.x * kk.x;
+          dot = dot + qq.y * kk.y;
+          dot = dot + qq.z * kk.z;
+          dot = dot + qq.w * kk.w;
         }
         if (c * 64 + lane < Lc) sc[c] = dot * scale;
       }
     }
+  }
+  // Softmax of each live wave's query: max, expf, the denominator folded in
+  // key order from 0.0 (entries past the last key are +0.0), then p = e / sum.
+  if (live) {
     float mloc = -INFINITY;
 #pragma unroll
     for (int c = 0; c < kTileMaxKeys / 64; ++c) mloc = fmaxf(mloc, sc[c]);
@@ -365,63 +375,65 @@ __global__ __launch_bounds__(kTileQ * 64) void k_attn_tiles(AttnArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
     __builtin_amdgcn_wave_barrier();
-    // Denominator in key order from 0.0; entries past the last key are +0.0.
-    const float inv = 1.0f / seq_fold_lds_batches((const float4*)sP, (Lc + 31) >> 5, 0.0f);
+    const float inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, (Lc + 15) >> 4, 0.0f);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int c = 0; c < kTileMaxKeys / 64; ++c)
       if (c < nch) sP[c * 64 + lane] = sc[c] * inv;
   }
-  __syncthreads();  // every wave is done with the K rows
 
-  // V rows replace them; rows [Lc, lpad) are zero so PV runs whole batches.
-  for (int idx = tid; idx < lpad * 16; idx += kTileQ * 64) {
-    const int key = idx >> 4;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (key < Lc) v = load_row4<T>(a.v, base + (int64_t)key * a.ldkv + (idx & 15) * 4);
-    *(float4*)(stage + key * kKRow + (idx & 15) * 4) = v;
-  }
-  __syncthreads();
-  if (!live) return;
-  // out_d = sum_k v_k[d] * p_k in key order, in batches of 8 keys whose
-  // values and probabilities are read one batch ahead (clamped inside the
-  // staged rows; past the last key p is +0 and the rows are zero).
-  const int nbat = lpad >> 3;
-  float va[8], vb[8];
-  float4 pa0, pa1, pb0, pb1;
-  auto load8 = [&](int k0, float (&v)[8], float4& p0, float4& p1) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = stage[(k0 + i) * kKRow + lane];
-    p0 = *(const float4*)(sP + k0);
-    p1 = *(const float4*)(sP + k0 + 4);
-  };
+  // out_d = sum_k v_k[d] * p_k in key order, chunk by chunk, in batches of 8
+  // keys read one batch ahead (clamped inside the chunk; past the last key p
+  // is +0 and the rows are zero, so the added products are +0).
   float o = 0.0f;
-  load8(0, va, pa0, pa1);
+#pragma unroll
+  for (int c = 0; c < kTileMaxKeys / 64; ++c) {
+    if (c < nch) {
+      __syncthreads();  // every wave has read the previous chunk (and its probabilities are in LDS)
+      *(float4*)srow = pre;
+      __syncthreads();
+      if (c + 1 < nch) pre = ld(a.v, c + 1);
+      if (live) {
+        const int kend = min(64, lpad - c * 64);  // a multiple of 8
+        const int nbat = kend >> 3;
+        float va[8], vb[8];
+        float4 pa0, pa1, pb0, pb1;
+        auto load8 = [&](int k0, float (&v)[8], float4& p0, float4& p1) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = stage[(k0 + i) * kKRow + lane];
+          p0 = *(const float4*)(sP + c * 64 + k0);
+          p1 = *(const float4*)(sP + c * 64 + k0 + 4);
+        };
+        load8(0, va, pa0, pa1);
 #pragma unroll 1
-  for (int bt = 0;;) {
-    load8(min((bt + 1) * 8, lpad - 8), vb, pb0, pb1);
-    __builtin_amdgcn_sched_barrier(0);
-    o = o + va[0] * pa0.x;
-    o = o + va[1] * pa0.y;
-    o = o + va[2] * pa0.z;
-    o = o + va[3] * pa0.w;
-    o = o + va[4] * pa1.x;
-    o = o + va[5] * pa1.y;
-    o = o + va[6] * pa1.z;
-    o = o + va[7] * pa1.w;
-    if (++bt >= nbat) break;
-    load8(min((bt + 1) * 8, lpad - 8), va, pa0, pa1);
-    __builtin_amdgcn_sched_barrier(0);
-    o = o + vb[0] * pb0.x;
-    o = o + vb[1] * pb0.y;
-    o = o + vb[2] * pb0.z;
-    o = o + vb[3] * pb0.w;
-    o = o + vb[4] * pb1.x;
-    o = o + vb[5] * pb1.y;
-    o = o + vb[6] * pb1.z;
-    o = o + vb[7] * pb1.w;
-    if (++bt >= nbat) break;
+        for (int bt = 0;;) {
+          load8(min((bt + 1) * 8, kend - 8), vb, pb0, pb1);
+          __builtin_amdgcn_sched_barrier(0);
+          o = o + va[0] * pa0.x;
+          o = o + va[1] * pa0.y;
+          o = o + va[2] * pa0.z;
+          o = o + va[3] * pa0.w;
+          o = o + va[4] * pa1.x;
+          o = o + va[5] * pa1.y;
+          o = o + va[6] * pa1.z;
+          o = o + va[7] * pa1.w;
+          if (++bt >= nbat) break;
+          load8(min((bt + 1) * 8, kend - 8), va, pa0, pa1);
+          __builtin_amdgcn_sched_barrier(0);
+          o = o + vb[0] * pb0.x;
+          o = o + vb[1] * pb0.y;
+          o = o + vb[2] * pb0.z;
+          o = o + vb[3] * pb0.w;
+          o = o + vb[4] * pb1.x;
+          o = o + vb[5] * pb1.y;
+          o = o + vb[6] * pb1.z;
+          o = o + vb[7] * pb1.w;
+          if (++bt >= nbat) break;
+        }
+      }
+    }
   }
+  if (!live) return;
   a.out[(int64_t)row * a.ldo + h * kHeadDim + lane] = o;
   const bool bad = !isfinite(o);
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
@@ -456,17 +468,11 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   // Packed self-attention with a tile list: keys staged once per tile.
   if (a.mode == ATT_SEQ && a.tiles && a.tiles_cap > 0 && a.max_keys <= kTileMaxKeys) {
     if ((int64_t)a.tiles_cap * a.heads > 0x7fffffff) return hipErrorInvalidValue;
-    AttnArgs t = a;
-    t.tile_keys_pad = (a.max_keys + 63) & ~63;  // probability stride; also >= every lpad
-    const size_t lds = ((size_t)t.tile_keys_pad * kKRow + (size_t)kTileQ * t.tile_keys_pad) * 4;
     const dim3 grid(a.tiles_cap * a.heads), block(kTileQ * 64);
-    auto kern = a.bf16 ? k_attn_tiles<uint16_t> : k_attn_tiles<float>;
-    if (lds > 64 * 1024) {
-      const hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(kern, grid, block, lds, s, t);
+    if (a.bf16)
+      hipLaunchKernelGGL(k_attn_tiles<uint16_t>, grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL(k_attn_tiles<float>, grid, block, 0, s, a);
     return hipGetLastError();
   }
   // Decode launches cover few rows: one round trip per row matters more

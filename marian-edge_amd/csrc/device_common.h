@@ -160,11 +160,12 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
   return s;
 }
 
-// The same fold over the first nb batches of 8 float4 (nb >= 1, a value known
-// only at run time).  The read-ahead is unconditional (past the last batch it
-// re-reads that batch, unused), so every wait is for the batch being added.
+// The same fold over the first nb batches of NB float4 (nb >= 1, a value
+// known only at run time).  The read-ahead is unconditional (past the last
+// batch it re-reads that batch, unused), so every wait is for the batch being
+// added.  NB trades registers (8 x NB) for fewer waits.
+template <int NB = 8>
 __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, float init) {
-  constexpr int NB = 8;
   float4 A[NB], B[NB];
   float s = init;
 #pragma unroll

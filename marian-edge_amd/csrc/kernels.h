@@ -153,7 +153,6 @@ struct AttnArgs {
   // launch_seq_tiles (tiles_cap = its bound) selects the tiled kernel (no amax).
   const uint32_t* tiles = nullptr;
   int tiles_cap = 0;
-  int tile_keys_pad = 0;  // set by the launcher
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 // Query tiles of packed sequences cu[0..nseq] for the tiled ATT_SEQ kernel:
