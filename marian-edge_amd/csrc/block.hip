@@ -30,9 +30,6 @@ __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
 
 __device__ __forceinline__ v4i zero4b() { return v4i{0, 0, 0, 0}; }
 
-// Native 4 x fp32 vector (HIP's float4 is a struct whose copies become memcpy,
-// which keeps an array of them out of registers).
-typedef float f4v __attribute__((ext_vector_type(4)));
 
 // ---- the input row, built by one wave: lane l holds elements 4l..4l+3 and
 // 256+4l..256+4l+3 of the kBlkD-wide row ---------------------------------------

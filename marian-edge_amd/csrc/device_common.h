@@ -21,6 +21,10 @@
 
 namespace mh {
 
+// Native 4 x fp32 vector (HIP's float4 is a struct whose copies become memcpy,
+// which keeps an array of them out of registers).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
 constexpr int kWave = 64;
 constexpr int kHeadDim = 64;           // per-head width supported by the kernels
 constexpr int kMaxPosition = 4096;     // marian-model manifest.rs:13
