@@ -127,6 +127,25 @@ def vocab_bytes(V, K, rows):
     return V * K + 8 * V + rows * (K + 4 + 8 * groups)
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_kernels_ragged64_traffic.json"
+
+
+def measured_traffic(prefix):
+    """HBM-side bytes per dispatch (fetched + written) of the kernels whose
+    name starts with `prefix`, dispatch-weighted, from the FETCH_SIZE /
+    WRITE_SIZE rocprofv3 runs summarized in profiles/ (copy-calibrated)."""
+    try:
+        kernels = json.loads(TRAFFIC_PROFILE.read_text())["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    ks = [v for k, v in kernels.items() if k.startswith(prefix)]
+    n = sum(v["dispatches"] for v in ks)
+    if not n:
+        return None
+    return round(sum((v["fetch_bytes_per_dispatch"] + v["write_bytes_per_dispatch"]) * v["dispatches"]
+                     for v in ks) / n)
+
+
 def block_bytes(kind, step, layer, src_lens, d, heads):
     """Algorithmic bytes of one attention-block launch at decode step `step`
     over the active rows whose source lengths are `src_lens`:
@@ -297,7 +316,8 @@ def main(argv=None):
             "algorithmic_bytes_per_launch": round(r["blk_algo"] / max(1, r["blk_launch"])),
             "launches": r["blk_launch"],
             "timing": "events recorded by each launch's dispatch, in a separate pass over the same batch",
-            "traffic": None,
+            "traffic": measured_traffic("k_attn_block"),
+            "traffic_source": "profiles/decode_kernels_ragged64_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, bytes per launch)",
         },
         "decode_gemm_roofline": {
             "kernel": "k_vocab_argmax (vocab projection + bias + mask + argmax partials)",
@@ -310,6 +330,7 @@ def main(argv=None):
             "algorithmic_bytes_per_launch": round(r["vocab_algo"] / max(1, r["vocab_launch"])),
             "launches": r["vocab_launch"],
             "timing": "events recorded by each launch's dispatch, in a separate pass over the same batch",
+            "traffic": measured_traffic("k_vocab_argmax"),
         },
         "cpu_baseline": cpu,
         "device": r["info"]["device"],

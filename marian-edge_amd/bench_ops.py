@@ -101,6 +101,56 @@ def run(out_path: str, reps: int) -> None:
     print(f"wrote {len(cases)} cases to {out_path}", flush=True)
 
 
+def copy_calibration(mb: int, reps: int) -> None:
+    """Device-to-device copies of `mb` MiB (the runtime's copy kernel): the
+    reference for what the memory-traffic counters read per byte moved."""
+    pkg = _load_package()
+    from importlib import import_module
+
+    dev = import_module(pkg.__name__ + ".device")
+    n = mb * 1024 * 1024
+    src = dev.DeviceArray.from_host(np.ones(n // 4, np.float32))
+    dst = dev.DeviceArray((n // 4,), np.float32)
+    for _ in range(reps):
+        dev.copy(dst, src)
+    dev.synchronize()
+    print(f"copied {mb} MiB x {reps}", flush=True)
+
+
+def pmc_summary(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_csv: str,
+                copy_mb: int) -> dict:
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the decode kernels from
+    two rocprofv3 --pmc runs of bench.py, scaled by what the same counters
+    read for the copy kernel per byte it moves."""
+    def per_kernel(path, counter):
+        out = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") != counter:
+                    continue
+                name = r["Kernel_Name"].replace("mh::(anonymous namespace)::", "").replace("void ", "")
+                out.setdefault(name.split("(")[0], []).append(float(r["Counter_Value"]))
+        return out
+
+    fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    cf, cw = per_kernel(copy_fetch_csv, "FETCH_SIZE"), per_kernel(copy_write_csv, "WRITE_SIZE")
+    copy_kib = copy_mb * 1024.0
+
+    def copy_factor(d):
+        vals = [v for k, vs in d.items() if "copyBuffer" in k for v in vs]
+        return copy_kib / statistics.median(vals) if vals else float("nan")
+
+    ff, fw = copy_factor(cf), copy_factor(cw)
+    res = {"copy_fetch_factor": ff, "copy_write_factor": fw, "kernels": {}}
+    for k in sorted(set(fetch) | set(write)):
+        if not k.startswith("k_"):
+            continue
+        fk = statistics.mean(fetch.get(k, [0.0])) * ff * 1024.0
+        wk = statistics.mean(write.get(k, [0.0])) * fw * 1024.0
+        res["kernels"][k] = {"fetch_bytes": fk, "write_bytes": wk, "dispatches": len(fetch.get(k, []))}
+    return res
+
+
 def summarize(run_path: str, trace_path: str) -> str:
     spec = json.loads(Path(run_path).read_text())
     rows = []
@@ -142,9 +192,23 @@ def main(argv=None) -> int:
     s = sub.add_parser("summarize")
     s.add_argument("run_json")
     s.add_argument("trace_csv")
+    c = sub.add_parser("copy")
+    c.add_argument("--mb", type=int, default=64)
+    c.add_argument("--reps", type=int, default=5)
+    pm = sub.add_parser("pmc")
+    pm.add_argument("fetch_csv")
+    pm.add_argument("write_csv")
+    pm.add_argument("copy_fetch_csv")
+    pm.add_argument("copy_write_csv")
+    pm.add_argument("--copy-mb", type=int, default=64)
     a = ap.parse_args(argv)
     if a.cmd == "run":
         run(a.out, a.reps)
+    elif a.cmd == "copy":
+        copy_calibration(a.mb, a.reps)
+    elif a.cmd == "pmc":
+        print(json.dumps(pmc_summary(a.fetch_csv, a.write_csv, a.copy_fetch_csv, a.copy_write_csv,
+                                     a.copy_mb), indent=1))
     else:
         print(summarize(a.run_json, a.trace_csv))
     return 0

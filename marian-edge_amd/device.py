@@ -72,6 +72,12 @@ def device_name(device: int = 0) -> str:
     return buf.value.decode()
 
 
+def copy(dst: DeviceArray, src: DeviceArray) -> None:
+    """Device-to-device copy of src's bytes into dst."""
+    n = min(dst.nbytes, src.nbytes)
+    _lib.check(_lib.load().marian_hip_memcpy_d2d(dst.ptr, src.ptr, n), "d2d")
+
+
 def synchronize() -> None:
     _lib.check(_lib.load().marian_hip_device_sync(), "device_sync")
 
