@@ -932,7 +932,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.pro = pend;  // the last LayerNorm, when the kernel builds its rows itself
       pend.kind = PRO_NONE;
       hipEvent_t ev[2];
-      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
+      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, g.pro.kind == PRO_LN ? 1u : 0u, ev));
       MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));
     }
     FinalizeArgs f;
@@ -1009,6 +1009,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   E->stats.max_active_rows = (uint32_t)n_active0;
   E->stats.vocab_kernel_ms = 0;
   E->stats.vocab_kernel_launches = 0;
+  // Like the step trace, the launch trace ends with the last step that ran on rows.
+  while (n_timed > 0 && E->kev_step[n_timed - 1] >= steps) --n_timed;
+  E->kev_kind.resize(n_timed);
+  E->kev_step.resize(n_timed);
+  E->kev_layer.resize(n_timed);
   E->kev_us.assign(n_timed, 0.0f);
   for (size_t i = 0; i < n_timed; ++i) {
     float ms = 0;

@@ -89,7 +89,7 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hi
 // recorded by the kernel's own dispatch (start and end of the kernel).
 hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
                                hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
-// LDS-tiled 128x128 MFMA GEMM for large M (EPI_STORE only).
+// LDS-tiled 64x64 MFMA GEMM for large M (EPI_STORE only); lda a multiple of 16.
 hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s);
 // Picks the kernel by M (host-known M only).
 hipError_t launch_gemm_store(const GemmArgs& g, const Epilogue& e, hipStream_t s);

@@ -114,3 +114,39 @@ def test_reference_caps_are_enforced_when_configured(pkg, full_model):
         out = e.translate_token_ids(np.array([5, 6, 7], np.int32), np.array([0, 3], np.uint32),
                                     [100], flags=pkg.FLAG_IGNORE_EOS)
         assert len(out.rows()[0]) == 6
+
+
+def test_timing_modes_keep_outputs_and_trace_launches(pkg, engine):
+    b = pkg.ragged_batch(seed=41, n=24)
+    print("timing modes: 24 sentences, off / per step / per launch", flush=True)
+    engine.set_timing(0)
+    base = engine.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, b.flags).rows()
+    try:
+        engine.set_timing(engine.TIME_STEPS)
+        stepped = engine.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, b.flags).rows()
+        rows, step_end = engine.last_step_trace()
+        engine.set_timing(engine.TIME_KERNELS)
+        timed = engine.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, b.flags).rows()
+        kt = engine.last_kernel_trace()
+    finally:
+        engine.set_timing(0)
+    assert stepped == base and timed == base
+    counts = np.array([len(r) for r in base])
+    steps = len(rows)
+    assert steps == counts.max()
+    # rows active at step t = sentences that produced more than t tokens
+    assert [int(r) for r in rows] == [int((counts > t).sum()) for t in range(steps)]
+    assert np.all(np.diff(step_end) > 0)
+    vocab = kt["kind"] == engine.KERNEL_VOCAB
+    assert sorted(kt["step"][vocab].tolist()) == list(range(steps))
+    assert set(kt["layer"][vocab].tolist()) <= {0, 1}
+    # the LayerNorm prologue variant is chosen by row count, which only falls
+    lv = kt["layer"][vocab][np.argsort(kt["step"][vocab])]
+    assert np.all(np.diff(lv.astype(np.int64)) >= 0)
+    blocks = ~vocab
+    assert set(kt["kind"][blocks].tolist()) <= {engine.KERNEL_SELF_BLOCK, engine.KERNEL_CROSS_BLOCK}
+    assert np.all(kt["us"] > 0)
+    # 24 sentences of at most 128 source tokens: while a step attends over at
+    # most 128 cached keys, both attention sublayers of both layers run as blocks
+    per_step = np.bincount(kt["step"][blocks], minlength=steps)
+    assert np.all(per_step[:128] == 4) and np.all(per_step <= 4)
