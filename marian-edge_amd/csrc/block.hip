@@ -20,11 +20,13 @@
 namespace mh {
 namespace {
 
-constexpr int kBlkThreads = 256;
+constexpr int kBlkRowWaves = 4;   // waves 0-3 build the input row
+constexpr int kBlkLoadWaves = 4;  // waves 4-7 load weights and keys, then project
+constexpr int kBlkThreads = 64 * (kBlkRowWaves + kBlkLoadWaves);
 constexpr int kBlkD = 512;             // model width handled (8 heads x 64)
 constexpr int kBlkMaxKeys = 128;       // keys staged in LDS
 constexpr int kBlkRow = kHeadDim + 4;  // padded LDS key row (floats)
-constexpr int kBlkKeyPer = kBlkMaxKeys * (kHeadDim / 4) / kBlkThreads;  // float4 per thread (8)
+static_assert(kBlkRowWaves == 4 && kBlkD == 4 * kSpecChunk, "the LayerNorm folds run as four chunks");
 
 __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
 
@@ -66,8 +68,35 @@ __device__ __forceinline__ void row_load(const RowPrologue& p, int r, int step, 
   }
 }
 
-// The row's values: LayerNorm(y + r) with its two sequential folds over an
-// LDS copy (sZ), or the scaled embedding plus the position row.
+// LayerNorm(y + r) built by the four row waves together (each loaded the
+// whole row): the mean and variance folds run as speculative four-chunk folds
+// (bit-identical to the sequential folds) over LDS copies of z and of the
+// squared deviations.  Every row wave returns the normalized row.
+__device__ __forceinline__ void row_build_ln4(const RowLoads<PRO_LN>& L, float* sZ, float* sT,
+                                              SpecFoldLds& fm, SpecFoldLds& fv, int w, int lane,
+                                              f4v (&o)[2]) {
+  f4v z[2], t[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) z[j] = L.a[j] + L.b[j];  // add_slices
+  spec_fold_chunk(z, sZ, -0.0f, fm, w, lane);
+  wg_lds_barrier();
+  const float mean = spec_fold_resolve(sZ, fm, lane) / (float)kBlkD;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const f4v c = z[j] - mean;
+    t[j] = c * c;
+  }
+  spec_fold_chunk(t, sT, -0.0f, fv, w, lane);
+  wg_lds_barrier();
+  const float var = spec_fold_resolve(sT, fv, lane) / (float)kBlkD;
+  const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) o[j] = ((z[j] - mean) * inv) * L.g[j] + L.bb[j];
+}
+
+// The row's values built by one wave: LayerNorm(y + r) with its two
+// sequential folds over an LDS copy (sZ), or the scaled embedding plus the
+// position row.
 template <int PK>
 __device__ __forceinline__ void row_build(const RowPrologue& p, const RowLoads<PK>& L, float* sZ,
                                           int lane, f4v (&o)[2]) {
@@ -130,21 +159,26 @@ __device__ __forceinline__ float row_quantize(const f4v (&o)[2], int8_t* sX, int
   return a_row;
 }
 
-// Work split: wave 0 builds the input row (its LayerNorm folds are a single
-// dependent chain, so it runs with nothing else live); waves 1-3 meanwhile
-// load this head's weight rows and stage the row's keys and values in LDS,
-// then run the projection; wave 0 attends.
-constexpr int kBlkLoaders = kBlkThreads - 64;  // threads of waves 1-3
-constexpr int kBlkStage = (kBlkMaxKeys * (kHeadDim / 4) + kBlkLoaders - 1) / kBlkLoaders;  // 11
+// Work split: waves 0-3 build the input row (a LayerNorm's folds as four
+// speculative chunks, with nothing else live in those waves; an embedding row
+// by wave 0 alone); waves 4-7 meanwhile load this head's weight rows and
+// stage the row's keys and values in LDS, passing the folds' two workgroup
+// barriers with their loads in flight, then run the projection; wave 0
+// attends.
+constexpr int kBlkLoaders = 64 * kBlkLoadWaves;
+constexpr int kBlkStage = kBlkMaxKeys * (kHeadDim / 4) / kBlkLoaders;  // float4 per loader (8)
+static_assert(kBlkStage * kBlkLoaders == kBlkMaxKeys * (kHeadDim / 4), "key staging");
 
 template <int MODE, int PK>
 __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   constexpr bool SELF = MODE == ATT_SELF;
   constexpr int NT = SELF ? 12 : 4;        // 16-column projection tiles: Q (+ K, V)
-  constexpr int TPW = (NT + 2) / 3;        // tiles per loader wave
+  constexpr int TPW = (NT + kBlkLoadWaves - 1) / kBlkLoadWaves;  // tiles per loader wave
   __shared__ __attribute__((aligned(16))) float sK[kBlkMaxKeys * kBlkRow];
   __shared__ __attribute__((aligned(16))) float sV[kBlkMaxKeys * kBlkRow];
   __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
+  __shared__ __attribute__((aligned(16))) float sT[PK == PRO_LN ? kBlkD : 4];
+  __shared__ SpecFoldLds sFm, sFv;
   __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
   __shared__ __attribute__((aligned(16))) float sQ[kHeadDim];
   __shared__ __attribute__((aligned(16))) float sP[kBlkMaxKeys];
@@ -164,14 +198,20 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   const int nk_ld = (int)min((int64_t)nkm, b.max_row - key0);                   // readable rows
   const int nkey = SELF ? nkm + 1 : nkm;                                       // keys attended
 
-  if (wave == 0) {
+  if (wave < kBlkRowWaves) {
     // ---- the input row ----------------------------------------------------------
+    if (PK != PRO_LN && wave != 0) return;  // an embedding row has no folds
     const uint64_t tab_v = kBlkExp2Tab[lane & 31];
     RowLoads<PK> in;
     row_load<PK>(b.pro, r, step, lane, in);
     if (r >= n) return;
     f4v o[2];
-    row_build<PK>(b.pro, in, sZ, lane, o);
+    if constexpr (PK == PRO_LN) {
+      row_build_ln4(in, sZ, sT, sFm, sFv, wave, lane, o);
+      if (wave != 0) return;
+    } else {
+      row_build<PK>(b.pro, in, sZ, lane, o);
+    }
     bool bad;
     const float a_row = row_quantize(o, sX, lane, bad);
     if (h == 0 && b.pro.out) {
@@ -183,13 +223,14 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     if (__any(bad) && lane == 0 && b.err) *b.err = 1;
     if (lane == 0 && nk_row > nkm && b.err) *b.err = 2;  // more keys than the LDS stages
   } else {
-    // ---- waves 1-3: weights, then the keys and values into LDS -----------------
+    // ---- waves 4-7: weights, then the keys and values into LDS -----------------
+    const int lw = wave - kBlkRowWaves;  // loader wave
     const int kq = (lane >> 4) * 16;
     v4i bf[TPW][kBlkD / 64];
     float wm[TPW], bi[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int tile = min((wave - 1) + 3 * i, NT - 1);  // 16 columns of Q, K or V
+      const int tile = min(lw + kBlkLoadWaves * i, NT - 1);  // 16 columns of Q, K or V
       const int n_w = (tile / 4) * kBlkD + h * kHeadDim + (tile % 4) * 16 + (lane & 15);
       const int8_t* wr = b.W + (int64_t)n_w * kBlkD + kq;
 #pragma unroll
@@ -197,10 +238,10 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       wm[i] = b.wmult[n_w];
       bi[i] = b.bias[n_w];
     }
-    // Key rows: loader thread u stages float4 (u + 192 j) % 16 of key (u + 192 j) / 16.
+    // Key rows: loader thread u stages float4 (u + 256 j) % 16 of key (u + 256 j) / 16.
     // Past the readable keys the last readable row is reloaded (all in bounds)
     // and not stored.
-    const int u = tid - 64;
+    const int u = tid - 64 * kBlkRowWaves;
     const int last = max(nk_ld - 1, 0);
     const int64_t base = key0 * b.ldkv + h * kHeadDim;
     f4v kv[kBlkStage], vv[kBlkStage];
@@ -213,6 +254,10 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       vv[j] = *(const f4v*)(b.v + off);
     }
     if (r >= n) return;
+    if constexpr (PK == PRO_LN) {  // the row waves' two fold barriers, loads still in flight
+      wg_lds_barrier();
+      wg_lds_barrier();
+    }
 #pragma unroll
     for (int j = 0; j < kBlkStage; ++j) {
       const int idx = u + kBlkLoaders * j;
@@ -231,7 +276,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     const float a_row = sA;
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int tile = (wave - 1) + 3 * i;
+      const int tile = lw + kBlkLoadWaves * i;
       if (tile >= NT) break;
       // Two independent accumulation chains over the two halves of K (exact
       // integers: their sum does not depend on the split).
@@ -364,30 +409,34 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 
 // ---------------------------------------------------------------------------
 // LayerNorm + up-projection block (the FFN's first layer on steps with few
-// rows): one 256-thread workgroup per (row, 128-column slice).  Wave 0 builds
-// the row's residual LayerNorm and quantizes it, as in the attention block;
-// waves 1-3 meanwhile load the slice's weight rows into registers, then run
-// the projection on MFMA (row 0 of a 16-row tile), dequantize, apply ReLU and
-// store.  Replaces the LayerNorm kernel and the skinny GEMM that followed it.
+// rows): one 512-thread workgroup per (row, 128-column slice).  Waves 0-3
+// build the row's residual LayerNorm (speculative four-chunk folds) and wave
+// 0 quantizes it, as in the attention block; waves 4-7 meanwhile load the
+// slice's weight rows into registers, then run the projection on MFMA (row 0
+// of a 16-row tile), dequantize, apply ReLU and store.  Replaces the
+// LayerNorm kernel and the skinny GEMM that followed it.
 // ---------------------------------------------------------------------------
-constexpr int kLgCols = 128;                 // output columns per workgroup
-constexpr int kLgTiles = kLgCols / 16;       // MFMA column tiles per workgroup
-constexpr int kLgTpw = (kLgTiles + 2) / 3;   // tiles per loader wave
+constexpr int kLgCols = 128;                                      // output columns per workgroup
+constexpr int kLgTiles = kLgCols / 16;                            // MFMA column tiles per workgroup
+constexpr int kLgTpw = (kLgTiles + kBlkLoadWaves - 1) / kBlkLoadWaves;  // tiles per loader wave
 
 __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
+  __shared__ __attribute__((aligned(16))) float sT[kBlkD];
+  __shared__ SpecFoldLds sFm, sFv;
   __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
   __shared__ float sA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int slices = a.N / kLgCols;
   const int slice = blockIdx.x % slices, r = blockIdx.x / slices;  // r < a.rows (host bound)
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
-  if (wave == 0) {
+  if (wave < kBlkRowWaves) {
     RowLoads<PRO_LN> in;
     row_load<PRO_LN>(a.pro, r, 0, lane, in);
     if (r >= n) return;
     f4v o[2];
-    row_build<PRO_LN>(a.pro, in, sZ, lane, o);
+    row_build_ln4(in, sZ, sT, sFm, sFv, wave, lane, o);
+    if (wave != 0) return;
     bool bad;
     const float a_row = row_quantize(o, sX, lane, bad);
     if (slice == 0 && a.pro.out) {
@@ -399,12 +448,13 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     __syncthreads();  // the quantized row is in LDS
     return;
   }
+  const int lw = wave - kBlkRowWaves;  // loader wave
   const int kq = (lane >> 4) * 16;
   v4i bf[kLgTpw][kBlkD / 64];
   float wm[kLgTpw], bi[kLgTpw];
 #pragma unroll
   for (int i = 0; i < kLgTpw; ++i) {
-    const int tile = min((wave - 1) + 3 * i, kLgTiles - 1);
+    const int tile = min(lw + kBlkLoadWaves * i, kLgTiles - 1);
     const int col = slice * kLgCols + tile * 16 + (lane & 15);
     const int8_t* wr = a.W + (int64_t)col * kBlkD + kq;
 #pragma unroll
@@ -413,11 +463,13 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     bi[i] = a.bias[col];
   }
   if (r >= n) return;
+  wg_lds_barrier();  // the row waves' two fold barriers, weight loads still in flight
+  wg_lds_barrier();
   __syncthreads();  // the quantized row is in LDS
   const float a_row = sA;
 #pragma unroll
   for (int i = 0; i < kLgTpw; ++i) {
-    const int tile = (wave - 1) + 3 * i;
+    const int tile = lw + kBlkLoadWaves * i;
     if (tile >= kLgTiles) break;
     v4i acc = zero4b(), acc2 = zero4b();
 #pragma unroll

@@ -164,6 +164,118 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
   return s;
 }
 
+// ---- speculative exact fold over 512 values ------------------------------------
+// The sequential fold init + p[0] + p[1] + ... + p[511], run by four waves at
+// once with the same result bits.  Wave w folds chunk w (elements [128w,
+// 128w + 128)): wave 0 from init, wave w >= 1 from each of 64 consecutive
+// floats (one per lane) centred on the double-precision sum of elements
+// [0, 128w).  The true start of chunk w is the end of chunk w - 1; when it is
+// among chunk w's candidates (compared bit for bit), that candidate's chain is
+// chunk w's exact end, otherwise chunk w is folded again from the true start.
+// Every step is the sequential fold's own float addition, so the result is
+// the sequential fold's whatever the estimates are: they only decide how often
+// a 128-term refold is needed.  Chunk ends stay within a few units in the last
+// place of the exact prefix for sums of non-negative terms; a prefix near zero
+// after cancellation can fall outside the window (about 3% of boundaries for
+// centred normal rows).
+//
+// Protocol: each of the four fold waves holds the whole row (lane l: elements
+// 4l..4l+3 in v[0], 256+4l..256+4l+3 in v[1]) and calls spec_fold_chunk,
+// which stores its chunk to p (LDS, 512 floats) and folds it; then every wave
+// of the workgroup passes wg_lds_barrier; then the fold waves call
+// spec_fold_resolve (each gets the result).  p and L stay unchanged until all
+// four have resolved.
+constexpr int kSpecChunk = 128;
+struct SpecFoldLds {
+  float start[3][64];  // candidate starts of chunks 1..3
+  float end[4][64];    // chain ends of chunks 0..3 (chunk 0: every lane the same)
+};
+
+__device__ __forceinline__ int float_order(float f) {  // monotone in f; +0 and -0 -> 0
+  const uint32_t b = __float_as_uint(f);
+  return (b >> 31) ? -(int)(b & 0x7fffffffu) : (int)b;
+}
+__device__ __forceinline__ float order_float(int o) {
+  return __uint_as_float(o >= 0 ? (uint32_t)o : (0x80000000u | (uint32_t)(-o)));
+}
+
+// All waves of the workgroup: this wave's LDS accesses complete, then the
+// workgroup barrier.  Outstanding global loads are not waited for.
+__device__ __forceinline__ void wg_lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Sum over the wave in double (any order; every lane returns it): DPP within
+// each 16-lane row, then the four row sums read out as scalars.
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)dpp_mov<CTRL>((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)dpp_mov<CTRL>((int)(uint32_t)(b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v += dpp_mov_f64<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov_f64<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov_f64<0x124>(v);  // row_ror:4
+  v += dpp_mov_f64<0x128>(v);  // row_ror:8
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  double r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 16 * i);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 16 * i);
+    r[i] = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+  }
+  return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
+__device__ __forceinline__ double sum4_f64(const f4v& x) {
+  return ((double)x.x + (double)x.y) + ((double)x.z + (double)x.w);
+}
+
+__device__ __forceinline__ void spec_fold_chunk(const f4v (&v)[2], float* p, float init,
+                                                SpecFoldLds& L, int w, int lane) {
+  // Chunk w is float4 w >> 1 of lanes 32 * (w & 1) .. + 31.
+  if ((lane >> 5) == (w & 1)) *(f4v*)(p + 4 * lane + 256 * (w >> 1)) = v[w >> 1];
+  float c = init;
+  if (w > 0) {
+    // Elements [0, 128w): the first float4 of lanes < 32w, and for w = 3 the
+    // second float4 of lanes < 32.
+    double e = lane < 32 * w ? sum4_f64(v[0]) : 0.0;
+    if (w == 3 && lane < 32) e += sum4_f64(v[1]);
+    e = wave_sum_f64(e);
+    c = order_float(float_order((float)e) + lane - 32);
+    L.start[w - 1][lane] = c;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's chunk is in LDS
+  __builtin_amdgcn_wave_barrier();
+  L.end[w][lane] = seq_fold_lds<kSpecChunk / 4>((const float4*)(p + kSpecChunk * w), c);
+}
+
+__device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFoldLds& L, int lane) {
+  float st[3], en[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    st[k] = L.start[k][lane];
+    en[k] = L.end[k + 1][lane];
+  }
+  float s = L.end[0][0];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    const uint64_t hit = __ballot(__float_as_uint(st[k - 1]) == __float_as_uint(s));
+    if (hit)
+      s = __int_as_float(
+          __builtin_amdgcn_readlane(__float_as_int(en[k - 1]), (int)__ffsll((unsigned long long)hit) - 1));
+    else
+      s = seq_fold_lds<kSpecChunk / 4>((const float4*)(p + kSpecChunk * k), s);
+  }
+  return s;
+}
+
 // The same fold over the first nb batches of NB float4 (nb >= 1, a value
 // known only at run time).  The read-ahead is unconditional (past the last
 // batch it re-reads that batch, unused), so every wait is for the batch being
