@@ -32,6 +32,13 @@ __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
 
 __device__ __forceinline__ v4i zero4b() { return v4i{0, 0, 0, 0}; }
 
+// Ends a batch of a software-pipelined loop: neither the IR optimizer nor the
+// scheduler moves memory accesses across it, so only one batch is read ahead.
+__device__ __forceinline__ void batch_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 
 // ---- the input row, built by one wave: lane l holds elements 4l..4l+3 and
 // 256+4l..256+4l+3 of the kBlkD-wide row ---------------------------------------
@@ -166,8 +173,7 @@ __device__ __forceinline__ float row_quantize(const f4v (&o)[2], int8_t* sX, int
 // barriers with their loads in flight, then run the projection; wave 0
 // attends.
 constexpr int kBlkLoaders = 64 * kBlkLoadWaves;
-constexpr int kBlkStage = kBlkMaxKeys * (kHeadDim / 4) / kBlkLoaders;  // float4 per loader (8)
-static_assert(kBlkStage * kBlkLoaders == kBlkMaxKeys * (kHeadDim / 4), "key staging");
+static_assert(kBlkRow % 4 == 0 && kBlkMaxKeys * (kBlkRow / 4) % 64 == 0, "key staging by wave instructions");
 
 template <int MODE, int PK>
 __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
@@ -238,36 +244,36 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       wm[i] = b.wmult[n_w];
       bi[i] = b.bias[n_w];
     }
-    // Key rows: loader thread u stages float4 (u + 256 j) % 16 of key (u + 256 j) / 16.
-    // Past the readable keys the last readable row is reloaded (all in bounds)
-    // and not stored.
-    const int u = tid - 64 * kBlkRowWaves;
-    const int last = max(nk_ld - 1, 0);
+    // Key and value rows go straight from memory into the padded LDS rows
+    // (global_load_lds, 16 bytes per lane, no registers): an LDS row is 17
+    // 16-byte slots, the last one padding.  Wave instruction i fills slots
+    // [64i, 64i + 64); lanes on padding or past the readable keys are masked
+    // off and leave their slot untouched.
     const int64_t base = key0 * b.ldkv + h * kHeadDim;
-    f4v kv[kBlkStage], vv[kBlkStage];
-#pragma unroll
-    for (int j = 0; j < kBlkStage; ++j) {
-      const int idx = u + kBlkLoaders * j;
-      const int key = min(idx >> 4, last);
-      const int64_t off = base + (int64_t)key * b.ldkv + (idx & 15) * 4;
-      kv[j] = *(const f4v*)(b.k + off);
-      vv[j] = *(const f4v*)(b.v + off);
+    constexpr int kSlots = kBlkRow / 4;  // 17
+    const int n_inst = (nk_ld * kSlots + 63) >> 6;
+    for (int i = lw; i < n_inst; i += kBlkLoadWaves) {
+      const int slot = 64 * i + lane, key = slot / kSlots, c = slot - key * kSlots;
+      if (c < kHeadDim / 4 && key < nk_ld) {
+        const int64_t off = base + (int64_t)key * b.ldkv + c * 4;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(b.k + off),
+                                         (__attribute__((address_space(3))) void*)(sK + 256 * i), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(b.v + off),
+                                         (__attribute__((address_space(3))) void*)(sV + 256 * i), 16, 0, 0);
+      }
     }
-    if (r >= n) return;
+    if (r >= n) {
+      __builtin_amdgcn_s_waitcnt(0);  // no LDS write may land after the workgroup ends
+      return;
+    }
     if constexpr (PK == PRO_LN) {  // the row waves' two fold barriers, loads still in flight
       wg_lds_barrier();
       wg_lds_barrier();
     }
-#pragma unroll
-    for (int j = 0; j < kBlkStage; ++j) {
-      const int idx = u + kBlkLoaders * j;
-      if ((idx >> 4) < nk_ld) {  // a live row's keys are all readable (nk_ld == nkm)
-        *(f4v*)(sK + (idx >> 4) * kBlkRow + (idx & 15) * 4) = kv[j];
-        *(f4v*)(sV + (idx >> 4) * kBlkRow + (idx & 15) * 4) = vv[j];
-      }
-    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's key and value rows are in LDS
     // Value rows from the last key up to the next multiple of 8 are zero, so
     // the PV loop's batches of 8 keys read no stale LDS.
+    const int u = tid - 64 * kBlkRowWaves;
     const int zrows = min((nkey + 7) & ~7, kBlkMaxKeys) - nkey;
     for (int idx = u; idx < zrows * 16; idx += kBlkLoaders)
       *(f4v*)(sV + (nkey + (idx >> 4)) * kBlkRow + (idx & 15) * 4) = f4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -313,41 +319,63 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 
   // ---- attention (wave 0) ---------------------------------------------------------
   // Scores: lane = key of chunk c (keys c*64 + lane), 64-term dot in
-  // dimension order.  The query and the key rows are read into registers
-  // first; with more than 64 keys the two chunks' chains run interleaved.
+  // dimension order.  The query is read into SGPRs one dimension at a time
+  // (readlane of the row lane d holds), the key rows from LDS in batches of 8
+  // dimensions, the next batch while the current one is used; with more than
+  // 64 keys the two chunks' chains run interleaved.  Registers stay within
+  // what two 512-thread workgroups per CU allow.
   const float scale = 1.0f / sqrtf((float)kHeadDim);
   float sc[2] = {-INFINITY, -INFINITY};
   {
-    f4v q[kHeadDim / 4], ka[kHeadDim / 4];
     const float* kra = sK + min(lane, nkey - 1) * kBlkRow;
+    const float* krb = sK + min(64 + lane, nkey - 1) * kBlkRow;
+    const int qv = __float_as_int(sQ[lane]);
+    f4v a0[2], b0[2], a1[2], b1[2];
+    auto rd = [&](int d0, bool two, f4v (&ka)[2], f4v (&kb)[2]) {
 #pragma unroll
-    for (int i = 0; i < kHeadDim / 4; ++i) {
-      q[i] = *(const f4v*)(sQ + 4 * i);
-      ka[i] = *(const f4v*)(kra + 4 * i);
-    }
+      for (int i = 0; i < 2; ++i) {
+        ka[i] = *(const f4v*)(kra + d0 + 4 * i);
+        if (two) kb[i] = *(const f4v*)(krb + d0 + 4 * i);
+      }
+    };
     if (nkey > 64) {
-      f4v kb[kHeadDim / 4];
-      const float* krb = sK + min(64 + lane, nkey - 1) * kBlkRow;
-#pragma unroll
-      for (int i = 0; i < kHeadDim / 4; ++i) kb[i] = *(const f4v*)(krb + 4 * i);
-      __builtin_amdgcn_sched_barrier(0);
       float da = -0.0f, db = -0.0f;
+      rd(0, true, a0, b0);
 #pragma unroll
-      for (int i = 0; i < kHeadDim / 4; ++i)
+      for (int d0 = 0; d0 < kHeadDim; d0 += 16) {
+        rd(d0 + 8, true, a1, b1);
+        batch_fence();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          da = da + q[i][j] * ka[i][j];
-          db = db + q[i][j] * kb[i][j];
+        for (int i = 0; i < 8; ++i) {
+          const float q = __int_as_float(__builtin_amdgcn_readlane(qv, d0 + i));
+          da = da + q * a0[i >> 2][i & 3];
+          db = db + q * b0[i >> 2][i & 3];
         }
+        if (d0 + 16 < kHeadDim) rd(d0 + 16, true, a0, b0);
+        batch_fence();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float q = __int_as_float(__builtin_amdgcn_readlane(qv, d0 + 8 + i));
+          da = da + q * a1[i >> 2][i & 3];
+          db = db + q * b1[i >> 2][i & 3];
+        }
+      }
       sc[0] = da * scale;
       if (64 + lane < nkey) sc[1] = db * scale;
     } else {
-      __builtin_amdgcn_sched_barrier(0);
       float da = -0.0f;
+      rd(0, false, a0, b0);
 #pragma unroll
-      for (int i = 0; i < kHeadDim / 4; ++i)
+      for (int d0 = 0; d0 < kHeadDim; d0 += 16) {
+        rd(d0 + 8, false, a1, b1);
+        batch_fence();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) da = da + q[i][j] * ka[i][j];
+        for (int i = 0; i < 8; ++i) da = da + __int_as_float(__builtin_amdgcn_readlane(qv, d0 + i)) * a0[i >> 2][i & 3];
+        if (d0 + 16 < kHeadDim) rd(d0 + 16, false, a0, b0);
+        batch_fence();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) da = da + __int_as_float(__builtin_amdgcn_readlane(qv, d0 + 8 + i)) * a1[i >> 2][i & 3];
+      }
       if (lane < nkey) sc[0] = da * scale;
     }
   }

@@ -113,9 +113,9 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // one is added, so the dependent chain never waits on LDS.  The batch loop is
 // kept rolled, which bounds the live registers (a fully unrolled fold lets
 // the scheduler hoist every read and spill) and the code size.
-template <int N4>
+template <int N4, int NB = 8>
 __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
-  constexpr int NB = 8, NBATCH = N4 / NB;
+  constexpr int NBATCH = N4 / NB;
   static_assert(N4 % (2 * NB) == 0, "pairs of batches");
   float4 A[NB], B[NB];
   float s = init;
@@ -186,6 +186,7 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
 // spec_fold_resolve (each gets the result).  p and L stay unchanged until all
 // four have resolved.
 constexpr int kSpecChunk = 128;
+constexpr int kSpecNB = 4;  // float4 read ahead per batch (bounds the fold waves' registers)
 struct SpecFoldLds {
   float start[3][64];  // candidate starts of chunks 1..3
   float end[4][64];    // chain ends of chunks 0..3 (chunk 0: every lane the same)
@@ -253,7 +254,7 @@ __device__ __forceinline__ void spec_fold_chunk(const f4v (&v)[2], float* p, flo
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's chunk is in LDS
   __builtin_amdgcn_wave_barrier();
-  L.end[w][lane] = seq_fold_lds<kSpecChunk / 4>((const float4*)(p + kSpecChunk * w), c);
+  L.end[w][lane] = seq_fold_lds<kSpecChunk / 4, kSpecNB>((const float4*)(p + kSpecChunk * w), c);
 }
 
 __device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFoldLds& L, int lane) {
@@ -271,7 +272,7 @@ __device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFol
       s = __int_as_float(
           __builtin_amdgcn_readlane(__float_as_int(en[k - 1]), (int)__ffsll((unsigned long long)hit) - 1));
     else
-      s = seq_fold_lds<kSpecChunk / 4>((const float4*)(p + kSpecChunk * k), s);
+      s = seq_fold_lds<kSpecChunk / 4, kSpecNB>((const float4*)(p + kSpecChunk * k), s);
   }
   return s;
 }
