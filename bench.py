@@ -174,21 +174,6 @@ def block_bytes(kind, step, layer, src_lens, d, heads):
     return w + rows_in + keys + out
 
 
-def vocab_variants(split):
-    """The vocabulary kernel's roofline per variant: launches that also built
-    the rows' last LayerNorm (two sequential 512-term folds on the kernel's
-    critical path) and launches over rows quantized beforehand."""
-    out = {}
-    for key, name in ((0, "rows_quantized_before"), (1, "layernorm_prologue")):
-        us, n, algo = split[key]
-        if not n:
-            continue
-        gbs = (algo / n) / (us / n * 1e-6) / 1e9
-        out[name] = {"launches": n, "avg_launch_us": round(us / n, 3), "achieved": round(gbs, 1),
-                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
-    return out
-
-
 def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
     """`warmup` untimed batches, then `steps` timed batches (device events at
     the batch start, after the encoder and after the decode loop only), then
@@ -229,7 +214,6 @@ def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
         lat += [float(step_end[c - 1]) for c in counts if c > 0]
 
     vocab_us, vocab_launch, vocab_algo = 0.0, 0, 0.0
-    vocab_split = {0: [0.0, 0, 0.0], 1: [0.0, 0, 0.0]}  # by LayerNorm prologue: us, launches, bytes
     blk_us, blk_launch, blk_algo = 0.0, 0, 0.0
     eng.set_timing(eng.TIME_KERNELS)
     for _ in range(extra_passes):
@@ -246,10 +230,6 @@ def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
                 vocab_us += float(us)
                 vocab_launch += 1
                 vocab_algo += vocab_bytes(V, K, len(active))
-                v = vocab_split[int(layer)]
-                v[0] += float(us)
-                v[1] += 1
-                v[2] += vocab_bytes(V, K, len(active))
             else:
                 blk_us += float(us)
                 blk_launch += 1
@@ -259,7 +239,6 @@ def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
     eng.close()
     return dict(dev_ms=dev_ms, wall_ms=wall_ms, lat=lat, ntok=ntok, info=info,
                 vocab_ms=vocab_us / 1000.0, vocab_launch=vocab_launch, vocab_algo=vocab_algo,
-                vocab_split=vocab_split,
                 blk_us=blk_us, blk_launch=blk_launch, blk_algo=blk_algo,
                 enc_ms=enc_ms, dec_ms=dec_ms, n_steps=n_steps)
 
@@ -352,7 +331,6 @@ def main(argv=None):
             "launches": r["vocab_launch"],
             "timing": "events recorded by each launch's dispatch, in a separate pass over the same batch",
             "traffic": measured_traffic("k_vocab_argmax"),
-            "by_variant": vocab_variants(r["vocab_split"]),
         },
         "cpu_baseline": cpu,
         "device": r["info"]["device"],

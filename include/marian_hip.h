@@ -193,8 +193,6 @@ int marian_hip_set_timing(marian_hip_engine* engine, uint32_t flags);
 /* With MARIAN_HIP_TIME_KERNELS: one record per timed decode launch of the last
  * translate call, in launch order: its kind, decode step, decoder layer and
  * device duration in microseconds (from events its own dispatch recorded).
- * For MARIAN_HIP_KERNEL_VOCAB the layer field is 1 when that launch also
- * built the rows' last LayerNorm (steps with few rows), else 0.
  * Writes min(cap, launches) entries and the launch count to *n. */
 int marian_hip_last_kernel_trace(const marian_hip_engine* engine, uint32_t* kind, uint32_t* step,
                                  uint32_t* layer, float* us, size_t cap, size_t* n);

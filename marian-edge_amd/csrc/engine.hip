@@ -655,15 +655,14 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   }
   constexpr int kAfMaxRows = 16;
   constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
-  constexpr int kLnFfnMaxRows = 16;  // ... and the LayerNorm + FFN up-projection block
-  constexpr int kLnVocabMaxRows = 16;  // ... and the vocabulary kernel's LayerNorm prologue
+  constexpr int kLnFfnMaxRows = 32;  // ... and the LayerNorm + FFN up-projection block
 
   // What one decode step launches is decided on the host: the row bound
   // (grid sizes; rows at or past the device row count exit early), the path
   // of each attention sublayer and the key bounds that pick kernel variants.
   struct StepPlan {
     int rows, self_keys, cross_keys;
-    bool blk_self, blk_cross, af, ln_ffn, ln_vocab;
+    bool blk_self, blk_cross, af, ln_ffn;
   };
   auto make_plan = [&](int rows, int self_keys, int cross_keys) {
     StepPlan P;
@@ -674,7 +673,6 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
     P.af = rows <= kAfMaxRows;
     P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
-    P.ln_vocab = rows <= kLnVocabMaxRows && d == 512;
     return P;
   };
 
@@ -911,7 +909,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       }
       MH_TRY(launch_quantize_rows(DH, F, rows, d_nact, F, DHQ, F, DHA, E->err_flag, s));
       MH_TRY(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
-      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld ? P.blk_self : P.ln_vocab));
+      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && P.blk_self));
     }
     {
       Epilogue e;
@@ -929,10 +927,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.wmult = E->emb.mult;
       g.bias = E->emb.bias;
       g.N = (int)E->V;
-      g.pro = pend;  // the last LayerNorm, when the kernel builds its rows itself
-      pend.kind = PRO_NONE;
       hipEvent_t ev[2];
-      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, g.pro.kind == PRO_LN ? 1u : 0u, ev));
+      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
       MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));
     }
     FinalizeArgs f;

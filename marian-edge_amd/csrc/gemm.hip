@@ -227,24 +227,11 @@ constexpr int kVocabCols = 4 * 16 * kVocabCT;     // 128 columns per workgroup
 constexpr int kVocabMaxK = 512;                   // K held in registers
 constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 
-// LNP: the rows (at most kVocabLnRows, K = 512) are the residual LayerNorm of
-// g.pro, built in the prologue while the weight loads are in flight: all
-// threads form z = y + r (thread t: row t / 16, float4 columns t % 16 + 16 j),
-// wave 0 folds the mean and the variance of each row in lane = row layout
-// over an LDS copy (normalize_row, tensor.rs:372-385), all threads normalize,
-// take each row's maximum over its 16 threads and quantize into the LDS rows
-// the matrix core reads.
-constexpr int kVocabLnRows = 16;
-constexpr int kVocabLnLdz = kVocabMaxK + 4;  // padded fp32 LDS row (floats)
-
-template <bool LNP>
 __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
   __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
   __shared__ float sAm[kSkinnyRows];
-  __shared__ __attribute__((aligned(16))) float sZ[LNP ? kVocabLnRows * kVocabLnLdz : 4];
-  __shared__ float sMean[LNP ? kVocabLnRows : 1], sInv[LNP ? kVocabLnRows : 1];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kq = (lane >> 4) * 16;
   const int ksteps = g.K >> 6;
@@ -279,84 +266,15 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   const int cpr = g.K >> 4;
   v4i st[kStage];
   float sa = 0.0f;
-  if constexpr (LNP) {
-    const RowPrologue& p = g.pro;
-    const int lr = tid >> 4, lc = tid & 15;
-    const bool rl = lr < g.M;  // rows below the host bound are allocated
-    f4v z[8], gm[8], bt[8];
+  const int rows_h = min(kSkinnyRows, g.M);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      gm[j] = *(const f4v*)(p.gamma + (lc + 16 * j) * 4);
-      bt[j] = *(const f4v*)(p.beta + (lc + 16 * j) * 4);
-    }
-    if (rl) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t off = (int64_t)lr * kVocabMaxK + (lc + 16 * j) * 4;
-        z[j] = *(const f4v*)(p.y + off) + *(const f4v*)(p.r + off);  // add_slices
-        *(f4v*)(sZ + lr * kVocabLnLdz + (lc + 16 * j) * 4) = z[j];
-      }
-    }
-    __syncthreads();
-    if (wave == 0 && lane < g.M)
-      sMean[lane] = seq_fold_lds<kVocabMaxK / 4>((const float4*)(sZ + lane * kVocabLnLdz), -0.0f) /
-                    (float)kVocabMaxK;
-    __syncthreads();
-    if (rl) {
-      const float m = sMean[lr];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f4v c = z[j] - m;
-        *(f4v*)(sZ + lr * kVocabLnLdz + (lc + 16 * j) * 4) = c * c;
-      }
-    }
-    __syncthreads();
-    if (wave == 0 && lane < g.M) {
-      const float var =
-          seq_fold_lds<kVocabMaxK / 4>((const float4*)(sZ + lane * kVocabLnLdz), -0.0f) / (float)kVocabMaxK;
-      sInv[lane] = 1.0f / sqrtf(var + kLayerNormEpsilon);
-    }
-    __syncthreads();
-    float mx = 0.0f;
-    bool bad = false;
-    const float m = rl ? sMean[lr] : 0.0f, iv = rl ? sInv[lr] : 0.0f;
-    if (rl) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        z[j] = ((z[j] - m) * iv) * gm[j] + bt[j];
-        bad |= !isfinite(z[j].x) || !isfinite(z[j].y) || !isfinite(z[j].z) || !isfinite(z[j].w);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(z[j].x), fabsf(z[j].y)), fmaxf(fabsf(z[j].z), fabsf(z[j].w))));
-      }
-    }
-    // the row's 16 threads are lanes 16k..16k+15 of one wave
-    mx = fmaxf(mx, xor_lane_f<1>(mx));
-    mx = fmaxf(mx, xor_lane_f<2>(mx));
-    mx = fmaxf(mx, xor_lane_f<4>(mx));
-    mx = fmaxf(mx, xor_lane_f<8>(mx));
-    const float a_row = row_multiplier(mx);
-    if (rl) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *(uint32_t*)(sA + lr * kVocabLds + (lc + 16 * j) * 4) =
-            (uint32_t)(quantize_one(z[j].x, a_row) & 0xFF) | ((uint32_t)(quantize_one(z[j].y, a_row) & 0xFF) << 8) |
-            ((uint32_t)(quantize_one(z[j].z, a_row) & 0xFF) << 16) |
-            ((uint32_t)(quantize_one(z[j].w, a_row) & 0xFF) << 24);
-      if (lc == 0) sAm[lr] = a_row;
-    }
-    const int n_dev = g.M_dev ? min(*g.M_dev, g.M) : g.M;
-    if (__any(bad && lr < n_dev) && lane == 0 && p.err) *p.err = 1;
-  } else {
-    const int rows_h = min(kSkinnyRows, g.M);
-#pragma unroll
-    for (int j = 0; j < kStage; ++j) {
-      const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
-      st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
-                                         : zero4();
-    }
-    if (tid < rows_h) sa = g.a[tid];
+  for (int j = 0; j < kStage; ++j) {
+    const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
+    st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
+                                       : zero4();
   }
+  if (tid < rows_h) sa = g.a[tid];
   const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
-  static_assert(!LNP || kVocabLnRows <= kSkinnyRows, "the prologue rows form the first chunk");
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
@@ -370,14 +288,12 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
       }
       sa = tid < rows ? g.a[m0 + tid] : 0.0f;
     }
-    if (!LNP) {
 #pragma unroll
-      for (int j = 0; j < kStage; ++j) {
-        const int c = tid + 256 * j;
-        *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
-      }
-      if (tid < kSkinnyRows) sAm[tid] = sa;
+    for (int j = 0; j < kStage; ++j) {
+      const int c = tid + 256 * j;
+      *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
     }
+    if (tid < kSkinnyRows) sAm[tid] = sa;
     __syncthreads();
     const int mt_n = (rows + 15) >> 4;
     // All live row tiles advance together over K: up to 4 x kVocabCT
@@ -651,12 +567,8 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hi
 hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
-  const RowPrologue& p = g.pro;
-  if (p.kind != PRO_NONE &&
-      (p.kind != PRO_LN || g.K != kVocabMaxK || g.M > kVocabLnRows || !p.y || !p.r || !p.gamma || !p.beta))
-    return hipErrorInvalidValue;
   const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
-  auto kern = p.kind == PRO_LN ? k_vocab_argmax<true> : k_vocab_argmax<false>;
+  auto kern = k_vocab_argmax;
   if (ev_start || ev_stop)
     hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
   else

@@ -51,9 +51,6 @@ struct GemmArgs {
   int64_t ldaf = 0;
   const float* Aamax = nullptr;
   int amax_parts = 0;
-  // Or (vocabulary kernel only) rows built from a residual LayerNorm in the
-  // kernel's prologue: kind PRO_LN, K = 512, at most 16 host rows.
-  RowPrologue pro;
 };
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };

@@ -197,8 +197,7 @@ class HipEngine:
 
     def last_kernel_trace(self) -> dict:
         """Per timed decode launch of the last call (kernel timing on):
-        kind (KERNEL_*), decode step, decoder layer (for KERNEL_VOCAB: 1 when the launch
-        also built the last LayerNorm), device microseconds."""
+        kind (KERNEL_*), decode step, decoder layer, device microseconds."""
         n = C.c_size_t(0)
         self._lib.marian_hip_last_kernel_trace(self._h, None, None, None, None, 0, C.byref(n))
         m = max(n.value, 1)

@@ -139,10 +139,8 @@ def test_timing_modes_keep_outputs_and_trace_launches(pkg, engine):
     assert np.all(np.diff(step_end) > 0)
     vocab = kt["kind"] == engine.KERNEL_VOCAB
     assert sorted(kt["step"][vocab].tolist()) == list(range(steps))
-    assert set(kt["layer"][vocab].tolist()) <= {0, 1}
-    # the LayerNorm prologue variant is chosen by row count, which only falls
-    lv = kt["layer"][vocab][np.argsort(kt["step"][vocab])]
-    assert np.all(np.diff(lv.astype(np.int64)) >= 0)
+    assert np.all(kt["layer"][vocab] == 0)
+    assert set(kt["layer"][~vocab].tolist()) <= {0, 1}  # two decoder layers
     blocks = ~vocab
     assert set(kt["kind"][blocks].tolist()) <= {engine.KERNEL_SELF_BLOCK, engine.KERNEL_CROSS_BLOCK}
     assert np.all(kt["us"] > 0)

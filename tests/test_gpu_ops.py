@@ -115,6 +115,69 @@ def test_residual_layer_norm_matches_oracle(pkg, orc, dev):
         assert np.array_equal(q.host(), q_ref) and np.array_equal(a.host(), a_ref)
 
 
+def _ln_edge_rows(rng, d=512):
+    """Rows whose sequential sums stress the four-chunk speculative folds:
+    prefixes cancelling to near zero at the chunk boundaries (the candidate
+    windows miss and chunks are refolded), exact zeros and negative zeros,
+    constants, wide and tiny magnitudes."""
+    rows = []
+    for _ in range(8):  # cancellation at 128, 256 and 384
+        z = rng.standard_normal(d).astype(np.float32) * np.float32(rng.uniform(0.5, 20))
+        for k in (128, 256, 384):
+            s = np.float32(-0.0)
+            for v in z[:k - 1]:
+                s = np.float32(s + v)
+            z[k - 1] = -s + np.float32(rng.standard_normal() * 1e-5)
+        rows.append(z)
+    rows.append(np.zeros(d, np.float32))
+    rows.append(np.full(d, -0.0, np.float32))
+    rows.append(np.full(d, 0.3, np.float32))
+    rows.append((rng.standard_normal(d) * 1e17).astype(np.float32))
+    rows.append((rng.standard_normal(d) * 1e-39).astype(np.float32))  # subnormal
+    alt = np.where(np.arange(d) % 2 == 0, 1e4, -1e4).astype(np.float32)
+    rows.append(alt + (rng.standard_normal(d) * 1e-3).astype(np.float32))
+    return np.stack(rows)
+
+
+def test_residual_layer_norm_few_rows_edge_cases(pkg, orc, dev):
+    """Few rows of width 512 take the four-wave kernel (speculative folds)."""
+    rng = np.random.default_rng(17)
+    z = _ln_edge_rows(rng)
+    base = rng.standard_normal((48, 512)).astype(np.float32) * 2
+    z = np.concatenate([z, base])
+    y = (z * np.float32(0.75)).astype(np.float32)
+    r = (z - y).astype(np.float32)  # y + r rounds back near z; the oracle sees the same y, r
+    g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(512)).astype(np.float32)
+    ref = orc.residual_layer_norm(y, r, g, b)
+    q_ref, a_ref = orc.quantize_rows(ref)
+    out = dev.DeviceArray.zeros(y.shape, np.float32)
+    q = dev.DeviceArray.zeros(y.shape, np.int8)
+    a = dev.DeviceArray.zeros(y.shape[0], np.float32)
+    dev.residual_layer_norm(dev.DeviceArray.from_host(y), dev.DeviceArray.from_host(r),
+                            dev.DeviceArray.from_host(g), dev.DeviceArray.from_host(b), out, q, a)
+    dev.synchronize()
+    got = out.host()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))  # bit for bit, signed zeros too
+    assert np.array_equal(q.host(), q_ref) and np.array_equal(a.host(), a_ref)
+    # non-finite inputs: the same positions turn NaN / infinite, and the flag is set
+    y2 = y[:4].copy()
+    y2[0, 100] = np.nan
+    y2[1, 300] = np.inf
+    y2[2, 5] = -np.inf
+    ref2 = orc.residual_layer_norm(y2, r[:4], g, b)
+    out2 = dev.DeviceArray.zeros(y2.shape, np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.residual_layer_norm(dev.DeviceArray.from_host(y2), dev.DeviceArray.from_host(r[:4]),
+                            dev.DeviceArray.from_host(g), dev.DeviceArray.from_host(b), out2, err=err)
+    dev.synchronize()
+    got2 = out2.host()
+    assert np.array_equal(np.isnan(got2), np.isnan(ref2))
+    fin = ~np.isnan(ref2)
+    assert np.array_equal(got2[fin], ref2[fin])
+    assert err.host()[0] == 1
+
+
 def _attention_case(pkg, orc, dev, q, k, v, cu, heads, bf16):
     T = q.shape[0]
     lens = np.diff(cu.astype(np.int64))
