@@ -26,7 +26,7 @@ constexpr int kBlkThreads = 64 * (kBlkRowWaves + kBlkLoadWaves);
 constexpr int kBlkD = 512;             // model width handled (8 heads x 64)
 constexpr int kBlkMaxKeys = 128;       // keys staged in LDS
 constexpr int kBlkRow = kHeadDim + 4;  // padded LDS key row (floats)
-static_assert(kBlkRowWaves == 4 && kBlkD == 4 * kSpecChunk, "the LayerNorm folds run as four chunks");
+static_assert(kBlkRowWaves == 4 && kBlkD == kSpecChunks * kSpecChunk, "the LayerNorm folds: four waves, eight chunks");
 
 __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
 
@@ -76,7 +76,7 @@ __device__ __forceinline__ void row_load(const RowPrologue& p, int r, int step, 
 }
 
 // LayerNorm(y + r) built by the four row waves together (each loaded the
-// whole row): the mean and variance folds run as speculative four-chunk folds
+// whole row): the mean and variance folds run as speculative eight-chunk folds
 // (bit-identical to the sequential folds) over LDS copies of z and of the
 // squared deviations.  Every row wave returns the normalized row.
 __device__ __forceinline__ void row_build_ln4(const RowLoads<PRO_LN>& L, float* sZ, float* sT,
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 // ---------------------------------------------------------------------------
 // LayerNorm + up-projection block (the FFN's first layer on steps with few
 // rows): one 512-thread workgroup per (row, 128-column slice).  Waves 0-3
-// build the row's residual LayerNorm (speculative four-chunk folds) and wave
+// build the row's residual LayerNorm (speculative eight-chunk folds) and wave
 // 0 quantizes it, as in the attention block; waves 4-7 meanwhile load the
 // slice's weight rows into registers, then run the projection on MFMA (row 0
 // of a 16-row tile), dequantize, apply ReLU and store.  Replaces the

@@ -166,38 +166,42 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
 
 // ---- speculative exact fold over 512 values ------------------------------------
 // The sequential fold init + p[0] + p[1] + ... + p[511], run by four waves at
-// once with the same result bits.  Wave w folds chunk w (elements [128w,
-// 128w + 128)): wave 0 from init, wave w >= 1 from each of 64 consecutive
-// floats (one per lane) centred on the double-precision sum of elements
-// [0, 128w).  The true start of chunk w is the end of chunk w - 1; when it is
-// among chunk w's candidates (compared bit for bit), that candidate's chain is
-// chunk w's exact end, otherwise chunk w is folded again from the true start.
-// Every step is the sequential fold's own float addition, so the result is
-// the sequential fold's whatever the estimates are: they only decide how often
-// a 128-term refold is needed.  Chunk ends stay within a few units in the last
-// place of the exact prefix for sums of non-negative terms; a prefix near zero
-// after cancellation can fall outside the window (about 3% of boundaries for
+// once with the same result bits.  The row is cut into eight 64-term chunks;
+// wave w folds chunks w and w + 4 as two interleaved chains.  Chunk 0 starts
+// from init; chunk c >= 1 starts from each of 64 consecutive floats (one per
+// lane) centred on an estimate of the prefix sum p[0] + ... + p[64c - 1]
+// (a float tree sum).  Floats are consecutive when their keys are (the key
+// is the bit pattern with the magnitude bits of negative values flipped: a
+// monotone, self-inverse map onto the 32-bit integers, with -0.0 just below
+// +0.0).  The true start of chunk c is the end of chunk c - 1: when its key
+// lies in chunk c's window, that candidate's chain is chunk c's exact end;
+// otherwise chunk c is folded again from the true start.  Every step is the
+// sequential fold's own float addition, so the result is the sequential
+// fold's whatever the estimates are: they only decide how often a 64-term
+// refold is needed.  Chunk ends stay within a few units in the last place of
+// the exact prefix for sums of non-negative terms; a prefix near zero after
+// cancellation can fall outside the window (a few percent of boundaries for
 // centred normal rows).
 //
 // Protocol: each of the four fold waves holds the whole row (lane l: elements
 // 4l..4l+3 in v[0], 256+4l..256+4l+3 in v[1]) and calls spec_fold_chunk,
-// which stores its chunk to p (LDS, 512 floats) and folds it; then every wave
-// of the workgroup passes wg_lds_barrier; then the fold waves call
+// which stores its two chunks to p (LDS, 512 floats) and folds them; then
+// every wave of the workgroup passes wg_lds_barrier; then the fold waves call
 // spec_fold_resolve (each gets the result).  p and L stay unchanged until all
 // four have resolved.
-constexpr int kSpecChunk = 128;
-constexpr int kSpecNB = 4;  // float4 read ahead per batch (bounds the fold waves' registers)
+constexpr int kSpecChunk = 64;
+constexpr int kSpecChunks = 8;
 struct SpecFoldLds {
-  float start[3][64];  // candidate starts of chunks 1..3
-  float end[4][64];    // chain ends of chunks 0..3 (chunk 0: every lane the same)
+  int end[kSpecChunks][64];  // keys of the chain ends (chunk 0: every lane the same)
+  int base[kSpecChunks];     // key of each window's lane 0
 };
 
-__device__ __forceinline__ int float_order(float f) {  // monotone in f; +0 and -0 -> 0
+__device__ __forceinline__ int float_key(float f) {
   const uint32_t b = __float_as_uint(f);
-  return (b >> 31) ? -(int)(b & 0x7fffffffu) : (int)b;
+  return (int)(b ^ ((uint32_t)((int)b >> 31) >> 1));
 }
-__device__ __forceinline__ float order_float(int o) {
-  return __uint_as_float(o >= 0 ? (uint32_t)o : (0x80000000u | (uint32_t)(-o)));
+__device__ __forceinline__ float key_float(int k) {
+  return __uint_as_float((uint32_t)k ^ ((uint32_t)(k >> 31) >> 1));
 }
 
 // All waves of the workgroup: this wave's LDS accesses complete, then the
@@ -209,72 +213,144 @@ __device__ __forceinline__ void wg_lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Sum over the wave in double (any order; every lane returns it): DPP within
+// Two wave sums at once (any order; every lane returns them): DPP within
 // each 16-lane row, then the four row sums read out as scalars.
-template <int CTRL>
-__device__ __forceinline__ double dpp_mov_f64(double v) {
-  const uint64_t b = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = (uint32_t)dpp_mov<CTRL>((int)(uint32_t)b);
-  const uint32_t hi = (uint32_t)dpp_mov<CTRL>((int)(uint32_t)(b >> 32));
-  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  v += dpp_mov_f64<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_mov_f64<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_mov_f64<0x124>(v);  // row_ror:4
-  v += dpp_mov_f64<0x128>(v);  // row_ror:8
-  const uint64_t b = (uint64_t)__double_as_longlong(v);
-  double r[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, 16 * i);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 16 * i);
-    r[i] = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-  }
-  return (r[0] + r[1]) + (r[2] + r[3]);
+__device__ __forceinline__ void wave_sum2(float& a, float& b) {
+  a += __int_as_float(dpp_mov<0xB1>(__float_as_int(a)));   // quad_perm [1,0,3,2]
+  b += __int_as_float(dpp_mov<0xB1>(__float_as_int(b)));
+  a += __int_as_float(dpp_mov<0x4E>(__float_as_int(a)));   // quad_perm [2,3,0,1]
+  b += __int_as_float(dpp_mov<0x4E>(__float_as_int(b)));
+  a += __int_as_float(dpp_mov<0x124>(__float_as_int(a)));  // row_ror:4
+  b += __int_as_float(dpp_mov<0x124>(__float_as_int(b)));
+  a += __int_as_float(dpp_mov<0x128>(__float_as_int(a)));  // row_ror:8
+  b += __int_as_float(dpp_mov<0x128>(__float_as_int(b)));
+  const int ia = __float_as_int(a), ib = __float_as_int(b);
+  a = (__int_as_float(__builtin_amdgcn_readlane(ia, 0)) + __int_as_float(__builtin_amdgcn_readlane(ia, 16))) +
+      (__int_as_float(__builtin_amdgcn_readlane(ia, 32)) + __int_as_float(__builtin_amdgcn_readlane(ia, 48)));
+  b = (__int_as_float(__builtin_amdgcn_readlane(ib, 0)) + __int_as_float(__builtin_amdgcn_readlane(ib, 16))) +
+      (__int_as_float(__builtin_amdgcn_readlane(ib, 32)) + __int_as_float(__builtin_amdgcn_readlane(ib, 48)));
 }
 
-__device__ __forceinline__ double sum4_f64(const f4v& x) {
-  return ((double)x.x + (double)x.y) + ((double)x.z + (double)x.w);
+// Two independent sequential folds of 16 float4 each (LDS, broadcast reads),
+// interleaved; batches of 4 float4 per chain read one batch ahead.
+__device__ __forceinline__ void seq_fold2_lds16(const float4* p, const float4* q, float& s, float& t) {
+  float4 A[4], B[4], C[4], D[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    A[b] = p[b];
+    C[b] = q[b];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k += 2) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      B[b] = p[(k + 1) * 4 + b];
+      D[b] = q[(k + 1) * 4 + b];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      s = s + A[b].x;
+      t = t + C[b].x;
+      s = s + A[b].y;
+      t = t + C[b].y;
+      s = s + A[b].z;
+      t = t + C[b].z;
+      s = s + A[b].w;
+      t = t + C[b].w;
+    }
+    if (k + 2 < 4) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        A[b] = p[(k + 2) * 4 + b];
+        C[b] = q[(k + 2) * 4 + b];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      s = s + B[b].x;
+      t = t + D[b].x;
+      s = s + B[b].y;
+      t = t + D[b].y;
+      s = s + B[b].z;
+      t = t + D[b].z;
+      s = s + B[b].w;
+      t = t + D[b].w;
+    }
+  }
 }
 
 __device__ __forceinline__ void spec_fold_chunk(const f4v (&v)[2], float* p, float init,
                                                 SpecFoldLds& L, int w, int lane) {
-  // Chunk w is float4 w >> 1 of lanes 32 * (w & 1) .. + 31.
-  if ((lane >> 5) == (w & 1)) *(f4v*)(p + 4 * lane + 256 * (w >> 1)) = v[w >> 1];
-  float c = init;
-  if (w > 0) {
-    // Elements [0, 128w): the first float4 of lanes < 32w, and for w = 3 the
-    // second float4 of lanes < 32.
-    double e = lane < 32 * w ? sum4_f64(v[0]) : 0.0;
-    if (w == 3 && lane < 32) e += sum4_f64(v[1]);
-    e = wave_sum_f64(e);
-    c = order_float(float_order((float)e) + lane - 32);
-    L.start[w - 1][lane] = c;
+  // Chunks w and w + 4 are float4 0 and 1 of lanes 16w .. 16w + 15.
+  if ((lane >> 4) == w) {
+    *(f4v*)(p + 4 * lane) = v[0];
+    *(f4v*)(p + 256 + 4 * lane) = v[1];
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's chunk is in LDS
+  // Prefix of chunk w: the first float4 of lanes < 16w; of chunk w + 4: every
+  // first float4 and the second float4 of lanes < 16w.
+  const float f0 = (v[0].x + v[0].y) + (v[0].z + v[0].w);
+  const float f1 = (v[1].x + v[1].y) + (v[1].z + v[1].w);
+  float ea = lane < 16 * w ? f0 : 0.0f;
+  float eb = f0 + (lane < 16 * w ? f1 : 0.0f);
+  wave_sum2(ea, eb);
+  // Window bases (key of lane 0), kept where base + 63 cannot overflow.
+  const int ba = (int)min(max((long long)float_key(ea) - 32, (long long)INT32_MIN), (long long)INT32_MAX - 63);
+  const int bb = (int)min(max((long long)float_key(eb) - 32, (long long)INT32_MIN), (long long)INT32_MAX - 63);
+  const float ca = w == 0 ? init : key_float(ba + lane);
+  const float cb = key_float(bb + lane);
+  if (lane == 0) {
+    L.base[w] = ba;
+    L.base[w + 4] = bb;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's chunks are in LDS
   __builtin_amdgcn_wave_barrier();
-  L.end[w][lane] = seq_fold_lds<kSpecChunk / 4, kSpecNB>((const float4*)(p + kSpecChunk * w), c);
+  float sa = ca, sb = cb;
+  seq_fold2_lds16((const float4*)(p + kSpecChunk * w), (const float4*)(p + 256 + kSpecChunk * w), sa, sb);
+  L.end[w][lane] = float_key(sa);
+  L.end[w + 4][lane] = float_key(sb);
 }
 
 __device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFoldLds& L, int lane) {
-  float st[3], en[3];
+  int en[kSpecChunks - 1], bs[kSpecChunks - 1];
 #pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    st[k] = L.start[k][lane];
-    en[k] = L.end[k + 1][lane];
+  for (int k = 1; k < kSpecChunks; ++k) {
+    en[k - 1] = L.end[k][lane];
+    bs[k - 1] = L.base[k];
   }
-  float s = L.end[0][0];
+  const int e0 = L.end[0][0];
+  // All of them requested here, one LDS round trip in all (left to itself the
+  // compiler sinks each read into the step that uses it).
+  asm volatile("" ::: "memory");
+  // The running key and the window bases are the same in every lane: the
+  // lookups run on the scalar unit, without branches while they hit; `miss`
+  // marks the chunks whose start was outside the window.  With the base at
+  // most INT32_MAX - 63, d < 64 exactly when the key is in the window.
+  int ks = __builtin_amdgcn_readfirstlane(e0);
+  uint32_t miss = 0;
 #pragma unroll
-  for (int k = 1; k < 4; ++k) {
-    const uint64_t hit = __ballot(__float_as_uint(st[k - 1]) == __float_as_uint(s));
-    if (hit)
-      s = __int_as_float(
-          __builtin_amdgcn_readlane(__float_as_int(en[k - 1]), (int)__ffsll((unsigned long long)hit) - 1));
-    else
-      s = seq_fold_lds<kSpecChunk / 4, kSpecNB>((const float4*)(p + kSpecChunk * k), s);
+  for (int k = 1; k < kSpecChunks; ++k) {
+    const uint32_t d = (uint32_t)ks - (uint32_t)__builtin_amdgcn_readfirstlane(bs[k - 1]);
+    const int t = __builtin_amdgcn_readlane(en[k - 1], (int)(d & 63u));
+    miss |= d < 64u ? 0u : 1u << k;
+    ks = miss ? ks : t;
   }
-  return s;
+  if (miss) {  // from the first miss on: fold again where a start is outside the window
+    const int km = __builtin_ctz(miss);
+    float s = key_float(ks);  // the true start of chunk km
+#pragma unroll 1
+    for (int k = km; k < kSpecChunks; ++k) {
+      const uint32_t d = (uint32_t)float_key(s) - (uint32_t)__builtin_amdgcn_readfirstlane(L.base[k]);
+      if (k > km && d < 64u)
+        s = key_float(__builtin_amdgcn_readfirstlane(L.end[k][d]));
+      else
+        s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(
+            seq_fold_lds<kSpecChunk / 4, 4>((const float4*)(p + kSpecChunk * k), s))));
+    }
+    return s;
+  }
+  return key_float(ks);
 }
 
 // The same fold over the first nb batches of NB float4 (nb >= 1, a value

@@ -139,11 +139,11 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
 }
 
 // The same LayerNorm for a few decode rows of width 512: one 256-thread
-// workgroup per row, the mean and variance folds as speculative four-chunk
-// folds (bit-identical to the sequential folds, a quarter of the dependent
+// workgroup per row, the mean and variance folds as speculative eight-chunk
+// folds (bit-identical to the sequential folds, an eighth of the dependent
 // chain); wave 0 then normalizes, stores and quantizes the row.  Lane l holds
 // elements 4l..4l+3 and 256+4l..256+4l+3.
-constexpr int kLnSpecD = 4 * kSpecChunk;  // 512
+constexpr int kLnSpecD = kSpecChunks * kSpecChunk;  // 512
 constexpr int kLnSpecMaxRows = 256;      // rows per launch taking the four-wave path
 __global__ __launch_bounds__(256) void k_residual_ln_spec(const float* y, const float* r,
                                                           const float* gamma, const float* beta,
