@@ -141,13 +141,27 @@ def pmc_summary(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_
         return copy_kib / statistics.median(vals) if vals else float("nan")
 
     ff, fw = copy_factor(cf), copy_factor(cw)
-    res = {"copy_fetch_factor": ff, "copy_write_factor": fw, "kernels": {}}
+    res = {
+        "workload": "64-sentence ragged greedy batch (bench.py --steps 2 --warmup 1 --no-cpu-baseline: "
+                    "5 translations)",
+        "counters": "FETCH_SIZE and WRITE_SIZE (KiB per dispatch), one rocprofv3 --pmc run each",
+        "calibration": {
+            "copy_mib": copy_mb,
+            "fetch_factor": round(ff, 4),
+            "write_factor": round(fw, 4),
+            "note": f"the runtime's copy kernel moving {copy_mb} MiB reads FETCH_SIZE = "
+                    f"{copy_mb / ff:.0f} MiB and WRITE_SIZE = {copy_mb / fw:.0f} MiB; kernel counts are "
+                    f"scaled by {copy_mb} MiB / those readings",
+        },
+        "kernels": {},
+    }
     for k in sorted(set(fetch) | set(write)):
         if not k.startswith("k_"):
             continue
         fk = statistics.mean(fetch.get(k, [0.0])) * ff * 1024.0
         wk = statistics.mean(write.get(k, [0.0])) * fw * 1024.0
-        res["kernels"][k] = {"fetch_bytes": fk, "write_bytes": wk, "dispatches": len(fetch.get(k, []))}
+        res["kernels"][k] = {"fetch_bytes_per_dispatch": round(fk), "write_bytes_per_dispatch": round(wk),
+                             "dispatches": len(fetch.get(k, []))}
     return res
 
 
