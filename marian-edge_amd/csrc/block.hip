@@ -210,6 +210,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     const uint64_t tab_v = kBlkExp2Tab[lane & 31];
     RowLoads<PK> in;
     row_load<PK>(b.pro, r, step, lane, in);
+    wg_lds_barrier();  // the row's loads are issued: the loader waves may start theirs
     if (r >= n) return;
     f4v o[2];
     if constexpr (PK == PRO_LN) {
@@ -231,16 +232,19 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   } else {
     // ---- waves 4-7: weights, then the keys and values into LDS -----------------
     const int lw = wave - kBlkRowWaves;  // loader wave
+    // The row's loads are on the critical path (its LayerNorm folds wait for
+    // them): they go to the memory pipeline first, the weights and keys after.
+    wg_lds_barrier();
     const int kq = (lane >> 4) * 16;
     v4i bf[TPW][kBlkD / 64];
     float wm[TPW], bi[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int tile = min(lw + kBlkLoadWaves * i, NT - 1);  // 16 columns of Q, K or V
-      const int n_w = (tile / 4) * kBlkD + h * kHeadDim + (tile % 4) * 16 + (lane & 15);
-      const int8_t* wr = b.W + (int64_t)n_w * kBlkD + kq;
+      const int c0 = (tile / 4) * kBlkD + h * kHeadDim + (tile % 4) * 16;
+      const int n_w = c0 + (lane & 15);
 #pragma unroll
-      for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = *(const v4i*)(wr + s * 64);
+      for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = frag_load(b.W, c0 / 16, kBlkD / 64, s, lane);
       wm[i] = b.wmult[n_w];
       bi[i] = b.bias[n_w];
     }
@@ -461,6 +465,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   if (wave < kBlkRowWaves) {
     RowLoads<PRO_LN> in;
     row_load<PRO_LN>(a.pro, r, 0, lane, in);
+    wg_lds_barrier();  // the row's loads are issued: the loader waves may start theirs
     if (r >= n) return;
     f4v o[2];
     row_build_ln4(in, sZ, sT, sFm, sFv, wave, lane, o);
@@ -477,6 +482,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     return;
   }
   const int lw = wave - kBlkRowWaves;  // loader wave
+  wg_lds_barrier();  // after the row's loads (its LayerNorm is the critical path)
   const int kq = (lane >> 4) * 16;
   v4i bf[kLgTpw][kBlkD / 64];
   float wm[kLgTpw], bi[kLgTpw];
@@ -484,9 +490,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   for (int i = 0; i < kLgTpw; ++i) {
     const int tile = min(lw + kBlkLoadWaves * i, kLgTiles - 1);
     const int col = slice * kLgCols + tile * 16 + (lane & 15);
-    const int8_t* wr = a.W + (int64_t)col * kBlkD + kq;
 #pragma unroll
-    for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = *(const v4i*)(wr + s * 64);
+    for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = frag_load(a.W, slice * kLgTiles + tile, kBlkD / 64, s, lane);
     wm[i] = a.wmult[col];
     bi[i] = a.bias[col];
   }

@@ -412,6 +412,16 @@ __device__ __forceinline__ float dequant(int32_t acc, float a, float w, float b)
   return (float)acc * inv + b;
 }
 
+// Weights in MFMA fragment order: for the 16-column tile t and the 64-wide
+// k-step s of an int8 matrix W[N, K] (K-contiguous), lane l's B fragment
+// W[16t + l % 16][64s + 16(l / 16) .. +16] is stored at byte
+// ((t * K/64 + s) * 64 + l) * 16, so a wave's fragment load reads 1 KB
+// contiguously (row-major fragments touch 16 rows x 64 bytes; measured 2-3x
+// slower to issue).  Tiles past N hold zeros.
+__device__ __forceinline__ v4i frag_load(const int8_t* Wf, int tile, int ksteps, int s, int lane) {
+  return *(const v4i*)(Wf + (((int64_t)tile * ksteps + s) * 64 + lane) * 16);
+}
+
 // Orderable 64-bit key: larger logit wins, equal logits prefer the lower id
 // (the reference's strict '>' scan in ascending id order).  0 = no candidate.
 // The scan starts from -inf at the first candidate and never takes a NaN, so

@@ -27,7 +27,8 @@ using namespace mh;
 namespace {
 
 struct Lin {
-  const int8_t* w = nullptr;
+  const int8_t* w = nullptr;   // [N, K], K-contiguous
+  const int8_t* wf = nullptr;  // the same in MFMA fragment order (decode kernels)
   const float* mult = nullptr;
   const float* bias = nullptr;
   int N = 0, K = 0;
@@ -205,11 +206,27 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     std::memcpy(host.data() + off, src, bytes);
     fixes.push_back({off, dst});
   };
-  auto add_lin = [&](const marian_hip_linear& l, int N, int K, Lin& out) -> bool {
+  // The decode kernels read their weights in MFMA fragment order: each
+  // 16-column tile and 64-wide k-step is one contiguous 1 KB block, lane l's
+  // 16 bytes W[16t + l % 16][64s + 16(l / 16) ..] at ((t * K/64 + s) * 64 + l) * 16.
+  auto add_frag = [&](const int8_t* w, int N, int K, const int8_t** dst) {
+    const int tiles = (N + 15) / 16, ks = K / 64;
+    std::vector<int8_t> f((size_t)tiles * ks * 1024, 0);
+    for (int t = 0; t < tiles; ++t)
+      for (int st = 0; st < ks; ++st)
+        for (int l = 0; l < 64; ++l) {
+          const int n = 16 * t + (l & 15);
+          if (n < N)
+            std::memcpy(&f[(((size_t)t * ks + st) * 64 + l) * 16], w + (size_t)n * K + 64 * st + 16 * (l >> 4), 16);
+        }
+    add(f.data(), f.size(), (const void**)dst);
+  };
+  auto add_lin = [&](const marian_hip_linear& l, int N, int K, Lin& out, bool frag = false) -> bool {
     if (!l.weight || !l.mult || !l.bias) return false;
     out.N = N;
     out.K = K;
     add(l.weight, (size_t)N * K, (const void**)&out.w);
+    if (frag) add_frag(l.weight, N, K, &out.wf);
     add(l.mult, (size_t)N * 4, (const void**)&out.mult);
     add(l.bias, (size_t)N * 4, (const void**)&out.bias);
     return true;
@@ -224,6 +241,7 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
   E->emb.N = V;
   E->emb.K = d;
   add(m->embedding, (size_t)V * d, (const void**)&E->emb.w);
+  add_frag(m->embedding, V, d, &E->emb.wf);
   add(m->embedding_mult, (size_t)V * 4, (const void**)&E->emb.mult);
   add(m->output_bias, (size_t)V * 4, (const void**)&E->emb.bias);
   E->enc.resize(E->Le);
@@ -239,10 +257,10 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
   for (uint32_t l = 0; l < E->Ld; ++l) {
     const marian_hip_decoder_layer& s = m->decoder[l];
     DecLayer& t = E->dec[l];
-    ok = ok && add_lin(s.self_qkv, 3 * d, d, t.self_qkv) &&
-         add_lin(s.self_out, d, d, t.self_out) && add_lin(s.cross_q, d, d, t.cross_q) &&
-         add_lin(s.cross_kv, 2 * d, d, t.cross_kv) && add_lin(s.cross_out, d, d, t.cross_out) &&
-         add_lin(s.ffn1, F, d, t.ffn1) && add_lin(s.ffn2, d, F, t.ffn2) &&
+    ok = ok && add_lin(s.self_qkv, 3 * d, d, t.self_qkv, true) &&
+         add_lin(s.self_out, d, d, t.self_out, true) && add_lin(s.cross_q, d, d, t.cross_q, true) &&
+         add_lin(s.cross_kv, 2 * d, d, t.cross_kv) && add_lin(s.cross_out, d, d, t.cross_out, true) &&
+         add_lin(s.ffn1, F, d, t.ffn1, true) && add_lin(s.ffn2, d, F, t.ffn2, true) &&
          add_vec(s.ln1_scale, d, &t.ln1_s) && add_vec(s.ln1_bias, d, &t.ln1_b) &&
          add_vec(s.ln2_scale, d, &t.ln2_s) && add_vec(s.ln2_bias, d, &t.ln2_b) &&
          add_vec(s.ln3_scale, d, &t.ln3_s) && add_vec(s.ln3_bias, d, &t.ln3_b);
@@ -702,6 +720,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.M_dev = d_nact;
       g.K = L.K;
       g.W = L.w;
+      g.Wf = L.wf;
       g.wmult = L.mult;
       g.bias = L.bias;
       g.N = L.N;
@@ -725,6 +744,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.M_dev = d_nact;
       g.K = L.K;
       g.W = L.w;
+      g.Wf = L.wf;
       g.wmult = L.mult;
       g.bias = L.bias;
       g.N = L.N;
@@ -772,7 +792,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ba.rows = rows;
       ba.rows_dev = d_nact;
       ba.heads = (int)H;
-      ba.W = L.w;
+      ba.W = L.wf;
       ba.wmult = L.mult;
       ba.bias = L.bias;
       ba.k = k;
@@ -894,7 +914,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         pend.kind = PRO_NONE;
         lg.rows = rows;
         lg.rows_dev = d_nact;
-        lg.W = L.ffn1.w;
+        lg.W = L.ffn1.wf;
         lg.wmult = L.ffn1.mult;
         lg.bias = L.ffn1.bias;
         lg.K = L.ffn1.K;
@@ -924,6 +944,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.M_dev = d_nact;
       g.K = d;
       g.W = E->emb.w;
+      g.Wf = E->emb.wf;
       g.wmult = E->emb.mult;
       g.bias = E->emb.bias;
       g.N = (int)E->V;

@@ -81,11 +81,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int n = min(n0 + ct * 16 + (lane & 15), g.N - 1);
+    const int tile = min((n0 >> 4) + ct, ((g.N + 15) >> 4) - 1);
     const int8_t* wr = g.W + (int64_t)n * g.K + kq;
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
       const int s = wave + NW * i;
-      bf[i][ct] = s < ksteps ? *(const v4i*)(wr + s * 64) : zero4();
+      bf[i][ct] = s >= ksteps ? zero4() : g.Wf ? frag_load(g.Wf, tile, ksteps, s, lane) : *(const v4i*)(wr + s * 64);
     }
   }
   // First chunk's activation fragments.
@@ -243,10 +244,11 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
 #pragma unroll
   for (int ct = 0; ct < kVocabCT; ++ct) {
     ncol[ct] = nbase + ct * 16 + (lane & 15);
+    const int tile = min((nbase >> 4) + ct, ((g.N + 15) >> 4) - 1);
     const int8_t* wr = g.W + (int64_t)min(ncol[ct], g.N - 1) * g.K + kq;
 #pragma unroll
     for (int s = 0; s < kVocabMaxK / 64; ++s)
-      bf[ct][s] = s < ksteps ? *(const v4i*)(wr + s * 64) : zero4();
+      bf[ct][s] = s >= ksteps ? zero4() : g.Wf ? frag_load(g.Wf, tile, ksteps, s, lane) : *(const v4i*)(wr + s * 64);
   }
   // Epilogue operands of this lane's columns.
   float wm[kVocabCT], bi[kVocabCT];

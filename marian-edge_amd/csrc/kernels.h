@@ -39,7 +39,8 @@ struct GemmArgs {
   int M = 0;                  // row count (host) ...
   const int* M_dev = nullptr; // ... or read on the device (decode active rows)
   int K = 0;                  // multiple of 64
-  const int8_t* W = nullptr;
+  const int8_t* W = nullptr;  // [N, K], K-contiguous
+  const int8_t* Wf = nullptr; // optional, skinny and vocabulary kernels: W in fragment order
   const float* wmult = nullptr;
   const float* bias = nullptr;
   int N = 0;
@@ -174,7 +175,7 @@ struct BlockArgs {
   int rows = 0;
   const int* rows_dev = nullptr;
   int heads = 0;
-  const int8_t* W = nullptr;  // [3d or d, d]
+  const int8_t* W = nullptr;  // [3d or d, d] in fragment order (frag_load)
   const float* wmult = nullptr;
   const float* bias = nullptr;
   const float* k = nullptr;  // key rows (ATT_SELF: the cache), stride ldkv
@@ -202,7 +203,7 @@ struct LnGemmArgs {
   RowPrologue pro;
   int rows = 0;
   const int* rows_dev = nullptr;
-  const int8_t* W = nullptr;  // [N, K]
+  const int8_t* W = nullptr;  // [N, K] in fragment order (frag_load)
   const float* wmult = nullptr;
   const float* bias = nullptr;
   int K = 0, N = 0;
