@@ -210,7 +210,6 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     const uint64_t tab_v = kBlkExp2Tab[lane & 31];
     RowLoads<PK> in;
     row_load<PK>(b.pro, r, step, lane, in);
-    wg_lds_barrier();  // the row's loads are issued: the loader waves may start theirs
     if (r >= n) return;
     f4v o[2];
     if constexpr (PK == PRO_LN) {
@@ -232,9 +231,6 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   } else {
     // ---- waves 4-7: weights, then the keys and values into LDS -----------------
     const int lw = wave - kBlkRowWaves;  // loader wave
-    // The row's loads are on the critical path (its LayerNorm folds wait for
-    // them): they go to the memory pipeline first, the weights and keys after.
-    wg_lds_barrier();
     const int kq = (lane >> 4) * 16;
     v4i bf[TPW][kBlkD / 64];
     float wm[TPW], bi[TPW];
@@ -465,7 +461,6 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   if (wave < kBlkRowWaves) {
     RowLoads<PRO_LN> in;
     row_load<PRO_LN>(a.pro, r, 0, lane, in);
-    wg_lds_barrier();  // the row's loads are issued: the loader waves may start theirs
     if (r >= n) return;
     f4v o[2];
     row_build_ln4(in, sZ, sT, sFm, sFv, wave, lane, o);
@@ -482,7 +477,6 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     return;
   }
   const int lw = wave - kBlkRowWaves;  // loader wave
-  wg_lds_barrier();  // after the row's loads (its LayerNorm is the critical path)
   const int kq = (lane >> 4) * 16;
   v4i bf[kLgTpw][kBlkD / 64];
   float wm[kLgTpw], bi[kLgTpw];
