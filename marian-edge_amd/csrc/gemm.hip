@@ -44,22 +44,30 @@ __device__ __forceinline__ float af_row_mult(const GemmArgs& g, int m) {
 
 // 16 consecutive fp32 values quantized with multiplier a, packed as the
 // 16 int8 bytes of an MFMA operand fragment (byte j = element j).
-__device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
+__device__ __forceinline__ v4i quantize_frag16(const float4 (&f)[4], float a) {
   v4i r;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float4 f = *(const float4*)(x + 4 * w);
-    r[w] = (quantize_one(f.x, a) & 0xFF) | ((quantize_one(f.y, a) & 0xFF) << 8) |
-           ((quantize_one(f.z, a) & 0xFF) << 16) | ((quantize_one(f.w, a) & 0xFF) << 24);
-  }
+  for (int w = 0; w < 4; ++w)
+    r[w] = (quantize_one(f[w].x, a) & 0xFF) | ((quantize_one(f[w].y, a) & 0xFF) << 8) |
+           ((quantize_one(f[w].z, a) & 0xFF) << 16) | ((quantize_one(f[w].w, a) & 0xFF) << 24);
   return r;
 }
+__device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
+  float4 f[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) f[w] = *(const float4*)(x + 4 * w);
+  return quantize_frag16(f, a);
+}
+constexpr int kAfMaxRows = 16;  // fp32 A source: one MFMA row tile
 
 // A sources of the skinny kernel: int8 rows with their multipliers, or fp32
 // rows quantized while loading.
 enum ASrc { A_I8 = 0, A_F32 = 1 };
 
-template <int MODE, int CT, int NW, int KSW, int ASRC>
+// FULL: K is exactly NW x KSW k-steps (every shape the engine uses), so no
+// k-step needs a guard and every prologue load is unconditional (guarded
+// loads become branches that the compiler waits on one by one).
+template <int MODE, int CT, int NW, int KSW, int ASRC, bool FULL>
 __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
   constexpr bool AF = ASRC == A_F32;
   constexpr int NT = NW * 64;
@@ -80,34 +88,52 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   v4i bf[KSW][CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
+    // Fragment order: the tile's next k-step is 1 KB further; row-major: 64
+    // bytes along the lane's weight row.
     const int n = min(n0 + ct * 16 + (lane & 15), g.N - 1);
     const int tile = min((n0 >> 4) + ct, ((g.N + 15) >> 4) - 1);
-    const int8_t* wr = g.W + (int64_t)n * g.K + kq;
+    const int8_t* wb = g.Wf ? g.Wf + ((int64_t)tile * ksteps * 64 + lane) * 16 : g.W + (int64_t)n * g.K + kq;
+    const int wstep = g.Wf ? 1024 : 64;
+    // Loads from clamped (in-bounds) k-steps, zeroed afterwards: no branch
+    // around a load, so every load of the prologue is in flight at once.
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
       const int s = wave + NW * i;
-      bf[i][ct] = s >= ksteps ? zero4() : g.Wf ? frag_load(g.Wf, tile, ksteps, s, lane) : *(const v4i*)(wr + s * 64);
+      const v4i v = *(const v4i*)(wb + (int64_t)min(s, ksteps - 1) * wstep);
+      bf[i][ct] = FULL || s < ksteps ? v : zero4();
     }
   }
   // First chunk's activation fragments.
   v4i af[KSW][4];
+  if constexpr (AF) {
+    // At most 16 rows (one MFMA row tile): every k-step's fp32 values and the
+    // row's maxima are requested together, then quantized.
+    const int m = min(lane & 15, Mh - 1);
+    const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
+    float4 raw[KSW][4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int m = min(mt * 16 + (lane & 15), Mh - 1);
-    if constexpr (AF) {
-      const float a_m = af_row_mult(g, m);
-      const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
+    for (int i = 0; i < KSW; ++i) {
+      const int s = min(wave + NW * i, ksteps - 1);  // past K: loaded, then unused
 #pragma unroll
-      for (int i = 0; i < KSW; ++i) {
-        const int s = wave + NW * i;
-        af[i][mt] = (s < ksteps && mt * 16 < Mh) ? quantize_frag16(ar + s * 64, a_m) : zero4();
-      }
-    } else {
+      for (int w = 0; w < 4; ++w) raw[i][w] = *(const float4*)(ar + s * 64 + 4 * w);
+    }
+    const float a_m = af_row_mult(g, m);
+#pragma unroll
+    for (int i = 0; i < KSW; ++i) {
+      af[i][0] = FULL || wave + NW * i < ksteps ? quantize_frag16(raw[i], a_m) : zero4();
+#pragma unroll
+      for (int mt = 1; mt < 4; ++mt) af[i][mt] = zero4();
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int m = min(mt * 16 + (lane & 15), Mh - 1);
       const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
 #pragma unroll
       for (int i = 0; i < KSW; ++i) {
         const int s = wave + NW * i;
-        af[i][mt] = (s < ksteps && mt * 16 < Mh) ? *(const v4i*)(ar + s * 64) : zero4();
+        const v4i v = *(const v4i*)(ar + min(s, ksteps - 1) * 64);
+        af[i][mt] = ((FULL || s < ksteps) && mt * 16 < Mh) ? v : zero4();
       }
     }
   }
@@ -164,7 +190,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       for (int ct = 0; ct < CT; ++ct) acc[mt][ct] = zero4();
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
-      if (wave + NW * i < ksteps) {
+      if (FULL || wave + NW * i < ksteps) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
           if (mt < mt_n)
@@ -228,6 +254,7 @@ constexpr int kVocabCols = 4 * 16 * kVocabCT;     // 128 columns per workgroup
 constexpr int kVocabMaxK = 512;                   // K held in registers
 constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 
+template <bool FULL>  // K = 512: every k-step live, unconditional weight loads
 __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
@@ -245,10 +272,14 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   for (int ct = 0; ct < kVocabCT; ++ct) {
     ncol[ct] = nbase + ct * 16 + (lane & 15);
     const int tile = min((nbase >> 4) + ct, ((g.N + 15) >> 4) - 1);
-    const int8_t* wr = g.W + (int64_t)min(ncol[ct], g.N - 1) * g.K + kq;
+    const int8_t* wb = g.Wf ? g.Wf + ((int64_t)tile * ksteps * 64 + lane) * 16
+                            : g.W + (int64_t)min(ncol[ct], g.N - 1) * g.K + kq;
+    const int wstep = g.Wf ? 1024 : 64;  // fragment order: 1 KB per k-step
 #pragma unroll
-    for (int s = 0; s < kVocabMaxK / 64; ++s)
-      bf[ct][s] = s >= ksteps ? zero4() : g.Wf ? frag_load(g.Wf, tile, ksteps, s, lane) : *(const v4i*)(wr + s * 64);
+    for (int s = 0; s < kVocabMaxK / 64; ++s) {
+      const v4i v = *(const v4i*)(wb + (int64_t)min(s, ksteps - 1) * wstep);
+      bf[ct][s] = FULL || s < ksteps ? v : zero4();
+    }
   }
   // Epilogue operands of this lane's columns.
   float wm[kVocabCT], bi[kVocabCT];
@@ -307,7 +338,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
       for (int ct = 0; ct < kVocabCT; ++ct) acc[mt][ct] = zero4();
 #pragma unroll
     for (int s = 0; s < kVocabMaxK / 64; ++s) {
-      if (s < ksteps) {
+      if (FULL || s < ksteps) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
           if (mt < mt_n) {
@@ -528,15 +559,20 @@ int skinny_cols(int N) { return N >= 8192 ? 64 : (N >= 1024 ? 32 : 16); }
 int skinny_groups(int N) { return (N + skinny_cols(N) - 1) / skinny_cols(N); }
 int argmax_groups(int N, int /*K*/) { return (N + kVocabCols - 1) / kVocabCols; }
 
-template <int MODE, int NW, int KSW, int ASRC>
-static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
+template <int MODE, int NW, int KSW, int ASRC, bool FULL>
+static hipError_t launch_skinny_kf(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const dim3 grid(skinny_groups(g.N)), block(NW * 64);
   switch (skinny_cols(g.N)) {
-    case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW, ASRC>), grid, block, 0, s, g, e); break;
-    case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW, ASRC>), grid, block, 0, s, g, e); break;
-    default: hipLaunchKernelGGL((k_gemm_skinny<MODE, 1, NW, KSW, ASRC>), grid, block, 0, s, g, e); break;
+    case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
+    case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
+    default: hipLaunchKernelGGL((k_gemm_skinny<MODE, 1, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
   }
   return hipGetLastError();
+}
+template <int MODE, int NW, int KSW, int ASRC>
+static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
+  return (g.K >> 6) == NW * KSW ? launch_skinny_kf<MODE, NW, KSW, ASRC, true>(g, e, s)
+                                : launch_skinny_kf<MODE, NW, KSW, ASRC, false>(g, e, s);
 }
 
 // Waves and per-wave k-steps by K: long K (the FFN down-projection) spreads
@@ -546,7 +582,8 @@ template <int MODE>
 static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const int ksteps = g.K >> 6;
   if (g.Af) {
-    if (ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4) return hipErrorInvalidValue;
+    if (ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4 || g.M > kAfMaxRows)
+      return hipErrorInvalidValue;
     return launch_skinny_k<MODE, 4, 2, A_F32>(g, e, s);
   }
   if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1, A_I8>(g, e, s);
@@ -570,7 +607,7 @@ hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
   const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
-  auto kern = k_vocab_argmax;
+  auto kern = g.K == kVocabMaxK ? k_vocab_argmax<true> : k_vocab_argmax<false>;
   if (ev_start || ev_stop)
     hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
   else
