@@ -671,7 +671,6 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     for (size_t b = 0; b < B; ++b) ends[limit[b]]++;
     for (uint32_t t = 1; t <= gen_limit; ++t) remaining[t] = remaining[t - 1] - ends[t];
   }
-  constexpr int kAfMaxRows = 16;
   constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
   constexpr int kLnFfnMaxRows = 32;  // ... and the LayerNorm + FFN up-projection block
 
@@ -680,7 +679,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   // of each attention sublayer and the key bounds that pick kernel variants.
   struct StepPlan {
     int rows, self_keys, cross_keys;
-    bool blk_self, blk_cross, af, ln_ffn;
+    bool blk_self, blk_cross, ln_ffn;
   };
   auto make_plan = [&](int rows, int self_keys, int cross_keys) {
     StepPlan P;
@@ -689,7 +688,6 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     P.cross_keys = cross_keys;
     P.blk_self = rows <= kBlkMaxRows && attn_block_supported(d, H, self_keys);
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
-    P.af = rows <= kAfMaxRows;
     P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
     return P;
   };
@@ -726,15 +724,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.N = L.N;
       return launch_gemm_skinny(g, mode, e, s);
     };
-    // Attention-output projection.  Up to kAfMaxRows rows, A is the fp32
-    // attention output, quantized while loading with the per-head maxima the
-    // attention kernel wrote; above that every workgroup would repeat the
-    // quantization of many rows, so a row-quantization pass runs first.
+    // Attention-output projection.  A is the fp32 attention output, quantized
+    // while loading with the per-head maxima the attention kernel wrote; each
+    // workgroup quantizes only its own 16 rows, so no row-quantization pass
+    // runs in between.
     auto agemm = [&](const Lin& L, const Epilogue& e) -> hipError_t {
-      if (!P.af) {
-        MH_TRY(launch_quantize_rows(DATT, d, rows, d_nact, d, DHQ, d, DHA, E->err_flag, s));
-        return dgemm(DHQ, DHA, L, EPI_STORE, e);
-      }
       GemmArgs g;
       g.Af = DATT;
       g.ldaf = d;
@@ -873,7 +867,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         sa.max_keys = P.self_keys;
         sa.out = DATT;
         sa.ldo = d;
-        sa.amax = P.af ? DAMAX : nullptr;
+        sa.amax = DAMAX;
         sa.err = E->err_flag;
         MH_TRY(launch_attention(sa, s));
       }
@@ -901,7 +895,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         ca.max_keys = P.cross_keys;
         ca.out = DATT;
         ca.ldo = d;
-        ca.amax = P.af ? DAMAX : nullptr;
+        ca.amax = DAMAX;
         ca.err = E->err_flag;
         MH_TRY(launch_attention(ca, s));
       }

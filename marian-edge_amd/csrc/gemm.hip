@@ -35,8 +35,8 @@ __device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
 // maxima (amax_parts = 8 per row, read as two 16-byte vectors so the loads
 // issue together).
 constexpr int kAfParts = 8;
-__device__ __forceinline__ float af_row_mult(const GemmArgs& g, int m) {
-  const float4* p = (const float4*)(g.Aamax + (int64_t)m * kAfParts);
+__device__ __forceinline__ float af_row_mult(const float* amax, int m) {
+  const float4* p = (const float4*)(amax + (int64_t)m * kAfParts);
   const float4 u = p[0], v = p[1];
   const float mx = fmaxf(fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)), fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
   return row_multiplier(fmaxf(mx, 0.0f));
@@ -58,7 +58,7 @@ __device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
   for (int w = 0; w < 4; ++w) f[w] = *(const float4*)(x + 4 * w);
   return quantize_frag16(f, a);
 }
-constexpr int kAfMaxRows = 16;  // fp32 A source: one MFMA row tile
+constexpr int kAfRows = 16;  // fp32 A source: one MFMA row tile per workgroup
 
 // A sources of the skinny kernel: int8 rows with their multipliers, or fp32
 // rows quantized while loading.
@@ -79,10 +79,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   const int n0 = blockIdx.x * COLS;
   const int kq = (lane >> 4) * 16;
   const int ksteps = g.K >> 6;
+  // An fp32 A source is split into 16-row groups over blockIdx.y: each
+  // workgroup quantizes only its own rows (one MFMA row tile).
+  const int r0 = AF ? (int)blockIdx.y * kAfRows : 0;
+  const float* Af = AF ? g.Af + (int64_t)r0 * g.ldaf : nullptr;
+  const float* Aamax = AF ? g.Aamax + (int64_t)r0 * kAfParts : nullptr;
+  float* out = e.out ? e.out + (int64_t)r0 * e.ldo : nullptr;
   // g.M bounds the rows on the host side; every row below it is allocated,
   // so the first row chunk's activations are loaded before the device row
   // count (g.M_dev) is known.
-  const int Mh = g.M;
+  const int Mh = AF ? min(g.M - r0, kAfRows) : g.M;
 
   // Every weight fragment of this wave (k-steps wave, wave+NW, ...).
   v4i bf[KSW][CT];
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
     // At most 16 rows (one MFMA row tile): every k-step's fp32 values and the
     // row's maxima are requested together, then quantized.
     const int m = min(lane & 15, Mh - 1);
-    const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
+    const float* ar = Af + (int64_t)m * g.ldaf + kq;
     float4 raw[KSW][4];
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
@@ -117,7 +123,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
       for (int w = 0; w < 4; ++w) raw[i][w] = *(const float4*)(ar + s * 64 + 4 * w);
     }
-    const float a_m = af_row_mult(g, m);
+    const float a_m = af_row_mult(Aamax, m);
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
       af[i][0] = FULL || wave + NW * i < ksteps ? quantize_frag16(raw[i], a_m) : zero4();
@@ -146,37 +152,28 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
   for (int k = 0; k < ROWS_PER_THREAD; ++k) {
     const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
-    am[k] = AF ? af_row_mult(g, m) : g.a[m];
+    am[k] = AF ? af_row_mult(Aamax, m) : g.a[m];
     if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
-  const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
+  const int Md = g.M_dev ? min(*g.M_dev, g.M) : g.M;
+  const int M = AF ? min(Md - r0, kAfRows) : Md;  // this workgroup's rows
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
-    if (m0 > 0) {
+    if (!AF && m0 > 0) {  // int8 A: next 64-row chunk
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int m = min(m0 + mt * 16 + (lane & 15), M - 1);
-        if constexpr (AF) {
-          const float a_m = af_row_mult(g, m);
-          const float* ar = g.Af + (int64_t)m * g.ldaf + kq;
+        const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
 #pragma unroll
-          for (int i = 0; i < KSW; ++i) {
-            const int s = wave + NW * i;
-            af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? quantize_frag16(ar + s * 64, a_m) : zero4();
-          }
-        } else {
-          const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
-#pragma unroll
-          for (int i = 0; i < KSW; ++i) {
-            const int s = wave + NW * i;
-            af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? *(const v4i*)(ar + s * 64) : zero4();
-          }
+        for (int i = 0; i < KSW; ++i) {
+          const int s = wave + NW * i;
+          af[i][mt] = (s < ksteps && m0 + mt * 16 < M) ? *(const v4i*)(ar + s * 64) : zero4();
         }
       }
 #pragma unroll
       for (int k = 0; k < ROWS_PER_THREAD; ++k) {
         const int m = min(m0 + tid / COLS + k * (NT / COLS), M - 1);
-        am[k] = AF ? af_row_mult(g, m) : g.a[m];
+        am[k] = g.a[m];
         if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
       }
     }
@@ -224,7 +221,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       if (e.relu) y = y > 0.0f ? y : 0.0f;
       if (MODE == EPI_QKV_CACHE) {
         if (n < e.d) {
-          e.out[(int64_t)m * e.ldo + n] = y;
+          out[(int64_t)m * e.ldo + n] = y;
         } else {
           if (n < 2 * e.d)
             e.kcache[crow[k] * e.d + (n - e.d)] = y;
@@ -232,7 +229,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
             e.vcache[crow[k] * e.d + (n - 2 * e.d)] = y;
         }
       } else {
-        if (e.out) e.out[(int64_t)m * e.ldo + n] = y;
+        if (out) out[(int64_t)m * e.ldo + n] = y;
         if (e.out_i32) e.out_i32[(int64_t)m * e.ldi + n] = iv;
       }
     }
@@ -561,7 +558,7 @@ int argmax_groups(int N, int /*K*/) { return (N + kVocabCols - 1) / kVocabCols; 
 
 template <int MODE, int NW, int KSW, int ASRC, bool FULL>
 static hipError_t launch_skinny_kf(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
-  const dim3 grid(skinny_groups(g.N)), block(NW * 64);
+  const dim3 grid(skinny_groups(g.N), ASRC == A_F32 ? (g.M + kAfRows - 1) / kAfRows : 1), block(NW * 64);
   switch (skinny_cols(g.N)) {
     case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
     case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
@@ -582,7 +579,8 @@ template <int MODE>
 static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const int ksteps = g.K >> 6;
   if (g.Af) {
-    if (ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4 || g.M > kAfMaxRows)
+    if (MODE != EPI_STORE || ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4 || e.out_i32 ||
+        g.M > 65535 * kAfRows)
       return hipErrorInvalidValue;
     return launch_skinny_k<MODE, 4, 2, A_F32>(g, e, s);
   }

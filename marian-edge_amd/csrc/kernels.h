@@ -47,7 +47,7 @@ struct GemmArgs {
   // Alternative A source (skinny kernel only): fp32 rows Af[M, ldaf] that are
   // quantized while loading, with row multiplier 127 / max_p Aamax[m*parts+p]
   // (the per-part |max| written by the producer: one per attention head;
-  // parts must be 8).
+  // parts must be 8).  Store epilogue only; each workgroup takes 16 rows.
   const float* Af = nullptr;
   int64_t ldaf = 0;
   const float* Aamax = nullptr;
