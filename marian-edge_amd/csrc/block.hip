@@ -166,6 +166,33 @@ __device__ __forceinline__ float row_quantize(const f4v (&o)[2], int8_t* sX, int
   return a_row;
 }
 
+// Row 0 of 16-row MFMA tiles against T column tiles whose weight fragments
+// are in registers.  Every lane reads the row's 16-byte k-slice from LDS (a
+// broadcast: rows 1-15 of the A tile repeat row 0, and their outputs are never
+// used), k-step outer, so one LDS read feeds every tile and the tiles' chains
+// run interleaved; with one or two tiles the k-steps alternate between two
+// chains per tile.  The sums are exact i32, so the split does not change them.
+// Returns row 0 (lanes 0-15: the tile's 16 columns).
+template <int T>
+__device__ __forceinline__ void row_tiles_mfma(const int8_t* sX, const v4i (&bf)[T][kBlkD / 64], int kq,
+                                               int32_t (&out)[T]) {
+  constexpr int CH = T <= 2 ? 2 : 1;
+  v4i acc[T][CH];
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) acc[i][c] = zero4b();
+#pragma unroll
+  for (int s = 0; s < kBlkD / 64; ++s) {
+    const v4i af = *(const v4i*)(sX + s * 64 + kq);
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+      acc[i][s % CH] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[i][s], acc[i][s % CH], 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < T; ++i) out[i] = CH == 2 ? acc[i][0][0] + acc[i][1][0] : acc[i][0][0];
+}
+
 // Work split: waves 0-3 build the input row (a LayerNorm's folds as four
 // speculative chunks, with nothing else live in those waves; an embedding row
 // by wave 0 alone); waves 4-7 meanwhile load this head's weight rows and
@@ -179,7 +206,8 @@ template <int MODE, int PK>
 __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   constexpr bool SELF = MODE == ATT_SELF;
   constexpr int NT = SELF ? 12 : 4;        // 16-column projection tiles: Q (+ K, V)
-  constexpr int TPW = (NT + kBlkLoadWaves - 1) / kBlkLoadWaves;  // tiles per loader wave
+  constexpr int TPW = NT / kBlkLoadWaves;  // tiles per loader wave
+  static_assert(NT % kBlkLoadWaves == 0, "every loader wave owns whole tiles");
   __shared__ __attribute__((aligned(16))) float sK[kBlkMaxKeys * kBlkRow];
   __shared__ __attribute__((aligned(16))) float sV[kBlkMaxKeys * kBlkRow];
   __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
@@ -236,7 +264,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     float wm[TPW], bi[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      const int tile = min(lw + kBlkLoadWaves * i, NT - 1);  // 16 columns of Q, K or V
+      const int tile = lw + kBlkLoadWaves * i;  // 16 columns of Q, K or V
       const int c0 = (tile / 4) * kBlkD + h * kHeadDim + (tile % 4) * 16;
       const int n_w = c0 + (lane & 15);
 #pragma unroll
@@ -278,27 +306,20 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     for (int idx = u; idx < zrows * 16; idx += kBlkLoaders)
       *(f4v*)(sV + (nkey + (idx >> 4)) * kBlkRow + (idx & 15) * 4) = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();  // the input row (wave 0) is in LDS
-    // ---- projection: row 0 of a 16-row MFMA tile ----------------------------------
+    // ---- projection: row 0 of 16-row MFMA tiles; the dequantization scales
+    // are computed while the matrix cores run ------------------------------------
     const float a_row = sA;
+    float inv[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) inv[i] = dequant_scale(a_row, wm[i]);
+    int32_t acc[TPW];
+    row_tiles_mfma<TPW>(sX, bf, kq, acc);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int tile = lw + kBlkLoadWaves * i;
-      if (tile >= NT) break;
-      // Two independent accumulation chains over the two halves of K (exact
-      // integers: their sum does not depend on the split).
-      v4i acc = zero4b(), acc2 = zero4b();
-#pragma unroll
-      for (int s = 0; s < kBlkD / 128; ++s) {
-        const int s2 = s + kBlkD / 128;
-        const v4i af = (lane & 15) == 0 ? *(const v4i*)(sX + s * 64 + kq) : zero4b();
-        const v4i af2 = (lane & 15) == 0 ? *(const v4i*)(sX + s2 * 64 + kq) : zero4b();
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[i][s], acc, 0, 0, 0);
-        acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af2, bf[i][s2], acc2, 0, 0, 0);
-      }
-      acc += acc2;
       if (lane < 16) {  // lanes 0..15 hold row 0 of the tile's 16 columns
         const int c = (tile % 4) * 16 + lane;
-        const float yv = dequant(acc[0], a_row, wm[i], bi[i]);
+        const float yv = dequant_apply(acc[i], inv[i], bi[i]);
         if (tile < 4) {
           sQ[c] = yv;
         } else if (tile < 8) {
@@ -446,7 +467,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 // ---------------------------------------------------------------------------
 constexpr int kLgCols = 128;                                      // output columns per workgroup
 constexpr int kLgTiles = kLgCols / 16;                            // MFMA column tiles per workgroup
-constexpr int kLgTpw = (kLgTiles + kBlkLoadWaves - 1) / kBlkLoadWaves;  // tiles per loader wave
+constexpr int kLgTpw = kLgTiles / kBlkLoadWaves;  // tiles per loader wave
+static_assert(kLgTiles % kBlkLoadWaves == 0, "every loader wave owns whole tiles");
 
 __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
@@ -482,7 +504,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   float wm[kLgTpw], bi[kLgTpw];
 #pragma unroll
   for (int i = 0; i < kLgTpw; ++i) {
-    const int tile = min(lw + kBlkLoadWaves * i, kLgTiles - 1);
+    const int tile = lw + kBlkLoadWaves * i;
     const int col = slice * kLgCols + tile * 16 + (lane & 15);
 #pragma unroll
     for (int s = 0; s < kBlkD / 64; ++s) bf[i][s] = frag_load(a.W, slice * kLgTiles + tile, kBlkD / 64, s, lane);
@@ -494,22 +516,16 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   wg_lds_barrier();
   __syncthreads();  // the quantized row is in LDS
   const float a_row = sA;
+  float inv[kLgTpw];
+#pragma unroll
+  for (int i = 0; i < kLgTpw; ++i) inv[i] = dequant_scale(a_row, wm[i]);
+  int32_t acc[kLgTpw];
+  row_tiles_mfma<kLgTpw>(sX, bf, kq, acc);
 #pragma unroll
   for (int i = 0; i < kLgTpw; ++i) {
     const int tile = lw + kBlkLoadWaves * i;
-    if (tile >= kLgTiles) break;
-    v4i acc = zero4b(), acc2 = zero4b();
-#pragma unroll
-    for (int s = 0; s < kBlkD / 128; ++s) {
-      const int s2 = s + kBlkD / 128;
-      const v4i af = (lane & 15) == 0 ? *(const v4i*)(sX + s * 64 + kq) : zero4b();
-      const v4i af2 = (lane & 15) == 0 ? *(const v4i*)(sX + s2 * 64 + kq) : zero4b();
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[i][s], acc, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(af2, bf[i][s2], acc2, 0, 0, 0);
-    }
-    acc += acc2;
     if (lane < 16) {  // lanes 0..15 hold row 0 of the tile's 16 columns
-      float y = dequant(acc[0], a_row, wm[i], bi[i]);
+      float y = dequant_apply(acc[i], inv[i], bi[i]);
       if (a.relu) y = y > 0.0f ? y : 0.0f;
       a.out[(int64_t)r * a.ldo + slice * kLgCols + tile * 16 + lane] = y;
     }

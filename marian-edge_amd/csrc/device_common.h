@@ -407,9 +407,10 @@ __device__ __forceinline__ float row_multiplier(float absmax) {
 
 // y = acc * (1 / (a * w)) + b: one multiply, one divide, one multiply, one add
 // (q8_gemm.rs:438-446).
+__device__ __forceinline__ float dequant_scale(float a, float w) { return 1.0f / (a * w); }
+__device__ __forceinline__ float dequant_apply(int32_t acc, float inv, float b) { return (float)acc * inv + b; }
 __device__ __forceinline__ float dequant(int32_t acc, float a, float w, float b) {
-  const float inv = 1.0f / (a * w);
-  return (float)acc * inv + b;
+  return dequant_apply(acc, dequant_scale(a, w), b);
 }
 
 // Weights in MFMA fragment order: for the 16-column tile t and the 64-wide
