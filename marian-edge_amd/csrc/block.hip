@@ -26,6 +26,8 @@ constexpr int kBlkThreads = 64 * (kBlkRowWaves + kBlkLoadWaves);
 constexpr int kBlkD = 512;             // model width handled (8 heads x 64)
 constexpr int kBlkMaxKeys = 128;       // keys staged in LDS
 constexpr int kBlkRow = kHeadDim + 4;  // padded LDS key row (floats)
+constexpr int kPvRow = kBlkMaxKeys + 4;  // padded LDS row of one dimension's PV products
+static_assert(kHeadDim * kPvRow <= kBlkMaxKeys * kBlkRow, "the PV products fit in the key rows");
 static_assert(kBlkRowWaves == 4 && kBlkD == kSpecChunks * kSpecChunk, "the LayerNorm folds: four waves, eight chunks");
 
 __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
@@ -218,6 +220,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   __shared__ __attribute__((aligned(16))) float sP[kBlkMaxKeys];
   __shared__ uint64_t sTab[32];
   __shared__ float sA;
+  __shared__ float sS[64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x % b.heads, r = blockIdx.x / b.heads;  // r < b.rows (host bound)
@@ -256,6 +259,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     if (lane < 32) sTab[lane] = tab_v;
     if (__any(bad) && lane == 0 && b.err) *b.err = 1;
     if (lane == 0 && nk_row > nkm && b.err) *b.err = 2;  // more keys than the LDS stages
+    __syncthreads();  // input row published; keys staged
+    __syncthreads();  // projection done
   } else {
     // ---- waves 4-7: weights, then the keys and values into LDS -----------------
     const int lw = wave - kBlkRowWaves;  // loader wave
@@ -299,10 +304,10 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       wg_lds_barrier();
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's key and value rows are in LDS
-    // Value rows from the last key up to the next multiple of 8 are zero, so
-    // the PV loop's batches of 8 keys read no stale LDS.
+    // Value rows from the last key up to the next multiple of 16 are zero, so
+    // the PV products of the folds' whole batches of 16 keys are +0.
     const int u = tid - 64 * kBlkRowWaves;
-    const int zrows = min((nkey + 7) & ~7, kBlkMaxKeys) - nkey;
+    const int zrows = min((nkey + 15) & ~15, kBlkMaxKeys) - nkey;
     for (int idx = u; idx < zrows * 16; idx += kBlkLoaders)
       *(f4v*)(sV + (nkey + (idx >> 4)) * kBlkRow + (idx & 15) * 4) = f4v{0.0f, 0.0f, 0.0f, 0.0f};
     __syncthreads();  // the input row (wave 0) is in LDS
@@ -333,121 +338,109 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       }
     }
     __syncthreads();  // query and keys are in LDS
-    return;
   }
-  __syncthreads();  // input row published; keys staged
-  __syncthreads();  // projection done
 
-  // ---- attention (wave 0) ---------------------------------------------------------
+  // ---- attention: wave 0, helped by waves 4-7 ----------------------------------
   // Scores: lane = key of chunk c (keys c*64 + lane), 64-term dot in
-  // dimension order.  The query is read into SGPRs one dimension at a time
-  // (readlane of the row lane d holds), the key rows from LDS in batches of 8
-  // dimensions, the next batch while the current one is used; with more than
-  // 64 keys the two chunks' chains run interleaved.  Registers stay within
-  // what two 512-thread workgroups per CU allow.
-  const float scale = 1.0f / sqrtf((float)kHeadDim);
-  float sc[2] = {-INFINITY, -INFINITY};
-  {
-    const float* kra = sK + min(lane, nkey - 1) * kBlkRow;
-    const float* krb = sK + min(64 + lane, nkey - 1) * kBlkRow;
-    const int qv = __float_as_int(sQ[lane]);
-    f4v a0[2], b0[2], a1[2], b1[2];
-    auto rd = [&](int d0, bool two, f4v (&ka)[2], f4v (&kb)[2]) {
+  // dimension order, one chain per wave: wave 0 takes chunk 0 and, with more
+  // than 64 keys, wave 5 (another SIMD) takes chunk 1, handed to wave 0
+  // through LDS.  The key rows and the query (every lane the same address: a
+  // broadcast) come from LDS in batches of 8 dimensions, read three batches
+  // ahead; the products of the next batch are formed between the dependent
+  // adds of the current one (one add and one multiply per scheduling group),
+  // so the adds wait only for each other.
+  const bool two = nkey > 64;
+  const int n16 = (nkey + 15) >> 4;  // the folds' batches of 16 keys
+  float sc = -INFINITY;
+  if (wave == 0 || (two && wave == kBlkRowWaves + 1)) {
+    const int c = wave == 0 ? 0 : 1;
+    const float* kr = sK + min(c * 64 + lane, nkey - 1) * kBlkRow;
+    constexpr int kNb = kHeadDim / 8;  // batches of 8 dimensions
+    f4v kb[4][2], qb[4][2];            // batch b in slot b % 4
+    float pr[2][8];                    // products of batch b in pr[b % 2]
+    auto rd = [&](int bt) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        ka[i] = *(const f4v*)(kra + d0 + 4 * i);
-        if (two) kb[i] = *(const f4v*)(krb + d0 + 4 * i);
+        kb[bt & 3][i] = *(const f4v*)(kr + 8 * bt + 4 * i);
+        qb[bt & 3][i] = *(const f4v*)(sQ + 8 * bt + 4 * i);
       }
     };
-    if (nkey > 64) {
-      float da = -0.0f, db = -0.0f;
-      rd(0, true, a0, b0);
+    const float scale = 1.0f / sqrtf((float)kHeadDim);
+    float da = -0.0f;
+    rd(0);
+    rd(1);
+    rd(2);
+    batch_fence();
 #pragma unroll
-      for (int d0 = 0; d0 < kHeadDim; d0 += 16) {
-        rd(d0 + 8, true, a1, b1);
-        batch_fence();
+    for (int i = 0; i < 8; ++i) pr[0][i] = qb[0][i >> 2][i & 3] * kb[0][i >> 2][i & 3];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float q = __int_as_float(__builtin_amdgcn_readlane(qv, d0 + i));
-          da = da + q * a0[i >> 2][i & 3];
-          db = db + q * b0[i >> 2][i & 3];
-        }
-        if (d0 + 16 < kHeadDim) rd(d0 + 16, true, a0, b0);
-        batch_fence();
+    for (int bt = 0; bt < kNb; ++bt) {
+      if (bt + 3 < kNb) rd(bt + 3);
+      batch_fence();
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float q = __int_as_float(__builtin_amdgcn_readlane(qv, d0 + 8 + i));
-          da = da + q * a1[i >> 2][i & 3];
-          db = db + q * b1[i >> 2][i & 3];
-        }
+      for (int i = 0; i < 8; ++i) {
+        da = da + pr[bt & 1][i];
+        if (bt + 1 < kNb) pr[(bt + 1) & 1][i] = qb[(bt + 1) & 3][i >> 2][i & 3] * kb[(bt + 1) & 3][i >> 2][i & 3];
+        __builtin_amdgcn_sched_barrier(0);
       }
-      sc[0] = da * scale;
-      if (64 + lane < nkey) sc[1] = db * scale;
-    } else {
-      float da = -0.0f;
-      rd(0, false, a0, b0);
+    }
+    if (c * 64 + lane < nkey) sc = da * scale;
+    if (c == 1) sS[lane] = sc;
+  }
+  if (two) wg_lds_barrier();  // chunk 1's scores are in LDS
+  if (wave == 0) {
+    const float sc1 = two ? sS[lane] : -INFINITY;
+    const float mx = wave_max(fmaxf(sc, sc1));
+    const float e0 = lane < nkey ? ref_expf(sc - mx, sTab) : 0.0f;
+    const float e1 = 64 + lane < nkey ? ref_expf(sc1 - mx, sTab) : 0.0f;
+    sP[lane] = e0;
+    sP[64 + lane] = e1;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+    __builtin_amdgcn_wave_barrier();
+    // Denominator: keys in order from 0.0 (softmax_in_place), folded over
+    // whole batches of 16 entries: past the last key they hold +0.0, which
+    // leaves the (non-negative) sum unchanged.
+    const float inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, n16, 0.0f);
+    __builtin_amdgcn_wave_barrier();
+    // p_k = e_k * inv (scale_in_place)
+    sP[lane] = e0 * inv;
+    sP[64 + lane] = e1 * inv;
+  }
+  wg_lds_barrier();  // p is in LDS; the key rows are no longer read
+  // PV: out_d = sum_k v_k[d] * p_k in key order.  Waves 4-7 form the
+  // products (the same roundings as inside the sum) into the freed key rows,
+  // transposed: row d (stride kPvRow) holds dimension d's products in key
+  // order.  Lane = key of a 64-key chunk; each wave owns fixed groups of four
+  // dimensions, all of its reads issued at once.  Wave 0 then folds its lane's
+  // row in key order, over whole batches of 16 keys: past the last key p is +0
+  // and the value rows are zero, so those products are +0 and leave the sum
+  // (never -0) unchanged.  Products of keys past the batches are not read.
+  float* sPv = sK;
+  if (wave >= kBlkRowWaves) {
+    constexpr int kGroups = kHeadDim / 4 / kBlkLoadWaves;  // 4-dimension groups per wave and chunk
+    const int lw = wave - kBlkRowWaves;
 #pragma unroll
-      for (int d0 = 0; d0 < kHeadDim; d0 += 16) {
-        rd(d0 + 8, false, a1, b1);
-        batch_fence();
+    for (int c = 0; c < 2; ++c) {
+      if (c == 1 && !two) break;
+      const float pj = sP[c * 64 + lane];
+      const float* vr = sV + (c * 64 + lane) * kBlkRow;
+      f4v v[kGroups];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) da = da + __int_as_float(__builtin_amdgcn_readlane(qv, d0 + i)) * a0[i >> 2][i & 3];
-        if (d0 + 16 < kHeadDim) rd(d0 + 16, false, a0, b0);
-        batch_fence();
+      for (int g = 0; g < kGroups; ++g) v[g] = *(const f4v*)(vr + 4 * (lw + kBlkLoadWaves * g));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) da = da + __int_as_float(__builtin_amdgcn_readlane(qv, d0 + 8 + i)) * a1[i >> 2][i & 3];
+      for (int g = 0; g < kGroups; ++g) {
+        const int d0 = 4 * (lw + kBlkLoadWaves * g);
+        float* t = sPv + d0 * kPvRow + c * 64 + lane;
+        t[0] = v[g].x * pj;
+        t[kPvRow] = v[g].y * pj;
+        t[2 * kPvRow] = v[g].z * pj;
+        t[3 * kPvRow] = v[g].w * pj;
       }
-      if (lane < nkey) sc[0] = da * scale;
     }
   }
-  const float mx = wave_max(fmaxf(sc[0], sc[1]));
-  float e[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int key = c * 64 + lane;
-    e[c] = key < nkey ? ref_expf(sc[c] - mx, sTab) : 0.0f;
-    sP[key] = e[c];
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
-  __builtin_amdgcn_wave_barrier();
-  // Denominator: keys in order from 0.0 (softmax_in_place), folded over whole
-  // batches of 32 entries: past the last key they hold +0.0, which leaves the
-  // (non-negative) sum unchanged.
-  const float inv = 1.0f / seq_fold_lds_batches((const float4*)sP, (nkey + 31) >> 5, 0.0f);
-  __builtin_amdgcn_wave_barrier();
-  // p_k = e_k * inv (scale_in_place), then out_d = sum_k v_k[d] * p_k in key
-  // order.  Keys are taken in batches of 8 whose V values and p are read one
-  // batch ahead; past the last key p is +0 and the value rows are zero, so
-  // the added products are +0 and leave the sum (never -0) unchanged.
-#pragma unroll
-  for (int c = 0; c < 2; ++c) sP[c * 64 + lane] = e[c] * inv;
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
-  const int nbat = (nkey + 7) >> 3;
-  f4v va[2], pa[2], vb[2], pb[2];
-  auto load8 = [&](int k0, f4v (&v)[2], f4v (&pp)[2]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i >> 2][i & 3] = sV[(k0 + i) * kBlkRow + lane];
-    pp[0] = *(const f4v*)(sP + k0);
-    pp[1] = *(const f4v*)(sP + k0 + 4);
-  };
-  // The read-ahead is unconditional (clamped inside the staged rows; past the
-  // last batch its values are unused), so each wait is for the batch in use.
-  float o = 0.0f;
-  load8(0, va, pa);
-#pragma unroll 1
-  for (int bt = 0;;) {
-    load8(min((bt + 1) * 8, kBlkMaxKeys - 8), vb, pb);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o = o + va[i >> 2][i & 3] * pa[i >> 2][i & 3];
-    if (++bt >= nbat) break;
-    load8(min((bt + 1) * 8, kBlkMaxKeys - 8), va, pa);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o = o + vb[i >> 2][i & 3] * pb[i >> 2][i & 3];
-    if (++bt >= nbat) break;
-  }
+  wg_lds_barrier();  // the products are in LDS
+  if (wave != 0) return;
+  const float o = seq_fold_lds_batches<4>((const float4*)(sPv + lane * kPvRow), n16, 0.0f);
   b.out[(int64_t)r * b.ldo + h * kHeadDim + lane] = o;
   const bool bad = !isfinite(o);
   const float am = wave_max(fabsf(o));
