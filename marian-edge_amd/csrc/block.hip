@@ -28,7 +28,7 @@ constexpr int kBlkMaxKeys = 128;       // keys staged in LDS
 constexpr int kBlkRow = kHeadDim + 4;  // padded LDS key row (floats)
 constexpr int kPvRow = kBlkMaxKeys + 4;  // padded LDS row of one dimension's PV products
 static_assert(kHeadDim * kPvRow <= kBlkMaxKeys * kBlkRow, "the PV products fit in the key rows");
-static_assert(kBlkRowWaves == 4 && kBlkD == kSpecChunks * kSpecChunk, "the LayerNorm folds: four waves, eight chunks");
+static_assert(kBlkRowWaves >= kSpecWaves && kBlkD == kSpecChunks * kSpecChunk, "the LayerNorm folds: two of the row waves, four chunks");
 
 __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
 
@@ -77,11 +77,11 @@ __device__ __forceinline__ void row_load(const RowPrologue& p, int r, int step, 
   }
 }
 
-// LayerNorm(y + r) built by the four row waves together (each loaded the
-// whole row): the mean and variance folds run as speculative eight-chunk folds
+// LayerNorm(y + r) built by the two fold waves together (each loaded the
+// whole row): the mean and variance folds run as speculative four-chunk folds
 // (bit-identical to the sequential folds) over LDS copies of z and of the
-// squared deviations.  Every row wave returns the normalized row.
-__device__ __forceinline__ void row_build_ln4(const RowLoads<PRO_LN>& L, float* sZ, float* sT,
+// squared deviations.  Both waves return the normalized row.
+__device__ __forceinline__ void row_build_ln_spec(const RowLoads<PRO_LN>& L, float* sZ, float* sT,
                                               SpecFoldLds& fm, SpecFoldLds& fv, int w, int lane,
                                               f4v (&o)[2]) {
   f4v z[2], t[2];
@@ -237,14 +237,14 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 
   if (wave < kBlkRowWaves) {
     // ---- the input row ----------------------------------------------------------
-    if (PK != PRO_LN && wave != 0) return;  // an embedding row has no folds
+    if (wave >= (PK == PRO_LN ? kSpecWaves : 1)) return;  // an embedding row has no folds
     const uint64_t tab_v = kBlkExp2Tab[lane & 31];
     RowLoads<PK> in;
     row_load<PK>(b.pro, r, step, lane, in);
     if (r >= n) return;
     f4v o[2];
     if constexpr (PK == PRO_LN) {
-      row_build_ln4(in, sZ, sT, sFm, sFv, wave, lane, o);
+      row_build_ln_spec(in, sZ, sT, sFm, sFv, wave, lane, o);
       if (wave != 0) return;
     } else {
       row_build<PK>(b.pro, in, sZ, lane, o);
@@ -474,11 +474,12 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   const int slice = blockIdx.x % slices, r = blockIdx.x / slices;  // r < a.rows (host bound)
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
   if (wave < kBlkRowWaves) {
+    if (wave >= kSpecWaves) return;  // the two fold waves build the row
     RowLoads<PRO_LN> in;
     row_load<PRO_LN>(a.pro, r, 0, lane, in);
     if (r >= n) return;
     f4v o[2];
-    row_build_ln4(in, sZ, sT, sFm, sFv, wave, lane, o);
+    row_build_ln_spec(in, sZ, sT, sFm, sFv, wave, lane, o);
     if (wave != 0) return;
     bool bad;
     const float a_row = row_quantize(o, sX, lane, bad);

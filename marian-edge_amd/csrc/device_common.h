@@ -165,35 +165,37 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
 }
 
 // ---- speculative exact fold over 512 values ------------------------------------
-// The sequential fold init + p[0] + p[1] + ... + p[511], run by four waves at
-// once with the same result bits.  The row is cut into eight 64-term chunks;
-// wave w folds chunks w and w + 4 as two interleaved chains.  Chunk 0 starts
-// from init; chunk c >= 1 starts from each of 64 consecutive floats (one per
-// lane) centred on an estimate of the prefix sum p[0] + ... + p[64c - 1]
-// (a float tree sum).  Floats are consecutive when their keys are (the key
-// is the bit pattern with the magnitude bits of negative values flipped: a
-// monotone, self-inverse map onto the 32-bit integers, with -0.0 just below
-// +0.0).  The true start of chunk c is the end of chunk c - 1: when its key
-// lies in chunk c's window, that candidate's chain is chunk c's exact end;
-// otherwise chunk c is folded again from the true start.  Every step is the
-// sequential fold's own float addition, so the result is the sequential
-// fold's whatever the estimates are: they only decide how often a 64-term
-// refold is needed.  Chunk ends stay within a few units in the last place of
-// the exact prefix for sums of non-negative terms; a prefix near zero after
-// cancellation can fall outside the window (a few percent of boundaries for
-// centred normal rows).
+// The sequential fold init + p[0] + p[1] + ... + p[511], run by two waves at
+// once with the same result bits.  The row is cut into four 128-term chunks;
+// wave w folds chunks 2w (lanes 0-31) and 2w + 1 (lanes 32-63) in one
+// instruction stream.  Chunk 0 starts from init; chunk c >= 1 starts from each
+// of 32 consecutive floats (one per lane of its half-wave) centred on an
+// estimate of the prefix sum p[0] + ... + p[128c - 1] (a float tree sum).
+// Floats are consecutive when their keys are (the key is the bit pattern with
+// the magnitude bits of negative values flipped: a monotone, self-inverse map
+// onto the 32-bit integers, with -0.0 just below +0.0).  The true start of
+// chunk c is the end of chunk c - 1: when its key lies in chunk c's window,
+// that candidate's chain is chunk c's exact end; otherwise chunk c is folded
+// again from the true start.  Every step is the sequential fold's own float
+// addition, so the result is the sequential fold's whatever the estimates
+// are: they only decide how often a 128-term refold is needed.  Chunk ends of
+// sums of non-negative terms stay within a few units in the last place of the
+// exact prefix; a prefix near zero after cancellation can fall outside the
+// window (a few percent of folds of centred normal rows).
 //
-// Protocol: each of the four fold waves holds the whole row (lane l: elements
-// 4l..4l+3 in v[0], 256+4l..256+4l+3 in v[1]) and calls spec_fold_chunk,
-// which stores its two chunks to p (LDS, 512 floats) and folds them; then
-// every wave of the workgroup passes wg_lds_barrier; then the fold waves call
-// spec_fold_resolve (each gets the result).  p and L stay unchanged until all
-// four have resolved.
-constexpr int kSpecChunk = 64;
-constexpr int kSpecChunks = 8;
+// Protocol: each of the two fold waves (w = 0, 1) holds the whole row (lane l:
+// elements 4l..4l+3 in v[0], 256+4l..256+4l+3 in v[1]) and calls
+// spec_fold_chunk, which stores v[w] (its two chunks) to p (LDS, 512 floats)
+// and folds them; then every wave of the workgroup passes wg_lds_barrier; then
+// the fold waves call spec_fold_resolve (each gets the result).  p and L stay
+// unchanged until both have resolved.
+constexpr int kSpecChunk = 128;
+constexpr int kSpecChunks = 4;
+constexpr int kSpecCand = 32;  // candidate starts per chunk: half a wave
+constexpr int kSpecWaves = 2;  // fold waves
 struct SpecFoldLds {
-  int end[kSpecChunks][64];  // keys of the chain ends (chunk 0: every lane the same)
-  int base[kSpecChunks];     // key of each window's lane 0
+  int end[kSpecChunks][kSpecCand];  // keys of the chain ends (chunk 0: every lane the same)
+  int base[kSpecChunks];            // key of each window's first candidate
 };
 
 __device__ __forceinline__ int float_key(float f) {
@@ -231,92 +233,32 @@ __device__ __forceinline__ void wave_sum2(float& a, float& b) {
       (__int_as_float(__builtin_amdgcn_readlane(ib, 32)) + __int_as_float(__builtin_amdgcn_readlane(ib, 48)));
 }
 
-// Two independent sequential folds of 16 float4 each (LDS, broadcast reads),
-// interleaved; batches of 4 float4 per chain read one batch ahead.
-__device__ __forceinline__ void seq_fold2_lds16(const float4* p, const float4* q, float& s, float& t) {
-  float4 A[4], B[4], C[4], D[4];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    A[b] = p[b];
-    C[b] = q[b];
-  }
-#pragma unroll
-  for (int k = 0; k < 4; k += 2) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      B[b] = p[(k + 1) * 4 + b];
-      D[b] = q[(k + 1) * 4 + b];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      s = s + A[b].x;
-      t = t + C[b].x;
-      s = s + A[b].y;
-      t = t + C[b].y;
-      s = s + A[b].z;
-      t = t + C[b].z;
-      s = s + A[b].w;
-      t = t + C[b].w;
-    }
-    if (k + 2 < 4) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        A[b] = p[(k + 2) * 4 + b];
-        C[b] = q[(k + 2) * 4 + b];
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      s = s + B[b].x;
-      t = t + D[b].x;
-      s = s + B[b].y;
-      t = t + D[b].y;
-      s = s + B[b].z;
-      t = t + D[b].z;
-      s = s + B[b].w;
-      t = t + D[b].w;
-    }
-  }
-}
-
 __device__ __forceinline__ void spec_fold_chunk(const f4v (&v)[2], float* p, float init,
                                                 SpecFoldLds& L, int w, int lane) {
-  // Chunks w and w + 4 are float4 0 and 1 of lanes 16w .. 16w + 15.
-  if ((lane >> 4) == w) {
-    *(f4v*)(p + 4 * lane) = v[0];
-    *(f4v*)(p + 256 + 4 * lane) = v[1];
-  }
-  // Prefix of chunk w: the first float4 of lanes < 16w; of chunk w + 4: every
-  // first float4 and the second float4 of lanes < 16w.
+  const int h = lane >> 5, c = 2 * w + h, cl = lane & 31;
+  *(f4v*)(p + 256 * w + 4 * lane) = v[w];  // chunks 2w and 2w + 1
+  // Prefix estimates: x = chunk 0 (w = 0) or chunks 0-1 (w = 1); y = chunk 2.
   const float f0 = (v[0].x + v[0].y) + (v[0].z + v[0].w);
   const float f1 = (v[1].x + v[1].y) + (v[1].z + v[1].w);
-  float ea = lane < 16 * w ? f0 : 0.0f;
-  float eb = f0 + (lane < 16 * w ? f1 : 0.0f);
-  wave_sum2(ea, eb);
-  // Window bases (key of lane 0), kept where base + 63 cannot overflow.
-  const int ba = (int)min(max((long long)float_key(ea) - 32, (long long)INT32_MIN), (long long)INT32_MAX - 63);
-  const int bb = (int)min(max((long long)float_key(eb) - 32, (long long)INT32_MIN), (long long)INT32_MAX - 63);
-  const float ca = w == 0 ? init : key_float(ba + lane);
-  const float cb = key_float(bb + lane);
-  if (lane == 0) {
-    L.base[w] = ba;
-    L.base[w + 4] = bb;
-  }
+  float x = (w == 1 || lane < 32) ? f0 : 0.0f;
+  float y = (w == 1 && lane < 32) ? f1 : 0.0f;
+  wave_sum2(x, y);
+  const float est = (w == 1 && h == 1) ? x + y : x;
+  // Window base (key of candidate 0), kept where base + 31 cannot overflow.
+  const int base = min(max(float_key(est), INT32_MIN + kSpecCand / 2), INT32_MAX - kSpecCand / 2 + 1) - kSpecCand / 2;
+  const float st = c == 0 ? init : key_float(base + cl);
+  if (cl == 0) L.base[c] = base;
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's chunks are in LDS
   __builtin_amdgcn_wave_barrier();
-  float sa = ca, sb = cb;
-  seq_fold2_lds16((const float4*)(p + kSpecChunk * w), (const float4*)(p + 256 + kSpecChunk * w), sa, sb);
-  L.end[w][lane] = float_key(sa);
-  L.end[w + 4][lane] = float_key(sb);
+  const float e = seq_fold_lds<kSpecChunk / 4, 4>((const float4*)(p + kSpecChunk * c), st);
+  L.end[c][cl] = float_key(e);
 }
 
 __device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFoldLds& L, int lane) {
   int en[kSpecChunks - 1], bs[kSpecChunks - 1];
 #pragma unroll
   for (int k = 1; k < kSpecChunks; ++k) {
-    en[k - 1] = L.end[k][lane];
+    en[k - 1] = L.end[k][lane & (kSpecCand - 1)];
     bs[k - 1] = L.base[k];
   }
   const int e0 = L.end[0][0];
@@ -326,14 +268,14 @@ __device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFol
   // The running key and the window bases are the same in every lane: the
   // lookups run on the scalar unit, without branches while they hit; `miss`
   // marks the chunks whose start was outside the window.  With the base at
-  // most INT32_MAX - 63, d < 64 exactly when the key is in the window.
+  // most INT32_MAX - 31, d < 32 exactly when the key is in the window.
   int ks = __builtin_amdgcn_readfirstlane(e0);
   uint32_t miss = 0;
 #pragma unroll
   for (int k = 1; k < kSpecChunks; ++k) {
     const uint32_t d = (uint32_t)ks - (uint32_t)__builtin_amdgcn_readfirstlane(bs[k - 1]);
-    const int t = __builtin_amdgcn_readlane(en[k - 1], (int)(d & 63u));
-    miss |= d < 64u ? 0u : 1u << k;
+    const int t = __builtin_amdgcn_readlane(en[k - 1], (int)(d & (kSpecCand - 1)));
+    miss |= d < (uint32_t)kSpecCand ? 0u : 1u << k;
     ks = miss ? ks : t;
   }
   if (miss) {  // from the first miss on: fold again where a start is outside the window
@@ -342,7 +284,7 @@ __device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFol
 #pragma unroll 1
     for (int k = km; k < kSpecChunks; ++k) {
       const uint32_t d = (uint32_t)float_key(s) - (uint32_t)__builtin_amdgcn_readfirstlane(L.base[k]);
-      if (k > km && d < 64u)
+      if (k > km && d < (uint32_t)kSpecCand)
         s = key_float(__builtin_amdgcn_readfirstlane(L.end[k][d]));
       else
         s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(

@@ -138,14 +138,14 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
   if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
-// The same LayerNorm for a few decode rows of width 512: one 256-thread
-// workgroup per row, the mean and variance folds as speculative eight-chunk
-// folds (bit-identical to the sequential folds, an eighth of the dependent
+// The same LayerNorm for a few decode rows of width 512: one two-wave
+// workgroup per row, the mean and variance folds as speculative four-chunk
+// folds (bit-identical to the sequential folds, a quarter of the dependent
 // chain); wave 0 then normalizes, stores and quantizes the row.  Lane l holds
 // elements 4l..4l+3 and 256+4l..256+4l+3.
 constexpr int kLnSpecD = kSpecChunks * kSpecChunk;  // 512
-constexpr int kLnSpecMaxRows = 256;      // rows per launch taking the four-wave path
-__global__ __launch_bounds__(256) void k_residual_ln_spec(const float* y, const float* r,
+constexpr int kLnSpecMaxRows = 256;      // rows per launch taking the speculative path
+__global__ __launch_bounds__(64 * kSpecWaves) void k_residual_ln_spec(const float* y, const float* r,
                                                           const float* gamma, const float* beta,
                                                           const int* rows_dev, float* out, int8_t* q,
                                                           float* a, int* err) {
@@ -416,7 +416,7 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
   // Few rows (decode steps): the row's folds are the latency, so four waves
   // share each row.  Many rows (the encoder's sequences): one wave per row.
   if (d == kLnSpecD && rows <= kLnSpecMaxRows) {
-    hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(256), 0, s, y, r, g, b, rows_dev, out, q, a, err);
+    hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(64 * kSpecWaves), 0, s, y, r, g, b, rows_dev, out, q, a, err);
     return hipGetLastError();
   }
   const dim3 grid((rows + 3) / 4), block(256);
