@@ -673,6 +673,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   }
   constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
   constexpr int kLnFfnMaxRows = 32;  // ... and the LayerNorm + FFN up-projection block
+  constexpr int kFfnAfMaxRows = 8;   // ... and the FFN down-projection quantizing its fp32 rows
 
   // What one decode step launches is decided on the host: the row bound
   // (grid sizes; rows at or past the device row count exit early), the path
@@ -921,8 +922,26 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       } else {
         MH_TRY(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
       }
-      MH_TRY(launch_quantize_rows(DH, F, rows, d_nact, F, DHQ, F, DHA, E->err_flag, s));
-      MH_TRY(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
+      if (rows <= kFfnAfMaxRows) {
+        // Few rows: the down-projection reads the fp32 hidden rows and finds
+        // their maxima itself, in place of a row-quantization pass.
+        GemmArgs g;
+        g.Af = DH;
+        g.ldaf = F;
+        g.err = E->err_flag;
+        g.M = rows;
+        g.M_dev = d_nact;
+        g.K = L.ffn2.K;
+        g.W = L.ffn2.w;
+        g.Wf = L.ffn2.wf;
+        g.wmult = L.ffn2.mult;
+        g.bias = L.ffn2.bias;
+        g.N = L.ffn2.N;
+        MH_TRY(launch_gemm_skinny(g, EPI_STORE, store_epi(DY, d, 0), s));
+      } else {
+        MH_TRY(launch_quantize_rows(DH, F, rows, d_nact, F, DHQ, F, DHA, E->err_flag, s));
+        MH_TRY(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
+      }
       MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && P.blk_self));
     }
     {

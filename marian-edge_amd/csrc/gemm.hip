@@ -61,20 +61,23 @@ __device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
 constexpr int kAfRows = 16;  // fp32 A source: one MFMA row tile per workgroup
 
 // A sources of the skinny kernel: int8 rows with their multipliers, or fp32
-// rows quantized while loading.
-enum ASrc { A_I8 = 0, A_F32 = 1 };
+// rows quantized while loading, with the row maxima of the producer (A_F32)
+// or found here over all of K (A_F32_MAX).
+enum ASrc { A_I8 = 0, A_F32 = 1, A_F32_MAX = 2 };
 
 // FULL: K is exactly NW x KSW k-steps (every shape the engine uses), so no
 // k-step needs a guard and every prologue load is unconditional (guarded
 // loads become branches that the compiler waits on one by one).
 template <int MODE, int CT, int NW, int KSW, int ASRC, bool FULL>
 __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
-  constexpr bool AF = ASRC == A_F32;
+  constexpr bool AF = ASRC != A_I8;        // fp32 A, quantized while loading
+  constexpr bool AX = ASRC == A_F32_MAX;   // ... with the row maxima found here
   constexpr int NT = NW * 64;
   constexpr int COLS = CT * 16;
   constexpr int LDC = COLS + 1;          // padded LDS row (i32)
   constexpr int ROWS_PER_THREAD = kSkinnyRows * COLS / NT;
   __shared__ int32_t sAcc[kSkinnyRows * LDC];
+  __shared__ float sRowMax[AX ? NW * kAfRows : 1];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n0 = blockIdx.x * COLS;
   const int kq = (lane >> 4) * 16;
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   // workgroup quantizes only its own rows (one MFMA row tile).
   const int r0 = AF ? (int)blockIdx.y * kAfRows : 0;
   const float* Af = AF ? g.Af + (int64_t)r0 * g.ldaf : nullptr;
-  const float* Aamax = AF ? g.Aamax + (int64_t)r0 * kAfParts : nullptr;
+  const float* Aamax = ASRC == A_F32 ? g.Aamax + (int64_t)r0 * kAfParts : nullptr;
   float* out = e.out ? e.out + (int64_t)r0 * e.ldo : nullptr;
   // g.M bounds the rows on the host side; every row below it is allocated,
   // so the first row chunk's activations are loaded before the device row
@@ -123,7 +126,32 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
       for (int w = 0; w < 4; ++w) raw[i][w] = *(const float4*)(ar + s * 64 + 4 * w);
     }
-    const float a_m = af_row_mult(Aamax, m);
+    float a_m;
+    if constexpr (AX) {
+      // Row |max| over all of K: this lane's 16 values per k-step, the four
+      // lanes of the row (its k-offsets), then the waves through LDS.
+      float mx = 0.0f;
+      bool bad = false;
+#pragma unroll
+      for (int i = 0; i < KSW; ++i)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float4 v = raw[i][w];
+          bad |= !isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w);
+          mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (lane < kAfRows) sRowMax[wave * kAfRows + lane] = mx;
+      if (__any(bad) && lane == 0 && g.err) *g.err = 1;
+      __syncthreads();
+      float rm = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + (lane & 15)]);
+      a_m = row_multiplier(rm);
+    } else {
+      a_m = af_row_mult(Aamax, m);
+    }
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
       af[i][0] = FULL || wave + NW * i < ksteps ? quantize_frag16(raw[i], a_m) : zero4();
@@ -152,7 +180,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
   for (int k = 0; k < ROWS_PER_THREAD; ++k) {
     const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
-    am[k] = AF ? af_row_mult(Aamax, m) : g.a[m];
+    if constexpr (AX) {
+      float rm = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + m]);
+      am[k] = row_multiplier(rm);
+    } else {
+      am[k] = AF ? af_row_mult(Aamax, m) : g.a[m];
+    }
     if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
   const int Md = g.M_dev ? min(*g.M_dev, g.M) : g.M;
@@ -558,7 +593,7 @@ int argmax_groups(int N, int /*K*/) { return (N + kVocabCols - 1) / kVocabCols; 
 
 template <int MODE, int NW, int KSW, int ASRC, bool FULL>
 static hipError_t launch_skinny_kf(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
-  const dim3 grid(skinny_groups(g.N), ASRC == A_F32 ? (g.M + kAfRows - 1) / kAfRows : 1), block(NW * 64);
+  const dim3 grid(skinny_groups(g.N), ASRC != A_I8 ? (g.M + kAfRows - 1) / kAfRows : 1), block(NW * 64);
   switch (skinny_cols(g.N)) {
     case 64: hipLaunchKernelGGL((k_gemm_skinny<MODE, 4, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
     case 32: hipLaunchKernelGGL((k_gemm_skinny<MODE, 2, NW, KSW, ASRC, FULL>), grid, block, 0, s, g, e); break;
@@ -578,6 +613,11 @@ static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStrea
 template <int MODE>
 static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const int ksteps = g.K >> 6;
+  if (g.Af && !g.Aamax) {  // row maxima found here: the FFN down-projection (K = 2048)
+    if (MODE != EPI_STORE || ksteps != 32 || g.ldaf % 4 || e.out_i32 || g.M > 65535 * kAfRows)
+      return hipErrorInvalidValue;
+    return launch_skinny_k<MODE, 8, 4, A_F32_MAX>(g, e, s);
+  }
   if (g.Af) {
     if (MODE != EPI_STORE || ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4 || e.out_i32 ||
         g.M > 65535 * kAfRows)

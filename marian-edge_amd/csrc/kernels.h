@@ -48,10 +48,14 @@ struct GemmArgs {
   // quantized while loading, with row multiplier 127 / max_p Aamax[m*parts+p]
   // (the per-part |max| written by the producer: one per attention head;
   // parts must be 8).  Store epilogue only; each workgroup takes 16 rows.
+  // Without Aamax the kernel finds each row's |max| over all of K itself (K =
+  // 2048: the FFN down-projection), as the row quantization would, and sets
+  // *err to 1 on a non-finite value.
   const float* Af = nullptr;
   int64_t ldaf = 0;
   const float* Aamax = nullptr;
   int amax_parts = 0;
+  int* err = nullptr;
 };
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
