@@ -942,7 +942,9 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         MH_TRY(launch_quantize_rows(DH, F, rows, d_nact, F, DHQ, F, DHA, E->err_flag, s));
         MH_TRY(dgemm(DHQ, DHA, L.ffn2, EPI_STORE, store_epi(DY, d, 0)));
       }
-      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld && P.blk_self));
+      // The last layer's LayerNorm goes into the vocabulary kernel's
+      // prologue on steps with very few rows.
+      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld ? P.blk_self : rows <= kVocabLnMaxRows));
     }
     {
       Epilogue e;
@@ -961,6 +963,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       g.wmult = E->emb.mult;
       g.bias = E->emb.bias;
       g.N = (int)E->V;
+      if (pend.kind == PRO_LN) {  // rows built in the kernel: its fp32 output is not needed
+        g.pro = pend;
+        g.pro.out = nullptr;
+        pend.kind = PRO_NONE;
+      }
       hipEvent_t ev[2];
       MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
       MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));

@@ -286,16 +286,42 @@ constexpr int kVocabCols = 4 * 16 * kVocabCT;     // 128 columns per workgroup
 constexpr int kVocabMaxK = 512;                   // K held in registers
 constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 
-template <bool FULL>  // K = 512: every k-step live, unconditional weight loads
+// FULL: K = 512, every k-step live, unconditional weight loads.  LNP: the
+// rows (at most kVocabLnMaxRows) are the residual LayerNorm of g.pro, built by
+// wave pair p (waves 2p, 2p + 1) for row p with the speculative folds while
+// the weight loads are in flight; their loads are issued before the weights'.
+// Each wave of the pair normalizes the whole row, takes its maximum and
+// quantizes its half into the LDS rows the matrix cores read.
+template <bool FULL, bool LNP>
 __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
+  static_assert(!LNP || 4 / kSpecWaves >= kVocabLnMaxRows, "a wave pair per prologue row");
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
   __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
   __shared__ float sAm[kSkinnyRows];
+  __shared__ __attribute__((aligned(16))) float sZ[LNP ? kVocabLnMaxRows * kVocabMaxK : 4];
+  __shared__ __attribute__((aligned(16))) float sT[LNP ? kVocabLnMaxRows * kVocabMaxK : 4];
+  __shared__ SpecFoldLds sFm[LNP ? kVocabLnMaxRows : 1], sFv[LNP ? kVocabLnMaxRows : 1];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kq = (lane >> 4) * 16;
   const int ksteps = g.K >> 6;
   const int nbase = blockIdx.x * kVocabCols + wave * 16 * kVocabCT;
+
+  // LayerNorm prologue: this wave pair's row (rows below the host bound are
+  // allocated), requested before the weights.
+  const int pr = wave / kSpecWaves, pw = wave % kSpecWaves;
+  const bool prow = LNP && pr < g.M;
+  f4v lz[2], lg[2], lb[2];
+  if constexpr (LNP) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = 4 * lane + 256 * j;
+      const int64_t off = (int64_t)min(pr, g.M - 1) * kVocabMaxK + c;
+      lz[j] = *(const f4v*)(g.pro.y + off) + *(const f4v*)(g.pro.r + off);  // add_slices
+      lg[j] = *(const f4v*)(g.pro.gamma + c);
+      lb[j] = *(const f4v*)(g.pro.beta + c);
+    }
+  }
 
   // Weight fragments for the wave's columns over all of K, issued first.
   v4i bf[kVocabCT][kVocabMaxK / 64];
@@ -332,14 +358,56 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   v4i st[kStage];
   float sa = 0.0f;
   const int rows_h = min(kSkinnyRows, g.M);
+  if constexpr (!LNP) {
 #pragma unroll
-  for (int j = 0; j < kStage; ++j) {
-    const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
-    st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
-                                       : zero4();
+    for (int j = 0; j < kStage; ++j) {
+      const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
+      st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
+                                         : zero4();
+    }
+    if (tid < rows_h) sa = g.a[tid];
   }
-  if (tid < rows_h) sa = g.a[tid];
   const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
+  if constexpr (LNP) {
+    // normalize_row (tensor.rs:372-385) with speculative folds; every wave
+    // passes both fold barriers.
+    float* zr = sZ + pr * kVocabMaxK;
+    float* tr = sT + pr * kVocabMaxK;
+    if (prow) spec_fold_chunk(lz, zr, -0.0f, sFm[pr], pw, lane);
+    wg_lds_barrier();
+    f4v lt[2];
+    float mean = 0.0f;
+    if (prow) {
+      mean = spec_fold_resolve(zr, sFm[pr], lane) / (float)kVocabMaxK;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f4v c = lz[j] - mean;
+        lt[j] = c * c;
+      }
+      spec_fold_chunk(lt, tr, -0.0f, sFv[pr], pw, lane);
+    }
+    wg_lds_barrier();
+    if (prow) {
+      const float var = spec_fold_resolve(tr, sFv[pr], lane) / (float)kVocabMaxK;
+      const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+      f4v o[2];
+      float mx = 0.0f;
+      bool bad = false;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        o[j] = ((lz[j] - mean) * inv) * lg[j] + lb[j];
+        bad |= !isfinite(o[j].x) || !isfinite(o[j].y) || !isfinite(o[j].z) || !isfinite(o[j].w);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
+      }
+      const float a_row = row_multiplier(wave_max(mx));
+      const f4v h = pw == 0 ? o[0] : o[1];
+      *(uint32_t*)(sA + pr * kVocabLds + 4 * lane + 256 * pw) =
+          (uint32_t)(quantize_one(h.x, a_row) & 0xFF) | ((uint32_t)(quantize_one(h.y, a_row) & 0xFF) << 8) |
+          ((uint32_t)(quantize_one(h.z, a_row) & 0xFF) << 16) | ((uint32_t)(quantize_one(h.w, a_row) & 0xFF) << 24);
+      if (pw == 0 && lane == 0) sAm[pr] = a_row;
+      if (__any(bad) && lane == 0 && pr < M && g.pro.err) *g.pro.err = 1;
+    }
+  }
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
@@ -353,12 +421,14 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
       }
       sa = tid < rows ? g.a[m0 + tid] : 0.0f;
     }
+    if constexpr (!LNP) {
 #pragma unroll
-    for (int j = 0; j < kStage; ++j) {
-      const int c = tid + 256 * j;
-      *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
+      for (int j = 0; j < kStage; ++j) {
+        const int c = tid + 256 * j;
+        *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
+      }
+      if (tid < kSkinnyRows) sAm[tid] = sa;
     }
-    if (tid < kSkinnyRows) sAm[tid] = sa;
     __syncthreads();
     const int mt_n = (rows + 15) >> 4;
     // All live row tiles advance together over K: up to 4 x kVocabCT
@@ -645,7 +715,13 @@ hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
   const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
-  auto kern = g.K == kVocabMaxK ? k_vocab_argmax<true> : k_vocab_argmax<false>;
+  const RowPrologue& p = g.pro;
+  if (p.kind != PRO_NONE &&
+      (p.kind != PRO_LN || g.K != kVocabMaxK || g.M > kVocabLnMaxRows || !p.y || !p.r || !p.gamma || !p.beta))
+    return hipErrorInvalidValue;
+  auto kern = p.kind == PRO_LN      ? k_vocab_argmax<true, true>
+              : g.K == kVocabMaxK ? k_vocab_argmax<true, false>
+                                  : k_vocab_argmax<false, false>;
   if (ev_start || ev_stop)
     hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev_start, ev_stop, 0, g, e);
   else

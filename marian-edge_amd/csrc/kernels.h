@@ -56,7 +56,12 @@ struct GemmArgs {
   const float* Aamax = nullptr;
   int amax_parts = 0;
   int* err = nullptr;
+  // Vocabulary kernel only: with pro.kind == PRO_LN the rows (at most
+  // kVocabLnMaxRows, K = 512) are LayerNorm(pro.y + pro.r), built in the
+  // kernel instead of read from A (pro.out is not written).
+  RowPrologue pro;
 };
+constexpr int kVocabLnMaxRows = 2;
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
 
