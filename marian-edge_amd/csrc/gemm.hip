@@ -431,23 +431,45 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     }
     __syncthreads();
     const int mt_n = (rows + 15) >> 4;
-    // All live row tiles advance together over K: up to 4 x kVocabCT
-    // independent accumulation chains keep the matrix core busy.
     v4i acc[4][kVocabCT];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int ct = 0; ct < kVocabCT; ++ct) acc[mt][ct] = zero4();
+    if (FULL && mt_n == 1) {
+      // One row tile (the common decode case): every k-step's A fragment is
+      // read at once, then the matrix cores run four independent chains
+      // (two column tiles x even / odd k-steps; exact integer sums).
+      constexpr int S = kVocabMaxK / 64;
+      v4i a1[S];
 #pragma unroll
-    for (int s = 0; s < kVocabMaxK / 64; ++s) {
-      if (FULL || s < ksteps) {
+      for (int s = 0; s < S; ++s) a1[s] = *(const v4i*)(sA + (lane & 15) * kVocabLds + kq + s * 64);
+      v4i acc2[kVocabCT];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          if (mt < mt_n) {
-            const v4i af = *(const v4i*)(sA + (mt * 16 + (lane & 15)) * kVocabLds + kq + s * 64);
+      for (int ct = 0; ct < kVocabCT; ++ct) acc2[ct] = zero4();
 #pragma unroll
-            for (int ct = 0; ct < kVocabCT; ++ct)
-              acc[mt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[ct][s], acc[mt][ct], 0, 0, 0);
+      for (int s = 0; s < S; s += 2)
+#pragma unroll
+        for (int ct = 0; ct < kVocabCT; ++ct) {
+          acc[0][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[s], bf[ct][s], acc[0][ct], 0, 0, 0);
+          acc2[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[s + 1], bf[ct][s + 1], acc2[ct], 0, 0, 0);
+        }
+#pragma unroll
+      for (int ct = 0; ct < kVocabCT; ++ct) acc[0][ct] += acc2[ct];
+    } else {
+      // All live row tiles advance together over K: up to 4 x kVocabCT
+      // independent accumulation chains keep the matrix core busy.
+#pragma unroll
+      for (int s = 0; s < kVocabMaxK / 64; ++s) {
+        if (FULL || s < ksteps) {
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt) {
+            if (mt < mt_n) {
+              const v4i af = *(const v4i*)(sA + (mt * 16 + (lane & 15)) * kVocabLds + kq + s * 64);
+#pragma unroll
+              for (int ct = 0; ct < kVocabCT; ++ct)
+                acc[mt][ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf[ct][s], acc[mt][ct], 0, 0, 0);
+            }
           }
         }
       }
