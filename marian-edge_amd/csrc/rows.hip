@@ -138,13 +138,12 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
   if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
-// The same LayerNorm for a few decode rows of width 512: one two-wave
+// The same LayerNorm for rows of width 512 (decode and encoder): one two-wave
 // workgroup per row, the mean and variance folds as speculative four-chunk
 // folds (bit-identical to the sequential folds, a quarter of the dependent
 // chain); wave 0 then normalizes, stores and quantizes the row.  Lane l holds
 // elements 4l..4l+3 and 256+4l..256+4l+3.
 constexpr int kLnSpecD = kSpecChunks * kSpecChunk;  // 512
-constexpr int kLnSpecMaxRows = 256;      // rows per launch taking the speculative path
 __global__ __launch_bounds__(64 * kSpecWaves) void k_residual_ln_spec(const float* y, const float* r,
                                                           const float* gamma, const float* beta,
                                                           const int* rows_dev, float* out, int8_t* q,
@@ -415,7 +414,7 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
   if (d % 64) return hipErrorInvalidValue;
   // Few rows (decode steps): the row's folds are the latency, so four waves
   // share each row.  Many rows (the encoder's sequences): one wave per row.
-  if (d == kLnSpecD && rows <= kLnSpecMaxRows) {
+  if (d == kLnSpecD) {
     hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(64 * kSpecWaves), 0, s, y, r, g, b, rows_dev, out, q, a, err);
     return hipGetLastError();
   }
