@@ -541,7 +541,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
 // rows at once) measured 15% slower on 4096 x 32000.
 // ---------------------------------------------------------------------------
 constexpr int kTm = 64;         // tile edge (rows and columns)
-constexpr int64_t kTileBigGrid = 1024;  // tiles above which K chunks are 256 wide
+constexpr int64_t kTileBigGrid = 256;  // tiles above which K chunks are 256 wide
 constexpr int kTout = kTm + 4;  // padded LDS row of the epilogue (words)
 
 template <int KC>  // K chunk staged in LDS: 512 (one round trip for K = 512) or 256
@@ -757,10 +757,11 @@ hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s)
   const int64_t tiles = (int64_t)((g.M + kTm - 1) / kTm) * ((g.N + kTm - 1) / kTm);
   if (tiles > (int64_t)INT32_MAX) return hipErrorInvalidValue;
   const int tiles_n = (g.N + kTm - 1) / kTm;
-  // Launches of more than two rounds of workgroups take the 256-wide chunks
-  // (34 KB of LDS, four workgroups per CU, more loads in flight per CU:
-  // 385 vs 469 us on 4096 x 32000); smaller ones the 512-wide chunks (one
-  // round trip for K = 512).
+  // Launches of more than one round of 512-wide-chunk workgroups (two per
+  // CU) take the 256-wide chunks (34 KB of LDS, four workgroups per CU, more
+  // loads in flight per CU: 385 vs 469 us on 4096 x 32000; the encoder's QKV
+  // and FFN1 in one round instead of two); smaller ones the 512-wide chunks
+  // (one round trip for K = 512).
   if (tiles > kTileBigGrid)
     hipLaunchKernelGGL(k_gemm_tile<256>, dim3((unsigned)tiles), dim3(256), 0, s, g, e, tiles_n, (int)tiles);
   else
