@@ -708,7 +708,7 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
   if (g.Af && !g.Aamax) {  // row maxima found here: the FFN down-projection (K = 2048)
     if (MODE != EPI_STORE || ksteps != 32 || g.ldaf % 4 || e.out_i32 || g.M > 65535 * kAfRows)
       return hipErrorInvalidValue;
-    return launch_skinny_k<MODE, 8, 4, A_F32_MAX>(g, e, s);
+    return launch_skinny_k<MODE, 16, 2, A_F32_MAX>(g, e, s);
   }
   if (g.Af) {
     if (MODE != EPI_STORE || ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4 || e.out_i32 ||
