@@ -20,7 +20,7 @@
 namespace mh {
 namespace {
 
-constexpr int kBlkRowWaves = 4;   // waves 0-3 build the input row
+constexpr int kBlkRowWaves = 4;   // waves 0-3: the input row (0-1 fold, 2-3 exit)
 constexpr int kBlkLoadWaves = 4;  // waves 4-7 load weights and keys, then project
 constexpr int kBlkThreads = 64 * (kBlkRowWaves + kBlkLoadWaves);
 constexpr int kBlkD = 512;             // model width handled (8 heads x 64)
@@ -195,12 +195,12 @@ __device__ __forceinline__ void row_tiles_mfma(const int8_t* sX, const v4i (&bf)
   for (int i = 0; i < T; ++i) out[i] = CH == 2 ? acc[i][0][0] + acc[i][1][0] : acc[i][0][0];
 }
 
-// Work split: waves 0-3 build the input row (a LayerNorm's folds as four
-// speculative chunks, with nothing else live in those waves; an embedding row
-// by wave 0 alone); waves 4-7 meanwhile load this head's weight rows and
-// stage the row's keys and values in LDS, passing the folds' two workgroup
-// barriers with their loads in flight, then run the projection; wave 0
-// attends.
+// Work split: waves 0-1 build the input row (a LayerNorm's two speculative
+// fold waves; an embedding row by wave 0 alone), waves 2-3 exit at once;
+// waves 4-7 meanwhile load this head's weight rows and stage the row's keys
+// and values in LDS, passing the folds' two workgroup barriers with their
+// loads in flight, then run the projection; wave 0 attends, helped by waves
+// 4-7 (wave 5: a second chunk of scores; all four: the PV products).
 constexpr int kBlkLoaders = 64 * kBlkLoadWaves;
 static_assert(kBlkRow % 4 == 0 && kBlkMaxKeys * (kBlkRow / 4) % 64 == 0, "key staging by wave instructions");
 
@@ -451,8 +451,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 
 // ---------------------------------------------------------------------------
 // LayerNorm + up-projection block (the FFN's first layer on steps with few
-// rows): one 512-thread workgroup per (row, 128-column slice).  Waves 0-3
-// build the row's residual LayerNorm (speculative eight-chunk folds) and wave
+// rows): one 512-thread workgroup per (row, 128-column slice).  Waves 0-1
+// build the row's residual LayerNorm (speculative four-chunk folds) and wave
 // 0 quantizes it, as in the attention block; waves 4-7 meanwhile load the
 // slice's weight rows into registers, then run the projection on MFMA (row 0
 // of a 16-row tile), dequantize, apply ReLU and store.  Replaces the

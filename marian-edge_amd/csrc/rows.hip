@@ -412,8 +412,8 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
                               float* a, int* err, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (d % 64) return hipErrorInvalidValue;
-  // Few rows (decode steps): the row's folds are the latency, so four waves
-  // share each row.  Many rows (the encoder's sequences): one wave per row.
+  // Width 512 (decode and encoder): two waves share each row's speculative
+  // folds.  Other widths (op level): one wave per row, sequential folds.
   if (d == kLnSpecD) {
     hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(64 * kSpecWaves), 0, s, y, r, g, b, rows_dev, out, q, a, err);
     return hipGetLastError();
