@@ -114,6 +114,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   }
   // First chunk's activation fragments.
   v4i af[KSW][4];
+  bool xbad = false;  // A_F32_MAX: a non-finite value in this lane's row (row lane % 16)
   if constexpr (AF) {
     // At most 16 rows (one MFMA row tile): every k-step's fp32 values and the
     // row's maxima are requested together, then quantized.
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       if (lane < kAfRows) sRowMax[wave * kAfRows + lane] = mx;
-      if (__any(bad) && lane == 0 && g.err) *g.err = 1;
+      xbad = bad;
       __syncthreads();
       float rm = 0.0f;
 #pragma unroll
@@ -192,6 +193,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   }
   const int Md = g.M_dev ? min(*g.M_dev, g.M) : g.M;
   const int M = AF ? min(Md - r0, kAfRows) : Md;  // this workgroup's rows
+  // Non-finite values count only in rows below the device row count, as in
+  // the row quantization.
+  if constexpr (AX)
+    if (__any(xbad && (lane & 15) < M) && lane == 0 && g.err) *g.err = 1;
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     if (!AF && m0 > 0) {  // int8 A: next 64-row chunk
