@@ -272,11 +272,11 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
   // loaded together with the device row count (one memory round trip); rows
   // at or past the count are dropped afterwards.
   const int ub = min(f.rows_ub, kMaxRowsPerCall);
-  const int n_dev = *f.n_active;
-  const int n = min(n_dev, ub);
-  if (tid == 0 && n_dev > ub && f.err) *f.err = 3;
-  if (tid == 0 && f.active_hist) f.active_hist[f.step] = (uint32_t)n;
   const int np = f.nparts;
+  // The device row count is first needed after the partials are requested;
+  // the stores that report it come last (a store before the loads would make
+  // every load wait for its completion).
+  int n = 0;
   // Wave w takes rows 4w..4w+3 of each 64-row pass; lane i < 4 owns row r0 + i.
   for (int r0 = 4 * wave; r0 < ub; r0 += 64) {
     const int rl = min(r0 + (lane & 3), ub - 1);
@@ -307,6 +307,7 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
     b2 = wave_max_u64(b2);
     b3 = wave_max_u64(b3);
     const uint64_t best = lane == 0 ? b0 : lane == 1 ? b1 : lane == 2 ? b2 : b3;
+    n = min(*f.n_active, ub);
     const int r = r0 + lane;
     if (lane < 4 && r < n) {
       const int32_t tok = argmax_key_id(best);
@@ -323,6 +324,8 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
     }
   }
   __syncthreads();
+  const int n_dev = *f.n_active;
+  n = min(n_dev, ub);
   int cnt = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -361,7 +364,11 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
       ++pos;
     }
   }
-  if (tid == 0) *f.n_active = s_total;
+  if (tid == 0) {
+    if (n_dev > ub && f.err) *f.err = 3;
+    if (f.active_hist) f.active_hist[f.step] = (uint32_t)n;
+    *f.n_active = s_total;
+  }
 }
 
 __global__ __launch_bounds__(256) void k_argmax_reduce(const uint64_t* partials, int nparts,
