@@ -135,7 +135,13 @@ typedef struct {
 
 typedef struct marian_hip_engine marian_hip_engine;
 
-/* Copies the model to device `device` and builds the position table. */
+/* Copies the model to device `device` and builds the position table.
+ * Supported geometry: 1-8 heads of width 64 (dim = 64 * heads), ffn_dim a
+ * multiple of 64 up to 2048, at least one decoder layer, vocab < 2^31.  The
+ * model is checked before the device is touched: every weight multiplier
+ * finite and positive, no weight -128, every tensor present (Q8Linear::new,
+ * crates/marian-cpu/src/q8_gemm.rs:96-110); otherwise MARIAN_HIP_ERR_MODEL,
+ * with the reason in marian_hip_last_op_error() on the calling thread. */
 int marian_hip_engine_create(const marian_hip_model* model, const marian_hip_limits* limits,
                              int device, marian_hip_engine** out_engine);
 void marian_hip_engine_destroy(marian_hip_engine* engine);
@@ -154,6 +160,27 @@ int marian_hip_translate_token_ids(marian_hip_engine* engine, const int32_t* tok
                                    const uint32_t* max_output_tokens, uint32_t flags,
                                    int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
                                    size_t* out_len);
+
+/* marian_hip_translate_token_ids that also copies out intermediate values, for
+ * checks below the token level.  No counterpart in the reference: it exposes
+ * what the reference's own tests read from its engine (the encoder states of
+ * Q8CpuEngine::encode, q8_engine.rs:511-574, and the logits that select_token
+ * scores, q8_engine.rs:749-790).  Same arguments and results as the plain call,
+ * plus (host memory, each may be NULL):
+ *   enc_out[n_tokens, dim]   the final encoder state of every packed row (fp32);
+ *   logits_out[B, vocab]     for decode step `probe_step` (0-based), the logits
+ *                            of every row still active at that step, masked ids
+ *                            -inf (rows not active there are left untouched);
+ *   active_out[B]            1 for the rows whose logits were written, else 0
+ *                            (needs logits_out).
+ * The extra copies synchronize the stream, so its timings are not
+ * representative. */
+int marian_hip_translate_probe(marian_hip_engine* engine, const int32_t* tokens, size_t n_tokens,
+                               const uint32_t* offsets, size_t n_offsets,
+                               const uint32_t* max_output_tokens, uint32_t flags,
+                               int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                               size_t* out_len, uint32_t probe_step, float* enc_out,
+                               float* logits_out, uint8_t* active_out);
 
 int marian_hip_is_ready(const marian_hip_engine* engine);
 /* Last error message of this engine ("" if none); valid until the next call. */

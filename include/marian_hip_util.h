@@ -45,6 +45,11 @@ int marian_hip_event_elapsed(void* start, void* stop, float* ms);
 /* Text of the last HIP error seen by the op-level or util entry points. */
 const char* marian_hip_last_op_error(void);
 
+/* SHA-256 (hex) of the sources this library was built from: csrc/*.hip,
+ * csrc/*.h and include/*.h, in name order, each as name, NUL, contents.
+ * Lets a caller check that a prebuilt library matches the checked-out code. */
+const char* marian_hip_build_id(void);
+
 #ifdef __cplusplus
 }
 #endif

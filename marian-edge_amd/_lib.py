@@ -83,6 +83,8 @@ SIGNATURES = {
     "marian_hip_engine_create": (C.c_int, [C.POINTER(Model), C.POINTER(Limits), C.c_int, C.POINTER(_P)]),
     "marian_hip_engine_destroy": (None, [_P]),
     "marian_hip_translate_token_ids": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, C.c_uint32, _P, _SZ, _P, C.POINTER(_SZ)]),
+    "marian_hip_translate_probe": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, C.c_uint32, _P, _SZ, _P, C.POINTER(_SZ),
+                                             C.c_uint32, _P, _P, _P]),
     "marian_hip_is_ready": (C.c_int, [_P]),
     "marian_hip_last_error": (C.c_char_p, [_P]),
     "marian_hip_info": (C.c_int, [_P, C.c_char_p, _SZ]),
@@ -116,6 +118,7 @@ SIGNATURES = {
     "marian_hip_event_sync": (C.c_int, [_P]),
     "marian_hip_event_elapsed": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
     "marian_hip_last_op_error": (C.c_char_p, []),
+    "marian_hip_build_id": (C.c_char_p, []),
 }
 
 _lib = None
@@ -142,6 +145,11 @@ def load() -> C.CDLL:
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+def build_id() -> str:
+    """Source hash the loaded library was built from."""
+    return load().marian_hip_build_id().decode()
 
 
 def op_error() -> str:

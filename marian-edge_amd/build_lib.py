@@ -36,6 +36,20 @@ HIPCC_FLAGS = [
 ]
 
 
+def source_hash() -> str:
+    """SHA-256 over every source the library is built from (csrc/ and the
+    public headers, in name order); compiled into the library as its build id."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.h")) + list(INCLUDE.glob("*.h")))
+    for f in files:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -43,9 +57,10 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str) -> Path:
+def _compile(src: str, build_id: str) -> Path:
     obj = BUILD_DIR / (Path(src).stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-DMARIAN_HIP_BUILD_ID=\"{build_id}\"", "-c",
+           str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr[-6000:]}")
@@ -56,8 +71,9 @@ def build(verbose: bool = False) -> Path:
     """Compiles every source and links the shared library; returns its path."""
     BUILD_DIR.mkdir(exist_ok=True)
     jobs = min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2))
+    build_id = source_hash()
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, build_id), SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)

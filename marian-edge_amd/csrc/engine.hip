@@ -47,8 +47,32 @@ struct DecLayer {
 enum Buf {
   B_META, B_DMETA, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_ATT, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
   B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DATT, B_DAMAX, B_DY, B_DH, B_DHQ, B_DHA,
-  B_PART, B_OUT, B_COUNT, B_HIST, B_TILES, B_COUNT_
+  B_PART, B_OUT, B_COUNT, B_HIST, B_TILES, B_COUNT_,
+  // allocated only by marian_hip_translate_probe: the probed step's logits
+  // and its active-row order
+  B_PLOG = B_COUNT_, B_PSLOT, B_ALL_
 };
+
+// What marian_hip_translate_probe copies out besides the tokens.
+struct Probe {
+  uint32_t step = UINT32_MAX;
+  float* enc = nullptr;      // [T, d]
+  float* logits = nullptr;   // [B, V]
+  uint8_t* active = nullptr; // [B]
+};
+
+// Load-time checks of one Q8 tensor (Q8Linear::new, q8_gemm.rs:96-110 with
+// validate_quant_mult :592-600; the intgemm8 loader, legacy_q8.rs:384-395):
+// no weight is -128 (symmetric range [-127, 127]) and every multiplier is
+// finite and positive.  Returns the first problem, or nullptr.
+const char* check_q8_tensor(const int8_t* w, const float* mult, size_t N, size_t K) {
+  for (size_t n = 0; n < N; ++n)
+    if (!(std::isfinite(mult[n]) && mult[n] > 0.0f)) return "weight multiplier is not finite and positive";
+  const size_t total = N * K;
+  for (size_t i = 0; i < total; ++i)
+    if (w[i] == INT8_MIN) return "symmetric Q8 weights must be in [-127, 127]";
+  return nullptr;
+}
 
 uint32_t host_positions(uint32_t dim, uint32_t count, float* out) {
   if (dim < 4 || dim % 2) return 1;
@@ -84,11 +108,16 @@ struct marian_hip_engine {
   std::vector<DecLayer> dec;
   float* pos = nullptr;
 
-  void* buf[B_COUNT_] = {};
-  size_t cap[B_COUNT_] = {};
+  void* buf[B_ALL_] = {};
+  size_t cap[B_ALL_] = {};
   int* err_flag = nullptr;
   int* pinned = nullptr;  // host-visible n_active polls
-  hipEvent_t ev[5] = {};  // start, encoder end, decode end, two poll slots
+  hipEvent_t ev[6] = {};  // start, encoder end, decode end, two poll slots, results on host
+  // Host staging reused across calls (grow-only, like the device buffers).
+  std::vector<char> h_meta, h_dmeta;
+  std::vector<int64_t> h_kv_base;
+  std::vector<uint32_t> h_limit, h_remaining, h_ends, h_count;
+  std::vector<int32_t> h_gen;
   // Kernel timing: start/stop event pairs of the timed launches and, per
   // launch, its kind (MARIAN_HIP_KERNEL_*), decode step and decoder layer.
   std::vector<hipEvent_t> kev;
@@ -113,7 +142,16 @@ struct marian_hip_engine {
     if (code == MARIAN_HIP_ERR_DEVICE) ready = false;
     return code;
   }
+  // A HIP error poisons the engine, except hipErrorInvalidValue from a launch
+  // helper: that is a host-side shape rejection (nothing was launched), so
+  // the stream is drained and the call fails as an inference error.
   int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorInvalidValue) {
+      const hipError_t d = hipStreamSynchronize(stream);
+      if (d == hipSuccess)
+        return fail(MARIAN_HIP_ERR_INFERENCE, "%s: shape not supported by the kernels", what);
+      e = d;
+    }
     return fail(MARIAN_HIP_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
   }
   // Returns nullptr on failure (error recorded).
@@ -153,12 +191,29 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
                              int device, marian_hip_engine** out_engine) {
   if (!m || !out_engine) return MARIAN_HIP_ERR_INVALID_INPUT;
   *out_engine = nullptr;
-  if (!m->embedding || !m->embedding_mult || !m->output_bias || !m->vocab || !m->heads ||
-      m->dim != m->heads * kHeadDim || m->dim % 64 || m->dim > 512 || m->ffn_dim % 64 ||
-      m->ffn_dim > 2048 ||
-      (m->encoder_layers && !m->encoder) || (m->decoder_layers && !m->decoder) ||
-      m->heads > 8)
+  auto model_fail = [](const char* fmt, ...) {
+    char msg[256];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(msg, sizeof msg, fmt, ap);
+    va_end(ap);
+    note_op_error(msg);
     return MARIAN_HIP_ERR_MODEL;
+  };
+  // Geometries every kernel of the path runs: heads of width 64 (d = 64 H,
+  // d <= 512: the vocabulary kernel and the fp32-input projections hold K
+  // <= 512), FFN widths that are multiples of 64 up to 2048 (the skinny
+  // kernel's K), at least one decoder layer (the decoder state the
+  // vocabulary projection scores), and a vocabulary below 2^31.
+  if (!m->embedding || !m->embedding_mult || !m->output_bias)
+    return model_fail("embedding, its multipliers and the output bias are required");
+  if (!m->vocab || m->vocab > (uint32_t)INT32_MAX) return model_fail("vocabulary size %u is not supported", m->vocab);
+  if (!m->heads || m->heads > 8 || m->dim != m->heads * kHeadDim)
+    return model_fail("dim %u with %u heads: supported are 1-8 heads of width %d", m->dim, m->heads, kHeadDim);
+  if (!m->ffn_dim || m->ffn_dim % 64 || m->ffn_dim > 2048)
+    return model_fail("ffn_dim %u: supported are multiples of 64 up to 2048", m->ffn_dim);
+  if (!m->decoder_layers || !m->decoder) return model_fail("the model needs at least one decoder layer");
+  if (m->encoder_layers && !m->encoder) return model_fail("encoder layers missing");
   auto* E = new marian_hip_engine();
   E->device = device;
   E->V = m->vocab;
@@ -180,18 +235,6 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     marian_hip_engine_destroy(E);
     return code;
   };
-  if (hipSetDevice(device) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
-    char name[256] = {0};
-    if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
-      std::snprintf(name, sizeof name, "%s", prop.name);
-    if (!name[0]) std::snprintf(name, sizeof name, "AMD GPU");  // no marketing name visible
-    E->device_name = std::string(name) + " (" + prop.gcnArchName + ")";
-  }
-  if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
-    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-
   // Pack every tensor into one host staging buffer (256-byte aligned pieces),
   // then copy to HBM once.
   std::vector<char> host;
@@ -221,8 +264,13 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
         }
     add(f.data(), f.size(), (const void**)dst);
   };
+  const char* bad = nullptr;  // first tensor problem found
   auto add_lin = [&](const marian_hip_linear& l, int N, int K, Lin& out, bool frag = false) -> bool {
-    if (!l.weight || !l.mult || !l.bias) return false;
+    if (!l.weight || !l.mult || !l.bias) {
+      bad = "a linear layer is missing its weight, multipliers or bias";
+      return false;
+    }
+    if ((bad = check_q8_tensor(l.weight, l.mult, (size_t)N, (size_t)K))) return false;
     out.N = N;
     out.K = K;
     add(l.weight, (size_t)N * K, (const void**)&out.w);
@@ -232,12 +280,19 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     return true;
   };
   auto add_vec = [&](const float* v, size_t n, const float** dst) -> bool {
-    if (!v) return false;
+    if (!v) {
+      bad = "a LayerNorm scale or bias is missing";
+      return false;
+    }
     add(v, n * 4, (const void**)dst);
     return true;
   };
   const int d = (int)E->d, F = (int)E->F, V = (int)E->V;
   bool ok = true;
+  if ((bad = check_q8_tensor(m->embedding, m->embedding_mult, (size_t)V, (size_t)d))) {
+    marian_hip_engine_destroy(E);
+    return model_fail("embedding: %s", bad);
+  }
   E->emb.N = V;
   E->emb.K = d;
   add(m->embedding, (size_t)V * d, (const void**)&E->emb.w);
@@ -265,17 +320,26 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
          add_vec(s.ln2_scale, d, &t.ln2_s) && add_vec(s.ln2_bias, d, &t.ln2_b) &&
          add_vec(s.ln3_scale, d, &t.ln3_s) && add_vec(s.ln3_bias, d, &t.ln3_b);
   }
-  if (!ok) return cleanup_fail(MARIAN_HIP_ERR_MODEL);
-  // Every weight multiplier must be finite and positive, and no weight -128
-  // (q8_gemm.rs:96-101 rejects both).
-  {
-    const float* em = m->embedding_mult;
-    for (int v = 0; v < V; ++v)
-      if (!(std::isfinite(em[v]) && em[v] > 0.0f)) return cleanup_fail(MARIAN_HIP_ERR_MODEL);
+  if (!ok) {
+    marian_hip_engine_destroy(E);
+    return model_fail("%s", bad ? bad : "invalid layer");
   }
   std::vector<float> posv((size_t)kMaxPosition * d);
   host_positions(E->d, kMaxPosition, posv.data());
   add(posv.data(), posv.size() * 4, (const void**)&E->pos);
+
+  // The model is valid: only now is the device touched.
+  if (hipSetDevice(device) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+    char name[256] = {0};
+    if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
+      std::snprintf(name, sizeof name, "%s", prop.name);
+    if (!name[0]) std::snprintf(name, sizeof name, "AMD GPU");  // no marketing name visible
+    E->device_name = std::string(name) + " (" + prop.gcnArchName + ")";
+  }
+  if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
 
   if (hipMalloc(&E->weights, host.size()) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
   if (hipMemcpy(E->weights, host.data(), host.size(), hipMemcpyHostToDevice) != hipSuccess)
@@ -293,9 +357,13 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
 
 void marian_hip_engine_destroy(marian_hip_engine* E) {
   if (!E) return;
+  if (!E->stream && !E->weights) {  // rejected before the device was touched
+    delete E;
+    return;
+  }
   hipSetDevice(E->device);
   if (E->stream) hipStreamSynchronize(E->stream);
-  for (int b = 0; b < B_COUNT_; ++b)
+  for (int b = 0; b < B_ALL_; ++b)
     if (E->buf[b]) hipFree(E->buf[b]);
   if (E->weights) hipFree(E->weights);
   if (E->err_flag) hipFree(E->err_flag);
@@ -363,11 +431,10 @@ int marian_hip_set_timing(marian_hip_engine* E, uint32_t flags) {
   return MARIAN_HIP_OK;
 }
 
-int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
-                                   const uint32_t* offsets, size_t n_offsets,
-                                   const uint32_t* max_output_tokens, uint32_t flags,
-                                   int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
-                                   size_t* out_len) {
+static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
+                     const uint32_t* offsets, size_t n_offsets, const uint32_t* max_output_tokens,
+                     uint32_t flags, int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                     size_t* out_len, const Probe& pr) {
   if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
   E->error.clear();
   if (!E->ready) return E->fail(MARIAN_HIP_ERR_NOT_READY, "engine is not ready after a device error");
@@ -405,7 +472,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
                      tokens[i], E->V);
 
   const uint32_t maxpos = std::min<uint32_t>(lim.max_position, kMaxPosition);
-  std::vector<uint32_t> limit(B);
+  std::vector<uint32_t>& limit = E->h_limit;
+  limit.assign(B, 0);
   uint32_t gen_limit = 0;
   uint64_t total_cap = 0;
   for (size_t b = 0; b < B; ++b) {
@@ -444,12 +512,44 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   // offsets.  Decoder, per active row (initially every sequence with a
   // non-zero limit, in order; the rest of the R rows padded with valid
   // values): its sequence, first KV-cache/output row, source range, previous
-  // token and generation limit; plus the device row count and step.
-  std::vector<int32_t> positions(T), seq_of_row(T);
-  std::vector<int64_t> kv_base(B);
-  std::vector<int32_t> r_slot(R, 0), r_srcn(R, 1), r_prev(R, -1);
-  std::vector<uint32_t> r_lim(R, 0);
-  std::vector<int64_t> r_kv0(R, 0), r_src0(R, 0);
+  // token and generation limit; plus the device row count and step.  Both
+  // are written straight into engine-owned host buffers that are reused
+  // across calls.
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  size_t cur = 0;
+  auto place = [&](size_t bytes) {
+    const size_t o = cur;
+    cur = align(cur + bytes);
+    return o;
+  };
+  const size_t o_tok = place(4ull * T), o_pos = place(4ull * T), o_seq = place(4ull * T),
+               o_cu = place(4 * (B + 1));
+  const size_t meta_bytes = cur;
+  cur = 0;
+  const size_t o_state = place(8), o_rslot = place(4 * R), o_rkv0 = place(8 * R),
+               o_rsrc0 = place(8 * R), o_rsrcn = place(4 * R), o_rprev = place(4 * R),
+               o_rlim = place(4 * R);
+  const size_t dmeta_bytes = cur;
+  std::vector<char>& meta = E->h_meta;
+  std::vector<char>& dmeta_h = E->h_dmeta;
+  meta.assign(meta_bytes, 0);
+  dmeta_h.assign(dmeta_bytes, 0);
+  int32_t* positions = (int32_t*)(meta.data() + o_pos);
+  int32_t* seq_of_row = (int32_t*)(meta.data() + o_seq);
+  if (T) std::memcpy(meta.data() + o_tok, tokens, 4 * (size_t)T);
+  std::memcpy(meta.data() + o_cu, offsets, 4 * (B + 1));
+  int32_t* r_slot = (int32_t*)(dmeta_h.data() + o_rslot);
+  int64_t* r_kv0 = (int64_t*)(dmeta_h.data() + o_rkv0);
+  int64_t* r_src0 = (int64_t*)(dmeta_h.data() + o_rsrc0);
+  int32_t* r_srcn = (int32_t*)(dmeta_h.data() + o_rsrcn);
+  int32_t* r_prev = (int32_t*)(dmeta_h.data() + o_rprev);
+  uint32_t* r_lim = (uint32_t*)(dmeta_h.data() + o_rlim);
+  for (size_t r = 0; r < R; ++r) {
+    r_srcn[r] = 1;
+    r_prev[r] = -1;
+  }
+  std::vector<int64_t>& kv_base = E->h_kv_base;
+  kv_base.assign(B, 0);
   int64_t run = 0;
   int n_active0 = 0;
   for (size_t b = 0; b < B; ++b) {
@@ -468,34 +568,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       ++n_active0;
     }
   }
-  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
-  size_t cur = 0;
-  auto place = [&](size_t bytes) {
-    const size_t o = cur;
-    cur = align(cur + bytes);
-    return o;
-  };
-  const size_t o_tok = place(4ull * T), o_pos = place(4ull * T), o_seq = place(4ull * T),
-               o_cu = place(4 * (B + 1));
-  const size_t meta_bytes = cur;
-  cur = 0;
-  const size_t o_state = place(8), o_rslot = place(4 * R), o_rkv0 = place(8 * R),
-               o_rsrc0 = place(8 * R), o_rsrcn = place(4 * R), o_rprev = place(4 * R),
-               o_rlim = place(4 * R);
-  const size_t dmeta_bytes = cur;
-  std::vector<char> meta(meta_bytes, 0), dmeta_h(dmeta_bytes, 0);
-  std::memcpy(meta.data() + o_tok, tokens, 4 * (size_t)T);
-  std::memcpy(meta.data() + o_pos, positions.data(), 4 * (size_t)T);
-  std::memcpy(meta.data() + o_seq, seq_of_row.data(), 4 * (size_t)T);
-  std::memcpy(meta.data() + o_cu, offsets, 4 * (B + 1));
   const int state0[2] = {n_active0, 0};  // device row count, decode step
   std::memcpy(dmeta_h.data() + o_state, state0, 8);
-  std::memcpy(dmeta_h.data() + o_rslot, r_slot.data(), 4 * R);
-  std::memcpy(dmeta_h.data() + o_rkv0, r_kv0.data(), 8 * R);
-  std::memcpy(dmeta_h.data() + o_rsrc0, r_src0.data(), 8 * R);
-  std::memcpy(dmeta_h.data() + o_rsrcn, r_srcn.data(), 4 * R);
-  std::memcpy(dmeta_h.data() + o_rprev, r_prev.data(), 4 * R);
-  std::memcpy(dmeta_h.data() + o_rlim, r_lim.data(), 4 * R);
 
   const uint32_t LdA = std::max<uint32_t>(E->Ld, 1);
   char* dmeta = (char*)E->get(B_META, meta_bytes);
@@ -535,6 +609,13 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   uint32_t* TILES = (uint32_t*)E->get(B_TILES, 4ull * (1 + 2 * (size_t)tiles_cap));
   for (int b = 0; b < B_COUNT_; ++b)
     if (!E->buf[b]) return E->fail(MARIAN_HIP_ERR_DEVICE, "device allocation failed");
+  float* PLOG = nullptr;  // probe: the probed step's logits [R, V], active-row order
+  int32_t* PSLOT = nullptr;  // probe: that step's row -> sequence map [R] and row count
+  if (pr.logits) {
+    PLOG = (float*)E->get(B_PLOG, 4ull * R * E->V);
+    PSLOT = (int32_t*)E->get(B_PSLOT, 4ull * (R + 1));
+    if (!PLOG || !PSLOT) return E->fail(MARIAN_HIP_ERR_DEVICE, "device allocation failed");
+  }
 
   int32_t* d_tok = (int32_t*)(dmeta + o_tok);
   int32_t* d_pos = (int32_t*)(dmeta + o_pos);
@@ -625,9 +706,11 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     MH_HIP(gemm(HQ, HA, T, L.ffn2, Y, 0));
     MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, XQ, XA, E->err_flag, s));
   }
+  if (pr.enc) MH_HIP(hipMemcpyAsync(pr.enc, X0, 4ull * T * d, hipMemcpyDeviceToHost, s));
   for (uint32_t l = 0; l < E->Ld; ++l)
     MH_HIP(gemm(XQ, XA, T, E->dec[l].cross_kv, CKV + (size_t)l * TR * 2 * d, 0));
   MH_HIP(hipEventRecord(E->ev[1], s));
+  if (PSLOT) MH_HIP(hipMemsetAsync(PSLOT + R, 0, sizeof(int32_t), s));  // no rows unless the step runs
 
   // ---- greedy decode with device-side active set ----
   E->kev_kind.clear();
@@ -664,10 +747,12 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     ++n_timed;
     return hipSuccess;
   };
-  std::vector<uint32_t> remaining(gen_limit + 1, 0);  // rows with limit > t
+  std::vector<uint32_t>& remaining = E->h_remaining;  // rows with limit > t
+  remaining.assign(gen_limit + 1, 0);
   for (size_t b = 0; b < B; ++b) remaining[0] += limit[b] > 0;
   {
-    std::vector<uint32_t> ends(gen_limit + 1, 0);
+    std::vector<uint32_t>& ends = E->h_ends;
+    ends.assign(gen_limit + 1, 0);
     for (size_t b = 0; b < B; ++b) ends[limit[b]]++;
     for (uint32_t t = 1; t <= gen_limit; ++t) remaining[t] = remaining[t - 1] - ends[t];
   }
@@ -680,7 +765,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   // of each attention sublayer and the key bounds that pick kernel variants.
   struct StepPlan {
     int rows, self_keys, cross_keys;
-    bool blk_self, blk_cross, ln_ffn;
+    bool blk_self, blk_cross, ln_ffn, ffn_af, vocab_ln;
   };
   auto make_plan = [&](int rows, int self_keys, int cross_keys) {
     StepPlan P;
@@ -690,6 +775,8 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     P.blk_self = rows <= kBlkMaxRows && attn_block_supported(d, H, self_keys);
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
     P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
+    P.ffn_af = rows <= kFfnAfMaxRows;
+    P.vocab_ln = rows <= kVocabLnMaxRows && vocab_ln_supported(d);
     return P;
   };
 
@@ -922,7 +1009,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       } else {
         MH_TRY(xgemm(L.ffn1, EPI_STORE, store_epi(DH, F, 1)));
       }
-      if (rows <= kFfnAfMaxRows) {
+      if (P.ffn_af) {
         // Few rows: the down-projection reads the fp32 hidden rows and finds
         // their maxima itself, in place of a row-quantization pass.
         GemmArgs g;
@@ -944,7 +1031,7 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
       }
       // The last layer's LayerNorm goes into the vocabulary kernel's
       // prologue on steps with very few rows.
-      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld ? P.blk_self : rows <= kVocabLnMaxRows));
+      MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld ? P.blk_self : P.vocab_ln));
     }
     {
       Epilogue e;
@@ -968,9 +1055,18 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
         g.pro.out = nullptr;
         pend.kind = PRO_NONE;
       }
+      const bool probed = PLOG && t == pr.step;
+      if (probed) {  // this step's logits too (same kernel, extra stores)
+        e.logits = PLOG;
+        e.ldl = E->V;
+      }
       hipEvent_t ev[2];
       MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
       MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));
+      if (probed) {  // the active-row order before the finalizer compacts it
+        MH_TRY(hipMemcpyAsync(PSLOT, rm.slot, 4ull * R, hipMemcpyDeviceToDevice, s));
+        MH_TRY(hipMemcpyAsync(PSLOT + R, d_nact, sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+      }
     }
     FinalizeArgs f;
     f.partials = PART;
@@ -1016,8 +1112,10 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   MH_HIP(hipEventRecord(E->ev[2], s));
 
   // ---- results back to the host ----
-  std::vector<uint32_t> count(B);
-  std::vector<int32_t> gen(cache_rows);
+  std::vector<uint32_t>& count = E->h_count;
+  std::vector<int32_t>& gen = E->h_gen;
+  count.assign(B, 0);
+  gen.assign(cache_rows, 0);
   int err_host = 0;
   E->step_rows.assign(steps, 0);
   if (steps) MH_HIP(hipMemcpyAsync(E->step_rows.data(), HIST, 4ull * steps, hipMemcpyDeviceToHost, s));
@@ -1030,15 +1128,13 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   const uint32_t launched = steps;
   while (steps > 0 && E->step_rows[steps - 1] == 0) --steps;
   E->step_rows.resize(steps);
-  hipEvent_t ev_end;
-  MH_HIP(hipEventCreate(&ev_end));
+  hipEvent_t ev_end = E->ev[5];
   MH_HIP(hipEventRecord(ev_end, s));
   MH_HIP(hipEventSynchronize(ev_end));
   float ms_total = 0, ms_enc = 0, ms_dec = 0;
   hipEventElapsedTime(&ms_total, E->ev[0], ev_end);
   hipEventElapsedTime(&ms_enc, E->ev[0], E->ev[1]);
   hipEventElapsedTime(&ms_dec, E->ev[1], E->ev[2]);
-  hipEventDestroy(ev_end);
   E->stats.total_ms = ms_total;
   E->stats.encoder_ms = ms_enc;
   E->stats.decode_ms = ms_dec;
@@ -1069,6 +1165,21 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
   if (err_host == 3) return E->fail(MARIAN_HIP_ERR_INFERENCE, "active rows exceed the step bound");
   if (err_host) return E->fail(MARIAN_HIP_ERR_INFERENCE, "activation is not finite");
 
+  if (pr.active) std::memset(pr.active, 0, B);
+  if (PLOG) {  // the probed step's rows, back in sequence order
+    std::vector<int32_t> slot(R + 1);
+    MH_HIP(hipMemcpy(slot.data(), PSLOT, 4ull * (R + 1), hipMemcpyDeviceToHost));
+    const size_t n = (size_t)std::min<int64_t>(std::max(slot[R], 0), (int64_t)std::min(R, B));
+    std::vector<float> lg(n * E->V);
+    if (n) MH_HIP(hipMemcpy(lg.data(), PLOG, 4ull * n * E->V, hipMemcpyDeviceToHost));
+    for (size_t r = 0; r < n; ++r) {
+      const int32_t b = slot[r];
+      if (b < 0 || (size_t)b >= B) continue;
+      std::memcpy(pr.logits + (size_t)b * E->V, lg.data() + r * E->V, 4ull * E->V);
+      if (pr.active) pr.active[b] = 1;
+    }
+  }
+
   size_t total = 0;
   for (size_t b = 0; b < B; ++b) total += count[b];
   E->stats.generated_tokens = total;
@@ -1083,6 +1194,32 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
     out_offsets[b + 1] = (uint32_t)o;
   }
   return MARIAN_HIP_OK;
+}
+
+int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
+                                   const uint32_t* offsets, size_t n_offsets,
+                                   const uint32_t* max_output_tokens, uint32_t flags,
+                                   int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                                   size_t* out_len) {
+  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, out_tokens,
+                   out_cap, out_offsets, out_len, Probe());
+}
+
+int marian_hip_translate_probe(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
+                               const uint32_t* offsets, size_t n_offsets,
+                               const uint32_t* max_output_tokens, uint32_t flags,
+                               int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                               size_t* out_len, uint32_t probe_step, float* enc_out,
+                               float* logits_out, uint8_t* active_out) {
+  if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (active_out && !logits_out) return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "active_out needs logits_out");
+  Probe pr;
+  pr.step = probe_step;
+  pr.enc = enc_out;
+  pr.logits = logits_out;
+  pr.active = active_out;
+  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, out_tokens,
+                   out_cap, out_offsets, out_len, pr);
 }
 
 }  // extern "C"

@@ -32,13 +32,21 @@ __device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
 // threads write consecutive columns.
 // ---------------------------------------------------------------------------
 // Row multiplier of row m of an fp32 A source from its producer's partial
-// maxima (amax_parts = 8 per row, read as two 16-byte vectors so the loads
-// issue together).
+// maxima (`parts` per row, one per attention head; eight of them are read as
+// two 16-byte vectors so the loads issue together).
 constexpr int kAfParts = 8;
-__device__ __forceinline__ float af_row_mult(const float* amax, int m) {
-  const float4* p = (const float4*)(amax + (int64_t)m * kAfParts);
-  const float4 u = p[0], v = p[1];
-  const float mx = fmaxf(fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)), fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+constexpr int kAfMaxParts = 16;
+__device__ __forceinline__ float af_row_mult(const float* amax, int m, int parts) {
+  float mx = 0.0f;
+  if (parts == kAfParts) {
+    const float4* p = (const float4*)(amax + (int64_t)m * kAfParts);
+    const float4 u = p[0], v = p[1];
+    mx = fmaxf(fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)), fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+  } else {
+#pragma unroll
+    for (int i = 0; i < kAfMaxParts; ++i)
+      if (i < parts) mx = fmaxf(mx, amax[(int64_t)m * parts + i]);
+  }
   return row_multiplier(fmaxf(mx, 0.0f));
 }
 
@@ -86,7 +94,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   // workgroup quantizes only its own rows (one MFMA row tile).
   const int r0 = AF ? (int)blockIdx.y * kAfRows : 0;
   const float* Af = AF ? g.Af + (int64_t)r0 * g.ldaf : nullptr;
-  const float* Aamax = ASRC == A_F32 ? g.Aamax + (int64_t)r0 * kAfParts : nullptr;
+  const float* Aamax = ASRC == A_F32 ? g.Aamax + (int64_t)r0 * g.amax_parts : nullptr;
   float* out = e.out ? e.out + (int64_t)r0 * e.ldo : nullptr;
   // g.M bounds the rows on the host side; every row below it is allocated,
   // so the first row chunk's activations are loaded before the device row
@@ -151,7 +159,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + (lane & 15)]);
       a_m = row_multiplier(rm);
     } else {
-      a_m = af_row_mult(Aamax, m);
+      a_m = af_row_mult(Aamax, m, g.amax_parts);
     }
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + m]);
       am[k] = row_multiplier(rm);
     } else {
-      am[k] = AF ? af_row_mult(Aamax, m) : g.a[m];
+      am[k] = AF ? af_row_mult(Aamax, m, g.amax_parts) : g.a[m];
     }
     if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
@@ -687,6 +695,7 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e, int t
 int skinny_cols(int N) { return N >= 8192 ? 64 : (N >= 1024 ? 32 : 16); }
 int skinny_groups(int N) { return (N + skinny_cols(N) - 1) / skinny_cols(N); }
 int argmax_groups(int N, int /*K*/) { return (N + kVocabCols - 1) / kVocabCols; }
+bool vocab_ln_supported(int K) { return K == kVocabMaxK; }
 
 template <int MODE, int NW, int KSW, int ASRC, bool FULL>
 static hipError_t launch_skinny_kf(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
@@ -710,13 +719,14 @@ static hipError_t launch_skinny_k(const GemmArgs& g, const Epilogue& e, hipStrea
 template <int MODE>
 static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   const int ksteps = g.K >> 6;
-  if (g.Af && !g.Aamax) {  // row maxima found here: the FFN down-projection (K = 2048)
-    if (MODE != EPI_STORE || ksteps != 32 || g.ldaf % 4 || e.out_i32 || g.M > 65535 * kAfRows)
+  if (g.Af && !g.Aamax) {  // row maxima found here: the FFN down-projection (K <= 2048)
+    if (MODE != EPI_STORE || ksteps > 32 || g.ldaf % 4 || e.out_i32 || g.M > 65535 * kAfRows)
       return hipErrorInvalidValue;
     return launch_skinny_k<MODE, 16, 2, A_F32_MAX>(g, e, s);
   }
   if (g.Af) {
-    if (MODE != EPI_STORE || ksteps > 8 || !g.Aamax || g.amax_parts != kAfParts || g.ldaf % 4 || e.out_i32 ||
+    if (MODE != EPI_STORE || ksteps > 8 || !g.Aamax || g.amax_parts < 1 || g.amax_parts > kAfMaxParts ||
+        g.ldaf % 4 || e.out_i32 ||
         g.M > 65535 * kAfRows)
       return hipErrorInvalidValue;
     return launch_skinny_k<MODE, 4, 2, A_F32>(g, e, s);

@@ -47,9 +47,9 @@ struct GemmArgs {
   // Alternative A source (skinny kernel only): fp32 rows Af[M, ldaf] that are
   // quantized while loading, with row multiplier 127 / max_p Aamax[m*parts+p]
   // (the per-part |max| written by the producer: one per attention head;
-  // parts must be 8).  Store epilogue only; each workgroup takes 16 rows.
-  // Without Aamax the kernel finds each row's |max| over all of K itself (K =
-  // 2048: the FFN down-projection), as the row quantization would, and sets
+  // 1 to 16 parts, K <= 512).  Store epilogue only; each workgroup takes 16
+  // rows.  Without Aamax the kernel finds each row's |max| over all of K itself
+  // (K <= 2048: the FFN down-projection), as the row quantization would, and sets
   // *err to 1 on a non-finite value.
   const float* Af = nullptr;
   int64_t ldaf = 0;
@@ -62,6 +62,8 @@ struct GemmArgs {
   RowPrologue pro;
 };
 constexpr int kVocabLnMaxRows = 2;
+// Whether the vocabulary kernel can build LayerNorm rows of width K itself.
+bool vocab_ln_supported(int K);
 
 enum EpiMode { EPI_STORE = 0, EPI_QKV_CACHE = 1, EPI_ARGMAX = 2 };
 
@@ -253,6 +255,9 @@ struct FinalizeArgs {
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 
 // Reduces argmax partials to token ids (op-level argmax).
+// Records the message marian_hip_last_op_error returns on this thread.
+void note_op_error(const char* msg);
+
 hipError_t launch_argmax_reduce(const uint64_t* partials, int nparts, int rows, int32_t* token,
                                 hipStream_t s);
 

@@ -58,6 +58,8 @@ void* scratch(int which, size_t bytes, hipStream_t s) {
 
 }  // namespace
 
+void mh::note_op_error(const char* msg) { g_op_error = msg ? msg : ""; }
+
 extern "C" {
 
 int marian_hip_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, float* a,
@@ -257,5 +259,10 @@ int marian_hip_event_elapsed(void* a, void* b, float* ms) {
   return op_status(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
 }
 const char* marian_hip_last_op_error(void) { return g_op_error.c_str(); }
+
+#ifndef MARIAN_HIP_BUILD_ID
+#define MARIAN_HIP_BUILD_ID "unknown"
+#endif
+const char* marian_hip_build_id(void) { return MARIAN_HIP_BUILD_ID; }
 
 }  // extern "C"

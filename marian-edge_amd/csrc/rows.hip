@@ -404,14 +404,34 @@ hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int
   return hipGetLastError();
 }
 
-#define MH_PER_DISPATCH(PER_VALUE, CALL) \
-  switch (PER_VALUE) {                   \
-    case 4: CALL(4); break;              \
-    case 6: CALL(6); break;              \
-    case 8: CALL(8); break;              \
-    case 12: CALL(12); break;            \
-    case 16: CALL(16); break;            \
+// Row widths d = 64 * PER: every width the engine accepts (PER 1-8) and the
+// op-level LayerNorm's up to 1024 (PER 9-16).
+#define MH_PER_DISPATCH_8(PER_VALUE, CALL) \
+  case 1: CALL(1); break;                  \
+  case 2: CALL(2); break;                  \
+  case 3: CALL(3); break;                  \
+  case 4: CALL(4); break;                  \
+  case 5: CALL(5); break;                  \
+  case 6: CALL(6); break;                  \
+  case 7: CALL(7); break;                  \
+  case 8: CALL(8); break;
+#define MH_PER_DISPATCH(PER_VALUE, CALL)  \
+  switch (PER_VALUE) {                    \
+    MH_PER_DISPATCH_8(PER_VALUE, CALL)    \
     default: return hipErrorInvalidValue; \
+  }
+#define MH_PER_DISPATCH_16(PER_VALUE, CALL) \
+  switch (PER_VALUE) {                      \
+    MH_PER_DISPATCH_8(PER_VALUE, CALL)      \
+    case 9: CALL(9); break;                 \
+    case 10: CALL(10); break;               \
+    case 11: CALL(11); break;               \
+    case 12: CALL(12); break;               \
+    case 13: CALL(13); break;               \
+    case 14: CALL(14); break;               \
+    case 15: CALL(15); break;               \
+    case 16: CALL(16); break;               \
+    default: return hipErrorInvalidValue;   \
   }
 
 hipError_t launch_residual_ln(const float* y, const float* r, const float* g, const float* b,
@@ -428,7 +448,7 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
   const dim3 grid((rows + 3) / 4), block(256);
 #define MH_LN(P) \
   hipLaunchKernelGGL(k_residual_ln<P>, grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err)
-  MH_PER_DISPATCH(d / 64, MH_LN)
+  MH_PER_DISPATCH_16(d / 64, MH_LN)
 #undef MH_LN
   return hipGetLastError();
 }

@@ -127,7 +127,8 @@ class HipEngine:
         rc = self._lib.marian_hip_engine_create(C.byref(structs.model), C.byref(self._limits),
                                                 device, C.byref(handle))
         if rc != _lib.OK:
-            raise _ERRORS.get(rc, BackendError)(f"engine creation failed ({rc})")
+            raise _ERRORS.get(rc, BackendError)(
+                f"engine creation failed ({rc}): {self._lib.marian_hip_last_op_error().decode(errors='replace')}")
         self._h = handle
         self.geometry = model.geometry
 
@@ -168,6 +169,34 @@ class HipEngine:
         if rc != _lib.OK:
             self._raise(rc)
         return BatchOutput(out[:n.value].copy(), out_offs.copy())
+
+    def translate_probe(self, tokens, offsets, max_output_tokens, flags: int = 0,
+                        probe_step: int = 0):
+        """translate_token_ids plus what the engine computed below the token
+        level: (BatchOutput, encoder states [T, d], logits [B, V] of decode step
+        probe_step, active [B] = rows whose logits were captured)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        offs = np.ascontiguousarray(offsets, np.uint32)
+        lim = np.ascontiguousarray(max_output_tokens, np.uint32)
+        B = max(0, offs.shape[0] - 1)
+        if lim.shape[0] != B:
+            raise InvalidInput("max_output_tokens does not match packed batch")
+        g = self.geometry
+        cap = int(np.minimum(lim.astype(np.int64), 4096).sum())
+        out = np.zeros(max(cap, 1), np.int32)
+        out_offs = np.zeros(max(offs.shape[0], 1), np.uint32)
+        enc = np.zeros((max(toks.size, 1), g.dim), np.float32)
+        logits = np.zeros((max(B, 1), g.vocab), np.float32)
+        active = np.zeros(max(B, 1), np.uint8)
+        n = C.c_size_t(0)
+        rc = self._lib.marian_hip_translate_probe(
+            self._h, _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+            _ptr(lim), flags, _ptr(out), out.size, _ptr(out_offs), C.byref(n), int(probe_step),
+            _ptr(enc), _ptr(logits), _ptr(active))
+        if rc != _lib.OK:
+            self._raise(rc)
+        return (BatchOutput(out[:n.value].copy(), out_offs.copy()), enc[:toks.size], logits[:B],
+                active[:B].astype(bool))
 
     TIME_STEPS, TIME_KERNELS = 1, 2
 

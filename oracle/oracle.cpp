@@ -619,7 +619,8 @@ bool select_token(const oracle_model* m, const Geometry& g, const float* state, 
 // Greedy decoding of one sentence given its encoder output.
 bool decode_sentence(const oracle_model* m, const Geometry& g, const float* enc, size_t L,
                      uint32_t limit, uint32_t flags, int order, Pool* pool, Scratch& s,
-                     std::vector<int32_t>& out, uint32_t stop_after, float* last_logits) {
+                     std::vector<int32_t>& out, uint32_t stop_after, int64_t probe_step,
+                     float* probe_logits, bool* probed) {
   const auto& pos = positions_for(m->dim);
   const size_t d = g.d;
   std::vector<std::vector<float>> ckv(g.Ld, std::vector<float>(L * 2 * d));
@@ -661,9 +662,10 @@ bool decode_sentence(const oracle_model* m, const Geometry& g, const float* enc,
       x.swap(x2);
     }
     int32_t token;
-    const bool want_logits = last_logits && stop_after && t + 1 == stop_after;
-    if (!select_token(m, g, x.data(), flags, &token, want_logits ? last_logits : nullptr))
+    const bool want_logits = probe_logits && (int64_t)t == probe_step;
+    if (!select_token(m, g, x.data(), flags, &token, want_logits ? probe_logits : nullptr))
       return false;
+    if (want_logits && probed) *probed = true;
     out.push_back(token);
     prev = token;
     if (stop_after && t + 1 == stop_after) break;
@@ -793,6 +795,18 @@ int oracle_translate(const oracle_model* model, const int32_t* tokens, size_t n_
                      const uint32_t* max_output_tokens, const oracle_limits* limits,
                      uint32_t flags, int order, int threads, int32_t* out_tokens, size_t out_cap,
                      uint32_t* out_offsets, size_t* out_len, char* err, size_t err_cap) {
+  return oracle_translate_probe(model, tokens, n_tokens, offsets, n_offsets, max_output_tokens,
+                                limits, flags, order, threads, out_tokens, out_cap, out_offsets,
+                                out_len, err, err_cap, UINT32_MAX, nullptr, nullptr, nullptr);
+}
+
+int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
+                           const uint32_t* offsets, size_t n_offsets,
+                           const uint32_t* max_output_tokens, const oracle_limits* limits,
+                           uint32_t flags, int order, int threads, int32_t* out_tokens,
+                           size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
+                           size_t err_cap, uint32_t probe_step, float* enc_out,
+                           float* logits_out, uint8_t* active_out) {
   Err e{err, err_cap};
   if (!model_ok(model)) return e.fail(-2, "invalid model description");
   std::vector<uint32_t> lim;
@@ -814,10 +828,16 @@ int oracle_translate(const oracle_model* model, const int32_t* tokens, size_t n_
       const size_t b = next.fetch_add(1);
       if (b >= B) return;
       const size_t L = offsets[b + 1] - offsets[b];
-      if (!encode_sentence(model, g, tokens + offsets[b], L, order, nullptr, s, enc) ||
-          !decode_sentence(model, g, enc.data(), L, lim[b], flags, order, nullptr, s, gen[b], 0,
-                           nullptr))
+      if (!encode_sentence(model, g, tokens + offsets[b], L, order, nullptr, s, enc)) {
         ok = false;
+        continue;
+      }
+      if (enc_out) std::memcpy(enc_out + (size_t)offsets[b] * g.d, enc.data(), L * g.d * sizeof(float));
+      bool probed = false;
+      if (!decode_sentence(model, g, enc.data(), L, lim[b], flags, order, nullptr, s, gen[b], 0,
+                           probe_step, logits_out ? logits_out + b * g.V : nullptr, &probed))
+        ok = false;
+      if (active_out) active_out[b] = probed ? 1 : 0;
     }
   };
   for (int i = 1; i < T; ++i) workers.emplace_back(work);
@@ -861,7 +881,7 @@ int oracle_last_step_logits(const oracle_model* model, const int32_t* tokens, si
   std::vector<int32_t> out;
   if (!encode_sentence(model, g, tokens, n_tokens, order, nullptr, s, enc)) return -2;
   if (!decode_sentence(model, g, enc.data(), n_tokens, steps, flags | ORACLE_FLAG_IGNORE_EOS,
-                       order, nullptr, s, out, steps, logits))
+                       order, nullptr, s, out, steps, (int64_t)steps - 1, logits, nullptr))
     return -2;
   return 0;
 }

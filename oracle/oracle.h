@@ -155,6 +155,18 @@ int oracle_translate(const oracle_model* model, const int32_t* tokens, size_t n_
                      size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
                      size_t err_cap);
 
+/* oracle_translate that also returns intermediate values (each may be NULL):
+ * enc_out[n_tokens, dim] the final encoder state of every packed row;
+ * logits_out[B, vocab] the logits of decode step probe_step (0-based) of every
+ * row that reaches it (masked ids -inf), active_out[B] = 1 for those rows. */
+int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
+                           const uint32_t* offsets, size_t n_offsets,
+                           const uint32_t* max_output_tokens, const oracle_limits* limits,
+                           uint32_t flags, int order, int threads, int32_t* out_tokens,
+                           size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
+                           size_t err_cap, uint32_t probe_step, float* enc_out,
+                           float* logits_out, uint8_t* active_out);
+
 /* Same contract, executed the way the reference x86 engine schedules the work
  * (padded encoder batch, all rows every decode step, AVX2 madd GEMM row-split
  * over `threads` when rows>1 && rows*N >= 8192, scalar output scoring).  Its

@@ -86,6 +86,9 @@ _SIG = {
                                                       C.POINTER(Limits), C.c_uint32, C.c_int,
                                                       C.c_int, _P, _SZ, _P, C.POINTER(_SZ),
                                                       C.c_char_p, _SZ]),
+    "oracle_translate_probe": (C.c_int, [C.POINTER(Model), _P, _SZ, _P, _SZ, _P, C.POINTER(Limits),
+                                         C.c_uint32, C.c_int, C.c_int, _P, _SZ, _P, C.POINTER(_SZ),
+                                         C.c_char_p, _SZ, C.c_uint32, _P, _P, _P]),
     "oracle_encode": (C.c_int, [C.POINTER(Model), _P, _SZ, _P, _SZ, C.c_int, C.c_int, _P]),
     "oracle_last_step_logits": (C.c_int, [C.POINTER(Model), _P, _SZ, C.c_uint32, C.c_uint32,
                                           C.c_int, _P]),
@@ -180,6 +183,35 @@ def translate(model: OracleModel, tokens, offsets, max_output_tokens, limits: di
     if rc != 0:
         raise OracleError(rc, err.value.decode())
     return [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(offs.size - 1)]
+
+
+def translate_probe(model: OracleModel, tokens, offsets, max_output_tokens, limits: dict,
+                    flags=0, probe_step=0, order=REFERENCE, threads=8):
+    """translate() plus the final encoder states [T, d] and, for decode step
+    probe_step, the logits [B, V] of the rows that reach it (active[b] = 1)."""
+    lib = load()
+    toks = np.ascontiguousarray(tokens, np.int32)
+    offs = np.ascontiguousarray(offsets, np.uint32)
+    req = np.ascontiguousarray(max_output_tokens, np.uint32)
+    B = offs.size - 1
+    g = model.geometry
+    cap = int(np.minimum(req.astype(np.int64), 4096).sum()) + 1
+    out = np.zeros(cap, np.int32)
+    out_offs = np.zeros(offs.size, np.uint32)
+    n = C.c_size_t(0)
+    err = C.create_string_buffer(512)
+    lim = make_limits(limits)
+    enc = np.zeros((max(toks.size, 1), g.dim), np.float32)
+    logits = np.zeros((max(B, 1), g.vocab), np.float32)
+    active = np.zeros(max(B, 1), np.uint8)
+    rc = lib.oracle_translate_probe(
+        C.byref(model.struct), _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+        _ptr(req), C.byref(lim), flags, order, threads, _ptr(out), cap, _ptr(out_offs), C.byref(n),
+        err, 512, probe_step, _ptr(enc), _ptr(logits), _ptr(active))
+    if rc != 0:
+        raise OracleError(rc, err.value.decode())
+    rows = [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(B)]
+    return rows, enc[:toks.size], logits[:B], active[:B].astype(bool)
 
 
 def expf(x: float, order=REFERENCE) -> float:

@@ -76,3 +76,15 @@ def test_engine_rejects_bad_model_without_touching_the_device(pkg):
     m = pkg.seeded_model(seed=1, geometry=g)
     with pytest.raises(pkg.ModelError):
         pkg.HipEngine(m)
+
+
+def test_library_build_id_matches_sources(pkg):
+    import importlib.util
+
+    from conftest import ROOT
+
+    spec = importlib.util.spec_from_file_location("marian_build_lib",
+                                                  ROOT / "marian-edge_amd" / "build_lib.py")
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    assert pkg._lib.build_id() == b.source_hash(), "libmarian_hip.so is stale: rebuild it"
