@@ -33,6 +33,10 @@
  *   marian_hip_attention       attention_into tensor.rs:251-318
  *   marian_hip_vocab_argmax    select_token q8_engine.rs:749-790
  *   marian_hip_positions       sinusoidal_positions crates/marian-model/src/position.rs:5-21
+ * The op-level entry points that need intermediate device buffers keep them
+ * in library scratch, one set per device: use one stream per device at a time
+ * (calls that overlap on one device race on that scratch).
+ * marian_hip_vocab_argmax_noalloc has no reference counterpart (see there).
  *
  * Threading: one engine handle belongs to one owner thread (the reference
  * backend is deliberately !Send, backend.rs:3-6).  The engine owns one HIP
@@ -277,6 +281,22 @@ int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_
                             const int8_t* emb, const float* emb_mult, const float* bias,
                             int64_t V, uint32_t flags, int32_t* token, float* logits,
                             void* stream);
+
+/* marian_hip_vocab_argmax without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that forbid hipMalloc).  Same
+ * arguments and results; the per-row partial argmax keys live in a fixed
+ * 1 MiB device array of the library (131072 keys, one per row and 128-column
+ * vocabulary group: M * ceil(V / 128) <= 131072, e.g. up to 524 rows at
+ * V = 32000; larger inputs return MARIAN_HIP_ERR_INVALID_INPUT and launch
+ * nothing).  Each device holds its own copy of that array until the process
+ * ends, and every call on a device shares it: calls that overlap on one
+ * device (two streams, two threads) race and must be serialized by the
+ * caller.  Nothing in it needs clearing between calls. */
+int marian_hip_vocab_argmax_noalloc(const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                                    const int8_t* emb, const float* emb_mult, const float* bias,
+                                    int64_t V, uint32_t flags, int32_t* token, float* logits,
+                                    void* stream);
 
 /* Host: sinusoidal position table [count, dim] (fp32), as the engine builds it. */
 int marian_hip_positions(uint32_t dim, uint32_t count, float* out);

@@ -27,7 +27,9 @@ int op_status(hipError_t e, const char* what) {
 
 // Library scratch for the op-level entry points that need intermediate
 // buffers (quantized activations, argmax partials).  Grow-only, one set per
-// device; calls that overlap on one device race on it.
+// device; calls that overlap on one device race on it (the entry points are
+// for one stream per device at a time).  A buffer that grows is freed only
+// after the whole device is idle, so no kernel on any stream still uses it.
 struct OpScratch {
   void* p[4] = {nullptr, nullptr, nullptr, nullptr};
   size_t cap[4] = {0, 0, 0, 0};
@@ -35,14 +37,15 @@ struct OpScratch {
 std::mutex g_scratch_mu;
 OpScratch g_scratch[64];
 
-void* scratch(int which, size_t bytes, hipStream_t s) {
+void* op_scratch(int which, size_t bytes, hipStream_t s) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
   std::lock_guard<std::mutex> g(g_scratch_mu);
   OpScratch& S = g_scratch[dev];
   if (S.cap[which] >= bytes && S.p[which]) return S.p[which];
   if (S.p[which]) {
-    hipStreamSynchronize(s);
+    (void)s;
+    hipDeviceSynchronize();
     hipFree(S.p[which]);
     S.p[which] = nullptr;
     S.cap[which] = 0;
@@ -54,6 +57,65 @@ void* scratch(int which, size_t bytes, hipStream_t s) {
   }
   S.cap[which] = want;
   return S.p[which];
+}
+
+// Partial argmax keys of marian_hip_vocab_argmax_noalloc, one u64 per (row,
+// 128-column vocabulary group): a fixed 1 MiB that each device holds for the
+// life of the process.  In host code `scratch` is only a handle for
+// hipGetSymbolAddress; kernels get the device address it returns.
+constexpr size_t kNoAllocPartials = 131072;
+static __device__ __align__(256) uint64_t scratch[kNoAllocPartials];
+
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[64] = {};  // device address of `scratch` on each device
+
+// Address of `scratch` on the current device, looked up on the first call
+// with that device current and kept; nullptr if the lookup fails.
+void* noalloc_scratch() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      op_status(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+      return nullptr;
+    }
+    g_noalloc_ptr[dev] = ptr;
+  }
+  return g_noalloc_ptr[dev];
+}
+
+// Vocabulary projection + argmax with the partial keys in `part` (M * nparts).
+int vocab_argmax_into(const int8_t* xq, const float* xa, int64_t M, int64_t K, const int8_t* emb,
+                      const float* emb_mult, const float* bias, int64_t V, uint32_t flags,
+                      int32_t* token, float* logits, uint64_t* part, int nparts, hipStream_t s) {
+  GemmArgs g;
+  g.A = xq;
+  g.a = xa;
+  g.lda = K;
+  g.M = (int)M;
+  g.K = (int)K;
+  g.W = emb;
+  g.wmult = emb_mult;
+  g.bias = bias;
+  g.N = (int)V;
+  Epilogue e;
+  e.partials = part;
+  e.partial_ld = nparts;
+  e.logits = logits;
+  e.ldl = V;
+  e.flags = flags;
+  int rc = op_status(launch_gemm_skinny(g, EPI_ARGMAX, e, s), "vocab_argmax gemm");
+  if (rc) return rc;
+  return op_status(launch_argmax_reduce(part, nparts, (int)M, token, s), "vocab_argmax reduce");
+}
+
+bool vocab_args_ok(const int8_t* xq, const float* xa, int64_t M, int64_t K, const int8_t* emb,
+                   const float* emb_mult, const float* bias, int64_t V, const int32_t* token) {
+  return xq && xa && emb && emb_mult && bias && token && M >= 0 && K > 0 && K % 64 == 0 &&
+         K <= 512 && V > 0 && M <= INT32_MAX && V <= INT32_MAX;
 }
 
 }  // namespace
@@ -80,8 +142,8 @@ int marian_hip_q8_linear(const float* x, const int8_t* xq, const float* xa, int6
   if (M == 0) return MARIAN_HIP_OK;
   hipStream_t s = (hipStream_t)stream;
   if (x) {
-    int8_t* q = (int8_t*)scratch(0, (size_t)M * K, s);
-    float* a = (float*)scratch(1, (size_t)M * 4, s);
+    int8_t* q = (int8_t*)op_scratch(0, (size_t)M * K, s);
+    float* a = (float*)op_scratch(1, (size_t)M * 4, s);
     if (!q || !a) return op_status(hipErrorOutOfMemory, "q8_linear scratch");
     int rc = op_status(launch_quantize_rows(x, K, (int)M, nullptr, (int)K, q, K, a, err, s),
                        "q8_linear quantize");
@@ -145,7 +207,7 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
   if (n_seqs > 0 && rows > 0 && max_keys <= 256) {
     // Packed self-attention: the query-tile list first (library scratch).
     const int cap = seq_tiles_bound((int)rows, (int)n_seqs);
-    uint32_t* tiles = (uint32_t*)scratch(3, (1 + 2 * (size_t)cap) * 4, (hipStream_t)stream);
+    uint32_t* tiles = (uint32_t*)op_scratch(3, (1 + 2 * (size_t)cap) * 4, (hipStream_t)stream);
     if (!tiles) return op_status(hipErrorOutOfMemory, "attention scratch");
     const int rc = op_status(launch_seq_tiles(cu_k, (int)n_seqs, tiles, cap, (hipStream_t)stream),
                              "attention tiles");
@@ -159,33 +221,33 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
 int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_t K,
                             const int8_t* emb, const float* emb_mult, const float* bias, int64_t V,
                             uint32_t flags, int32_t* token, float* logits, void* stream) {
-  if (!xq || !xa || !emb || !emb_mult || !bias || !token || M < 0 || K <= 0 || K % 64 ||
-      K > 512 || V <= 0 || M > INT32_MAX || V > INT32_MAX)
-    return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (!vocab_args_ok(xq, xa, M, K, emb, emb_mult, bias, V, token)) return MARIAN_HIP_ERR_INVALID_INPUT;
   if (M == 0) return MARIAN_HIP_OK;
   hipStream_t s = (hipStream_t)stream;
   const int nparts = argmax_groups((int)V, (int)K);
-  uint64_t* part = (uint64_t*)scratch(2, (size_t)M * nparts * 8, s);
+  uint64_t* part = (uint64_t*)op_scratch(2, (size_t)M * nparts * 8, s);
   if (!part) return op_status(hipErrorOutOfMemory, "vocab_argmax scratch");
-  GemmArgs g;
-  g.A = xq;
-  g.a = xa;
-  g.lda = K;
-  g.M = (int)M;
-  g.K = (int)K;
-  g.W = emb;
-  g.wmult = emb_mult;
-  g.bias = bias;
-  g.N = (int)V;
-  Epilogue e;
-  e.partials = part;
-  e.partial_ld = nparts;
-  e.logits = logits;
-  e.ldl = V;
-  e.flags = flags;
-  int rc = op_status(launch_gemm_skinny(g, EPI_ARGMAX, e, s), "vocab_argmax gemm");
-  if (rc) return rc;
-  return op_status(launch_argmax_reduce(part, nparts, (int)M, token, s), "vocab_argmax reduce");
+  return vocab_argmax_into(xq, xa, M, K, emb, emb_mult, bias, V, flags, token, logits, part, nparts, s);
+}
+
+int marian_hip_vocab_argmax_noalloc(const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                                    const int8_t* emb, const float* emb_mult, const float* bias,
+                                    int64_t V, uint32_t flags, int32_t* token, float* logits,
+                                    void* stream) {
+  if (!vocab_args_ok(xq, xa, M, K, emb, emb_mult, bias, V, token)) return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (M == 0) return MARIAN_HIP_OK;
+  const int nparts = argmax_groups((int)V, (int)K);
+  if ((uint64_t)M * (uint64_t)nparts > kNoAllocPartials) {
+    char msg[160];
+    snprintf(msg, sizeof msg, "vocab_argmax_noalloc: %lld rows x %d groups exceed the %zu partial keys",
+             (long long)M, nparts, kNoAllocPartials);
+    g_op_error = msg;
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  }
+  uint64_t* part = (uint64_t*)noalloc_scratch();
+  if (!part) return MARIAN_HIP_ERR_DEVICE;
+  return vocab_argmax_into(xq, xa, M, K, emb, emb_mult, bias, V, flags, token, logits, part, nparts,
+                           (hipStream_t)stream);
 }
 
 // ---- util ------------------------------------------------------------------
