@@ -29,7 +29,10 @@
  *   marian_hip_quantize_rows   quantize_symmetric_u8_into q8_gemm.rs:569-590
  *   marian_hip_q8_linear       Q8Linear::run_into q8_gemm.rs:380-448 (+ the
  *                              exact kernel q8_avx2.rs:125-229)
+ *   marian_hip_q8_linear_static  the same with the static activation multiplier
+ *                              of the reference's Q8 models (legacy_q8.rs:544-552)
  *   marian_hip_residual_layer_norm  residual_layer_norm_into tensor.rs:132-155
+ *   marian_hip_ssru_layer_norm ssru_update_layer_norm_into tensor.rs:184-218
  *   marian_hip_attention       attention_into tensor.rs:251-318
  *   marian_hip_vocab_argmax    select_token q8_engine.rs:749-790
  *   marian_hip_positions       sinusoidal_positions crates/marian-model/src/position.rs:5-21
@@ -253,6 +256,27 @@ int marian_hip_q8_linear(const float* x, const int8_t* xq, const float* xa, int6
                          int64_t K, const int8_t* w, const float* w_mult, const float* bias,
                          int64_t N, int relu, int32_t* out_i32, float* out_f32, int* err,
                          void* stream);
+
+/* marian_hip_q8_linear with the reference's static activation multiplier
+ * (Q8Linear::run_into with activation_quant_mult, q8_gemm.rs:380-448 and
+ * quantize_symmetric_u8_into :569-590; the model's per-tensor QuantMultA,
+ * legacy_q8.rs:544-552): q = clamp(rne(x * act_mult), -127, 127) for every row,
+ * y = acc * (1 / (act_mult * w_mult[n])) + bias[n].  act_mult must be finite
+ * and positive; a non-finite x sets *err. */
+int marian_hip_q8_linear_static(const float* x, int64_t M, int64_t K, float act_mult,
+                                const int8_t* w, const float* w_mult, const float* bias, int64_t N,
+                                int relu, int32_t* out_i32, float* out_f32, int* err, void* stream);
+
+/* SSRU update + LayerNorm of the reference's SSRU decoder
+ * (ssru_update_layer_norm_into, crates/marian-cpu/src/tensor.rs:184-218):
+ * per element gate = 1 / (1 + exp(-forget)), state = gate * state +
+ * (1 - gate) * cand (in place); out = LN(relu(state) + residual) (eps 1e-6),
+ * optionally quantized per row into q / a.  All rows [rows, dim], dim a
+ * multiple of 64 up to 1024. */
+int marian_hip_ssru_layer_norm(const float* cand, const float* forget, float* state,
+                               const float* residual, const float* scale, const float* bias,
+                               int64_t rows, int64_t dim, float* out, int8_t* q, float* a, int* err,
+                               void* stream);
 
 /* out = LN(x + r) (eps 1e-6), optional int8 quantization of out (q, a). */
 int marian_hip_residual_layer_norm(const float* x, const float* r, const float* scale,

@@ -24,7 +24,9 @@ Cases:
     clipped to [4, 256], 8 heads x 64, Q/K/V fp32 and bf16, as packed
     self-attention (the query-tile list, then the key-staging kernel).
     Algorithmic bytes 3 * T * d * b + 4 * T * d (Q, K, V in their type, fp32
-    O out).
+    O out).  Also as cross-attention at decode shape: one query per sentence
+    (its first row's Q) over the sentence's packed K/V, one wave per (query,
+    head); bytes 2 * T * d * b + B * d * b + 4 * B * d.
 """
 
 from __future__ import annotations
@@ -94,6 +96,23 @@ def run(out_path: str, reps: int) -> None:
         cases.append(dict(label=f"attention {'bf16' if bf16 else 'fp32'} T={T}", kind="attention",
                           T=T, calls=reps, kernels_per_call=2,
                           bytes=3 * T * d * b + 4 * T * d, flops=4 * d * int((np.diff(cu.astype(np.int64)) ** 2).sum())))
+        for t in (dq, dk, dv, dseq, dcu, do):
+            t.free()
+        # Cross-attention at decode shape: one query per sentence over its
+        # packed keys and values (one wave per (query, head)).
+        B = len(cu) - 1
+        qc = hq[cu[:-1].astype(np.int64)]
+        dq, dk, dv = (D.from_host(t) for t in (qc, hk, hv))
+        dseq, dcu = D.from_host(np.arange(B, dtype=np.int32)), D.from_host(cu)
+        do = D((B, d), np.float32)
+        for _ in range(reps):
+            dev.attention(dq, dk, dv, dseq, dcu, do, heads=d // 64, max_keys=lmax, bf16=bf16,
+                          packed_self=False)
+        dev.synchronize()
+        # K and V of every sentence read once, B queries in, B fp32 rows out.
+        cases.append(dict(label=f"cross-attention {'bf16' if bf16 else 'fp32'} B={B} T={T}",
+                          kind="attention", T=T, calls=reps, kernels_per_call=1,
+                          bytes=2 * T * d * b + B * d * b + 4 * B * d, flops=4 * d * T))
         for t in (dq, dk, dv, dseq, dcu, do):
             t.free()
     Path(out_path).parent.mkdir(parents=True, exist_ok=True)

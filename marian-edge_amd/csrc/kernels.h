@@ -111,6 +111,17 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
                               int rows, const int* rows_dev, int d, float* out, int8_t* q,
                               float* a, int* err, hipStream_t s);
 
+// Quantization with one static activation multiplier for every row (a[row] =
+// mult); rejects a multiplier that is not finite and positive.
+hipError_t launch_quantize_rows_static(const float* x, int64_t ldx, int rows, int cols, float mult,
+                                       int8_t* q, int64_t ldq, float* a, int* err, hipStream_t s);
+
+// SSRU update + LayerNorm: state <- gate * state + (1 - gate) * cand with
+// gate = sigmoid(forget); out = LN(relu(state) + resid) (+ quantization).
+hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, const float* resid,
+                          const float* g, const float* b, int rows, int d, float* out, int8_t* q,
+                          float* a, int* err, hipStream_t s);
+
 struct EmbedArgs {
   const int8_t* emb = nullptr;
   const float* emb_mult = nullptr;

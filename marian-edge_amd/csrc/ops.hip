@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -168,6 +169,52 @@ int marian_hip_q8_linear(const float* x, const int8_t* xq, const float* xa, int6
   e.ldi = N;
   e.relu = relu;
   return op_status(launch_gemm_store(g, e, s), "q8_linear gemm");
+}
+
+int marian_hip_q8_linear_static(const float* x, int64_t M, int64_t K, float act_mult,
+                                const int8_t* w, const float* w_mult, const float* bias, int64_t N,
+                                int relu, int32_t* out_i32, float* out_f32, int* err, void* stream) {
+  if (!x || M < 0 || K <= 0 || K % 64 || N <= 0 || !w || !w_mult || !bias || M > INT32_MAX ||
+      N > INT32_MAX || K > INT32_MAX || (!out_i32 && !out_f32) || !(act_mult > 0.0f) ||
+      !std::isfinite(act_mult))
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (M == 0) return MARIAN_HIP_OK;
+  hipStream_t s = (hipStream_t)stream;
+  int8_t* q = (int8_t*)op_scratch(0, (size_t)M * K, s);
+  float* a = (float*)op_scratch(1, (size_t)M * 4, s);
+  if (!q || !a) return op_status(hipErrorOutOfMemory, "q8_linear_static scratch");
+  int rc = op_status(launch_quantize_rows_static(x, K, (int)M, (int)K, act_mult, q, K, a, err, s),
+                     "q8_linear_static quantize");
+  if (rc) return rc;
+  GemmArgs g;
+  g.A = q;
+  g.a = a;
+  g.lda = K;
+  g.M = (int)M;
+  g.K = (int)K;
+  g.W = w;
+  g.wmult = w_mult;
+  g.bias = bias;
+  g.N = (int)N;
+  Epilogue e;
+  e.out = out_f32;
+  e.ldo = N;
+  e.out_i32 = out_i32;
+  e.ldi = N;
+  e.relu = relu;
+  return op_status(launch_gemm_store(g, e, s), "q8_linear_static gemm");
+}
+
+int marian_hip_ssru_layer_norm(const float* cand, const float* forget, float* state,
+                               const float* residual, const float* scale, const float* bias,
+                               int64_t rows, int64_t dim, float* out, int8_t* q, float* a, int* err,
+                               void* stream) {
+  if (!cand || !forget || !state || !residual || !scale || !bias || !out || rows < 0 ||
+      rows > INT32_MAX || dim <= 0 || dim % 64 || dim > 1024 || (q && !a))
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  return op_status(launch_ssru_ln(cand, forget, state, residual, scale, bias, (int)rows, (int)dim, out,
+                                  q, a, err, (hipStream_t)stream),
+                   "ssru_layer_norm");
 }
 
 int marian_hip_residual_layer_norm(const float* x, const float* r, const float* scale,

@@ -32,6 +32,27 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float* x, int64_t l
   if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
+// Quantization with a static per-tensor activation multiplier (the reference's
+// own mode, quantize_symmetric_u8_into q8_gemm.rs:569-590 with the model's
+// QuantMultA, legacy_q8.rs:544-552): q = clamp(rne(x * mult), -127, 127), and
+// a[row] = mult so the GEMM epilogue dequantizes with 1 / (mult * w).
+__global__ __launch_bounds__(256) void k_quantize_rows_static(const float* x, int64_t ldx, int rows,
+                                                              int cols, float mult, int8_t* q,
+                                                              int64_t ldq, float* a, int* err) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* xr = x + (int64_t)row * ldx;
+  int8_t* qr = q + (int64_t)row * ldq;
+  bool bad = false;
+  for (int i = lane; i < cols; i += 64) {
+    const float v = xr[i];
+    bad |= !isfinite(v);
+    qr[i] = (int8_t)quantize_one(v, mult);
+  }
+  if (lane == 0) a[row] = mult;
+  if (__any(bad) && lane == 0 && err) *err = 1;
+}
+
 // Same, for rows of V4*256 values held in registers: one 16-byte load and one
 // 4-byte store per lane per 256 columns.
 template <int V4>
@@ -68,41 +89,18 @@ __global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_
   if (__any(bad) && lane == 0 && err) *err = 1;
 }
 
-// out = LN(y + r), optionally quantized for the next GEMM.  One wave per row.
-// normalize_row (tensor.rs:372-385) sums the row strictly left to right, so
-// the wave parks z = y + r in LDS and every lane folds the row sequentially;
-// the centred squares are formed lane-parallel and parked the same way.
+// LayerNorm of one row z (lane holds z[lane + 64 j]) by one wave, stored to
+// out (and quantized into q / a when q is set): normalize_row
+// (tensor.rs:372-385) sums the row strictly left to right, so the wave parks z
+// in LDS (zr, D floats) and every lane folds the row sequentially; the centred
+// squares are formed lane-parallel and parked the same way.
 template <int PER>
-__global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float* r,
-                                                     const float* gamma, const float* beta,
-                                                     int rows, const int* rows_dev, float* out,
-                                                     int8_t* q, float* a, int* err) {
+__device__ __forceinline__ void ln_row_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
+                                            const float (&bv)[PER], int row, int lane, float* out,
+                                            int8_t* q, float* a, int* err) {
   constexpr int D = PER * 64;
-  __shared__ __attribute__((aligned(16))) float sZ[4][D];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + wave;
-  if (row >= rows) return;  // uniform per wave; the waves share no barrier
-  // Rows below the host bound are always backed by memory, so every load is
-  // issued before the device row count arrives.
-  const float* yr = y + (int64_t)row * D;
-  const float* rr = r + (int64_t)row * D;
-  float yv[PER], rv[PER], gv[PER], bv[PER];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    yv[j] = yr[lane + 64 * j];
-    rv[j] = rr[lane + 64 * j];
-    gv[j] = gamma[lane + 64 * j];
-    bv[j] = beta[lane + 64 * j];
-  }
-  const int n = rows_dev ? *rows_dev : rows;
-  if (row >= n) return;
-  float* zr = sZ[wave];
-  float z[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    z[j] = yv[j] + rv[j];
-    zr[lane + 64 * j] = z[j];
-  }
+  for (int j = 0; j < PER; ++j) zr[lane + 64 * j] = z[j];
   // The wave's LDS writes complete before its reads below.
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   __builtin_amdgcn_wave_barrier();
@@ -136,6 +134,75 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
     if (lane == 0) a[row] = sc;
   }
   if (__any(bad) && lane == 0 && err) *err = 1;
+}
+
+// out = LN(y + r), optionally quantized for the next GEMM.  One wave per row.
+template <int PER>
+__global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float* r,
+                                                     const float* gamma, const float* beta,
+                                                     int rows, const int* rows_dev, float* out,
+                                                     int8_t* q, float* a, int* err) {
+  constexpr int D = PER * 64;
+  __shared__ __attribute__((aligned(16))) float sZ[4][D];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= rows) return;  // uniform per wave; the waves share no barrier
+  // Rows below the host bound are always backed by memory, so every load is
+  // issued before the device row count arrives.
+  const float* yr = y + (int64_t)row * D;
+  const float* rr = r + (int64_t)row * D;
+  float yv[PER], rv[PER], gv[PER], bv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    yv[j] = yr[lane + 64 * j];
+    rv[j] = rr[lane + 64 * j];
+    gv[j] = gamma[lane + 64 * j];
+    bv[j] = beta[lane + 64 * j];
+  }
+  const int n = rows_dev ? *rows_dev : rows;
+  if (row >= n) return;
+  float z[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) z[j] = yv[j] + rv[j];
+  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err);
+}
+
+// SSRU state update + LayerNorm (ssru_update_layer_norm_into, tensor.rs:184-218,
+// the reference's SSRU decoder, q8_engine.rs:394-408).  Per element: gate =
+// 1 / (1 + exp(-f)) with the C library's expf, s' = gate * s + (1 - gate) * c
+// (each product, the difference and the sum rounded on their own), the state
+// is overwritten with s'; then out = LN(relu(s') + residual) (relu_residual
+// :718-724, relu as max(x, 0) with NaN and -0.0 giving +0.0) with the
+// sequential folds of normalize_row.  One wave per row.
+__constant__ uint64_t kRowsExp2Tab[32] = {MH_EXP2_TABLE_32};
+template <int PER>
+__global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float* forget, float* state,
+                                                 const float* resid, const float* gamma,
+                                                 const float* beta, int rows, float* out, int8_t* q,
+                                                 float* a, int* err) {
+  constexpr int D = PER * 64;
+  __shared__ __attribute__((aligned(16))) float sZ[4][D];
+  __shared__ uint64_t sTab[32];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (threadIdx.x < 32) sTab[threadIdx.x] = kRowsExp2Tab[threadIdx.x];
+  __syncthreads();
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const int64_t base = (int64_t)row * D;
+  float z[PER], gv[PER], bv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int64_t i = base + lane + 64 * j;
+    const float c = cand[i], f = forget[i], st = state[i], r = resid[i];
+    gv[j] = gamma[lane + 64 * j];
+    bv[j] = beta[lane + 64 * j];
+    const float e = ref_expf(-f, sTab);
+    const float gate = 1.0f / (1.0f + e);
+    const float next = gate * st + (1.0f - gate) * c;
+    state[i] = next;
+    z[j] = (next > 0.0f ? next : 0.0f) + r;
+  }
+  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err);
 }
 
 // The same LayerNorm for rows of width 512 (decode and encoder): one two-wave
@@ -450,6 +517,28 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
   hipLaunchKernelGGL(k_residual_ln<P>, grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err)
   MH_PER_DISPATCH_16(d / 64, MH_LN)
 #undef MH_LN
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows_static(const float* x, int64_t ldx, int rows, int cols, float mult,
+                                       int8_t* q, int64_t ldq, float* a, int* err, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (!(mult > 0.0f) || !(mult < __builtin_huge_valf())) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_quantize_rows_static, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, rows, cols,
+                     mult, q, ldq, a, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, const float* resid,
+                          const float* g, const float* b, int rows, int d, float* out, int8_t* q,
+                          float* a, int* err, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (d % 64) return hipErrorInvalidValue;
+  const dim3 grid((rows + 3) / 4), block(256);
+#define MH_SSRU(P) \
+  hipLaunchKernelGGL(k_ssru_ln<P>, grid, block, 0, s, cand, forget, state, resid, g, b, rows, out, q, a, err)
+  MH_PER_DISPATCH_16(d / 64, MH_SSRU)
+#undef MH_SSRU
   return hipGetLastError();
 }
 

@@ -100,6 +100,24 @@ def q8_linear(x: DeviceArray | None, w: DeviceArray, mult: DeviceArray, bias: De
         _p(out_f32), _p(err), stream), "q8_linear")
 
 
+def q8_linear_static(x: DeviceArray, act_mult: float, w: DeviceArray, mult: DeviceArray,
+                     bias: DeviceArray, out_i32: DeviceArray | None, out_f32: DeviceArray | None,
+                     relu: bool = False, err: DeviceArray | None = None, stream=None) -> None:
+    M, K = x.shape
+    N = w.shape[0]
+    _lib.check(_lib.load().marian_hip_q8_linear_static(
+        x.ptr, M, K, float(act_mult), w.ptr, mult.ptr, bias.ptr, N, int(relu), _p(out_i32),
+        _p(out_f32), _p(err), stream), "q8_linear_static")
+
+
+def ssru_layer_norm(cand, forget, state, residual, scale, bias, out, q=None, a=None, err=None,
+                    stream=None) -> None:
+    rows, dim = cand.shape
+    _lib.check(_lib.load().marian_hip_ssru_layer_norm(
+        cand.ptr, forget.ptr, state.ptr, residual.ptr, scale.ptr, bias.ptr, rows, dim, out.ptr,
+        _p(q), _p(a), _p(err), stream), "ssru_layer_norm")
+
+
 def residual_layer_norm(x, r, scale, bias, out, q=None, a=None, err=None, stream=None) -> None:
     rows, dim = x.shape
     _lib.check(_lib.load().marian_hip_residual_layer_norm(

@@ -767,6 +767,50 @@ int oracle_linear_forward(const float* x, size_t M, size_t K, const oracle_linea
   return 0;
 }
 
+// Q8Linear::run_into with the model's static activation multiplier
+// (q8_gemm.rs:380-448, quantize_symmetric_u8_into :569-590): every row is
+// quantized with act_mult, then the exact GEMM and dequant of the dynamic path.
+int oracle_linear_forward_static(const float* x, size_t M, size_t K, const oracle_linear* lin,
+                                 size_t N, float act_mult, int relu, float* y, int32_t* acc,
+                                 int8_t* qa, int threads) {
+  if (!(std::isfinite(act_mult) && act_mult > 0.0f)) return -1;
+  std::vector<int8_t> q(M * K);
+  for (size_t i = 0; i < M * K; ++i) {
+    if (!std::isfinite(x[i])) return -1;  // :578-583 rejects non-finite input
+    q[i] = quantize_one(x[i], act_mult);
+  }
+  std::vector<int32_t> ac(M * N);
+  Pool pool(threads);
+  if (!gemm_i8(&pool, q.data(), M, K, lin->weight, N, ac.data())) return -2;
+  std::vector<float> a(M, act_mult);
+  dequant(ac.data(), a.data(), M, lin, N, relu != 0, y);
+  if (acc) std::memcpy(acc, ac.data(), M * N * sizeof(int32_t));
+  if (qa) std::memcpy(qa, q.data(), M * K);
+  return 0;
+}
+
+// ssru_update_layer_norm_into (tensor.rs:184-218): per element
+// gate = 1 / (1 + exp(-f)), state = gate * state + (1 - gate) * cand; then
+// out = normalize_row(relu(state) + residual) (relu_residual :718-724; the x86
+// relu is _mm256_max_ps(x, 0), which gives +0.0 for NaN and -0.0).
+int oracle_ssru_layer_norm(const float* cand, const float* forget, float* state,
+                           const float* residual, const float* scale, const float* bias,
+                           size_t rows, size_t d, int order, float* out) {
+  if (!rows || !d) return 0;
+  std::vector<float> z(d), zero(d, 0.0f);
+  for (size_t m = 0; m < rows; ++m) {
+    for (size_t i = 0; i < d; ++i) {
+      const size_t k = m * d + i;
+      const float gate = 1.0f / (1.0f + exp_op(-forget[k], order));
+      const float next = gate * state[k] + (1.0f - gate) * cand[k];
+      state[k] = next;
+      z[i] = next > 0.0f ? next : 0.0f;
+    }
+    residual_ln(z.data(), residual + m * d, scale, bias, 1, d, order, out + m * d);
+  }
+  return 0;
+}
+
 int oracle_residual_layer_norm(const float* x, const float* r, const float* scale,
                                const float* bias, size_t rows, size_t d, int order, float* out) {
   residual_ln(x, r, scale, bias, rows, d, order, out);

@@ -16,6 +16,8 @@
  *                       crates/marian-cpu/src/q8_avx2.rs:125-358 (x86 kernel)
  *   dequant + bias      crates/marian-cpu/src/q8_gemm.rs:438-446
  *   residual LayerNorm  crates/marian-cpu/src/tensor.rs:132-155, 372-425
+ *   SSRU + LayerNorm    crates/marian-cpu/src/tensor.rs:184-218, 718-724
+ *   static activation   crates/marian-cpu/src/legacy_q8.rs:544-552 (QuantMultA)
  *   attention           crates/marian-cpu/src/tensor.rs:251-318, 594-637, 745-754
  *   positions           crates/marian-model/src/position.rs:5-21
  *   embedding           crates/marian-cpu/src/q8_engine.rs:53-74, 586-630
@@ -131,6 +133,19 @@ int32_t oracle_dot_u8_i8(const uint8_t* a, const int8_t* w, size_t n);
 int oracle_linear_forward(const float* x, size_t M, size_t K, const oracle_linear* lin,
                           size_t N, int relu, float* y, int32_t* acc, int8_t* qa, float* a,
                           int threads);
+
+/* Q8 linear with a static activation multiplier for every row (the
+ * reference's own mode): q = clamp(rne(x*act_mult), -127, 127).  -1 on a
+ * non-finite input or multiplier.  acc/qa may be NULL. */
+int oracle_linear_forward_static(const float* x, size_t M, size_t K, const oracle_linear* lin,
+                                 size_t N, float act_mult, int relu, float* y, int32_t* acc,
+                                 int8_t* qa, int threads);
+
+/* SSRU update + LayerNorm (tensor.rs:184-218): state updated in place,
+ * out = LN(relu(state) + residual). */
+int oracle_ssru_layer_norm(const float* cand, const float* forget, float* state,
+                           const float* residual, const float* scale, const float* bias,
+                           size_t rows, size_t d, int order, float* out);
 
 /* out = LN(x + r) per row of length d (eps 1e-6). */
 int oracle_residual_layer_norm(const float* x, const float* r, const float* scale,

@@ -77,6 +77,9 @@ _SIG = {
     "oracle_linear_forward": (C.c_int, [_P, _SZ, _SZ, C.POINTER(Linear), _SZ, C.c_int, _P, _P,
                                         _P, _P, C.c_int]),
     "oracle_residual_layer_norm": (C.c_int, [_P, _P, _P, _P, _SZ, _SZ, C.c_int, _P]),
+    "oracle_linear_forward_static": (C.c_int, [_P, _SZ, _SZ, C.POINTER(Linear), _SZ, C.c_float,
+                                               C.c_int, _P, _P, _P, C.c_int]),
+    "oracle_ssru_layer_norm": (C.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, C.c_int, _P]),
     "oracle_attention": (C.c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, C.c_int, _P,
                                    _SZ]),
     "oracle_translate": (C.c_int, [C.POINTER(Model), _P, _SZ, _P, _SZ, _P, C.POINTER(Limits),
@@ -297,6 +300,39 @@ def linear_forward(x: np.ndarray, weight, mult, bias, relu=False, threads=8):
     if rc != 0:
         raise OracleError(rc, "non-finite activation or accumulator overflow")
     return y, acc, q, a
+
+
+def linear_forward_static(x: np.ndarray, weight, mult, bias, act_mult: float, relu=False,
+                          threads=8):
+    """Q8 linear with one static activation multiplier: (y, acc, q)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(weight, np.int8)
+    mult = np.ascontiguousarray(mult, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.zeros((M, N), np.float32)
+    acc = np.zeros((M, N), np.int32)
+    q = np.zeros((M, K), np.int8)
+    lin = Linear(_ptr(w), _ptr(mult), _ptr(bias))
+    rc = load().oracle_linear_forward_static(_ptr(x), M, K, C.byref(lin), N, act_mult, int(relu),
+                                             _ptr(y), _ptr(acc), _ptr(q), threads)
+    if rc != 0:
+        raise OracleError(rc, "non-finite input, invalid multiplier or accumulator overflow")
+    return y, acc, q
+
+
+def ssru_layer_norm(cand, forget, state, residual, scale, bias, order=REFERENCE):
+    """Returns (out, updated state); the inputs are not modified."""
+    cand, forget, residual = (np.ascontiguousarray(t, np.float32) for t in (cand, forget, residual))
+    st = np.array(state, np.float32, copy=True, order="C")
+    scale = np.ascontiguousarray(scale, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    rows, d = cand.shape
+    out = np.zeros_like(cand)
+    load().oracle_ssru_layer_norm(_ptr(cand), _ptr(forget), _ptr(st), _ptr(residual), _ptr(scale),
+                                  _ptr(bias), rows, d, order, _ptr(out))
+    return out, st
 
 
 def residual_layer_norm(x, r, scale, bias, order=REFERENCE):

@@ -210,6 +210,33 @@ def test_varlen_attention_full_workload(pkg, orc, dev, bf16):
     _attention_case(pkg, orc, dev, q, k, v, cu, 8, bf16)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_cross_attention_decode_shape(pkg, orc, dev, bf16):
+    """The 256-sentence attention workload as cross-attention: one query per
+    sentence (cu_q != cu_k) over that sentence's packed keys and values."""
+    q, k, v, cu = pkg.attention_inputs()
+    B = len(cu) - 1
+    lens = np.diff(cu.astype(np.int64))
+    qc = np.ascontiguousarray(q[cu[:-1].astype(np.int64)])
+    if bf16:
+        qh, kh, vh = (pkg.synthetic.bf16_round(x) for x in (qc, k, v))
+        qc, k, v = (pkg.synthetic.bf16_to_f32(x) for x in (qh, kh, vh))
+        dq, dk, dv = (dev.DeviceArray.from_host(x) for x in (qh, kh, vh))
+    else:
+        dq, dk, dv = (dev.DeviceArray.from_host(x) for x in (qc, k, v))
+    cu_q = np.arange(B + 1, dtype=np.uint32)
+    ref = orc.attention(qc, k, v, cu_q, cu, 8)
+    print(f"cross-attention B={B} T={k.shape[0]} bf16={bf16}", flush=True)
+    out = dev.DeviceArray.zeros((B, 512), np.float32)
+    dev.attention(dq, dk, dv, dev.DeviceArray.from_host(np.arange(B, dtype=np.int32)),
+                  dev.DeviceArray.from_host(cu), out, heads=8, max_keys=int(lens.max()), bf16=bf16,
+                  packed_self=False)
+    dev.synchronize()
+    got = out.host()
+    assert rel_err(got, ref) <= REL_TOL
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "cross-attention not bit-identical"
+
+
 def test_attention_edges(pkg, orc, dev):
     rng = np.random.default_rng(14)
     # single key, 64/65 keys (chunk boundary), a 1000-key row (large variant),
@@ -321,3 +348,68 @@ def test_vocab_argmax_nonfinite_logits_follow_strict_scan(pkg, dev):
     b[50] = 0.0
     b[100] = -0.0
     assert run(b) == [50, 50]
+
+
+# ---- static activation multiplier (the reference's Q8 models) ---------------------
+@pytest.mark.parametrize("K,N", [(512, 1536), (2048, 512), (512, 32000)])
+@pytest.mark.parametrize("M", [1, 8, 64, 256])
+def test_q8_linear_static_matches_oracle(pkg, orc, dev, M, K, N):
+    a, w, mult, bias = pkg.gemm_inputs(M, K, N, seed=9)
+    act = float(np.float32(127) / np.float32(np.abs(a).max() * 0.75))  # a few saturate
+    print(f"q8_linear_static M={M} K={K} N={N} act_mult={act:.4f}", flush=True)
+    y_ref, acc_ref, _ = orc.linear_forward_static(a, w, mult, bias, act, threads=16)
+    da, dw, dm, db = (dev.DeviceArray.from_host(x) for x in (a, w, mult, bias))
+    di = dev.DeviceArray.zeros((M, N), np.int32)
+    df = dev.DeviceArray.zeros((M, N), np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.q8_linear_static(da, act, dw, dm, db, di, df, err=err)
+    dev.synchronize()
+    assert err.host()[0] == 0
+    assert np.array_equal(di.host(), acc_ref), "i32 accumulators differ"
+    assert np.array_equal(df.host().view(np.uint32), y_ref.view(np.uint32))
+
+
+def test_q8_linear_static_reference_kat(pkg, dev, kats):
+    """q8_gemm.rs:620-668 on the GPU: K padded to 64 with zero activations
+    and weights (quantized to 0, so the accumulators are unchanged)."""
+    k = kats["linear_integer_oracle"]
+    w = np.zeros((2, 64), np.int8)
+    w[:, :4] = np.array(k["weights_out_in"], np.int8)
+    mult = np.full(2, k["weight_mult"], np.float32)
+    bias = np.array(k["bias"], np.float32)
+    dw, dm, db = (dev.DeviceArray.from_host(x) for x in (w, mult, bias))
+    for rows in k["inputs"]:
+        x = np.zeros((len(rows), 64), np.float32)
+        x[:, :4] = np.array(rows, np.float32)
+        q = np.clip(np.rint(x * 4.0), -127, 127).astype(np.int64)
+        expected = (q @ w.T.astype(np.int64)).astype(np.float32) / np.float32(32.0) + bias
+        dx = dev.DeviceArray.from_host(x)
+        df = dev.DeviceArray.zeros((len(rows), 2), np.float32)
+        dev.q8_linear_static(dx, k["activation_mult"], dw, dm, db, None, df)
+        dev.synchronize()
+        assert np.array_equal(df.host(), expected)
+
+
+@pytest.mark.parametrize("d", [64, 384, 512])
+@pytest.mark.parametrize("rows", [1, 7, 300])
+def test_ssru_layer_norm_matches_oracle(pkg, orc, dev, rows, d):
+    rng = np.random.default_rng(rows * 1000 + d)
+    c, f, s, r = (rng.standard_normal((rows, d)).astype(np.float32) * 2 for _ in range(4))
+    f[0, :8] = [np.inf, -np.inf, 0.0, -0.0, 88.7, -88.7, 104.0, -104.0]  # gate saturation edges
+    s[0, 8:12] = [-0.0, 0.0, -1e-30, 1e-30]
+    g = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(d)).astype(np.float32)
+    out_ref, st_ref = orc.ssru_layer_norm(c, f, s, r, g, b)
+    q_ref, a_ref = orc.quantize_rows(out_ref)
+    print(f"ssru rows={rows} d={d}", flush=True)
+    dc, dfg, ds, dr, dg, dbb = (dev.DeviceArray.from_host(x) for x in (c, f, s, r, g, b))
+    out = dev.DeviceArray.zeros((rows, d), np.float32)
+    q = dev.DeviceArray.zeros((rows, d), np.int8)
+    a = dev.DeviceArray.zeros(rows, np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.ssru_layer_norm(dc, dfg, ds, dr, dg, dbb, out, q=q, a=a, err=err)
+    dev.synchronize()
+    assert err.host()[0] == 0
+    assert np.array_equal(ds.host().view(np.uint32), st_ref.view(np.uint32)), "state differs"
+    assert np.array_equal(out.host().view(np.uint32), out_ref.view(np.uint32)), "output differs"
+    assert np.array_equal(q.host(), q_ref) and np.array_equal(a.host(), a_ref)

@@ -351,3 +351,74 @@ def test_summation_order_sensitivity(pkg, orc, full_model):
     drift = float(np.max(np.abs(enc_c - enc_r) / np.maximum(np.abs(enc_r), 1.0)))
     print(f"encoder output drift between summation orders: {drift:.3g}")
     assert 0 < drift < 0.1
+
+
+# ---- static activation multiplier (the reference's own Q8 mode) ----------------
+def test_linear_static_kat(orc, kats):
+    """q8_gemm.rs:620-668 run as written: static activation multiplier 4,
+    weight multiplier 8, expected acc / 32 + bias for 1-4 rows."""
+    k = kats["linear_integer_oracle"]
+    w = np.array(k["weights_out_in"], np.int8)
+    bias = np.array(k["bias"], np.float32)
+    mult = np.full(2, k["weight_mult"], np.float32)
+    for rows in k["inputs"]:
+        x = np.array(rows, np.float32)
+        y, acc, q = orc.linear_forward_static(x, w, mult, bias, k["activation_mult"])
+        u8 = orc.quantize_static_u8(x.ravel(), k["activation_mult"]).reshape(x.shape)
+        assert np.array_equal(q.astype(np.int64), u8.astype(np.int64) - 127)
+        expected_acc = q.astype(np.int64) @ w.T.astype(np.int64)
+        assert np.array_equal(acc, expected_acc)
+        assert np.array_equal(y, expected_acc.astype(np.float32) / np.float32(32.0) + bias)
+    with pytest.raises(orc.OracleError):
+        orc.linear_forward_static(np.array([[np.inf, 0, 0, 0]], np.float32), w, mult, bias, 4.0)
+    with pytest.raises(orc.OracleError):
+        orc.linear_forward_static(np.zeros((1, 4), np.float32), w, mult, bias, 0.0)
+
+
+def test_linear_static_matches_int64_brute_force(orc):
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((9, 192)) * 3).astype(np.float32)
+    w = rng.integers(-127, 128, size=(70, 192)).astype(np.int8)
+    mult = rng.uniform(20, 900, size=70).astype(np.float32)
+    bias = (rng.standard_normal(70) * 0.1).astype(np.float32)
+    a = np.float32(127) / np.float32(np.abs(x).max() * 0.5)  # some values saturate at +-127
+    y, acc, q = orc.linear_forward_static(x, w, mult, bias, float(a), relu=True)
+    qe = np.clip(np.rint(x.astype(np.float64) * np.float64(a)), -127, 127)
+    assert np.array_equal(q, qe.astype(np.int8))
+    assert np.abs(q).max() == 127
+    ae = qe.astype(np.int64) @ w.T.astype(np.int64)
+    assert np.array_equal(acc, ae)
+    inv = (np.float32(1) / (a * mult)).astype(np.float32)
+    assert np.array_equal(y, np.maximum(ae.astype(np.float32) * inv + bias, np.float32(0)))
+
+
+# ---- SSRU (the reference's decoder recurrence) -------------------------------------
+def test_ssru_kat(orc, kats):
+    k = kats["ssru_state_update"]
+    out, st = orc.ssru_layer_norm([k["candidate"]], [k["forget"]], [k["state"]], [k["residual"]],
+                                  k["scale"], k["bias"])
+    assert st[0].tolist() == k["expected_state"]
+    assert np.allclose(out[0], k["expected_output"], atol=k["tolerance"], rtol=0)
+
+
+def test_ssru_closed_forms(orc):
+    rng = np.random.default_rng(21)
+    rows, d = 5, 128
+    c, f, s, r = (rng.standard_normal((rows, d)).astype(np.float32) for _ in range(4))
+    g = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(d)).astype(np.float32)
+    f[0] = np.inf    # gate 1: the state is kept
+    f[1] = -np.inf   # gate 0: the state becomes the candidate
+    f[2] = 0.0       # gate 1/2
+    out, st = orc.ssru_layer_norm(c, f, s, r, g, b)
+    assert np.array_equal(st[0], s[0]) and np.array_equal(st[1], c[1])
+    assert np.array_equal(st[2], np.float32(0.5) * s[2] + np.float32(0.5) * c[2])
+    # float64 closed form of the whole update
+    gate = 1.0 / (1.0 + np.exp(-f.astype(np.float64)))
+    s64 = gate * s + (1 - gate) * c
+    assert np.allclose(st, s64, rtol=1e-6, atol=1e-6)
+    z = np.maximum(s64, 0) + r
+    mu = z.mean(1, keepdims=True)
+    var = ((z - mu) ** 2).mean(1, keepdims=True)
+    want = (z - mu) / np.sqrt(var + 1e-6) * g + b
+    assert np.abs(out - want).max() < 1e-5
