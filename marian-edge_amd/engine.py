@@ -249,10 +249,20 @@ class HipEngine:
 
 
 class HipBackend:
-    """TranslationBackend surface at the token level (backend.rs:7-38)."""
+    """TranslationBackend surface at the token level (backend.rs:7-38).
 
-    def __init__(self, engine: HipEngine):
+    duplicate_batch_width: how many physical rows a logical input repeated by
+    the scheduler may occupy (translate_batch_with_repetitions, backend.rs:25-37;
+    the Metal backend materializes up to this many copies to reach its device's
+    occupancy knee, crates/marian-metal/src/backend.rs:319-354).  The default 1
+    materializes none: a decode step here costs about the same from 1 to 4 rows
+    and more above, so copies of a row only add work."""
+
+    def __init__(self, engine: HipEngine, duplicate_batch_width: int = 1):
+        if duplicate_batch_width < 1:
+            raise InvalidInput("duplicate_batch_width must be at least 1")
         self.engine = engine
+        self.duplicate_batch_width = int(duplicate_batch_width)
 
     def info(self) -> dict:
         return self.engine.info()
@@ -263,15 +273,28 @@ class HipBackend:
     def translate_token_batch(self, sentences: list[list[int]], max_output_tokens: list[int],
                               repetitions: list[int] | None = None, flags: int = 0):
         """One output per logical input, like translate_batch_with_repetitions
-        (backend.rs:30-37); repetitions do not change the result."""
-        if repetitions is not None and len(repetitions) != len(sentences):
-            raise InvalidInput("repetitions do not match inputs")
-        offs = np.zeros(len(sentences) + 1, np.uint32)
-        offs[1:] = np.cumsum([len(s) for s in sentences])
-        toks = np.concatenate([np.asarray(s, np.int32) for s in sentences]) if sentences else \
+        (backend.rs:30-37): logical input i is run as min(repetitions[i],
+        duplicate_batch_width) physical rows and the first copy's output is
+        returned; repetitions do not change the result."""
+        if repetitions is None:
+            repetitions = [1] * len(sentences)
+        if len(repetitions) != len(sentences) or any(int(c) <= 0 for c in repetitions):
+            raise InvalidInput("logical batch repetitions are malformed")
+        if len(max_output_tokens) != len(sentences):
+            raise InvalidInput("max_output_tokens does not match inputs")
+        physical, limits, first = [], [], []
+        for sent, lim, count in zip(sentences, max_output_tokens, repetitions):
+            first.append(len(physical))
+            for _ in range(min(int(count), self.duplicate_batch_width)):
+                physical.append(sent)
+                limits.append(lim)
+        offs = np.zeros(len(physical) + 1, np.uint32)
+        offs[1:] = np.cumsum([len(s) for s in physical])
+        toks = np.concatenate([np.asarray(s, np.int32) for s in physical]) if physical else \
             np.zeros(0, np.int32)
-        out = self.engine.translate_token_ids(toks, offs, max_output_tokens, flags)
+        out = self.engine.translate_token_ids(toks, offs, limits, flags)
         rows = out.rows()
-        if len(rows) != len(sentences):
-            raise InferenceError("backend returned a different number of outputs")
-        return rows
+        if len(rows) != len(physical):
+            raise InferenceError(f"backend returned {len(rows)} physical outputs for "
+                                 f"{len(physical)} rows")
+        return [rows[i] for i in first]

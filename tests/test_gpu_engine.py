@@ -148,3 +148,14 @@ def test_timing_modes_keep_outputs_and_trace_launches(pkg, engine):
     # most 128 cached keys, both attention sublayers of both layers run as blocks
     per_step = np.bincount(kt["step"][blocks], minlength=steps)
     assert np.all(per_step[:128] == 4) and np.all(per_step <= 4)
+
+
+def test_backend_repetitions_on_device(pkg, engine):
+    b = pkg.ragged_batch(seed=51, n=6)
+    sents = [b.tokens[b.offsets[i]:b.offsets[i + 1]].tolist() for i in range(6)]
+    lims = b.max_output_tokens.tolist()
+    plain = pkg.HipBackend(engine).translate_token_batch(sents, lims)
+    wide = pkg.HipBackend(engine, duplicate_batch_width=3)
+    out = wide.translate_token_batch(sents, lims, repetitions=[1, 4, 2, 1, 3, 1])
+    assert out == plain
+    assert engine.last_stats()["max_active_rows"] == 1 + 3 + 2 + 1 + 3 + 1
