@@ -80,6 +80,26 @@ def _cpu_worker(rows):
     return ntok, time.perf_counter() - t0, done_ms
 
 
+def host_info(cores_used: int) -> dict:
+    """The CPU the baseline ran on: visible cores, model, and the oracle's compiler."""
+    import __graft_entry__ as ge
+
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"nproc": usable, "cpu_count": os.cpu_count(), "cpu_model": model,
+            "cores_used": cores_used, "compiler": ge.load_oracle().build_info()}
+
+
 def cpu_baseline(pkg, model, batch, cores: int, threads: int = 4):
     import __graft_entry__ as ge
 
@@ -267,6 +287,17 @@ def main(argv=None):
     cpu = None
     if not args.no_cpu_baseline and args.workload == "ragged":
         cpu = cpu_baseline(pkg, model, batch, args.cpu_cores)
+        # The same batch under the reference's own limits (length factor 2, at
+        # most 256 steps, padded-cell cap): fewer generated tokens per row.
+        capped = pkg.synthetic.Batch(batch.name, batch.tokens, batch.offsets,
+                                     batch.max_output_tokens, batch.flags,
+                                     dict(pkg.REFERENCE_LIMITS))
+        cap = cpu_baseline(pkg, model, capped, args.cpu_cores)
+        cpu["capped_limits"] = {"value": cap["value"], "unit": "tokens/s", "p50_ms": cap["p50_ms"],
+                                "wall_s": cap["wall_s"],
+                                "limits": "reference caps: factor 2, 256 steps, batch 256, "
+                                          "256 source tokens, 65536 padded cells"}
+        cpu["host"] = host_info(cpu["cores"])
 
     r = run_translate_bench(pkg, model, batch, args.steps, args.warmup)
     ms = statistics.mean(r["dev_ms"])

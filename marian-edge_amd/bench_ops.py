@@ -184,6 +184,120 @@ def pmc_summary(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_
     return res
 
 
+def counter_summary(csv_paths: list[str], trace_csv: str | None = None) -> dict:
+    """Dispatch-averaged counter values per kernel from rocprofv3 --pmc
+    counter_collection.csv files (any counters), with two derived figures
+    where their counters were collected:
+      * dram_read_share: TCC_EA0_RDREQ_DRAM_sum / TCC_EA0_RDREQ_sum, the share
+        of the L2's read requests that go out to the memory controller;
+      * mfma_util: SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), the
+        matrix cores' busy fraction over the dispatch (1024 SIMDs: 256 CUs x 4);
+    and, with a kernel trace of the same command, the int8 MFMA throughput
+    SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 ops / average duration."""
+    vals: dict = {}
+    for path in csv_paths:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"].replace("mh::(anonymous namespace)::", "").replace("void ", "")
+                name = name.split("(")[0]
+                key = (r.get("Dispatch_Id") or r.get("Correlation_Id"), r["Counter_Name"])
+                vals.setdefault(name, {}).setdefault(r["Counter_Name"], {})
+                d = vals[name][r["Counter_Name"]]
+                d[key] = d.get(key, 0.0) + float(r["Counter_Value"])
+    durations: dict = {}
+    if trace_csv:
+        with open(trace_csv, newline="") as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"].replace("mh::(anonymous namespace)::", "").replace("void ", "")
+                durations.setdefault(name.split("(")[0], []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    out = {}
+    for name, counters in sorted(vals.items()):
+        row = {c: round(statistics.mean(v.values()), 1) for c, v in counters.items()}
+        row["dispatches"] = max(len(v) for v in counters.values())
+        if "TCC_EA0_RDREQ_DRAM_sum" in row and row.get("TCC_EA0_RDREQ_sum"):
+            row["dram_read_share"] = round(row["TCC_EA0_RDREQ_DRAM_sum"] / row["TCC_EA0_RDREQ_sum"], 4)
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in row and row.get("GRBM_GUI_ACTIVE"):
+            row["mfma_util"] = round(row["SQ_VALU_MFMA_BUSY_CYCLES"] / (row["GRBM_GUI_ACTIVE"] * 1024), 5)
+        if "SQ_INSTS_VALU_MFMA_MOPS_I8" in row and durations.get(name):
+            us = statistics.mean(durations[name])
+            ops = row["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
+            row["avg_us"] = round(us, 3)
+            row["int8_tops"] = round(ops / (us * 1e-6) / 1e12, 2)
+            row["int8_frac_of_5pops"] = round(ops / (us * 1e-6) / INT8_PEAK, 5)
+        out[name] = row
+    return out
+
+
+def _short(name: str) -> str:
+    return name.replace("mh::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+
+def stats_table(stats_csv: str, batches: int) -> str:
+    """Markdown table of a rocprofv3 --stats kernel_stats.csv."""
+    with open(stats_csv, newline="") as f:
+        rows = list(csv.DictReader(f))
+    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    out = ["| kernel | calls | calls / batch | avg us | min us | max us | total ms | % |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        out.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {int(r['Calls']) / batches:.1f} | "
+                   f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                   f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                   f"{float(r['Percentage']):.1f} |")
+    out.append(f"\nTotal kernel time {tot / 1e6:.3f} ms over {batches} batches = "
+               f"{tot / 1e6 / batches:.3f} ms per batch.")
+    return "\n".join(out)
+
+
+def step_breakdown(trace_csv: str, steps_per_batch: int, batches: int, rows_at: list[int],
+                   first_batch: int = 0) -> str:
+    """Per decode step of a bench.py kernel trace: the kernels in launch order
+    and their average durations, grouped by the number of active rows.  A
+    step ends with k_finalize; the encoder's kernels are dropped."""
+    with open(trace_csv, newline="") as f:
+        ks = [( _short(r["Kernel_Name"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+              for r in csv.DictReader(f)]
+    ks.sort(key=lambda k: k[1])
+    steps, cur = [], []
+    for k in ks:
+        if k[0].startswith("__amd"):
+            continue
+        cur.append(k)
+        if k[0] == "k_finalize":
+            steps.append(cur)
+            cur = []
+    enc = ("k_gemm_tile", "k_attn_tiles", "k_seq_tiles", "k_embed", "k_quantize_rows_v4<2>")
+    groups = [(1, 1), (2, 4), (5, 8), (9, 16), (17, 32), (33, 64), (65, 4096)]
+    agg: dict = {}
+    for b in range(first_batch, first_batch + batches):
+        for t in range(steps_per_batch):
+            st = steps[b * steps_per_batch + t]
+            if t == 0:  # the encoder runs before step 0
+                i = max(j for j, k in enumerate(st) if k[0].startswith(enc)) + 1 if any(
+                    k[0].startswith(enc) for k in st) else 0
+                st = st[i:]
+            g = next(g for g in groups if g[0] <= rows_at[t] <= g[1])
+            a = agg.setdefault(g, {"steps": 0, "sum": 0.0, "kernels": {}})
+            a["steps"] += 1
+            a["sum"] += sum(k[2] - k[1] for k in st) / 1000.0
+            for i, k in enumerate(st):
+                a["kernels"].setdefault((i, k[0]), []).append((k[2] - k[1]) / 1000.0)
+    out = []
+    for g in groups:
+        if g not in agg:
+            continue
+        a = agg[g]
+        label = f"{g[0]}" if g[0] == g[1] else f"{g[0]}-{g[1]}"
+        out.append(f"\n**{label} active rows** ({a['steps']} steps; kernel time per step "
+                   f"{a['sum'] / a['steps']:.1f} us)\n")
+        out.append("| # | kernel | avg us | launches |")
+        out.append("|---:|---|---:|---:|")
+        for (i, name), d in sorted(a["kernels"].items()):
+            out.append(f"| {i} | `{name}` | {statistics.mean(d):.2f} | {len(d)} |")
+    return "\n".join(out)
+
+
 def summarize(run_path: str, trace_path: str) -> str:
     spec = json.loads(Path(run_path).read_text())
     rows = []
@@ -234,6 +348,15 @@ def main(argv=None) -> int:
     pm.add_argument("copy_fetch_csv")
     pm.add_argument("copy_write_csv")
     pm.add_argument("--copy-mb", type=int, default=64)
+    st = sub.add_parser("stats")
+    st.add_argument("stats_csv")
+    st.add_argument("--batches", type=int, required=True)
+    sb = sub.add_parser("steps", help="per-step kernel breakdown of a bench.py trace (ragged batch)")
+    sb.add_argument("trace_csv")
+    sb.add_argument("--batches", type=int, default=6, help="untimed-event batches at the start")
+    cc = sub.add_parser("counters")
+    cc.add_argument("csv", nargs="+")
+    cc.add_argument("--trace", default=None)
     a = ap.parse_args(argv)
     if a.cmd == "run":
         run(a.out, a.reps)
@@ -242,6 +365,16 @@ def main(argv=None) -> int:
     elif a.cmd == "pmc":
         print(json.dumps(pmc_summary(a.fetch_csv, a.write_csv, a.copy_fetch_csv, a.copy_write_csv,
                                      a.copy_mb), indent=1))
+    elif a.cmd == "stats":
+        print(stats_table(a.stats_csv, a.batches))
+    elif a.cmd == "steps":
+        pkg = _load_package()
+        b = pkg.ragged_batch()
+        lim = b.max_output_tokens.astype(np.int64)
+        n = int(lim.max())
+        print(step_breakdown(a.trace_csv, n, a.batches, [int((lim > t).sum()) for t in range(n)]))
+    elif a.cmd == "counters":
+        print(json.dumps(counter_summary(a.csv, a.trace), indent=1))
     else:
         print(summarize(a.run_json, a.trace_csv))
     return 0

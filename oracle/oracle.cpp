@@ -703,6 +703,13 @@ extern "C" {
 
 float oracle_expf(float x, int order) { return exp_op(x, order); }
 
+#ifndef ORACLE_COMPILER
+#define ORACLE_COMPILER "unknown"
+#endif
+const char* oracle_build_info(void) {
+  return ORACLE_COMPILER ", -O3 -ffp-contract=off, AVX2 integer kernels (target attribute, no AVX-512)";
+}
+
 float oracle_row_sum(const float* x, size_t n, int order) { return row_sum(x, n, order); }
 
 // position.rs:5-21: f_i = exp(-i * ln(10000) / (half-1)) in f32;

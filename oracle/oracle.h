@@ -106,6 +106,9 @@ typedef struct {
   uint64_t max_padded_cells;     /* [65536] batch * Lmax^2 */
 } oracle_limits;
 
+/* Compiler and flags this library was built with (for the CPU-baseline record). */
+const char* oracle_build_info(void);
+
 /* ---- elementary ops ---------------------------------------------------- */
 float oracle_expf(float x, int order);
 float oracle_row_sum(const float* x, size_t n, int order);

@@ -66,6 +66,7 @@ class Limits(C.Structure):
 
 _P, _SZ = C.c_void_p, C.c_size_t
 _SIG = {
+    "oracle_build_info": (C.c_char_p, []),
     "oracle_expf": (C.c_float, [C.c_float, C.c_int]),
     "oracle_row_sum": (C.c_float, [_P, _SZ, C.c_int]),
     "oracle_positions": (C.c_int, [C.c_uint32, C.c_uint32, _P]),
@@ -215,6 +216,10 @@ def translate_probe(model: OracleModel, tokens, offsets, max_output_tokens, limi
         raise OracleError(rc, err.value.decode())
     rows = [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(B)]
     return rows, enc[:toks.size], logits[:B], active[:B].astype(bool)
+
+
+def build_info() -> str:
+    return load().oracle_build_info().decode()
 
 
 def expf(x: float, order=REFERENCE) -> float:
