@@ -321,6 +321,71 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
+// End of a decode step for at most kFinalizeWaveRows rows (the decode tail):
+// the same work as k_finalize by one wave, with no LDS and no barriers.  The
+// rows' partials are reduced four rows at a time (the lanes stride a row's
+// partials, then a wave maximum); lane i then owns row i for the stop rules,
+// and the kept rows are compacted in order with a ballot and a prefix count.
+constexpr int kFinalizeWaveRows = 16;
+__global__ __launch_bounds__(64) void k_finalize_wave(FinalizeArgs f) {
+  const int lane = threadIdx.x;
+  const int ub = min(f.rows_ub, kFinalizeWaveRows);
+  const int np = f.nparts;
+  // Every lane loads a row's state (rows below the host bound are allocated),
+  // together with the partials, before the device row count is needed.
+  const int rl = min(lane, ub - 1);
+  const int slot = f.rows.slot[rl];
+  const int64_t kv0 = f.rows.kv0[rl];
+  const int64_t src0 = f.rows.src0[rl];
+  const int srcn = f.rows.srcn[rl];
+  const uint32_t lim = f.rows.limit[rl];
+  uint64_t mine = 0;
+  for (int r0 = 0; r0 < ub; r0 += 4) {
+    const uint64_t* p0 = f.partials + (int64_t)r0 * np;
+    const uint64_t* p1 = f.partials + (int64_t)min(r0 + 1, ub - 1) * np;
+    const uint64_t* p2 = f.partials + (int64_t)min(r0 + 2, ub - 1) * np;
+    const uint64_t* p3 = f.partials + (int64_t)min(r0 + 3, ub - 1) * np;
+    uint64_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll 4
+    for (int p = lane; p < np; p += 64) {
+      b0 = umax64(b0, p0[p]);
+      b1 = umax64(b1, p1[p]);
+      b2 = umax64(b2, p2[p]);
+      b3 = umax64(b3, p3[p]);
+    }
+    b0 = wave_max_u64(b0);
+    b1 = wave_max_u64(b1);
+    b2 = wave_max_u64(b2);
+    b3 = wave_max_u64(b3);
+    mine = lane == r0 ? b0 : lane == r0 + 1 ? b1 : lane == r0 + 2 ? b2 : lane == r0 + 3 ? b3 : mine;
+  }
+  const int n_dev = *f.n_active;
+  const int n = min(n_dev, ub);
+  const int32_t tok = argmax_key_id(mine);
+  bool keep = false;
+  if (lane < n) {
+    f.out_tok[kv0 + f.step] = tok;
+    f.count[slot] = (uint32_t)f.step + 1u;
+    const bool fin = (tok == 0 && !(f.flags & 1u)) || (uint32_t)f.step + 1u >= lim;
+    keep = !fin;
+  }
+  const uint64_t kept = __ballot(keep);
+  const int pos = __popcll(kept & ((1ull << lane) - 1ull));  // kept rows before this one
+  if (keep) {
+    f.rows.slot[pos] = slot;
+    f.rows.kv0[pos] = kv0;
+    f.rows.src0[pos] = src0;
+    f.rows.srcn[pos] = srcn;
+    f.rows.limit[pos] = lim;
+    f.rows.prev[pos] = tok;
+  }
+  if (lane == 0) {
+    if (n_dev > ub && f.err) *f.err = 3;
+    if (f.active_hist) f.active_hist[f.step] = (uint32_t)n;
+    *f.n_active = __popcll(kept);
+  }
+}
+
 // End of a decode step: reduce each active row's argmax partials to a token,
 // append it, apply the stop rules of q8_engine.rs:383-390, 444-448, and
 // compact the active list in order.  One workgroup; rows <= kMaxRowsPerCall.
@@ -554,7 +619,10 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
 
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
   if (f.rows_ub <= 0 || f.rows_ub > kMaxRowsPerCall || f.nparts <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_finalize, dim3(1), dim3(1024), 0, s, f);
+  if (f.rows_ub <= kFinalizeWaveRows)
+    hipLaunchKernelGGL(k_finalize_wave, dim3(1), dim3(64), 0, s, f);
+  else
+    hipLaunchKernelGGL(k_finalize, dim3(1), dim3(1024), 0, s, f);
   return hipGetLastError();
 }
 
