@@ -35,6 +35,8 @@
  *   marian_hip_ssru_layer_norm ssru_update_layer_norm_into tensor.rs:184-218
  *   marian_hip_attention       attention_into tensor.rs:251-318
  *   marian_hip_vocab_argmax    select_token q8_engine.rs:749-790
+ *   marian_hip_candidate_argmax  select_token over a lexical shortlist's candidates
+ *                              (shortlist.rs:150-198)
  *   marian_hip_positions       sinusoidal_positions crates/marian-model/src/position.rs:5-21
  * The op-level entry points that need intermediate device buffers keep them
  * in library scratch, one set per device: use one stream per device at a time
@@ -305,6 +307,22 @@ int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_
                             const int8_t* emb, const float* emb_mult, const float* bias,
                             int64_t V, uint32_t flags, int32_t* token, float* logits,
                             void* stream);
+
+/* Output scoring over per-row candidate lists, e.g. a lexical shortlist's
+ * (select_token over LexicalShortlist::candidates, q8_engine.rs:749-790 and
+ * crates/marian-model/src/shortlist.rs:150-198): row m scores the vocabulary
+ * ids cand[cand_offsets[m] .. cand_offsets[m+1]) (device arrays, ids sorted
+ * ascending, every list non-empty) as logit = acc * (1/(xa[m]*mult[id])) +
+ * bias[id] and token[m] = the first maximum in list order (a row whose logits
+ * are all -inf or NaN gets its first candidate).  max_cands bounds every list's
+ * length (grid size).  logits (optional) receives each candidate's logit at
+ * its position in cand.  An id >= V sets *err (may be NULL) and is skipped.
+ * K a multiple of 64 up to 4096, M <= 65535. */
+int marian_hip_candidate_argmax(const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                                const int8_t* emb, const float* emb_mult, const float* bias,
+                                int64_t V, const uint32_t* cand, const uint32_t* cand_offsets,
+                                int64_t max_cands, int32_t* token, float* logits, int* err,
+                                void* stream);
 
 /* marian_hip_vocab_argmax without any device allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code

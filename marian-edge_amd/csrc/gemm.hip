@@ -687,7 +687,73 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e, int t
   }
 }
 
+// ---------------------------------------------------------------------------
+// Output scoring over a candidate list (the lexical shortlist's ids, sorted
+// ascending): select_token (q8_engine.rs:749-790) for row m scores only
+// cand[off[m] .. off[m+1]).  One workgroup per (row, 128 candidates): each of
+// its 4 waves gathers the embedding rows of two 16-candidate tiles (lane l
+// loads 16 bytes of row cand[16t + l % 16] per 64-wide k-step) and runs them
+// against the row's quantized state on the matrix cores (every row of the A
+// tile is the state, so output row 0 is the dot products).  Keys (logit,
+// inverted id) give the first maximum in candidate order, as the strict '>'
+// scan does; one key per workgroup goes to partials[m * nparts + chunk].
+// ---------------------------------------------------------------------------
+constexpr int kCandChunk = 128;
+__global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
+  __shared__ uint64_t sKey[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = blockIdx.y, chunk = blockIdx.x;
+  const int ksteps = c.K >> 6, kq = (lane >> 4) * 16;
+  const int64_t c0 = c.off[m], n = (int64_t)c.off[m + 1] - c0;
+  const int8_t* xr = c.xq + (int64_t)m * c.K;
+  const float am = c.xa[m];
+  uint64_t best = 0;
+  bool bad = false;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t i = (int64_t)chunk * kCandChunk + wave * 32 + t * 16 + (lane & 15);
+    bool live = i < n;
+    uint32_t id = live ? c.cand[c0 + i] : 0u;
+    if (id >= (uint32_t)c.V) {  // not a vocabulary id: reported, never scored
+      bad = true;
+      live = false;
+      id = 0u;
+    }
+    const int8_t* er = c.emb + (int64_t)id * c.K + kq;
+    v4i acc = zero4();
+    for (int s = 0; s < ksteps; ++s) {
+      const v4i a = *(const v4i*)(xr + kq + s * 64);
+      const v4i b = *(const v4i*)(er + s * 64);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+    }
+    // Lanes 0-15 hold row 0 (register 0) for candidates 16t + lane.
+    if (lane < 16 && live) {
+      const float y = dequant(acc[0], am, c.mult[id], c.bias[id]);
+      if (c.logits) c.logits[c0 + i] = y;
+      const uint64_t k = argmax_key(y, id);
+      best = k > best ? k : best;
+    }
+  }
+  if (__any(bad) && lane == 0 && c.err) *c.err = 1;
+  best = wave_max_u64(best);
+  if (lane == 0) sKey[wave] = best;
+  __syncthreads();
+  if (tid == 0)
+    c.partials[(int64_t)m * c.nparts + chunk] = umax64(umax64(sKey[0], sKey[1]), umax64(sKey[2], sKey[3]));
+}
+
 }  // namespace
+
+hipError_t launch_cand_argmax(const CandArgs& c, hipStream_t s) {
+  if (c.M <= 0) return hipSuccess;
+  if (c.K <= 0 || c.K % 64 || c.V <= 0 || c.max_cands <= 0 || c.M > 65535 || !c.partials)
+    return hipErrorInvalidValue;
+  const int chunks = cand_groups(c.max_cands);
+  if (c.nparts < chunks) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_cand_argmax, dim3(chunks, c.M), dim3(256), 0, s, c);
+  return hipGetLastError();
+}
+int cand_groups(int max_cands) { return (max_cands + kCandChunk - 1) / kCandChunk; }
 
 // Columns per skinny workgroup: wide enough that the vocabulary projection
 // does not re-read the activations too often, narrow enough that the small

@@ -265,6 +265,30 @@ struct FinalizeArgs {
 };
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 
+// Output scoring over per-row candidate lists (a lexical shortlist): row m
+// scores the ids cand[off[m] .. off[m+1]) (ascending) against its quantized
+// state xq / xa; one argmax key per (row, 128 candidates) goes to
+// partials[m * nparts + chunk] (nparts >= cand_groups(max_cands)).  logits
+// (optional) receives each candidate's logit at its position in cand.  An id
+// outside the vocabulary sets *err to 1 and is not scored.
+struct CandArgs {
+  const int8_t* xq = nullptr;  // [M, K]
+  const float* xa = nullptr;   // [M]
+  int M = 0, K = 0, V = 0;
+  const int8_t* emb = nullptr;  // [V, K] row-major
+  const float* mult = nullptr;
+  const float* bias = nullptr;
+  const uint32_t* cand = nullptr;
+  const uint32_t* off = nullptr;  // [M + 1]
+  int max_cands = 0;              // host bound on off[m+1] - off[m]
+  uint64_t* partials = nullptr;
+  int nparts = 0;
+  float* logits = nullptr;
+  int* err = nullptr;
+};
+int cand_groups(int max_cands);
+hipError_t launch_cand_argmax(const CandArgs& c, hipStream_t s);
+
 // Reduces argmax partials to token ids (op-level argmax).
 // Records the message marian_hip_last_op_error returns on this thread.
 void note_op_error(const char* msg);

@@ -277,6 +277,41 @@ int marian_hip_vocab_argmax(const int8_t* xq, const float* xa, int64_t M, int64_
   return vocab_argmax_into(xq, xa, M, K, emb, emb_mult, bias, V, flags, token, logits, part, nparts, s);
 }
 
+int marian_hip_candidate_argmax(const int8_t* xq, const float* xa, int64_t M, int64_t K,
+                                const int8_t* emb, const float* emb_mult, const float* bias,
+                                int64_t V, const uint32_t* cand, const uint32_t* cand_offsets,
+                                int64_t max_cands, int32_t* token, float* logits, int* err,
+                                void* stream) {
+  if (!xq || !xa || !emb || !emb_mult || !bias || !cand || !cand_offsets || !token || M < 0 ||
+      M > 65535 || K <= 0 || K % 64 || K > 4096 || V <= 0 || V > INT32_MAX || max_cands <= 0 ||
+      max_cands > INT32_MAX / 2)
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (M == 0) return MARIAN_HIP_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int nparts = cand_groups((int)max_cands);
+  uint64_t* part = (uint64_t*)op_scratch(2, (size_t)M * nparts * 8, s);
+  if (!part) return op_status(hipErrorOutOfMemory, "candidate_argmax scratch");
+  CandArgs c;
+  c.xq = xq;
+  c.xa = xa;
+  c.M = (int)M;
+  c.K = (int)K;
+  c.V = (int)V;
+  c.emb = emb;
+  c.mult = emb_mult;
+  c.bias = bias;
+  c.cand = cand;
+  c.off = cand_offsets;
+  c.max_cands = (int)max_cands;
+  c.partials = part;
+  c.nparts = nparts;
+  c.logits = logits;
+  c.err = err;
+  int rc = op_status(launch_cand_argmax(c, s), "candidate_argmax");
+  if (rc) return rc;
+  return op_status(launch_argmax_reduce(part, nparts, (int)M, token, s), "candidate_argmax reduce");
+}
+
 int marian_hip_vocab_argmax_noalloc(const int8_t* xq, const float* xa, int64_t M, int64_t K,
                                     const int8_t* emb, const float* emb_mult, const float* bias,
                                     int64_t V, uint32_t flags, int32_t* token, float* logits,

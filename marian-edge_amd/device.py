@@ -144,6 +144,15 @@ def vocab_argmax(xq, xa, emb, emb_mult, bias, token, logits=None, flags: int = 0
         stream), "vocab_argmax")
 
 
+def candidate_argmax(xq, xa, emb, emb_mult, bias, cand, cand_offsets, max_cands: int, token,
+                     logits=None, err=None, stream=None):
+    M, K = xq.shape
+    V = emb.shape[0]
+    _lib.check(_lib.load().marian_hip_candidate_argmax(
+        xq.ptr, xa.ptr, M, K, emb.ptr, emb_mult.ptr, bias.ptr, V, cand.ptr, cand_offsets.ptr,
+        int(max_cands), token.ptr, _p(logits), _p(err), stream), "candidate_argmax")
+
+
 def positions(dim: int, count: int) -> np.ndarray:
     out = np.zeros((count, dim), np.float32)
     _lib.check(_lib.load().marian_hip_positions(dim, count, out.ctypes.data), "positions")

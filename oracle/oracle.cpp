@@ -818,6 +818,35 @@ int oracle_ssru_layer_norm(const float* cand, const float* forget, float* state,
   return 0;
 }
 
+// select_token over explicit candidate lists (q8_engine.rs:749-790): for row m
+// and each candidate c in list order, logit = acc * (1/(xa[m]*mult[c])) +
+// bias[c]; the strict '>' scan from -inf keeps the first maximum, and a row
+// whose logits never exceed -inf keeps its first candidate.
+int oracle_candidate_argmax(const int8_t* xq, const float* xa, size_t M, size_t K,
+                            const int8_t* emb, const float* mult, const float* bias, size_t V,
+                            const uint32_t* cand, const uint32_t* offs, int32_t* token,
+                            float* logits) {
+  for (size_t m = 0; m < M; ++m) {
+    if (offs[m + 1] <= offs[m]) return -1;  // "cannot select from an empty candidate list"
+    int32_t best = (int32_t)cand[offs[m]];
+    float best_v = -INFINITY;
+    for (uint32_t i = offs[m]; i < offs[m + 1]; ++i) {
+      const uint32_t c = cand[i];
+      if (c >= V) return -1;  // "output candidate exceeds vocabulary"
+      const int64_t acc = dot_i8_scalar(xq + m * K, emb + (size_t)c * K, K);
+      const float inv = 1.0f / (xa[m] * mult[c]);
+      const float logit = (float)acc * inv + bias[c];
+      if (logits) logits[i] = logit;
+      if (logit > best_v) {
+        best_v = logit;
+        best = (int32_t)c;
+      }
+    }
+    token[m] = best;
+  }
+  return 0;
+}
+
 int oracle_residual_layer_norm(const float* x, const float* r, const float* scale,
                                const float* bias, size_t rows, size_t d, int order, float* out) {
   residual_ln(x, r, scale, bias, rows, d, order, out);

@@ -150,6 +150,13 @@ int oracle_ssru_layer_norm(const float* cand, const float* forget, float* state,
                            const float* residual, const float* scale, const float* bias,
                            size_t rows, size_t d, int order, float* out);
 
+/* select_token over candidate lists: row m scores cand[offs[m] .. offs[m+1])
+ * (logits per list position, optional); -1 on an empty list or an id >= V. */
+int oracle_candidate_argmax(const int8_t* xq, const float* xa, size_t M, size_t K,
+                            const int8_t* emb, const float* mult, const float* bias, size_t V,
+                            const uint32_t* cand, const uint32_t* offs, int32_t* token,
+                            float* logits);
+
 /* out = LN(x + r) per row of length d (eps 1e-6). */
 int oracle_residual_layer_norm(const float* x, const float* r, const float* scale,
                                const float* bias, size_t rows, size_t d, int order,

@@ -80,6 +80,7 @@ _SIG = {
     "oracle_residual_layer_norm": (C.c_int, [_P, _P, _P, _P, _SZ, _SZ, C.c_int, _P]),
     "oracle_linear_forward_static": (C.c_int, [_P, _SZ, _SZ, C.POINTER(Linear), _SZ, C.c_float,
                                                C.c_int, _P, _P, _P, C.c_int]),
+    "oracle_candidate_argmax": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P, _SZ, _P, _P, _P, _P]),
     "oracle_ssru_layer_norm": (C.c_int, [_P, _P, _P, _P, _P, _P, _SZ, _SZ, C.c_int, _P]),
     "oracle_attention": (C.c_int, [_P, _SZ, _P, _SZ, _P, _SZ, _P, _P, _SZ, _SZ, _SZ, C.c_int, _P,
                                    _SZ]),
@@ -325,6 +326,25 @@ def linear_forward_static(x: np.ndarray, weight, mult, bias, act_mult: float, re
     if rc != 0:
         raise OracleError(rc, "non-finite input, invalid multiplier or accumulator overflow")
     return y, acc, q
+
+
+def candidate_argmax(xq, xa, emb, mult, bias, cand, offsets):
+    """select_token over candidate lists: (tokens [M], logits per list position)."""
+    xq = np.ascontiguousarray(xq, np.int8)
+    xa = np.ascontiguousarray(xa, np.float32)
+    emb = np.ascontiguousarray(emb, np.int8)
+    mult = np.ascontiguousarray(mult, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    cand = np.ascontiguousarray(cand, np.uint32)
+    offs = np.ascontiguousarray(offsets, np.uint32)
+    M, K = xq.shape
+    tok = np.zeros(M, np.int32)
+    lg = np.zeros(max(cand.size, 1), np.float32)
+    rc = load().oracle_candidate_argmax(_ptr(xq), _ptr(xa), M, K, _ptr(emb), _ptr(mult), _ptr(bias),
+                                        emb.shape[0], _ptr(cand), _ptr(offs), _ptr(tok), _ptr(lg))
+    if rc != 0:
+        raise OracleError(rc, "empty candidate list or id outside the vocabulary")
+    return tok, lg[:cand.size]
 
 
 def ssru_layer_norm(cand, forget, state, residual, scale, bias, order=REFERENCE):

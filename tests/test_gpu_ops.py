@@ -413,3 +413,70 @@ def test_ssru_layer_norm_matches_oracle(pkg, orc, dev, rows, d):
     assert np.array_equal(ds.host().view(np.uint32), st_ref.view(np.uint32)), "state differs"
     assert np.array_equal(out.host().view(np.uint32), out_ref.view(np.uint32)), "output differs"
     assert np.array_equal(q.host(), q_ref) and np.array_equal(a.host(), a_ref)
+
+
+# ---- lexical shortlist: scoring only the candidate ids ----------------------------
+def test_candidate_argmax_matches_oracle(pkg, orc, dev, full_model):
+    import importlib
+
+    sl = importlib.import_module(pkg.__name__ + ".shortlist")
+    m = full_model
+    V, K = m.geometry.vocab, m.geometry.dim
+    rng = np.random.default_rng(33)
+    # a synthetic shortlist: 100 source ids, 40 targets each, firstNum 100
+    src_v = 100
+    offs_t = np.arange(0, 40 * src_v + 1, 40, dtype=np.int64)
+    targets = rng.integers(0, V, size=40 * src_v).astype(np.uint32)
+    short = sl.LexicalShortlist.from_bytes(sl.LexicalShortlist.to_bytes(100, offs_t, targets), src_v, V)
+    lists = [short.candidates(rng.integers(0, src_v, size=n)) for n in (3, 17, 60, 1)]
+    lists.append(sl.LexicalShortlist.from_bytes(None, src_v, V).candidates([]))  # the full vocabulary
+    M = len(lists)
+    xq = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+    xa = rng.uniform(1.0, 50.0, size=M).astype(np.float32)
+    flat, offs, mx = sl.pack_candidates(lists)
+    tok_ref, lg_ref = orc.candidate_argmax(xq, xa, m.embedding, m.embedding_mult, m.output_bias,
+                                           flat, offs)
+    print(f"candidate_argmax: {M} rows, list lengths {np.diff(offs).tolist()}", flush=True)
+    d = {k: dev.DeviceArray.from_host(v) for k, v in dict(
+        xq=xq, xa=xa, emb=m.embedding, mult=m.embedding_mult, bias=m.output_bias, cand=flat,
+        offs=offs).items()}
+    tok = dev.DeviceArray.zeros(M, np.int32)
+    lg = dev.DeviceArray.zeros(flat.size, np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.candidate_argmax(d["xq"], d["xa"], d["emb"], d["mult"], d["bias"], d["cand"], d["offs"], mx,
+                         tok, logits=lg, err=err)
+    dev.synchronize()
+    assert err.host()[0] == 0
+    assert np.array_equal(tok.host(), tok_ref)
+    assert np.array_equal(lg.host().view(np.uint32), lg_ref.view(np.uint32))
+    # the full-vocabulary list scores like the vocabulary kernel (masked ids excluded)
+    dt = dev.DeviceArray.zeros(1, np.int32)
+    dev.vocab_argmax(dev.DeviceArray.from_host(xq[-1:]), dev.DeviceArray.from_host(xa[-1:]),
+                     d["emb"], d["mult"], d["bias"], dt)
+    dev.synchronize()
+    assert dt.host()[0] == tok.host()[-1]
+
+
+def test_candidate_argmax_ties_and_bad_ids(pkg, orc, dev):
+    rng = np.random.default_rng(35)
+    V, K = 300, 64
+    emb = rng.integers(-127, 128, size=(V, K)).astype(np.int8)
+    emb[201] = emb[200]
+    mult = np.full(V, 100.0, np.float32)
+    bias = np.zeros(V, np.float32)
+    xq = emb[200:201].copy()
+    xa = np.ones(1, np.float32)
+    cand = np.array([0, 5, 200, 201, 250], np.uint32)
+    offs = np.array([0, 5], np.uint32)
+    tok_ref, _ = orc.candidate_argmax(xq, xa, emb, mult, bias, cand, offs)
+    assert tok_ref[0] == 200
+    D = dev.DeviceArray.from_host
+    tok = dev.DeviceArray.zeros(1, np.int32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.candidate_argmax(D(xq), D(xa), D(emb), D(mult), D(bias), D(cand), D(offs), 5, tok, err=err)
+    dev.synchronize()
+    assert tok.host()[0] == 200 and err.host()[0] == 0
+    bad = np.array([0, 5, 200, V + 7, 201], np.uint32)
+    dev.candidate_argmax(D(xq), D(xa), D(emb), D(mult), D(bias), D(bad), D(offs), 5, tok, err=err)
+    dev.synchronize()
+    assert err.host()[0] == 1 and tok.host()[0] == 200
