@@ -62,7 +62,7 @@
 extern "C" {
 #endif
 
-#define MARIAN_HIP_ABI_VERSION 1
+#define MARIAN_HIP_ABI_VERSION 2 /* 2: marian_hip_attention takes head_dim */
 
 enum {
   MARIAN_HIP_OK = 0,
@@ -287,8 +287,10 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
 
 /* Variable-length attention: query row i belongs to sequence seq_of_row[i]
  * and attends over key rows [cu_k[s], cu_k[s+1]); max_keys bounds every range
- * (at most 4096); heads <= 16.  Row strides in elements.  in_bf16 != 0 reads
- * q/k/v as bfloat16 (converted exactly to fp32); out is fp32 [rows, heads*64].
+ * (at most 4096); heads <= 16 of width head_dim (64, or 48 as in the
+ * reference's 384-wide model; head h is columns [h*head_dim, (h+1)*head_dim)).
+ * Row strides in elements.  in_bf16 != 0 reads q/k/v as bfloat16 (converted
+ * exactly to fp32); out is fp32 [rows, heads*head_dim].
  * n_seqs > 0 declares packed self-attention: the query rows are the key rows
  * (row i lies in [cu_k[s], cu_k[s+1]) for s = seq_of_row[i]), cu_k has
  * n_seqs + 1 entries, rows = cu_k[n_seqs]; then ranges of at most 256 keys
@@ -296,8 +298,8 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
  * n_seqs = 0: one (row, head) wave each, for any query/key pairing. */
 int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
                          const int32_t* seq_of_row, const uint32_t* cu_k, int64_t n_seqs,
-                         int64_t rows, int64_t heads, int64_t max_keys, int in_bf16, float* out,
-                         int64_t ldo, void* stream);
+                         int64_t rows, int64_t heads, int64_t head_dim, int64_t max_keys,
+                         int in_bf16, float* out, int64_t ldo, void* stream);
 
 /* Vocabulary projection + bias + generation mask + argmax per row:
  * token[m] = argmax_v (acc[m,v] * (1/(xa[m]*mult[v])) + bias[v]) with ties to

@@ -97,7 +97,7 @@ SIGNATURES = {
     "marian_hip_q8_linear_static": (C.c_int, [_P, _I64, _I64, C.c_float, _P, _P, _P, _I64, C.c_int, _P, _P, _P, _P]),
     "marian_hip_ssru_layer_norm": (C.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "marian_hip_residual_layer_norm": (C.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
-    "marian_hip_attention": (C.c_int, [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, C.c_int, _P, _I64, _P]),
+    "marian_hip_attention": (C.c_int, [_P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, C.c_int, _P, _I64, _P]),
     "marian_hip_vocab_argmax": (C.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _I64, C.c_uint32, _P, _P, _P]),
     "marian_hip_candidate_argmax": (C.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _P]),
     "marian_hip_vocab_argmax_noalloc": (C.c_int, [_P, _P, _I64, _I64, _P, _P, _P, _I64, C.c_uint32, _P, _P, _P]),

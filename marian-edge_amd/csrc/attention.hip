@@ -1,7 +1,8 @@
 // attention.hip — variable-length multi-head attention: one single-wave
-// workgroup per (query row, head), head_dim = 64.
+// workgroup per (query row, head), head_dim 64 or 48 (the reference's 384-wide,
+// 8-head production model).
 //
-// Semantics of attention_into (tensor.rs:251-318): score_k = (q . k_k) * 1/8,
+// Semantics of attention_into (tensor.rs:251-318): score_k = (q . k_k) * 1/sqrt(dh),
 // softmax as max, exp(s - max), sum, multiply by 1/sum, then
 // out = sum_k p_k v_k in key order.  Mapping onto the wave:
 //   * K and V rows arrive by coalesced 16-byte loads and pass through a
@@ -59,11 +60,13 @@ __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
   }
 }
 
-// Lane l loads dims 4*(l%16)..+3 of keys first + l/16 + 4i (i < 16), clamped.
+// Lane l loads dims 4*(l%16)..+3 of keys first + l/16 + 4i (i < 16), both
+// clamped (with head_dim 48 the lanes past dim 47 reload dims 44-47 into tile
+// columns that are never read).
 #define MH_LOAD_CHUNK(T, P, BASE, LD, FIRST, NK, LANE, OUT)                                   \
   _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_) {                                         \
     const int key_ = min((FIRST) + ((LANE) >> 4) + 4 * i_, (NK)-1);                           \
-    OUT[i_] = load_row4<T>((P), (BASE) + (int64_t)key_ * (LD) + ((LANE)&15) * 4);             \
+    OUT[i_] = load_row4<T>((P), (BASE) + (int64_t)key_ * (LD) + min(((LANE)&15) * 4, DH - 4)); \
   }
 #define MH_STORE_CHUNK(TILE, LANE, IN)                                                         \
   _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_)                                            \
@@ -71,8 +74,9 @@ __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
 
 // PRE (two chunks only): all four K/V chunks are requested up front, so a
 // decode row waits for one memory round trip after its key range is known.
-template <int CH, typename T, bool PRE>
+template <int CH, typename T, bool PRE, int DH>
 __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
+  static_assert(DH == 64 || DH == 48, "head widths");
   static_assert(!PRE || CH == 2, "up-front loads hold two chunks");
   static_assert(CH * 64 <= 64 * kKRow, "the tile holds every probability of a row");
   __shared__ __attribute__((aligned(16))) float tile[64 * kKRow];
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   const bool too_long = nk > CH * 64;
   if (too_long) nk = CH * 64;
   const int nch = (nk + 63) >> 6;
-  const int64_t kbase = key0 * a.ldkv + h * kHeadDim;
+  const int64_t kbase = key0 * a.ldkv + h * DH;
 
   // Keys of a stale row may run past the buffer: its last readable key.
   const int nk_ld = a.mode == ATT_SEQ ? nk : (int)min((int64_t)nk, a.max_row - key0);
@@ -115,14 +119,14 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
     }
   }
   // q of this head, one element per lane; broadcast 16 values at a time.
-  const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * kHeadDim + lane));
+  const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * DH + min(lane, DH - 1)));
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
   if (r >= n) return;
   if (too_long && threadIdx.x == 0 && a.err) *a.err = 2;
 
-  // Scores: lane = key within the chunk, 64-term dot in dimension order.  The
+  // Scores: lane = key within the chunk, DH-term dot in dimension order.  The
   // next chunk's K rows are loaded while this chunk's dot runs.
-  const float scale = 1.0f / sqrtf((float)kHeadDim);
+  const float scale = 1.0f / sqrtf((float)DH);
   if (lane < 32) sTab[lane] = tab_v;  // published by the first barrier below
   float s[CH];
 #pragma unroll
@@ -145,7 +149,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
       __syncthreads();
       float dot = -0.0f;
 #pragma unroll
-      for (int i0 = 0; i0 < kHeadDim; i0 += 16) {
+      for (int i0 = 0; i0 < DH; i0 += 16) {
         float kr[16], qs[16];
 #pragma unroll
         for (int i = 0; i < 16; i += 4) {
@@ -230,11 +234,11 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
     }
   }
 
-  a.out[(int64_t)r * a.ldo + h * kHeadDim + lane] = o;
+  if (lane < DH) a.out[(int64_t)r * a.ldo + h * DH + lane] = o;
   // |max| of this head's slice: the consumer derives the row's quantization
   // multiplier from the maxima of all heads.
-  const bool bad = !isfinite(o);
-  const float m = wave_max(fabsf(o));
+  const bool bad = lane < DH && !isfinite(o);
+  const float m = wave_max(lane < DH ? fabsf(o) : 0.0f);
   if (lane == 0 && a.amax) a.amax[(int64_t)r * a.heads + h] = m;
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
@@ -295,7 +299,7 @@ __global__ __launch_bounds__(1024) void k_seq_tiles(const uint32_t* cu, int nseq
 }
 
 // Two workgroups per CU: at most 64 VGPRs (eight waves per SIMD).
-template <typename T>
+template <typename T, int DH>
 __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_attn_tiles(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float stage[64 * kKRow];            // one 64-key chunk
   __shared__ __attribute__((aligned(16))) float sPall[kTileQ * kTileMaxKeys];  // per-wave probabilities
@@ -313,7 +317,7 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   const int nch = (Lc + 63) >> 6;
   const int lpad = (Lc + 7) & ~7;
   float* sP = sPall + w * kTileMaxKeys;
-  const int64_t base = key0 * a.ldkv + h * kHeadDim;
+  const int64_t base = key0 * a.ldkv + h * DH;
   if (tid < 32) sTab[tid] = kExp2Tab[tid];
   if (L > Lc && tid == 0 && a.err) *a.err = 2;
 
@@ -321,18 +325,18 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   // past the last are zero.  The next chunk is requested while this one is used.
   auto ld = [&](const void* src, int c) {
     const int key = c * 64 + (tid >> 4);
-    return key < Lc ? load_row4<T>(src, base + (int64_t)key * a.ldkv + (tid & 15) * 4)
+    return key < Lc ? load_row4<T>(src, base + (int64_t)key * a.ldkv + min((tid & 15) * 4, DH - 4))
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   };
   float4 pre = ld(a.k, 0);
   const bool live = w < nq;
   const int row = (int)key0 + q0 + w;
   const float* sQ = sQall + w * kHeadDim;
-  if (live) sQall[w * kHeadDim + lane] = Io<T>::at(a.q, (int64_t)row * a.ldq + h * kHeadDim + lane);
+  if (live && lane < DH) sQall[w * kHeadDim + lane] = Io<T>::at(a.q, (int64_t)row * a.ldq + h * DH + lane);
   float* srow = stage + (tid >> 4) * kKRow + (tid & 15) * 4;
 
-  // Scores: lane = key of the chunk, 64-term dot in dimension order.
-  const float scale = 1.0f / sqrtf((float)kHeadDim);
+  // Scores: lane = key of the chunk, DH-term dot in dimension order.
+  const float scale = 1.0f / sqrtf((float)DH);
   float sc[kTileMaxKeys / 64];
 #pragma unroll
   for (int c = 0; c < kTileMaxKeys / 64; ++c) {
@@ -347,7 +351,7 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
         // The query is read from LDS as broadcasts (published by the barrier above).
         float dot = -0.0f;
 #pragma unroll
-        for (int i = 0; i < kHeadDim; i += 4) {
+        for (int i = 0; i < DH; i += 4) {
           const float4 kk = *(const float4*)(kr + i);
           const float4 qq = *(const float4*)(sQ + i);
           dot = dot + qq.x * kk.x;
@@ -434,20 +438,31 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
     }
   }
   if (!live) return;
-  a.out[(int64_t)row * a.ldo + h * kHeadDim + lane] = o;
-  const bool bad = !isfinite(o);
+  if (lane < DH) a.out[(int64_t)row * a.ldo + h * DH + lane] = o;
+  const bool bad = lane < DH && !isfinite(o);
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
 template <int CH, typename T, bool PRE>
 hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((k_attention<CH, T, PRE>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
+  if (a.head_dim == 48)
+    hipLaunchKernelGGL((k_attention<CH, T, PRE, 48>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_attention<CH, T, PRE, 64>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 
 template <int CH, bool PRE = false>
 hipError_t launch_ch(const AttnArgs& a, hipStream_t s) {
   return a.bf16 ? launch_t<CH, uint16_t, PRE>(a, s) : launch_t<CH, float, PRE>(a, s);
+}
+
+template <typename T>
+void launch_tiles(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
+  if (a.head_dim == 48)
+    hipLaunchKernelGGL((k_attn_tiles<T, 48>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((k_attn_tiles<T, 64>), grid, block, 0, s, a);
 }
 
 }  // namespace
@@ -462,7 +477,7 @@ hipError_t launch_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles, int c
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
-  if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out ||
+  if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out || (a.head_dim != 64 && a.head_dim != 48) ||
       (int64_t)a.rows * a.heads > 0x7fffffff)
     return hipErrorInvalidValue;
   // Packed self-attention with a tile list: keys staged once per tile.
@@ -470,9 +485,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     if ((int64_t)a.tiles_cap * a.heads > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 grid(a.tiles_cap * a.heads), block(kTileQ * 64);
     if (a.bf16)
-      hipLaunchKernelGGL(k_attn_tiles<uint16_t>, grid, block, 0, s, a);
+      launch_tiles<uint16_t>(a, grid, block, s);
     else
-      hipLaunchKernelGGL(k_attn_tiles<float>, grid, block, 0, s, a);
+      launch_tiles<float>(a, grid, block, s);
     return hipGetLastError();
   }
   // Decode launches cover few rows: one round trip per row matters more

@@ -200,16 +200,19 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     note_op_error(msg);
     return MARIAN_HIP_ERR_MODEL;
   };
-  // Geometries every kernel of the path runs: heads of width 64 (d = 64 H,
-  // d <= 512: the vocabulary kernel and the fp32-input projections hold K
-  // <= 512), FFN widths that are multiples of 64 up to 2048 (the skinny
-  // kernel's K), at least one decoder layer (the decoder state the
-  // vocabulary projection scores), and a vocabulary below 2^31.
+  // Geometries every kernel of the path runs: 1-8 heads of width 64 or 48
+  // (the reference's 384-wide production model) with d a multiple of 64 up to
+  // 512 (the vocabulary kernel and the fp32-input projections hold K <= 512),
+  // FFN widths that are multiples of 64 up to 2048 (the skinny kernel's K), at
+  // least one decoder layer (the decoder state the vocabulary projection
+  // scores), and a vocabulary below 2^31.
   if (!m->embedding || !m->embedding_mult || !m->output_bias)
     return model_fail("embedding, its multipliers and the output bias are required");
   if (!m->vocab || m->vocab > (uint32_t)INT32_MAX) return model_fail("vocabulary size %u is not supported", m->vocab);
-  if (!m->heads || m->heads > 8 || m->dim != m->heads * kHeadDim)
-    return model_fail("dim %u with %u heads: supported are 1-8 heads of width %d", m->dim, m->heads, kHeadDim);
+  if (!m->heads || m->heads > 8 || m->dim % m->heads || m->dim % 64 || m->dim > 512 ||
+      (m->dim / m->heads != kHeadDim && m->dim / m->heads != 48))
+    return model_fail("dim %u with %u heads: supported are 1-8 heads of width 64 or 48, dim a multiple of 64 up to 512",
+                      m->dim, m->heads);
   if (!m->ffn_dim || m->ffn_dim % 64 || m->ffn_dim > 2048)
     return model_fail("ffn_dim %u: supported are multiples of 64 up to 2048", m->ffn_dim);
   if (!m->decoder_layers || !m->decoder) return model_fail("the model needs at least one decoder layer");
@@ -686,6 +689,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     aa.v = QKV + 2 * d;
     aa.ldkv = 3 * d;
     aa.heads = H;
+    aa.head_dim = d / H;
     aa.rows = T;
     aa.seq_of_row = d_seq;
     aa.cu = d_cu;
@@ -947,6 +951,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
         sa.v = vc;
         sa.ldkv = d;
         sa.heads = H;
+        sa.head_dim = d / H;
         sa.rows = rows;
         sa.rows_dev = d_nact;
         sa.row_key0 = rm.kv0;
@@ -975,6 +980,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
         ca.v = ckv + d;
         ca.ldkv = 2 * d;
         ca.heads = H;
+        ca.head_dim = d / H;
         ca.rows = rows;
         ca.rows_dev = d_nact;
         ca.row_key0 = rm.src0;

@@ -153,6 +153,7 @@ struct AttnArgs {
   int64_t ldkv = 0;
   int bf16 = 0;
   int heads = 0;
+  int head_dim = 64;  // 64 or 48; head h is columns [h * head_dim, (h + 1) * head_dim)
   int rows = 0;
   const int* rows_dev = nullptr;
   // ATT_SEQ: keys of row r are [cu[seq_of_row[r]], cu[seq_of_row[r]+1])

@@ -230,11 +230,11 @@ int marian_hip_residual_layer_norm(const float* x, const float* r, const float* 
 
 int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* v, int64_t ldkv,
                          const int32_t* seq_of_row, const uint32_t* cu_k, int64_t n_seqs,
-                         int64_t rows, int64_t heads, int64_t max_keys, int in_bf16, float* out,
-                         int64_t ldo, void* stream) {
+                         int64_t rows, int64_t heads, int64_t head_dim, int64_t max_keys,
+                         int in_bf16, float* out, int64_t ldo, void* stream) {
   if (!q || !k || !v || !seq_of_row || !cu_k || !out || rows < 0 || rows > INT32_MAX ||
-      heads <= 0 || heads > 16 || ldq % 8 || ldkv % 8 || max_keys <= 0 || max_keys > 4096 ||
-      n_seqs < 0 || n_seqs > 16 * 1024)
+      heads <= 0 || heads > 16 || (head_dim != 64 && head_dim != 48) || ldq % 8 || ldkv % 8 ||
+      max_keys <= 0 || max_keys > 4096 || n_seqs < 0 || n_seqs > 16 * 1024)
     return MARIAN_HIP_ERR_INVALID_INPUT;
   AttnArgs a;
   a.mode = ATT_SEQ;
@@ -245,6 +245,7 @@ int marian_hip_attention(const void* q, int64_t ldq, const void* k, const void* 
   a.ldkv = ldkv;
   a.bf16 = in_bf16 ? 1 : 0;
   a.heads = (int)heads;
+  a.head_dim = (int)head_dim;
   a.rows = (int)rows;
   a.seq_of_row = seq_of_row;
   a.cu = cu_k;

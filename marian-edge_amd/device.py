@@ -126,14 +126,16 @@ def residual_layer_norm(x, r, scale, bias, out, q=None, a=None, err=None, stream
 
 
 def attention(q, k, v, seq_of_row, cu, out, heads: int, max_keys: int, ldq=None, ldkv=None,
-              ldo=None, bf16: bool = False, packed_self: bool = True, stream=None) -> None:
+              ldo=None, bf16: bool = False, packed_self: bool = True, head_dim: int = 64,
+              stream=None) -> None:
     """packed_self: the query rows are the key rows of the cu-packed sequences
     (passes the sequence count, which allows the key-staging kernel)."""
     rows = seq_of_row.shape[0]
     n_seqs = cu.shape[0] - 1 if packed_self else 0
     _lib.check(_lib.load().marian_hip_attention(
         q.ptr, ldq or q.shape[1], k.ptr, v.ptr, ldkv or k.shape[1], seq_of_row.ptr, cu.ptr, n_seqs,
-        rows, heads, max_keys, int(bf16), out.ptr, ldo or out.shape[1], stream), "attention")
+        rows, heads, head_dim, max_keys, int(bf16), out.ptr, ldo or out.shape[1], stream),
+        "attention")
 
 
 def vocab_argmax(xq, xa, emb, emb_mult, bias, token, logits=None, flags: int = 0, stream=None):

@@ -480,3 +480,32 @@ def test_candidate_argmax_ties_and_bad_ids(pkg, orc, dev):
     dev.candidate_argmax(D(xq), D(xa), D(emb), D(mult), D(bias), D(bad), D(offs), 5, tok, err=err)
     dev.synchronize()
     assert err.host()[0] == 1 and tok.host()[0] == 200
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_attention_head_dim_48(pkg, orc, dev, packed):
+    """Heads of width 48 (the reference's 384-wide, 8-head model): packed
+    self-attention (key-staging kernel, ranges up to 256 keys) and the
+    one-wave-per-(row, head) kernel, against the oracle bit for bit."""
+    rng = np.random.default_rng(48)
+    lens = np.array([1, 5, 47, 64, 65, 130, 256, 3], np.int64)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint32)
+    T = int(cu[-1])
+    q, k, v = (rng.standard_normal((T, 384)).astype(np.float32) for _ in range(3))
+    ref = orc.attention(q, k, v, cu, cu, 8)
+    seq = np.repeat(np.arange(len(lens), dtype=np.int32), lens)
+    D = dev.DeviceArray.from_host
+    out = dev.DeviceArray.zeros((T, 384), np.float32)
+    dev.attention(D(q), D(k), D(v), D(seq), D(cu), out, heads=8, max_keys=int(lens.max()),
+                  packed_self=packed, head_dim=48)
+    dev.synchronize()
+    assert np.array_equal(out.host().view(np.uint32), ref.view(np.uint32))
+    # cross-attention shape: one query per sequence
+    B = len(lens)
+    qc = np.ascontiguousarray(q[cu[:-1].astype(np.int64)])
+    refc = orc.attention(qc, k, v, np.arange(B + 1, dtype=np.uint32), cu, 8)
+    outc = dev.DeviceArray.zeros((B, 384), np.float32)
+    dev.attention(D(qc), D(k), D(v), D(np.arange(B, dtype=np.int32)), D(cu), outc, heads=8,
+                  max_keys=int(lens.max()), packed_self=False, head_dim=48)
+    dev.synchronize()
+    assert np.array_equal(outc.host().view(np.uint32), refc.view(np.uint32))

@@ -131,7 +131,9 @@ def test_probe_ragged_64(pkg, orc, full, step):
 
 @pytest.mark.parametrize("geom", [dict(dim=256, heads=4, ffn_dim=1024),
                                   dict(dim=512, heads=8, ffn_dim=1536),
-                                  dict(dim=128, heads=2, ffn_dim=320)])
+                                  dict(dim=128, heads=2, ffn_dim=320),
+                                  dict(dim=384, heads=8, ffn_dim=1536),
+                                  dict(dim=192, heads=4, ffn_dim=768)])
 def test_other_geometries_token_exact(pkg, orc, geom):
     g = pkg.Geometry(vocab=3000, encoder_layers=2, decoder_layers=2, **geom)
     model = pkg.seeded_model(seed=13, geometry=g)

@@ -58,7 +58,8 @@ def test_embedding_checks(pkg, tiny):
 @pytest.mark.parametrize("geom,needle", [
     (dict(dim=576, heads=9), "heads"),          # 9 heads: more than the kernels hold
     (dict(dim=100, heads=2), "heads"),          # head width 50
-    (dict(dim=384, heads=8), "heads"),          # head width 48
+    (dict(dim=256, heads=8), "heads"),          # head width 32
+    (dict(dim=576, heads=12), "heads"),         # width 48 but d > 512
     (dict(ffn_dim=96), "ffn_dim"),              # not a multiple of 64
     (dict(ffn_dim=2112), "ffn_dim"),            # above the skinny kernel's K
     (dict(decoder_layers=0), "decoder layer"),  # nothing for the vocabulary to score
