@@ -148,6 +148,7 @@ def vocab_bytes(V, K, rows):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_kernels_ragged64_traffic.json"
+STATS_PROFILE = ROOT / "profiles" / "decode_kernels_ragged64_stats.json"
 
 
 def measured_traffic(prefix):
@@ -164,6 +165,29 @@ def measured_traffic(prefix):
         return None
     return round(sum((v["fetch_bytes_per_dispatch"] + v["write_bytes_per_dispatch"]) * v["dispatches"]
                      for v in ks) / n)
+
+
+def traced_launch_us(prefix):
+    """Average traced duration (us) of the kernels whose name starts with
+    `prefix`, call-weighted, from the rocprofv3 --kernel-trace --stats run of
+    this workload summarized in profiles/."""
+    try:
+        kernels = json.loads(STATS_PROFILE.read_text())["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    ks = [v for k, v in kernels.items() if k.startswith(prefix)]
+    n = sum(v["calls"] for v in ks)
+    return round(sum(v["avg_us"] * v["calls"] for v in ks) / n, 4) if n else None
+
+
+def traced_fields(algo_bytes_per_launch, prefix):
+    us = traced_launch_us(prefix)
+    if not us:
+        return {"traced_avg_launch_us": None}
+    gbs = algo_bytes_per_launch / (us * 1e-6) / 1e9
+    return {"traced_avg_launch_us": us, "traced_achieved": round(gbs, 1),
+            "traced_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traced_source": "profiles/decode_kernels_ragged64_stats.json (rocprofv3 --kernel-trace --stats)"}
 
 
 def block_bytes(kind, step, layer, src_lens, d, heads):
@@ -347,6 +371,7 @@ def main(argv=None):
             "algorithmic_bytes_per_launch": round(r["blk_algo"] / max(1, r["blk_launch"])),
             "launches": r["blk_launch"],
             "timing": "events recorded by each launch's dispatch, in a separate pass over the same batch",
+            **traced_fields(r["blk_algo"] / max(1, r["blk_launch"]), "k_attn_block"),
             "traffic": measured_traffic("k_attn_block"),
             "traffic_source": "profiles/decode_kernels_ragged64_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, bytes per launch)",
         },
@@ -361,6 +386,7 @@ def main(argv=None):
             "algorithmic_bytes_per_launch": round(r["vocab_algo"] / max(1, r["vocab_launch"])),
             "launches": r["vocab_launch"],
             "timing": "events recorded by each launch's dispatch, in a separate pass over the same batch",
+            **traced_fields(r["vocab_algo"] / max(1, r["vocab_launch"]), "k_vocab_argmax"),
             "traffic": measured_traffic("k_vocab_argmax"),
         },
         "cpu_baseline": cpu,

@@ -145,8 +145,10 @@ typedef struct {
 typedef struct marian_hip_engine marian_hip_engine;
 
 /* Copies the model to device `device` and builds the position table.
- * Supported geometry: 1-8 heads of width 64 (dim = 64 * heads), ffn_dim a
- * multiple of 64 up to 2048, at least one decoder layer, vocab < 2^31.  The
+ * Supported geometry: 1-8 heads of width 64 or 48 (dim = 64 * heads or
+ * 48 * heads, a multiple of 64, at most 512: 384 with 8 heads of 48 is the
+ * reference's small production shape), ffn_dim a multiple of 64 up to 2048,
+ * at least one decoder layer, vocab < 2^31.  The
  * model is checked before the device is touched: every weight multiplier
  * finite and positive, no weight -128, every tensor present (Q8Linear::new,
  * crates/marian-cpu/src/q8_gemm.rs:96-110); otherwise MARIAN_HIP_ERR_MODEL,

@@ -250,6 +250,17 @@ def stats_table(stats_csv: str, batches: int) -> str:
     return "\n".join(out)
 
 
+def stats_json(stats_csv: str, batches: int) -> dict:
+    """Per-kernel calls and average traced duration of a rocprofv3 --stats
+    kernel_stats.csv, for bench.py to set beside its event-timed averages."""
+    with open(stats_csv, newline="") as f:
+        rows = list(csv.DictReader(f))
+    return {"source": "rocprofv3 --kernel-trace --stats", "batches": batches,
+            "kernels": {_short(r["Name"]): {"calls": int(r["Calls"]),
+                                            "avg_us": round(float(r["AverageNs"]) / 1e3, 4)}
+                        for r in rows}}
+
+
 def step_breakdown(trace_csv: str, steps_per_batch: int, batches: int, rows_at: list[int],
                    first_batch: int = 0) -> str:
     """Per decode step of a bench.py kernel trace: the kernels in launch order
@@ -264,7 +275,7 @@ def step_breakdown(trace_csv: str, steps_per_batch: int, batches: int, rows_at: 
         if k[0].startswith("__amd"):
             continue
         cur.append(k)
-        if k[0] == "k_finalize":
+        if k[0].startswith("k_finalize"):
             steps.append(cur)
             cur = []
     enc = ("k_gemm_tile", "k_attn_tiles", "k_seq_tiles", "k_embed", "k_quantize_rows_v4<2>")
@@ -351,6 +362,7 @@ def main(argv=None) -> int:
     st = sub.add_parser("stats")
     st.add_argument("stats_csv")
     st.add_argument("--batches", type=int, required=True)
+    st.add_argument("--json", action="store_true", help="per-kernel calls and averages as JSON")
     sb = sub.add_parser("steps", help="per-step kernel breakdown of a bench.py trace (ragged batch)")
     sb.add_argument("trace_csv")
     sb.add_argument("--batches", type=int, default=6, help="untimed-event batches at the start")
@@ -366,7 +378,8 @@ def main(argv=None) -> int:
         print(json.dumps(pmc_summary(a.fetch_csv, a.write_csv, a.copy_fetch_csv, a.copy_write_csv,
                                      a.copy_mb), indent=1))
     elif a.cmd == "stats":
-        print(stats_table(a.stats_csv, a.batches))
+        print(json.dumps(stats_json(a.stats_csv, a.batches), indent=1) if a.json
+              else stats_table(a.stats_csv, a.batches))
     elif a.cmd == "steps":
         pkg = _load_package()
         b = pkg.ragged_batch()
