@@ -22,6 +22,12 @@
  *                              ABI's error slot (marian-worker-wasm/src/lib.rs:381-389)
  *   marian_hip_engine_destroy  Drop of the engine on its owner thread
  *                              (crates/marian-core/src/backend.rs:3-6)
+ *   marian_hip_engine_create_ssru
+ *                              Q8CpuEngine::from_model over the reference's own
+ *                              Transformer-SSRU graph, q8_engine.rs:195-212, 828-877
+ *   marian_hip_translate_shortlisted
+ *                              translate_token_ids with the lexical shortlist's
+ *                              candidates, q8_engine.rs:361-362, 576-584, 749-790
  *
  * Op-level entry points (device pointers, caller's stream) replace the
  * reference's building blocks and exist so each kernel can be checked and timed
@@ -62,7 +68,8 @@
 extern "C" {
 #endif
 
-#define MARIAN_HIP_ABI_VERSION 2 /* 2: marian_hip_attention takes head_dim */
+#define MARIAN_HIP_ABI_VERSION 3 /* 2: marian_hip_attention takes head_dim;
+                                    3: the Transformer-SSRU engine, shortlisted translate */
 
 enum {
   MARIAN_HIP_OK = 0,
@@ -192,6 +199,86 @@ int marian_hip_translate_probe(marian_hip_engine* engine, const int32_t* tokens,
                                int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
                                size_t* out_len, uint32_t probe_step, float* enc_out,
                                float* logits_out, uint8_t* active_out);
+
+/* ---- The reference's own graph: Transformer encoder, SSRU decoder ----
+ *
+ * Q8CpuEngine's fixed graph (crates/marian-cpu/src/q8_engine.rs:76-114,
+ * 511-574, 382-451) over a Marian binary model: every dense layer has ONE
+ * weight multiplier and ONE static activation multiplier (the intgemm8
+ * payload's quantization multiplier and the <name>_QuantMultA tensor,
+ * legacy_q8.rs:390-403, 544-552, 646-674), so a layer computes
+ *   q = clamp(rne(x * act_mult), -127, 127),  y = acc * (1 / (act_mult * weight_mult)) + bias
+ * (q8_gemm.rs:380-448, 569-590).  Encoder and decoder embeddings are separate
+ * tables, each with one multiplier; the decoder embedding is also the tied
+ * output projection, whose input is quantized with output_act_mult.  A decoder
+ * layer is SSRU (tensor.rs:184-218), then cross-attention, then the FFN. */
+typedef struct {
+  const int8_t* weight; /* [out, in] int8 in [-127, 127], input-contiguous */
+  float weight_mult;    /* real weight = q / weight_mult */
+  float act_mult;       /* static activation multiplier */
+  const float* bias;    /* [out], or NULL: no bias (adds 0.0, q8_gemm.rs:444) */
+} marian_hip_static_linear;
+
+typedef struct {
+  marian_hip_static_linear wq, wk, wv, wo; /* [d, d] each (q8_engine.rs:528-544) */
+  const float* attn_ln_scale;
+  const float* attn_ln_bias;
+  marian_hip_static_linear w1; /* [F, d], ReLU */
+  marian_hip_static_linear w2; /* [d, F] */
+  const float* ffn_ln_scale;
+  const float* ffn_ln_bias;
+} marian_hip_ssru_encoder_layer;
+
+typedef struct {
+  marian_hip_static_linear ssru_w;  /* [d, d] candidate, no bias (q8_engine.rs:394, 942-958) */
+  marian_hip_static_linear ssru_wf; /* [d, d] forget gate input (q8_engine.rs:395) */
+  const float* ssru_ln_scale;
+  const float* ssru_ln_bias;
+  marian_hip_static_linear wq, wk, wv, wo; /* context attention; wk/wv on the encoder output */
+  const float* context_ln_scale;
+  const float* context_ln_bias;
+  marian_hip_static_linear w1, w2;
+  const float* ffn_ln_scale;
+  const float* ffn_ln_bias;
+} marian_hip_ssru_decoder_layer;
+
+typedef struct {
+  uint32_t source_vocab, target_vocab, dim, heads, ffn_dim, encoder_layers, decoder_layers;
+  const int8_t* encoder_embedding; /* [source_vocab, dim] */
+  float encoder_embedding_mult;
+  const int8_t* decoder_embedding; /* [target_vocab, dim]; also the output projection */
+  float decoder_embedding_mult;
+  float output_act_mult;           /* decoder_output_activation_mult, the QuantMultA of
+                                      decoder_Wemb (q8_engine.rs:834-836) */
+  const float* output_bias;        /* [target_vocab] */
+  const marian_hip_ssru_encoder_layer* encoder;
+  const marian_hip_ssru_decoder_layer* decoder;
+} marian_hip_ssru_model;
+
+/* Engine for the graph above (Q8CpuEngine::from_model, q8_engine.rs:195-212).
+ * Same geometry rules as marian_hip_engine_create; multipliers must be finite
+ * and positive, weights in [-127, 127].  marian_hip_translate_token_ids and
+ * marian_hip_translate_probe on it score the full target vocabulary with the
+ * generation mask, which is what the reference's engine does without a
+ * shortlist file (LexicalShortlist::from_bytes(None), shortlist.rs:55-65). */
+int marian_hip_engine_create_ssru(const marian_hip_ssru_model* model,
+                                  const marian_hip_limits* limits, int device,
+                                  marian_hip_engine** out_engine);
+
+/* marian_hip_translate_token_ids with per-sentence output candidates: sentence
+ * b is scored only over candidates[candidate_offsets[b] .. candidate_offsets[b+1]),
+ * in list order, the first maximum winning (select_token over
+ * LexicalShortlist::candidates: prepare_candidates, q8_engine.rs:576-584, and
+ * :749-790).  The lists come from the caller (the reference builds them from
+ * the source ids with its shortlist, shortlist.rs:150-198); no generation mask
+ * is applied to them.  An empty list or an id >= the target vocabulary is
+ * MARIAN_HIP_ERR_INVALID_INPUT.  Works on either engine kind. */
+int marian_hip_translate_shortlisted(marian_hip_engine* engine, const int32_t* tokens,
+                                     size_t n_tokens, const uint32_t* offsets, size_t n_offsets,
+                                     const uint32_t* max_output_tokens, uint32_t flags,
+                                     const uint32_t* candidates,
+                                     const uint32_t* candidate_offsets, int32_t* out_tokens,
+                                     size_t out_cap, uint32_t* out_offsets, size_t* out_len);
 
 int marian_hip_is_ready(const marian_hip_engine* engine);
 /* Last error message of this engine ("" if none); valid until the next call. */

@@ -9,8 +9,9 @@ from . import _lib
 from .engine import (BackendError, BatchOutput, BufferTooSmall, DeviceError, HipBackend,
                      HipEngine, InferenceError, InvalidInput, ModelError, make_limits)
 from .synthetic import (Batch, Geometry, LIFTED_LIMITS, REFERENCE_LIMITS, SeededModel,
-                        attention_inputs, gemm_inputs, ragged_batch, seeded_model,
-                        single_sentence_batch, stress_batch, GEMM_SHAPES, GEMM_ROWS)
+                        SsruGeometry, SsruModel, attention_inputs, gemm_inputs, ragged_batch,
+                        seeded_model, seeded_ssru_model, single_sentence_batch, stress_batch,
+                        GEMM_SHAPES, GEMM_ROWS)
 
 FLAG_IGNORE_EOS = _lib.FLAG_IGNORE_EOS
 FLAG_NO_GENERATION_MASK = _lib.FLAG_NO_GENERATION_MASK
@@ -18,7 +19,8 @@ FLAG_NO_GENERATION_MASK = _lib.FLAG_NO_GENERATION_MASK
 __all__ = [
     "BackendError", "BatchOutput", "BufferTooSmall", "DeviceError", "HipBackend", "HipEngine",
     "InferenceError", "InvalidInput", "ModelError", "make_limits", "Batch", "Geometry",
-    "LIFTED_LIMITS", "REFERENCE_LIMITS", "SeededModel", "attention_inputs", "gemm_inputs",
+    "LIFTED_LIMITS", "REFERENCE_LIMITS", "SeededModel", "SsruGeometry", "SsruModel",
+    "seeded_ssru_model", "attention_inputs", "gemm_inputs",
     "ragged_batch", "seeded_model", "single_sentence_batch", "stress_batch", "GEMM_SHAPES",
     "GEMM_ROWS", "FLAG_IGNORE_EOS", "FLAG_NO_GENERATION_MASK", "load_library",
 ]

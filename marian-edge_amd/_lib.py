@@ -56,6 +56,43 @@ class Model(C.Structure):
     ]
 
 
+class StaticLinear(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("weight_mult", C.c_float), ("act_mult", C.c_float),
+                ("bias", C.c_void_p)]
+
+
+class SsruEncoderLayer(C.Structure):
+    _fields_ = [
+        ("wq", StaticLinear), ("wk", StaticLinear), ("wv", StaticLinear), ("wo", StaticLinear),
+        ("attn_ln_scale", C.c_void_p), ("attn_ln_bias", C.c_void_p),
+        ("w1", StaticLinear), ("w2", StaticLinear),
+        ("ffn_ln_scale", C.c_void_p), ("ffn_ln_bias", C.c_void_p),
+    ]
+
+
+class SsruDecoderLayer(C.Structure):
+    _fields_ = [
+        ("ssru_w", StaticLinear), ("ssru_wf", StaticLinear),
+        ("ssru_ln_scale", C.c_void_p), ("ssru_ln_bias", C.c_void_p),
+        ("wq", StaticLinear), ("wk", StaticLinear), ("wv", StaticLinear), ("wo", StaticLinear),
+        ("context_ln_scale", C.c_void_p), ("context_ln_bias", C.c_void_p),
+        ("w1", StaticLinear), ("w2", StaticLinear),
+        ("ffn_ln_scale", C.c_void_p), ("ffn_ln_bias", C.c_void_p),
+    ]
+
+
+class SsruModel(C.Structure):
+    _fields_ = [
+        ("source_vocab", C.c_uint32), ("target_vocab", C.c_uint32), ("dim", C.c_uint32),
+        ("heads", C.c_uint32), ("ffn_dim", C.c_uint32), ("encoder_layers", C.c_uint32),
+        ("decoder_layers", C.c_uint32),
+        ("encoder_embedding", C.c_void_p), ("encoder_embedding_mult", C.c_float),
+        ("decoder_embedding", C.c_void_p), ("decoder_embedding_mult", C.c_float),
+        ("output_act_mult", C.c_float), ("output_bias", C.c_void_p),
+        ("encoder", C.POINTER(SsruEncoderLayer)), ("decoder", C.POINTER(SsruDecoderLayer)),
+    ]
+
+
 class Limits(C.Structure):
     _fields_ = [
         ("max_length_factor", C.c_uint32), ("max_generation_steps", C.c_uint32),
@@ -85,6 +122,10 @@ SIGNATURES = {
     "marian_hip_translate_token_ids": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, C.c_uint32, _P, _SZ, _P, C.POINTER(_SZ)]),
     "marian_hip_translate_probe": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, C.c_uint32, _P, _SZ, _P, C.POINTER(_SZ),
                                              C.c_uint32, _P, _P, _P]),
+    "marian_hip_engine_create_ssru": (C.c_int, [C.POINTER(SsruModel), C.POINTER(Limits), C.c_int,
+                                                 C.POINTER(_P)]),
+    "marian_hip_translate_shortlisted": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, C.c_uint32, _P, _P, _P, _SZ,
+                                                   _P, C.POINTER(_SZ)]),
     "marian_hip_is_ready": (C.c_int, [_P]),
     "marian_hip_last_error": (C.c_char_p, [_P]),
     "marian_hip_info": (C.c_int, [_P, C.c_char_p, _SZ]),

@@ -42,12 +42,94 @@ struct DecLayer {
   const float *ln1_s, *ln1_b, *ln2_s, *ln2_b, *ln3_s, *ln3_b;
 };
 
+// The Transformer-SSRU graph (q8_engine.rs:76-114): dense layers with one
+// static activation multiplier each.  Layers that read the same input are row
+// blocks of one fused weight; when their multipliers agree (`shared`) one
+// quantization and one GEMM serve them all.
+struct SGroup {
+  Lin all;  // [parts * n, K]
+  int parts = 0, n = 0;
+  float act[3] = {};
+  bool shared = false;
+  Lin part(int i) const {
+    Lin l = all;
+    l.N = n;
+    l.w = all.w + (size_t)i * n * all.K;
+    l.wf = all.wf ? all.wf + (size_t)i * (n / 16) * (all.K / 64) * 1024 : nullptr;
+    l.mult = all.mult + (size_t)i * n;
+    l.bias = all.bias + (size_t)i * n;
+    return l;
+  }
+};
+struct SEncLayer {
+  SGroup qkv;  // Wq, Wk, Wv (q8_engine.rs:528-530)
+  Lin o, w1, w2;
+  float ao = 0, a1 = 0, a2 = 0;
+  const float *ln1_s, *ln1_b, *ln2_s, *ln2_b;
+};
+struct SDecLayer {
+  SGroup uf;   // SSRU W (candidate) and Wf (forget gate input), q8_engine.rs:394-395
+  Lin q;       // context Wq
+  SGroup kv;   // context Wk, Wv on the encoder output
+  Lin o, w1, w2;
+  float aq = 0, ao = 0, a1 = 0, a2 = 0;
+  const float *ln0_s, *ln0_b, *ln1_s, *ln1_b, *ln2_s, *ln2_b;  // SSRU, context, FFN
+};
+
+// Host staging of every tensor the engine uploads: 256-byte aligned pieces of
+// one buffer, copied to HBM once; each fix records which engine pointer gets
+// which offset.
+struct Packer {
+  std::vector<char> host;
+  struct Fix {
+    size_t off;
+    const void** dst;
+  };
+  std::vector<Fix> fixes;
+  size_t reserve(size_t bytes, const void** dst) {
+    const size_t off = (host.size() + 255) & ~size_t(255);
+    host.resize(off + bytes);
+    fixes.push_back({off, dst});
+    return off;
+  }
+  void add(const void* src, size_t bytes, const void** dst) {
+    const size_t off = reserve(bytes, dst);
+    std::memcpy(host.data() + off, src, bytes);
+  }
+  // The decode kernels read their weights in MFMA fragment order: each
+  // 16-column tile and 64-wide k-step is one contiguous 1 KB block, lane l's
+  // 16 bytes W[16t + l % 16][64s + 16(l / 16) ..] at ((t * K/64 + s) * 64 + l) * 16.
+  void add_frag(const int8_t* w, int N, int K, const int8_t** dst) {
+    const int tiles = (N + 15) / 16, ks = K / 64;
+    std::vector<int8_t> f((size_t)tiles * ks * 1024, 0);
+    for (int t = 0; t < tiles; ++t)
+      for (int st = 0; st < ks; ++st)
+        for (int l = 0; l < 64; ++l) {
+          const int n = 16 * t + (l & 15);
+          if (n < N)
+            std::memcpy(&f[(((size_t)t * ks + st) * 64 + l) * 16], w + (size_t)n * K + 64 * st + 16 * (l >> 4), 16);
+        }
+    add(f.data(), f.size(), (const void**)dst);
+  }
+};
+
+// Records a model error for marian_hip_last_op_error and returns its code.
+int model_fail(const char* fmt, ...) {
+  char msg[256];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  note_op_error(msg);
+  return MARIAN_HIP_ERR_MODEL;
+}
+
 // Grow-only device buffers reused across calls (the reference pools its
 // scratch too, q8_engine.rs:733-747).
 enum Buf {
   B_META, B_DMETA, B_X0, B_X1, B_XQ, B_XA, B_QKV, B_ATT, B_OQ, B_OA, B_Y, B_H, B_HQ, B_HA, B_CKV,
   B_KC, B_VC, B_DX0, B_DX1, B_DXQ, B_DXA, B_DQ, B_DATT, B_DAMAX, B_DY, B_DH, B_DHQ, B_DHA,
-  B_PART, B_OUT, B_COUNT, B_HIST, B_TILES, B_COUNT_,
+  B_PART, B_OUT, B_COUNT, B_HIST, B_TILES, B_STATE, B_DUF, B_COUNT_,
   // allocated only by marian_hip_translate_probe: the probed step's logits
   // and its active-row order
   B_PLOG = B_COUNT_, B_PSLOT, B_ALL_
@@ -94,8 +176,10 @@ uint32_t host_positions(uint32_t dim, uint32_t count, float* out) {
 struct marian_hip_engine {
   int device = 0;
   hipStream_t stream = nullptr;
-  uint32_t V = 0, d = 0, H = 0, F = 0, Le = 0, Ld = 0;
+  // V: target vocabulary (scoring, decoder input); Vs: source vocabulary
+  uint32_t V = 0, Vs = 0, d = 0, H = 0, F = 0, Le = 0, Ld = 0;
   float emb_scale = 1.0f;
+  bool ssru = false;  // the Transformer-SSRU graph with static multipliers
   marian_hip_limits limits{};
   bool ready = true;
   uint32_t timing = 0;  // MARIAN_HIP_TIME_* flags
@@ -103,9 +187,13 @@ struct marian_hip_engine {
   std::string device_name;
 
   void* weights = nullptr;
-  Lin emb;
+  Lin emb;      // decoder input embedding and tied output projection
+  Lin src_emb;  // encoder input embedding (the same table in the transformer graph)
   std::vector<EncLayer> enc;
   std::vector<DecLayer> dec;
+  std::vector<SEncLayer> senc;
+  std::vector<SDecLayer> sdec;
+  float out_act = 0.0f;  // static multiplier of the scored decoder state
   float* pos = nullptr;
 
   void* buf[B_ALL_] = {};
@@ -187,86 +275,122 @@ int marian_hip_positions(uint32_t dim, uint32_t count, float* out) {
   return MARIAN_HIP_OK;
 }
 
+// Geometry every kernel of the path runs: 1-8 heads of width 64 or 48 (the
+// reference's 384-wide production model) with d a multiple of 64 up to 512
+// (the vocabulary kernel and the fp32-input projections hold K <= 512), FFN
+// widths that are multiples of 64 up to 2048 (the skinny kernel's K), and at
+// least one decoder layer (the decoder state the vocabulary projection
+// scores).  Returns 0 or a model error with the reason noted.
+static int check_geometry(uint32_t dim, uint32_t heads, uint32_t ffn, uint32_t dec_layers,
+                          bool have_decoder) {
+  if (!heads || heads > 8 || dim % heads || dim % 64 || dim > 512 ||
+      (dim / heads != kHeadDim && dim / heads != 48))
+    return model_fail("dim %u with %u heads: supported are 1-8 heads of width 64 or 48, dim a multiple of 64 up to 512",
+                      dim, heads);
+  if (!ffn || ffn % 64 || ffn > 2048)
+    return model_fail("ffn_dim %u: supported are multiples of 64 up to 2048", ffn);
+  if (!dec_layers || !have_decoder) return model_fail("the model needs at least one decoder layer");
+  return 0;
+}
+
+static void apply_limits(marian_hip_engine* E, const marian_hip_limits* limits) {
+  E->limits = limits ? *limits : marian_hip_limits{2, 256, 4096, 256, 256, 65536};
+  if (E->limits.max_position > (uint32_t)kMaxPosition || E->limits.max_position == 0)
+    E->limits.max_position = kMaxPosition;
+}
+
+// Whether every tensor the kernels read has a device address (each staged
+// piece was bound to the engine's own pointer).
+static bool tensors_placed(const marian_hip_engine* E) {
+  auto lin = [](const Lin& l, bool frag) { return l.w && l.mult && l.bias && (!frag || l.wf); };
+  bool ok = E->pos && lin(E->emb, true) && E->src_emb.w && E->src_emb.mult;
+  for (const EncLayer& L : E->enc)
+    ok = ok && lin(L.qkv, false) && lin(L.out, false) && lin(L.ffn1, false) && lin(L.ffn2, false) &&
+         L.ln1_s && L.ln1_b && L.ln2_s && L.ln2_b;
+  for (const DecLayer& L : E->dec)
+    ok = ok && lin(L.self_qkv, true) && lin(L.self_out, true) && lin(L.cross_q, true) &&
+         lin(L.cross_kv, false) && lin(L.cross_out, true) && lin(L.ffn1, true) && lin(L.ffn2, true) &&
+         L.ln1_s && L.ln1_b && L.ln2_s && L.ln2_b && L.ln3_s && L.ln3_b;
+  for (const SEncLayer& L : E->senc)
+    ok = ok && lin(L.qkv.all, false) && lin(L.o, false) && lin(L.w1, false) && lin(L.w2, false) &&
+         L.ln1_s && L.ln1_b && L.ln2_s && L.ln2_b;
+  for (const SDecLayer& L : E->sdec)
+    ok = ok && lin(L.uf.all, true) && lin(L.q, true) && lin(L.kv.all, false) && lin(L.o, true) &&
+         lin(L.w1, true) && lin(L.w2, true) && L.ln0_s && L.ln0_b && L.ln1_s && L.ln1_b && L.ln2_s &&
+         L.ln2_b;
+  return ok;
+}
+
+// The model is valid: copy the staged weights to the device and create the
+// engine's stream, flags and events.
+static int engine_finish(marian_hip_engine* E, Packer& pk, int device, marian_hip_engine** out_engine) {
+  auto cleanup_fail = [&](int code) {
+    marian_hip_engine_destroy(E);
+    return code;
+  };
+  std::vector<float> posv((size_t)kMaxPosition * E->d);
+  host_positions(E->d, kMaxPosition, posv.data());
+  pk.add(posv.data(), posv.size() * 4, (const void**)&E->pos);
+  // Binds every staged piece at `base`.  First at a stand-in base that is
+  // never dereferenced: a tensor the kernels read that no staged piece is
+  // bound to is an error here, before the device is touched.
+  auto bind = [&](const char* base) {
+    for (const Packer::Fix& f : pk.fixes) *f.dst = base + f.off;
+    if (!E->ssru) E->src_emb = E->emb;  // the transformer graph has one table
+  };
+  bind(reinterpret_cast<const char*>(uintptr_t(256)));
+  if (!tensors_placed(E)) {
+    marian_hip_engine_destroy(E);
+    return model_fail("internal error: a model tensor has no device address");
+  }
+
+  if (hipSetDevice(device) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+    char name[256] = {0};
+    if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
+      std::snprintf(name, sizeof name, "%s", prop.name);
+    if (!name[0]) std::snprintf(name, sizeof name, "AMD GPU");  // no marketing name visible
+    E->device_name = std::string(name) + " (" + prop.gcnArchName + ")";
+  }
+  if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+
+  if (hipMalloc(&E->weights, pk.host.size()) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  if (hipMemcpy(E->weights, pk.host.data(), pk.host.size(), hipMemcpyHostToDevice) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  bind((const char*)E->weights);
+
+  if (hipMalloc(&E->err_flag, sizeof(int)) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  if (hipHostMalloc((void**)&E->pinned, 64 * sizeof(int)) != hipSuccess)
+    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  for (auto& ev : E->ev)
+    if (hipEventCreate(&ev) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
+  *out_engine = E;
+  return MARIAN_HIP_OK;
+}
+
 int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits* limits,
                              int device, marian_hip_engine** out_engine) {
   if (!m || !out_engine) return MARIAN_HIP_ERR_INVALID_INPUT;
   *out_engine = nullptr;
-  auto model_fail = [](const char* fmt, ...) {
-    char msg[256];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(msg, sizeof msg, fmt, ap);
-    va_end(ap);
-    note_op_error(msg);
-    return MARIAN_HIP_ERR_MODEL;
-  };
-  // Geometries every kernel of the path runs: 1-8 heads of width 64 or 48
-  // (the reference's 384-wide production model) with d a multiple of 64 up to
-  // 512 (the vocabulary kernel and the fp32-input projections hold K <= 512),
-  // FFN widths that are multiples of 64 up to 2048 (the skinny kernel's K), at
-  // least one decoder layer (the decoder state the vocabulary projection
-  // scores), and a vocabulary below 2^31.
   if (!m->embedding || !m->embedding_mult || !m->output_bias)
     return model_fail("embedding, its multipliers and the output bias are required");
   if (!m->vocab || m->vocab > (uint32_t)INT32_MAX) return model_fail("vocabulary size %u is not supported", m->vocab);
-  if (!m->heads || m->heads > 8 || m->dim % m->heads || m->dim % 64 || m->dim > 512 ||
-      (m->dim / m->heads != kHeadDim && m->dim / m->heads != 48))
-    return model_fail("dim %u with %u heads: supported are 1-8 heads of width 64 or 48, dim a multiple of 64 up to 512",
-                      m->dim, m->heads);
-  if (!m->ffn_dim || m->ffn_dim % 64 || m->ffn_dim > 2048)
-    return model_fail("ffn_dim %u: supported are multiples of 64 up to 2048", m->ffn_dim);
-  if (!m->decoder_layers || !m->decoder) return model_fail("the model needs at least one decoder layer");
+  if (int rc = check_geometry(m->dim, m->heads, m->ffn_dim, m->decoder_layers, m->decoder != nullptr)) return rc;
   if (m->encoder_layers && !m->encoder) return model_fail("encoder layers missing");
   auto* E = new marian_hip_engine();
   E->device = device;
-  E->V = m->vocab;
+  E->V = E->Vs = m->vocab;
   E->d = m->dim;
   E->H = m->heads;
   E->F = m->ffn_dim;
   E->Le = m->encoder_layers;
   E->Ld = m->decoder_layers;
   E->emb_scale = std::sqrt((float)m->dim);
-  if (limits) {
-    E->limits = *limits;
-  } else {
-    E->limits = marian_hip_limits{2, 256, 4096, 256, 256, 65536};
-  }
-  if (E->limits.max_position > (uint32_t)kMaxPosition || E->limits.max_position == 0)
-    E->limits.max_position = kMaxPosition;
+  apply_limits(E, limits);
 
-  auto cleanup_fail = [&](int code) {
-    marian_hip_engine_destroy(E);
-    return code;
-  };
-  // Pack every tensor into one host staging buffer (256-byte aligned pieces),
-  // then copy to HBM once.
-  std::vector<char> host;
-  struct Fix {
-    size_t off;
-    const void** dst;
-  };
-  std::vector<Fix> fixes;
-  auto add = [&](const void* src, size_t bytes, const void** dst) {
-    size_t off = (host.size() + 255) & ~size_t(255);
-    host.resize(off + bytes);
-    std::memcpy(host.data() + off, src, bytes);
-    fixes.push_back({off, dst});
-  };
-  // The decode kernels read their weights in MFMA fragment order: each
-  // 16-column tile and 64-wide k-step is one contiguous 1 KB block, lane l's
-  // 16 bytes W[16t + l % 16][64s + 16(l / 16) ..] at ((t * K/64 + s) * 64 + l) * 16.
-  auto add_frag = [&](const int8_t* w, int N, int K, const int8_t** dst) {
-    const int tiles = (N + 15) / 16, ks = K / 64;
-    std::vector<int8_t> f((size_t)tiles * ks * 1024, 0);
-    for (int t = 0; t < tiles; ++t)
-      for (int st = 0; st < ks; ++st)
-        for (int l = 0; l < 64; ++l) {
-          const int n = 16 * t + (l & 15);
-          if (n < N)
-            std::memcpy(&f[(((size_t)t * ks + st) * 64 + l) * 16], w + (size_t)n * K + 64 * st + 16 * (l >> 4), 16);
-        }
-    add(f.data(), f.size(), (const void**)dst);
-  };
+  Packer pk;
   const char* bad = nullptr;  // first tensor problem found
   auto add_lin = [&](const marian_hip_linear& l, int N, int K, Lin& out, bool frag = false) -> bool {
     if (!l.weight || !l.mult || !l.bias) {
@@ -276,10 +400,10 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     if ((bad = check_q8_tensor(l.weight, l.mult, (size_t)N, (size_t)K))) return false;
     out.N = N;
     out.K = K;
-    add(l.weight, (size_t)N * K, (const void**)&out.w);
-    if (frag) add_frag(l.weight, N, K, &out.wf);
-    add(l.mult, (size_t)N * 4, (const void**)&out.mult);
-    add(l.bias, (size_t)N * 4, (const void**)&out.bias);
+    pk.add(l.weight, (size_t)N * K, (const void**)&out.w);
+    if (frag) pk.add_frag(l.weight, N, K, &out.wf);
+    pk.add(l.mult, (size_t)N * 4, (const void**)&out.mult);
+    pk.add(l.bias, (size_t)N * 4, (const void**)&out.bias);
     return true;
   };
   auto add_vec = [&](const float* v, size_t n, const float** dst) -> bool {
@@ -287,7 +411,7 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
       bad = "a LayerNorm scale or bias is missing";
       return false;
     }
-    add(v, n * 4, (const void**)dst);
+    pk.add(v, n * 4, (const void**)dst);
     return true;
   };
   const int d = (int)E->d, F = (int)E->F, V = (int)E->V;
@@ -298,10 +422,10 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
   }
   E->emb.N = V;
   E->emb.K = d;
-  add(m->embedding, (size_t)V * d, (const void**)&E->emb.w);
-  add_frag(m->embedding, V, d, &E->emb.wf);
-  add(m->embedding_mult, (size_t)V * 4, (const void**)&E->emb.mult);
-  add(m->output_bias, (size_t)V * 4, (const void**)&E->emb.bias);
+  pk.add(m->embedding, (size_t)V * d, (const void**)&E->emb.w);
+  pk.add_frag(m->embedding, V, d, &E->emb.wf);
+  pk.add(m->embedding_mult, (size_t)V * 4, (const void**)&E->emb.mult);
+  pk.add(m->output_bias, (size_t)V * 4, (const void**)&E->emb.bias);
   E->enc.resize(E->Le);
   E->dec.resize(E->Ld);
   for (uint32_t l = 0; l < E->Le; ++l) {
@@ -327,35 +451,168 @@ int marian_hip_engine_create(const marian_hip_model* m, const marian_hip_limits*
     marian_hip_engine_destroy(E);
     return model_fail("%s", bad ? bad : "invalid layer");
   }
-  std::vector<float> posv((size_t)kMaxPosition * d);
-  host_positions(E->d, kMaxPosition, posv.data());
-  add(posv.data(), posv.size() * 4, (const void**)&E->pos);
-
   // The model is valid: only now is the device touched.
-  if (hipSetDevice(device) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
-    char name[256] = {0};
-    if (hipDeviceGetName(name, sizeof name, device) != hipSuccess || !name[0])
-      std::snprintf(name, sizeof name, "%s", prop.name);
-    if (!name[0]) std::snprintf(name, sizeof name, "AMD GPU");  // no marketing name visible
-    E->device_name = std::string(name) + " (" + prop.gcnArchName + ")";
+  return engine_finish(E, pk, device, out_engine);
+}
+
+int marian_hip_engine_create_ssru(const marian_hip_ssru_model* m, const marian_hip_limits* limits,
+                                  int device, marian_hip_engine** out_engine) {
+  if (!m || !out_engine) return MARIAN_HIP_ERR_INVALID_INPUT;
+  *out_engine = nullptr;
+  if (!m->encoder_embedding || !m->decoder_embedding || !m->output_bias)
+    return model_fail("both embeddings and the output bias are required");
+  if (!m->source_vocab || m->source_vocab > (uint32_t)INT32_MAX || !m->target_vocab ||
+      m->target_vocab > (uint32_t)INT32_MAX)
+    return model_fail("vocabulary sizes %u / %u are not supported", m->source_vocab, m->target_vocab);
+  if (int rc = check_geometry(m->dim, m->heads, m->ffn_dim, m->decoder_layers, m->decoder != nullptr)) return rc;
+  if (m->encoder_layers && !m->encoder) return model_fail("encoder layers missing");
+  auto* E = new marian_hip_engine();
+  E->ssru = true;
+  E->device = device;
+  E->V = m->target_vocab;
+  E->Vs = m->source_vocab;
+  E->d = m->dim;
+  E->H = m->heads;
+  E->F = m->ffn_dim;
+  E->Le = m->encoder_layers;
+  E->Ld = m->decoder_layers;
+  E->emb_scale = std::sqrt((float)m->dim);  // EMBEDDING_SCALE = sqrt(384) (q8_engine.rs:23)
+  apply_limits(E, limits);
+
+  Packer pk;
+  const char* bad = nullptr;
+  const char* where = "";
+  const int d = (int)E->d, F = (int)E->F;
+  // A dense layer of the reference's per-tensor scheme: its multiplier and
+  // bias expanded to one entry per output (the kernels' per-channel form; the
+  // product 1 / (act * w) is the reference's inverse_scale, q8_gemm.rs:438),
+  // 0.0 where it has no bias.
+  auto check_static = [&](const marian_hip_static_linear& l, int N, int K, const char* name) -> bool {
+    where = name;
+    if (!l.weight) {
+      bad = "a dense layer is missing its weight";
+      return false;
+    }
+    if (!(std::isfinite(l.act_mult) && l.act_mult > 0.0f)) {
+      bad = "activation multiplier is not finite and positive";
+      return false;
+    }
+    std::vector<float> mult((size_t)N, l.weight_mult);
+    return !(bad = check_q8_tensor(l.weight, mult.data(), (size_t)N, (size_t)K));
+  };
+  auto put = [&](const marian_hip_static_linear& l, int N, int K, size_t wofs, size_t vofs, Lin& all) {
+    std::memcpy(pk.host.data() + wofs, l.weight, (size_t)N * K);
+    float* mv = (float*)(pk.host.data() + vofs);
+    std::fill(mv, mv + N, l.weight_mult);
+    float* bv = (float*)(pk.host.data() + vofs + 4ull * all.N);
+    if (l.bias) std::memcpy(bv, l.bias, 4ull * N);
+    else std::fill(bv, bv + N, 0.0f);
+  };
+  // One or more layers reading the same input, as row blocks of one fused
+  // weight [parts * N, K] (plus its fragment-order copy when `frag`).  The
+  // staged pieces are bound to `all`, which must be the engine's own Lin: the
+  // device addresses are written into it when the weights are uploaded.
+  auto add_block = [&](std::initializer_list<const marian_hip_static_linear*> ls, int N, int K,
+                       const char* name, Lin& all, float* act, bool& shared, bool frag) -> bool {
+    for (const marian_hip_static_linear* l : ls)
+      if (!check_static(*l, N, K, name)) return false;
+    all.N = (int)ls.size() * N;
+    all.K = K;
+    const size_t wofs = pk.reserve((size_t)all.N * K, (const void**)&all.w);
+    const size_t vofs = pk.reserve(8ull * all.N, (const void**)&all.mult);
+    pk.fixes.push_back({vofs + 4ull * all.N, (const void**)&all.bias});
+    int i = 0;
+    shared = true;
+    for (const marian_hip_static_linear* l : ls) {
+      put(*l, N, K, wofs + (size_t)i * N * K, vofs + 4ull * i * N, all);
+      act[i] = l->act_mult;
+      shared = shared && l->act_mult == act[0];
+      ++i;
+    }
+    if (frag) {  // from a copy: add_frag grows (and may move) the staging buffer
+      const std::vector<int8_t> w((const int8_t*)pk.host.data() + wofs,
+                                  (const int8_t*)pk.host.data() + wofs + (size_t)all.N * K);
+      pk.add_frag(w.data(), all.N, K, &all.wf);
+    }
+    return true;
+  };
+  auto add_group = [&](std::initializer_list<const marian_hip_static_linear*> ls, int N, int K,
+                       const char* name, SGroup& g, bool frag) -> bool {
+    g.parts = (int)ls.size();
+    g.n = N;
+    return add_block(ls, N, K, name, g.all, g.act, g.shared, frag);
+  };
+  auto add_one = [&](const marian_hip_static_linear& l, int N, int K, const char* name, Lin& out,
+                     float& act, bool frag) -> bool {
+    bool single = true;
+    return add_block({&l}, N, K, name, out, &act, single, frag);
+  };
+  auto add_vec = [&](const float* v, const float** dst, const char* name) -> bool {
+    where = name;
+    if (!v) {
+      bad = "a LayerNorm scale or bias is missing";
+      return false;
+    }
+    pk.add(v, 4ull * d, (const void**)dst);
+    return true;
+  };
+  auto add_table = [&](const int8_t* w, float mult, int V, Lin& out, bool frag, const char* name) -> bool {
+    where = name;
+    std::vector<float> mv((size_t)V, mult);
+    if ((bad = check_q8_tensor(w, mv.data(), (size_t)V, (size_t)d))) return false;
+    out.N = V;
+    out.K = d;
+    pk.add(w, (size_t)V * d, (const void**)&out.w);
+    if (frag) pk.add_frag(w, V, d, &out.wf);
+    pk.add(mv.data(), 4ull * V, (const void**)&out.mult);
+    return true;
+  };
+  bool ok = add_table(m->encoder_embedding, m->encoder_embedding_mult, (int)E->Vs, E->src_emb, false,
+                      "encoder embedding") &&
+            add_table(m->decoder_embedding, m->decoder_embedding_mult, (int)E->V, E->emb, true,
+                      "decoder embedding");
+  if (ok) {
+    pk.add(m->output_bias, 4ull * E->V, (const void**)&E->emb.bias);
+    where = "output multiplier";
+    ok = std::isfinite(m->output_act_mult) && m->output_act_mult > 0.0f;
+    if (!ok) bad = "activation multiplier is not finite and positive";
+    E->out_act = m->output_act_mult;
   }
-  if (hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking) != hipSuccess)
-    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-
-  if (hipMalloc(&E->weights, host.size()) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  if (hipMemcpy(E->weights, host.data(), host.size(), hipMemcpyHostToDevice) != hipSuccess)
-    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  for (const Fix& f : fixes) *f.dst = (const char*)E->weights + f.off;
-
-  if (hipMalloc(&E->err_flag, sizeof(int)) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  if (hipHostMalloc((void**)&E->pinned, 64 * sizeof(int)) != hipSuccess)
-    return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  for (auto& ev : E->ev)
-    if (hipEventCreate(&ev) != hipSuccess) return cleanup_fail(MARIAN_HIP_ERR_DEVICE);
-  *out_engine = E;
-  return MARIAN_HIP_OK;
+  E->senc.resize(E->Le);
+  E->sdec.resize(E->Ld);
+  for (uint32_t l = 0; ok && l < E->Le; ++l) {
+    const marian_hip_ssru_encoder_layer& s = m->encoder[l];
+    SEncLayer& t = E->senc[l];
+    ok = add_group({&s.wq, &s.wk, &s.wv}, d, d, "encoder attention", t.qkv, false) &&
+         add_one(s.wo, d, d, "encoder Wo", t.o, t.ao, false) &&
+         add_vec(s.attn_ln_scale, &t.ln1_s, "encoder LayerNorm") &&
+         add_vec(s.attn_ln_bias, &t.ln1_b, "encoder LayerNorm") &&
+         add_one(s.w1, F, d, "encoder W1", t.w1, t.a1, false) &&
+         add_one(s.w2, d, F, "encoder W2", t.w2, t.a2, false) &&
+         add_vec(s.ffn_ln_scale, &t.ln2_s, "encoder LayerNorm") &&
+         add_vec(s.ffn_ln_bias, &t.ln2_b, "encoder LayerNorm");
+  }
+  for (uint32_t l = 0; ok && l < E->Ld; ++l) {
+    const marian_hip_ssru_decoder_layer& s = m->decoder[l];
+    SDecLayer& t = E->sdec[l];
+    ok = add_group({&s.ssru_w, &s.ssru_wf}, d, d, "SSRU", t.uf, true) &&
+         add_vec(s.ssru_ln_scale, &t.ln0_s, "SSRU LayerNorm") &&
+         add_vec(s.ssru_ln_bias, &t.ln0_b, "SSRU LayerNorm") &&
+         add_one(s.wq, d, d, "context Wq", t.q, t.aq, true) &&
+         add_group({&s.wk, &s.wv}, d, d, "context Wk/Wv", t.kv, false) &&
+         add_one(s.wo, d, d, "context Wo", t.o, t.ao, true) &&
+         add_vec(s.context_ln_scale, &t.ln1_s, "context LayerNorm") &&
+         add_vec(s.context_ln_bias, &t.ln1_b, "context LayerNorm") &&
+         add_one(s.w1, F, d, "decoder W1", t.w1, t.a1, true) &&
+         add_one(s.w2, d, F, "decoder W2", t.w2, t.a2, true) &&
+         add_vec(s.ffn_ln_scale, &t.ln2_s, "decoder LayerNorm") &&
+         add_vec(s.ffn_ln_bias, &t.ln2_b, "decoder LayerNorm");
+  }
+  if (!ok) {
+    marian_hip_engine_destroy(E);
+    return model_fail("%s: %s", where, bad ? bad : "invalid layer");
+  }
+  return engine_finish(E, pk, device, out_engine);
 }
 
 void marian_hip_engine_destroy(marian_hip_engine* E) {
@@ -388,10 +645,12 @@ const char* marian_hip_last_error(const marian_hip_engine* E) {
 int marian_hip_info(const marian_hip_engine* E, char* buf, size_t cap) {
   if (!E || !buf || !cap) return MARIAN_HIP_ERR_INVALID_INPUT;
   const int n = snprintf(buf, cap,
-                         "{\"name\":\"hip\",\"device\":\"%s\",\"model\":\"transformer-q8 d=%u "
-                         "heads=%u ffn=%u enc=%u dec=%u vocab=%u\",\"precision\":\"q8\","
+                         "{\"name\":\"hip\",\"device\":\"%s\",\"model\":\"%s d=%u "
+                         "heads=%u ffn=%u enc=%u dec=%u vocab=%u/%u\",\"precision\":\"%s\","
                          "\"attention\":\"varlen-fused\",\"supports_batching\":true}",
-                         E->device_name.c_str(), E->d, E->H, E->F, E->Le, E->Ld, E->V);
+                         E->device_name.c_str(), E->ssru ? "transformer-ssru-q8" : "transformer-q8",
+                         E->d, E->H, E->F, E->Le, E->Ld, E->Vs, E->V,
+                         E->ssru ? "q8 static" : "q8");
   return (n < 0 || (size_t)n >= cap) ? MARIAN_HIP_ERR_BUFFER : MARIAN_HIP_OK;
 }
 
@@ -436,7 +695,8 @@ int marian_hip_set_timing(marian_hip_engine* E, uint32_t flags) {
 
 static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
                      const uint32_t* offsets, size_t n_offsets, const uint32_t* max_output_tokens,
-                     uint32_t flags, int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                     uint32_t flags, const uint32_t* cand, const uint32_t* cand_off,
+                     int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
                      size_t* out_len, const Probe& pr) {
   if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
   E->error.clear();
@@ -470,9 +730,26 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   if (Lmax > (size_t)kMaxPosition)
     return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "source longer than the position table");
   for (size_t i = 0; i < n_tokens; ++i)
-    if (tokens[i] < 0 || (uint32_t)tokens[i] >= E->V)
+    if (tokens[i] < 0 || (uint32_t)tokens[i] >= E->Vs)
       return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "source token %d is outside vocabulary %u",
-                     tokens[i], E->V);
+                     tokens[i], E->Vs);
+  // Output candidates per sentence (select_token's candidates, q8_engine.rs:749-766).
+  size_t n_cand = 0;
+  int max_cands = 0;
+  if (cand || cand_off) {
+    if (!cand || !cand_off || cand_off[0] != 0)
+      return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "invalid candidate offsets");
+    if (pr.logits) return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "logits are probed without candidates only");
+    for (size_t b = 0; b < B; ++b) {
+      if (cand_off[b + 1] <= cand_off[b])
+        return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "cannot select from an empty candidate list");
+      max_cands = std::max<int>(max_cands, (int)std::min<uint64_t>(cand_off[b + 1] - cand_off[b], INT32_MAX));
+    }
+    n_cand = cand_off[B];
+    for (size_t i = 0; i < n_cand; ++i)
+      if (cand[i] >= E->V)
+        return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "output candidate %u exceeds vocabulary %u", cand[i], E->V);
+  }
 
   const uint32_t maxpos = std::min<uint32_t>(lim.max_position, kMaxPosition);
   std::vector<uint32_t>& limit = E->h_limit;
@@ -526,7 +803,8 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     return o;
   };
   const size_t o_tok = place(4ull * T), o_pos = place(4ull * T), o_seq = place(4ull * T),
-               o_cu = place(4 * (B + 1));
+               o_cu = place(4 * (B + 1)), o_cand = place(4 * n_cand),
+               o_coff = place(cand ? 4 * (B + 1) : 0);
   const size_t meta_bytes = cur;
   cur = 0;
   const size_t o_state = place(8), o_rslot = place(4 * R), o_rkv0 = place(8 * R),
@@ -541,6 +819,10 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   int32_t* seq_of_row = (int32_t*)(meta.data() + o_seq);
   if (T) std::memcpy(meta.data() + o_tok, tokens, 4 * (size_t)T);
   std::memcpy(meta.data() + o_cu, offsets, 4 * (B + 1));
+  if (cand) {
+    std::memcpy(meta.data() + o_cand, cand, 4 * n_cand);
+    std::memcpy(meta.data() + o_coff, cand_off, 4 * (B + 1));
+  }
   int32_t* r_slot = (int32_t*)(dmeta_h.data() + o_rslot);
   int64_t* r_kv0 = (int64_t*)(dmeta_h.data() + o_rkv0);
   int64_t* r_src0 = (int64_t*)(dmeta_h.data() + o_rsrc0);
@@ -590,8 +872,13 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   int8_t* HQ = (int8_t*)E->get(B_HQ, (size_t)T * F);
   float* HA = (float*)E->get(B_HA, 4ull * T);
   float* CKV = (float*)E->get(B_CKV, 8ull * TR * d * LdA);
-  float* KC = (float*)E->get(B_KC, 4ull * CR * d * LdA);
-  float* VC = (float*)E->get(B_VC, 4ull * CR * d * LdA);
+  // Self-attention caches (transformer graph); the SSRU graph keeps one
+  // recurrent state row per sequence and layer instead, and two projections
+  // per row for the SSRU's inputs.
+  float* KC = (float*)E->get(B_KC, E->ssru ? 0 : 4ull * CR * d * LdA);
+  float* VC = (float*)E->get(B_VC, E->ssru ? 0 : 4ull * CR * d * LdA);
+  float* STATE = (float*)E->get(B_STATE, E->ssru ? 4ull * R * d * LdA : 0);
+  float* DUF = (float*)E->get(B_DUF, E->ssru ? 8ull * R * d : 0);
   float* DX0 = (float*)E->get(B_DX0, 4ull * R * d);
   float* DX1 = (float*)E->get(B_DX1, 4ull * R * d);
   int8_t* DXQ = (int8_t*)E->get(B_DXQ, R * d);
@@ -603,7 +890,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   float* DH = (float*)E->get(B_DH, 4ull * R * F);
   int8_t* DHQ = (int8_t*)E->get(B_DHQ, R * F);
   float* DHA = (float*)E->get(B_DHA, 4ull * R);
-  const int nparts = argmax_groups((int)E->V, (int)E->d);
+  const int nparts = cand ? cand_groups(max_cands) : argmax_groups((int)E->V, (int)E->d);
   uint64_t* PART = (uint64_t*)E->get(B_PART, 8ull * R * nparts);
   int32_t* OUT = (int32_t*)E->get(B_OUT, 4ull * CR);
   uint32_t* COUNT = (uint32_t*)E->get(B_COUNT, 4ull * R);
@@ -624,6 +911,8 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   int32_t* d_pos = (int32_t*)(dmeta + o_pos);
   int32_t* d_seq = (int32_t*)(dmeta + o_seq);
   uint32_t* d_cu = (uint32_t*)(dmeta + o_cu);
+  const uint32_t* d_cand = cand ? (const uint32_t*)(dmeta + o_cand) : nullptr;
+  const uint32_t* d_coff = cand ? (const uint32_t*)(dmeta + o_coff) : nullptr;
   int* d_nact = (int*)(ddec + o_state);
   int* d_step = d_nact + 1;
   RowMeta rm;
@@ -638,14 +927,20 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   MH_HIP(hipMemcpyAsync(ddec, dmeta_h.data(), dmeta_bytes, hipMemcpyHostToDevice, s));
   MH_HIP(hipMemsetAsync(E->err_flag, 0, sizeof(int), s));
   MH_HIP(hipMemsetAsync(COUNT, 0, 4 * B, s));
+  if (E->ssru) MH_HIP(hipMemsetAsync(STATE, 0, 4ull * R * d * LdA, s));  // states start at zero
   // The timed region starts with the packed inputs resident in HBM.
   MH_HIP(hipEventRecord(E->ev[0], s));
 
   // ---- encoder over packed rows ----
+  // The SSRU graph quantizes every dense layer's input with that layer's
+  // static multiplier: a LayerNorm or the embedding quantizes with the next
+  // layer's (or group's shared) multiplier when there is exactly one, and a
+  // separate pass runs per layer otherwise.
+  const SGroup* qkv0 = E->ssru && E->Le ? &E->senc[0].qkv : nullptr;
   {
     EmbedArgs ea;
-    ea.emb = E->emb.w;
-    ea.emb_mult = E->emb.mult;
+    ea.emb = E->src_emb.w;
+    ea.emb_mult = E->src_emb.mult;
     ea.pos = E->pos;
     ea.scale = E->emb_scale;
     ea.d = d;
@@ -653,15 +948,17 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     ea.positions = d_pos;
     ea.rows = T;
     ea.x = X0;
-    ea.xq = XQ;
+    ea.xq = !E->ssru || (qkv0 && qkv0->shared) ? XQ : nullptr;
     ea.xa = XA;
+    ea.qmult = qkv0 && qkv0->shared ? qkv0->act[0] : 0.0f;
     ea.err = E->err_flag;
     MH_HIP(launch_embed(ea, s));
   }
   // Query tiles of the packed sentences for the encoder's self-attention.
   const bool tiled = Lmax <= 256;
   if (tiled) MH_HIP(launch_seq_tiles(d_cu, Bi, TILES, tiles_cap, s));
-  auto gemm = [&](const int8_t* A, const float* a, int M, const Lin& L, float* out, int relu) {
+  auto gemm = [&](const int8_t* A, const float* a, int M, const Lin& L, float* out, int relu,
+                  int64_t ldo = 0) {
     GemmArgs g;
     g.A = A;
     g.a = a;
@@ -674,13 +971,26 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     g.N = L.N;
     Epilogue e;
     e.out = out;
-    e.ldo = L.N;
+    e.ldo = ldo ? ldo : L.N;
     e.relu = relu;
     return launch_gemm_store(g, e, s);
   };
-  for (uint32_t l = 0; l < E->Le; ++l) {
-    const EncLayer& L = E->enc[l];
-    MH_HIP(gemm(XQ, XA, T, L.qkv, QKV, 0));
+  auto qstatic = [&](const float* x, int64_t ldx, int M, int K, float mult, int8_t* q, float* a,
+                     const int* rows_dev) {
+    return launch_quantize_rows_static(x, ldx, M, K, mult, q, K, a, E->err_flag, s, rows_dev);
+  };
+  // A group of static layers over the packed rows x (already quantized into
+  // XQ when shared), written side by side into out (row stride parts * n).
+  auto sgroup = [&](const SGroup& G, const float* x, float* out) -> hipError_t {
+    if (G.shared) return gemm(XQ, XA, T, G.all, out, 0);
+    for (int i = 0; i < G.parts; ++i) {
+      hipError_t rc = qstatic(x, d, T, d, G.act[i], XQ, XA, nullptr);
+      if (rc == hipSuccess) rc = gemm(XQ, XA, T, G.part(i), out + (size_t)i * G.n, 0, (int64_t)G.parts * G.n);
+      if (rc != hipSuccess) return rc;
+    }
+    return hipSuccess;
+  };
+  auto enc_attention = [&]() {
     AttnArgs aa;
     aa.mode = ATT_SEQ;
     aa.q = QKV;
@@ -701,18 +1011,49 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     aa.out = ATT;
     aa.ldo = d;
     aa.err = E->err_flag;
-    MH_HIP(launch_attention(aa, s));
-    MH_HIP(launch_quantize_rows(ATT, d, T, nullptr, d, OQ, d, OA, E->err_flag, s));
-    MH_HIP(gemm(OQ, OA, T, L.out, Y, 0));
-    MH_HIP(launch_residual_ln(Y, X0, L.ln1_s, L.ln1_b, T, nullptr, d, X1, XQ, XA, E->err_flag, s));
-    MH_HIP(gemm(XQ, XA, T, L.ffn1, Hb, 1));
-    MH_HIP(launch_quantize_rows(Hb, F, T, nullptr, F, HQ, F, HA, E->err_flag, s));
-    MH_HIP(gemm(HQ, HA, T, L.ffn2, Y, 0));
-    MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, XQ, XA, E->err_flag, s));
+    return launch_attention(aa, s);
+  };
+  if (!E->ssru) {
+    for (uint32_t l = 0; l < E->Le; ++l) {
+      const EncLayer& L = E->enc[l];
+      MH_HIP(gemm(XQ, XA, T, L.qkv, QKV, 0));
+      MH_HIP(enc_attention());
+      MH_HIP(launch_quantize_rows(ATT, d, T, nullptr, d, OQ, d, OA, E->err_flag, s));
+      MH_HIP(gemm(OQ, OA, T, L.out, Y, 0));
+      MH_HIP(launch_residual_ln(Y, X0, L.ln1_s, L.ln1_b, T, nullptr, d, X1, XQ, XA, E->err_flag, s));
+      MH_HIP(gemm(XQ, XA, T, L.ffn1, Hb, 1));
+      MH_HIP(launch_quantize_rows(Hb, F, T, nullptr, F, HQ, F, HA, E->err_flag, s));
+      MH_HIP(gemm(HQ, HA, T, L.ffn2, Y, 0));
+      MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, XQ, XA, E->err_flag, s));
+    }
+    if (pr.enc) MH_HIP(hipMemcpyAsync(pr.enc, X0, 4ull * T * d, hipMemcpyDeviceToHost, s));
+    for (uint32_t l = 0; l < E->Ld; ++l)
+      MH_HIP(gemm(XQ, XA, T, E->dec[l].cross_kv, CKV + (size_t)l * TR * 2 * d, 0));
+  } else {
+    // encode (q8_engine.rs:526-558): Q, K and V from their own layers.
+    for (uint32_t l = 0; l < E->Le; ++l) {
+      const SEncLayer& L = E->senc[l];
+      MH_HIP(sgroup(L.qkv, X0, QKV));
+      MH_HIP(enc_attention());
+      MH_HIP(qstatic(ATT, d, T, d, L.ao, OQ, OA, nullptr));
+      MH_HIP(gemm(OQ, OA, T, L.o, Y, 0));
+      MH_HIP(launch_residual_ln(Y, X0, L.ln1_s, L.ln1_b, T, nullptr, d, X1, XQ, XA, E->err_flag, s, L.a1));
+      MH_HIP(gemm(XQ, XA, T, L.w1, Hb, 1));
+      MH_HIP(qstatic(Hb, F, T, F, L.a2, HQ, HA, nullptr));
+      MH_HIP(gemm(HQ, HA, T, L.w2, Y, 0));
+      const SGroup* nx = l + 1 < E->Le ? &E->senc[l + 1].qkv : nullptr;
+      MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, nx && nx->shared ? XQ : nullptr,
+                                XA, E->err_flag, s, nx && nx->shared ? nx->act[0] : 0.0f));
+    }
+    if (pr.enc) MH_HIP(hipMemcpyAsync(pr.enc, X0, 4ull * T * d, hipMemcpyDeviceToHost, s));
+    // Cross K/V (q8_engine.rs:560-567): Wk and Wv of each decoder layer side
+    // by side, [T, 2d].
+    for (uint32_t l = 0; l < E->Ld; ++l) {
+      const SGroup& G = E->sdec[l].kv;
+      if (G.shared) MH_HIP(qstatic(X0, d, T, d, G.act[0], XQ, XA, nullptr));
+      MH_HIP(sgroup(G, X0, CKV + (size_t)l * TR * 2 * d));
+    }
   }
-  if (pr.enc) MH_HIP(hipMemcpyAsync(pr.enc, X0, 4ull * T * d, hipMemcpyDeviceToHost, s));
-  for (uint32_t l = 0; l < E->Ld; ++l)
-    MH_HIP(gemm(XQ, XA, T, E->dec[l].cross_kv, CKV + (size_t)l * TR * 2 * d, 0));
   MH_HIP(hipEventRecord(E->ev[1], s));
   if (PSLOT) MH_HIP(hipMemsetAsync(PSLOT + R, 0, sizeof(int32_t), s));  // no rows unless the step runs
 
@@ -780,7 +1121,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
     P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
     P.ffn_af = rows <= kFfnAfMaxRows;
-    P.vocab_ln = rows <= kVocabLnMaxRows && vocab_ln_supported(d);
+    P.vocab_ln = rows <= kVocabLnMaxRows && vocab_ln_supported(d) && !cand;
     return P;
   };
 
@@ -789,6 +1130,81 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     const hipError_t e_ = (expr);               \
     if (e_ != hipSuccess) return e_;            \
   } while (0)
+
+  // Token selection at the end of step t over the rows in DXQ / DXA (or the
+  // LayerNorm still pending in `pend`, built by the vocabulary kernel), then
+  // the stop rules and the compaction of the active set.  With candidates
+  // every row scores its sentence's list (select_token, q8_engine.rs:749-790);
+  // without, the whole vocabulary under the generation mask.
+  auto score = [&](int rows, uint32_t t, RowPrologue& pend) -> hipError_t {
+    if (cand) {
+      CandArgs c;
+      c.xq = DXQ;
+      c.xa = DXA;
+      c.M = rows;
+      c.K = d;
+      c.V = (int)E->V;
+      c.emb = E->emb.w;
+      c.mult = E->emb.mult;
+      c.bias = E->emb.bias;
+      c.cand = d_cand;
+      c.off = d_coff;
+      c.row_slot = rm.slot;
+      c.rows_dev = d_nact;
+      c.max_cands = max_cands;
+      c.partials = PART;
+      c.nparts = nparts;
+      c.err = E->err_flag;
+      MH_TRY(launch_cand_argmax(c, s));
+    } else {
+      Epilogue e;
+      e.partials = PART;
+      e.partial_ld = nparts;
+      e.flags = flags;
+      GemmArgs g;
+      g.A = DXQ;
+      g.a = DXA;
+      g.lda = d;
+      g.M = rows;
+      g.M_dev = d_nact;
+      g.K = d;
+      g.W = E->emb.w;
+      g.Wf = E->emb.wf;
+      g.wmult = E->emb.mult;
+      g.bias = E->emb.bias;
+      g.N = (int)E->V;
+      if (pend.kind == PRO_LN) {  // rows built in the kernel: its fp32 output is not needed
+        g.pro = pend;
+        g.pro.out = nullptr;
+        pend.kind = PRO_NONE;
+      }
+      const bool probed = PLOG && t == pr.step;
+      if (probed) {  // this step's logits too (same kernel, extra stores)
+        e.logits = PLOG;
+        e.ldl = E->V;
+      }
+      hipEvent_t ev[2];
+      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
+      MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));
+      if (probed) {  // the active-row order before the finalizer compacts it
+        MH_TRY(hipMemcpyAsync(PSLOT, rm.slot, 4ull * R, hipMemcpyDeviceToDevice, s));
+        MH_TRY(hipMemcpyAsync(PSLOT + R, d_nact, sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+      }
+    }
+    FinalizeArgs f;
+    f.partials = PART;
+    f.nparts = nparts;
+    f.rows = rm;
+    f.n_active = d_nact;
+    f.rows_ub = rows;
+    f.err = E->err_flag;
+    f.out_tok = OUT;
+    f.count = COUNT;
+    f.step = (int)t;
+    f.flags = flags;
+    f.active_hist = HIST;
+    return launch_finalize(f, s);
+  };
 
   // The launches of decode step t.
   auto emit_step = [&](const StepPlan& P, uint32_t t) -> hipError_t {
@@ -1039,54 +1455,113 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       // prologue on steps with very few rows.
       MH_TRY(layer_norm(DY, L.ln3_s, L.ln3_b, l + 1 < E->Ld ? P.blk_self : P.vocab_ln));
     }
-    {
-      Epilogue e;
-      e.partials = PART;
-      e.partial_ld = nparts;
-      e.flags = flags;
+    return score(rows, t, pend);
+  };
+
+  // The launches of decode step t in the SSRU graph (q8_engine.rs:392-436):
+  // the decoder input, then per layer the SSRU sublayer (W and Wf on the
+  // layer input, gate, state update and LayerNorm), cross-attention over the
+  // row's sentence and the FFN, every dense layer's input quantized with that
+  // layer's static multiplier.  No fused blocks: the generic kernels.
+  auto emit_step_ssru = [&](int rows, uint32_t t) -> hipError_t {
+    float* xres = DX0;
+    float* xalt = DX1;
+    auto dgemm = [&](const Lin& L, const int8_t* A, const float* a, float* out, int64_t ldo,
+                     int relu) {
       GemmArgs g;
-      g.A = DXQ;
-      g.a = DXA;
-      g.lda = d;
+      g.A = A;
+      g.a = a;
+      g.lda = L.K;
       g.M = rows;
       g.M_dev = d_nact;
-      g.K = d;
-      g.W = E->emb.w;
-      g.Wf = E->emb.wf;
-      g.wmult = E->emb.mult;
-      g.bias = E->emb.bias;
-      g.N = (int)E->V;
-      if (pend.kind == PRO_LN) {  // rows built in the kernel: its fp32 output is not needed
-        g.pro = pend;
-        g.pro.out = nullptr;
-        pend.kind = PRO_NONE;
+      g.K = L.K;
+      g.W = L.w;
+      g.Wf = L.wf;
+      g.wmult = L.mult;
+      g.bias = L.bias;
+      g.N = L.N;
+      Epilogue e;
+      e.out = out;
+      e.ldo = ldo;
+      e.relu = relu;
+      return launch_gemm_skinny(g, EPI_STORE, e, s);
+    };
+    auto qs = [&](const float* x, int K, float mult, int8_t* q, float* a) {
+      return launch_quantize_rows_static(x, K, rows, K, mult, q, K, a, E->err_flag, s, d_nact);
+    };
+    const SGroup& uf0 = E->sdec[0].uf;
+    EmbedArgs ea;
+    ea.emb = E->emb.w;
+    ea.emb_mult = E->emb.mult;
+    ea.pos = E->pos;
+    ea.scale = E->emb_scale;
+    ea.d = d;
+    ea.row_prev = rm.prev;
+    ea.step = (int)t;
+    ea.rows = rows;
+    ea.rows_dev = d_nact;
+    ea.x = xres;
+    ea.xq = uf0.shared ? DXQ : nullptr;
+    ea.xa = DXA;
+    ea.qmult = uf0.shared ? uf0.act[0] : 0.0f;
+    ea.err = E->err_flag;
+    MH_TRY(launch_embed(ea, s));
+    for (uint32_t l = 0; l < E->Ld; ++l) {
+      const SDecLayer& L = E->sdec[l];
+      // ---- SSRU: candidate and forget-gate inputs side by side in DUF ----
+      if (L.uf.shared) {
+        MH_TRY(dgemm(L.uf.all, DXQ, DXA, DUF, 2 * d, 0));
+      } else {
+        for (int i = 0; i < 2; ++i) {
+          MH_TRY(qs(xres, d, L.uf.act[i], DXQ, DXA));
+          MH_TRY(dgemm(L.uf.part(i), DXQ, DXA, DUF + (size_t)i * d, 2 * d, 0));
+        }
       }
-      const bool probed = PLOG && t == pr.step;
-      if (probed) {  // this step's logits too (same kernel, extra stores)
-        e.logits = PLOG;
-        e.ldl = E->V;
-      }
-      hipEvent_t ev[2];
-      MH_TRY(timer(MARIAN_HIP_KERNEL_VOCAB, t, 0, ev));
-      MH_TRY(launch_vocab_argmax(g, e, s, ev[0], ev[1]));
-      if (probed) {  // the active-row order before the finalizer compacts it
-        MH_TRY(hipMemcpyAsync(PSLOT, rm.slot, 4ull * R, hipMemcpyDeviceToDevice, s));
-        MH_TRY(hipMemcpyAsync(PSLOT + R, d_nact, sizeof(int32_t), hipMemcpyDeviceToDevice, s));
-      }
+      MH_TRY(launch_ssru_ln(DUF, DUF + d, STATE + (size_t)l * R * d, xres, L.ln0_s, L.ln0_b, rows, d, xalt,
+                            DXQ, DXA, E->err_flag, s, 2 * d, d_nact, rm.slot, L.aq));
+      std::swap(xres, xalt);
+      // ---- cross-attention over the row's sentence ----
+      MH_TRY(dgemm(L.q, DXQ, DXA, DQ, d, 0));
+      AttnArgs ca;
+      ca.mode = ATT_CROSS;
+      ca.q = DQ;
+      ca.ldq = d;
+      const float* ckv = CKV + (size_t)l * TR * 2 * d;
+      ca.k = ckv;
+      ca.v = ckv + d;
+      ca.ldkv = 2 * d;
+      ca.heads = H;
+      ca.head_dim = d / H;
+      ca.rows = rows;
+      ca.rows_dev = d_nact;
+      ca.row_key0 = rm.src0;
+      ca.row_nk = rm.srcn;
+      ca.max_row = (int64_t)TR;
+      ca.max_keys = (int)Lmax;
+      ca.out = DATT;
+      ca.ldo = d;
+      ca.amax = DAMAX;
+      ca.err = E->err_flag;
+      MH_TRY(launch_attention(ca, s));
+      MH_TRY(qs(DATT, d, L.ao, DXQ, DXA));
+      MH_TRY(dgemm(L.o, DXQ, DXA, DY, d, 0));
+      MH_TRY(launch_residual_ln(DY, xres, L.ln1_s, L.ln1_b, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag, s,
+                                L.a1));
+      std::swap(xres, xalt);
+      // ---- feed-forward ----
+      MH_TRY(dgemm(L.w1, DXQ, DXA, DH, F, 1));
+      MH_TRY(qs(DH, F, L.a2, DHQ, DHA));
+      MH_TRY(dgemm(L.w2, DHQ, DHA, DY, d, 0));
+      // quantized for what reads it next: the next layer's SSRU inputs (when
+      // they share a multiplier) or the output scoring
+      const SGroup* nx = l + 1 < E->Ld ? &E->sdec[l + 1].uf : nullptr;
+      const float qm = nx ? (nx->shared ? nx->act[0] : 0.0f) : E->out_act;
+      MH_TRY(launch_residual_ln(DY, xres, L.ln2_s, L.ln2_b, rows, d_nact, d, xalt, qm > 0.0f ? DXQ : nullptr,
+                                DXA, E->err_flag, s, qm));
+      std::swap(xres, xalt);
     }
-    FinalizeArgs f;
-    f.partials = PART;
-    f.nparts = nparts;
-    f.rows = rm;
-    f.n_active = d_nact;
-    f.rows_ub = rows;
-    f.err = E->err_flag;
-    f.out_tok = OUT;
-    f.count = COUNT;
-    f.step = (int)t;
-    f.flags = flags;
-    f.active_hist = HIST;
-    return launch_finalize(f, s);
+    RowPrologue none;
+    return score(rows, t, none);
   };
 
   // Poll the active count without blocking; stop launching once it has
@@ -1109,7 +1584,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   for (uint32_t t = 0; t < gen_limit && !done; ++t) {
     const int rows = (int)remaining[t];
     if (rows == 0) break;
-    MH_HIP(emit_step(make_plan(rows, (int)t + 1, (int)Lmax), t));
+    MH_HIP(E->ssru ? emit_step_ssru(rows, t) : emit_step(make_plan(rows, (int)t + 1, (int)Lmax), t));
     if (time_steps) MH_HIP(hipEventRecord(E->step_ev[t], s));
     ++steps;
     if ((t + 1) % kPoll == 0) MH_HIP(poll());
@@ -1207,8 +1682,23 @@ int marian_hip_translate_token_ids(marian_hip_engine* E, const int32_t* tokens, 
                                    const uint32_t* max_output_tokens, uint32_t flags,
                                    int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
                                    size_t* out_len) {
-  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, out_tokens,
-                   out_cap, out_offsets, out_len, Probe());
+  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, nullptr, nullptr,
+                   out_tokens, out_cap, out_offsets, out_len, Probe());
+}
+
+int marian_hip_translate_shortlisted(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
+                                     const uint32_t* offsets, size_t n_offsets,
+                                     const uint32_t* max_output_tokens, uint32_t flags,
+                                     const uint32_t* candidates, const uint32_t* candidate_offsets,
+                                     int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets,
+                                     size_t* out_len) {
+  if (!E) return MARIAN_HIP_ERR_INVALID_INPUT;
+  if (!candidates || !candidate_offsets) {
+    E->error = "candidate lists are required";
+    return MARIAN_HIP_ERR_INVALID_INPUT;
+  }
+  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, candidates,
+                   candidate_offsets, out_tokens, out_cap, out_offsets, out_len, Probe());
 }
 
 int marian_hip_translate_probe(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens,
@@ -1224,8 +1714,8 @@ int marian_hip_translate_probe(marian_hip_engine* E, const int32_t* tokens, size
   pr.enc = enc_out;
   pr.logits = logits_out;
   pr.active = active_out;
-  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, out_tokens,
-                   out_cap, out_offsets, out_len, pr);
+  return translate(E, tokens, n_tokens, offsets, n_offsets, max_output_tokens, flags, nullptr, nullptr,
+                   out_tokens, out_cap, out_offsets, out_len, pr);
 }
 
 }  // extern "C"

@@ -703,8 +703,10 @@ __global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
   __shared__ uint64_t sKey[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = blockIdx.y, chunk = blockIdx.x;
+  if (c.rows_dev && m >= *c.rows_dev) return;  // uniform per workgroup
   const int ksteps = c.K >> 6, kq = (lane >> 4) * 16;
-  const int64_t c0 = c.off[m], n = (int64_t)c.off[m + 1] - c0;
+  const int b = c.row_slot ? c.row_slot[m] : m;
+  const int64_t c0 = c.off[b], n = (int64_t)c.off[b + 1] - c0;
   const int8_t* xr = c.xq + (int64_t)m * c.K;
   const float am = c.xa[m];
   uint64_t best = 0;

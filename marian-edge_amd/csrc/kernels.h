@@ -107,20 +107,28 @@ hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int
                                 int cols, int8_t* q, int64_t ldq, float* a, int* err,
                                 hipStream_t s);
 
+// qmult > 0: q is quantized with that static multiplier (the next layer's)
+// instead of each row's own.
 hipError_t launch_residual_ln(const float* y, const float* r, const float* g, const float* b,
                               int rows, const int* rows_dev, int d, float* out, int8_t* q,
-                              float* a, int* err, hipStream_t s);
+                              float* a, int* err, hipStream_t s, float qmult = 0.0f);
 
 // Quantization with one static activation multiplier for every row (a[row] =
 // mult); rejects a multiplier that is not finite and positive.
 hipError_t launch_quantize_rows_static(const float* x, int64_t ldx, int rows, int cols, float mult,
-                                       int8_t* q, int64_t ldq, float* a, int* err, hipStream_t s);
+                                       int8_t* q, int64_t ldq, float* a, int* err, hipStream_t s,
+                                       const int* rows_dev = nullptr);
 
 // SSRU update + LayerNorm: state <- gate * state + (1 - gate) * cand with
-// gate = sigmoid(forget); out = LN(relu(state) + resid) (+ quantization).
+// gate = sigmoid(forget); out = LN(relu(state) + resid) (+ quantization, with
+// qmult when > 0).  cand/forget rows are ldc floats apart (0: d); row r's
+// state is state row state_row[r] when state_row is set; rows at or past
+// *rows_dev are skipped.
 hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, const float* resid,
                           const float* g, const float* b, int rows, int d, float* out, int8_t* q,
-                          float* a, int* err, hipStream_t s);
+                          float* a, int* err, hipStream_t s, int64_t ldc = 0,
+                          const int* rows_dev = nullptr, const int* state_row = nullptr,
+                          float qmult = 0.0f);
 
 struct EmbedArgs {
   const int8_t* emb = nullptr;
@@ -137,8 +145,9 @@ struct EmbedArgs {
   int rows = 0;
   const int* rows_dev = nullptr;
   float* x = nullptr;
-  int8_t* xq = nullptr;
+  int8_t* xq = nullptr;  // null: no quantized copy
   float* xa = nullptr;
+  float qmult = 0.0f;    // > 0: quantize with this static multiplier
   int* err = nullptr;
 };
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
@@ -280,8 +289,10 @@ struct CandArgs {
   const float* mult = nullptr;
   const float* bias = nullptr;
   const uint32_t* cand = nullptr;
-  const uint32_t* off = nullptr;  // [M + 1]
-  int max_cands = 0;              // host bound on off[m+1] - off[m]
+  const uint32_t* off = nullptr;  // [M + 1], or [sequences + 1] with row_slot
+  const int* row_slot = nullptr;  // decode loop: row m scores sequence row_slot[m]'s list
+  const int* rows_dev = nullptr;  // decode loop: rows at or past *rows_dev are skipped
+  int max_cands = 0;              // host bound on the lists' lengths
   uint64_t* partials = nullptr;
   int nparts = 0;
   float* logits = nullptr;

@@ -37,10 +37,11 @@ __global__ __launch_bounds__(256) void k_quantize_rows(const float* x, int64_t l
 // QuantMultA, legacy_q8.rs:544-552): q = clamp(rne(x * mult), -127, 127), and
 // a[row] = mult so the GEMM epilogue dequantizes with 1 / (mult * w).
 __global__ __launch_bounds__(256) void k_quantize_rows_static(const float* x, int64_t ldx, int rows,
-                                                              int cols, float mult, int8_t* q,
-                                                              int64_t ldq, float* a, int* err) {
+                                                              const int* rows_dev, int cols,
+                                                              float mult, int8_t* q, int64_t ldq,
+                                                              float* a, int* err) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= rows) return;
+  if (row >= (rows_dev ? min(*rows_dev, rows) : rows)) return;
   const float* xr = x + (int64_t)row * ldx;
   int8_t* qr = q + (int64_t)row * ldq;
   bool bad = false;
@@ -90,14 +91,15 @@ __global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_
 }
 
 // LayerNorm of one row z (lane holds z[lane + 64 j]) by one wave, stored to
-// out (and quantized into q / a when q is set): normalize_row
+// out (and quantized into q / a when q is set, with the row's own multiplier
+// or, when qmult > 0, the next layer's static one): normalize_row
 // (tensor.rs:372-385) sums the row strictly left to right, so the wave parks z
 // in LDS (zr, D floats) and every lane folds the row sequentially; the centred
 // squares are formed lane-parallel and parked the same way.
 template <int PER>
 __device__ __forceinline__ void ln_row_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
                                             const float (&bv)[PER], int row, int lane, float* out,
-                                            int8_t* q, float* a, int* err) {
+                                            int8_t* q, float* a, int* err, float qmult) {
   constexpr int D = PER * 64;
 #pragma unroll
   for (int j = 0; j < PER; ++j) zr[lane + 64 * j] = z[j];
@@ -128,7 +130,7 @@ __device__ __forceinline__ void ln_row_wave(const float (&z)[PER], float* zr, co
   }
   if (q) {
     m = wave_max(m);
-    const float sc = row_multiplier(m);
+    const float sc = qmult > 0.0f ? qmult : row_multiplier(m);
 #pragma unroll
     for (int j = 0; j < PER; ++j) q[(int64_t)row * D + lane + 64 * j] = (int8_t)quantize_one(o[j], sc);
     if (lane == 0) a[row] = sc;
@@ -141,7 +143,7 @@ template <int PER>
 __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float* r,
                                                      const float* gamma, const float* beta,
                                                      int rows, const int* rows_dev, float* out,
-                                                     int8_t* q, float* a, int* err) {
+                                                     int8_t* q, float* a, int* err, float qmult) {
   constexpr int D = PER * 64;
   __shared__ __attribute__((aligned(16))) float sZ[4][D];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
   float z[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) z[j] = yv[j] + rv[j];
-  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err);
+  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err, qmult);
 }
 
 // SSRU state update + LayerNorm (ssru_update_layer_norm_into, tensor.rs:184-218,
@@ -173,13 +175,16 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
 // (each product, the difference and the sum rounded on their own), the state
 // is overwritten with s'; then out = LN(relu(s') + residual) (relu_residual
 // :718-724, relu as max(x, 0) with NaN and -0.0 giving +0.0) with the
-// sequential folds of normalize_row.  One wave per row.
+// sequential folds of normalize_row.  One wave per row.  In the decode loop
+// the state of active row r is state row state_row[r] (its sequence), and
+// rows at or past *rows_dev are skipped.
 __constant__ uint64_t kRowsExp2Tab[32] = {MH_EXP2_TABLE_32};
 template <int PER>
-__global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float* forget, float* state,
-                                                 const float* resid, const float* gamma,
-                                                 const float* beta, int rows, float* out, int8_t* q,
-                                                 float* a, int* err) {
+__global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float* forget, int64_t ldc,
+                                                 float* state, const float* resid, const float* gamma,
+                                                 const float* beta, int rows, const int* rows_dev,
+                                                 const int* state_row, float* out, int8_t* q,
+                                                 float* a, int* err, float qmult) {
   constexpr int D = PER * 64;
   __shared__ __attribute__((aligned(16))) float sZ[4][D];
   __shared__ uint64_t sTab[32];
@@ -187,22 +192,23 @@ __global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float*
   if (threadIdx.x < 32) sTab[threadIdx.x] = kRowsExp2Tab[threadIdx.x];
   __syncthreads();
   const int row = blockIdx.x * 4 + wave;
-  if (row >= rows) return;
-  const int64_t base = (int64_t)row * D;
+  if (row >= (rows_dev ? min(*rows_dev, rows) : rows)) return;
+  const int64_t srow = state_row ? state_row[row] : row;
   float z[PER], gv[PER], bv[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int64_t i = base + lane + 64 * j;
-    const float c = cand[i], f = forget[i], st = state[i], r = resid[i];
-    gv[j] = gamma[lane + 64 * j];
-    bv[j] = beta[lane + 64 * j];
+    const int e_ = lane + 64 * j;
+    const float c = cand[row * ldc + e_], f = forget[row * ldc + e_];
+    const float st = state[srow * D + e_], r = resid[(int64_t)row * D + e_];
+    gv[j] = gamma[e_];
+    bv[j] = beta[e_];
     const float e = ref_expf(-f, sTab);
     const float gate = 1.0f / (1.0f + e);
     const float next = gate * st + (1.0f - gate) * c;
-    state[i] = next;
+    state[srow * D + e_] = next;
     z[j] = (next > 0.0f ? next : 0.0f) + r;
   }
-  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err);
+  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err, qmult);
 }
 
 // The same LayerNorm for rows of width 512 (decode and encoder): one two-wave
@@ -214,7 +220,7 @@ constexpr int kLnSpecD = kSpecChunks * kSpecChunk;  // 512
 __global__ __launch_bounds__(64 * kSpecWaves) void k_residual_ln_spec(const float* y, const float* r,
                                                           const float* gamma, const float* beta,
                                                           const int* rows_dev, float* out, int8_t* q,
-                                                          float* a, int* err) {
+                                                          float* a, int* err, float qmult) {
   __shared__ __attribute__((aligned(16))) float sZ[kLnSpecD];
   __shared__ __attribute__((aligned(16))) float sT[kLnSpecD];
   __shared__ SpecFoldLds sFm, sFv;
@@ -256,7 +262,7 @@ __global__ __launch_bounds__(64 * kSpecWaves) void k_residual_ln_spec(const floa
     *(f4v*)(out + (int64_t)row * kLnSpecD + 4 * lane + 256 * j) = o[j];
   }
   if (q) {
-    const float sc = row_multiplier(wave_max(m));
+    const float sc = qmult > 0.0f ? qmult : row_multiplier(wave_max(m));
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       *(uint32_t*)(q + (int64_t)row * kLnSpecD + 4 * lane + 256 * j) =
@@ -268,7 +274,9 @@ __global__ __launch_bounds__(64 * kSpecWaves) void k_residual_ln_spec(const floa
 }
 
 // x = (q/mult)*sqrt(d) + pos[p] (q8_engine.rs:53-74, 586-630); token < 0 gives
-// pos[p] alone (the decoder's first step).  Fused quantization of x.
+// pos[p] alone (the decoder's first step).  Fused quantization of x with its
+// own multiplier or, when a.qmult > 0, the next layer's static one; none
+// when a.xq is null.
 template <int PER>
 __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
   constexpr int D = PER * 64;
@@ -313,11 +321,13 @@ __global__ __launch_bounds__(256) void k_embed(EmbedArgs a) {
     m = fmaxf(m, fabsf(o[j]));
     a.x[(int64_t)row * D + lane + 64 * j] = o[j];
   }
-  m = wave_max(m);
-  const float sc = row_multiplier(m);
+  if (a.xq) {
+    m = wave_max(m);
+    const float sc = a.qmult > 0.0f ? a.qmult : row_multiplier(m);
 #pragma unroll
-  for (int j = 0; j < PER; ++j) a.xq[(int64_t)row * D + lane + 64 * j] = (int8_t)quantize_one(o[j], sc);
-  if (lane == 0) a.xa[row] = sc;
+    for (int j = 0; j < PER; ++j) a.xq[(int64_t)row * D + lane + 64 * j] = (int8_t)quantize_one(o[j], sc);
+    if (lane == 0) a.xa[row] = sc;
+  }
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
@@ -568,40 +578,44 @@ hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int
 
 hipError_t launch_residual_ln(const float* y, const float* r, const float* g, const float* b,
                               int rows, const int* rows_dev, int d, float* out, int8_t* q,
-                              float* a, int* err, hipStream_t s) {
+                              float* a, int* err, hipStream_t s, float qmult) {
   if (rows <= 0) return hipSuccess;
   if (d % 64) return hipErrorInvalidValue;
   // Width 512 (decode and encoder): two waves share each row's speculative
   // folds.  Other widths (op level): one wave per row, sequential folds.
   if (d == kLnSpecD) {
-    hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(64 * kSpecWaves), 0, s, y, r, g, b, rows_dev, out, q, a, err);
+    hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(64 * kSpecWaves), 0, s, y, r, g, b, rows_dev, out, q, a, err,
+                       qmult);
     return hipGetLastError();
   }
   const dim3 grid((rows + 3) / 4), block(256);
 #define MH_LN(P) \
-  hipLaunchKernelGGL(k_residual_ln<P>, grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err)
+  hipLaunchKernelGGL(k_residual_ln<P>, grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err, qmult)
   MH_PER_DISPATCH_16(d / 64, MH_LN)
 #undef MH_LN
   return hipGetLastError();
 }
 
 hipError_t launch_quantize_rows_static(const float* x, int64_t ldx, int rows, int cols, float mult,
-                                       int8_t* q, int64_t ldq, float* a, int* err, hipStream_t s) {
+                                       int8_t* q, int64_t ldq, float* a, int* err, hipStream_t s,
+                                       const int* rows_dev) {
   if (rows <= 0) return hipSuccess;
   if (!(mult > 0.0f) || !(mult < __builtin_huge_valf())) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_quantize_rows_static, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, rows, cols,
-                     mult, q, ldq, a, err);
+  hipLaunchKernelGGL(k_quantize_rows_static, dim3((rows + 3) / 4), dim3(256), 0, s, x, ldx, rows, rows_dev,
+                     cols, mult, q, ldq, a, err);
   return hipGetLastError();
 }
 
 hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, const float* resid,
                           const float* g, const float* b, int rows, int d, float* out, int8_t* q,
-                          float* a, int* err, hipStream_t s) {
+                          float* a, int* err, hipStream_t s, int64_t ldc, const int* rows_dev,
+                          const int* state_row, float qmult) {
   if (rows <= 0) return hipSuccess;
   if (d % 64) return hipErrorInvalidValue;
   const dim3 grid((rows + 3) / 4), block(256);
 #define MH_SSRU(P) \
-  hipLaunchKernelGGL(k_ssru_ln<P>, grid, block, 0, s, cand, forget, state, resid, g, b, rows, out, q, a, err)
+  hipLaunchKernelGGL(k_ssru_ln<P>, grid, block, 0, s, cand, forget, ldc > 0 ? ldc : d, state, resid, g, b, rows, \
+                     rows_dev, state_row, out, q, a, err, qmult)
   MH_PER_DISPATCH_16(d / 64, MH_SSRU)
 #undef MH_SSRU
   return hipGetLastError();

@@ -18,7 +18,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .synthetic import SeededModel, REFERENCE_LIMITS
+from .synthetic import SeededModel, SsruModel, REFERENCE_LIMITS
 
 
 class BackendError(RuntimeError):
@@ -108,6 +108,46 @@ class _ModelStructs:
         self._keep = (keep, enc, dec)
 
 
+class _SsruModelStructs:
+    """ctypes description of a Transformer-SSRU model (synthetic.SsruModel)."""
+
+    def __init__(self, m: SsruModel):
+        g = m.geometry
+        keep = []
+
+        def arr(a, dtype):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dtype)
+            keep.append(a)
+            return _ptr(a)
+
+        def lin(d):
+            return _lib.StaticLinear(arr(d["weight"], np.int8), d["weight_mult"], d["act_mult"],
+                                     arr(d["bias"], np.float32))
+
+        def ln(d):
+            return arr(d["scale"], np.float32), arr(d["bias"], np.float32)
+
+        enc = (_lib.SsruEncoderLayer * max(1, len(m.encoder)))()
+        for i, L in enumerate(m.encoder):
+            enc[i] = _lib.SsruEncoderLayer(lin(L["wq"]), lin(L["wk"]), lin(L["wv"]), lin(L["wo"]),
+                                           *ln(L["attn_ln"]), lin(L["w1"]), lin(L["w2"]),
+                                           *ln(L["ffn_ln"]))
+        dec = (_lib.SsruDecoderLayer * max(1, len(m.decoder)))()
+        for i, L in enumerate(m.decoder):
+            dec[i] = _lib.SsruDecoderLayer(lin(L["ssru_w"]), lin(L["ssru_wf"]), *ln(L["ssru_ln"]),
+                                           lin(L["wq"]), lin(L["wk"]), lin(L["wv"]), lin(L["wo"]),
+                                           *ln(L["context_ln"]), lin(L["w1"]), lin(L["w2"]),
+                                           *ln(L["ffn_ln"]))
+        self.model = _lib.SsruModel(
+            g.source_vocab, g.target_vocab, g.dim, g.heads, g.ffn_dim, len(m.encoder), len(m.decoder),
+            arr(m.encoder_embedding, np.int8), m.encoder_embedding_mult,
+            arr(m.decoder_embedding, np.int8), m.decoder_embedding_mult, m.output_act_mult,
+            arr(m.output_bias, np.float32), enc, dec)
+        self._keep = (keep, enc, dec)
+
+
 def make_limits(limits: dict | None) -> _lib.Limits:
     d = dict(REFERENCE_LIMITS)
     if limits:
@@ -119,13 +159,22 @@ def make_limits(limits: dict | None) -> _lib.Limits:
 class HipEngine:
     """Owns one marian_hip_engine (one device, one stream, one owner thread)."""
 
-    def __init__(self, model: SeededModel, limits: dict | None = None, device: int = 0):
+    def __init__(self, model: SeededModel | SsruModel, limits: dict | None = None, device: int = 0):
+        """A SeededModel gives the transformer-decoder engine
+        (marian_hip_engine_create), an SsruModel the reference's
+        Transformer-SSRU graph (marian_hip_engine_create_ssru)."""
         self._lib = _lib.load()
-        structs = _ModelStructs(model)
         self._limits = make_limits(limits)
         handle = C.c_void_p()
-        rc = self._lib.marian_hip_engine_create(C.byref(structs.model), C.byref(self._limits),
-                                                device, C.byref(handle))
+        if isinstance(model, SsruModel):
+            structs = _SsruModelStructs(model)
+            create = self._lib.marian_hip_engine_create_ssru
+            self.target_vocab = model.geometry.target_vocab
+        else:
+            structs = _ModelStructs(model)
+            create = self._lib.marian_hip_engine_create
+            self.target_vocab = model.geometry.vocab
+        rc = create(C.byref(structs.model), C.byref(self._limits), device, C.byref(handle))
         if rc != _lib.OK:
             raise _ERRORS.get(rc, BackendError)(
                 f"engine creation failed ({rc}): {self._lib.marian_hip_last_op_error().decode(errors='replace')}")
@@ -153,7 +202,11 @@ class HipEngine:
         msg = self._lib.marian_hip_last_error(self._h).decode(errors="replace")
         raise _ERRORS.get(rc, BackendError)(msg)
 
-    def translate_token_ids(self, tokens, offsets, max_output_tokens, flags: int = 0) -> BatchOutput:
+    def translate_token_ids(self, tokens, offsets, max_output_tokens, flags: int = 0,
+                            candidates=None, candidate_offsets=None) -> BatchOutput:
+        """With candidates (concatenated per-sentence lists and their offsets
+        [B + 1], e.g. from shortlist.pack_candidates) each sentence is scored
+        only over its list (marian_hip_translate_shortlisted)."""
         toks = np.ascontiguousarray(tokens, np.int32)
         offs = np.ascontiguousarray(offsets, np.uint32)
         lim = np.ascontiguousarray(max_output_tokens, np.uint32)
@@ -163,9 +216,19 @@ class HipEngine:
         out = np.zeros(max(cap, 1), np.int32)
         out_offs = np.zeros(max(offs.shape[0], 1), np.uint32)
         n = C.c_size_t(0)
-        rc = self._lib.marian_hip_translate_token_ids(
-            self._h, _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
-            _ptr(lim), flags, _ptr(out), out.size, _ptr(out_offs), C.byref(n))
+        if candidates is not None or candidate_offsets is not None:
+            cand = np.ascontiguousarray(candidates, np.uint32)
+            coff = np.ascontiguousarray(candidate_offsets, np.uint32)
+            if coff.shape[0] != offs.shape[0]:
+                raise InvalidInput("candidate offsets do not match the packed batch")
+            rc = self._lib.marian_hip_translate_shortlisted(
+                self._h, _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+                _ptr(lim), flags, _ptr(cand) if cand.size else None, _ptr(coff), _ptr(out), out.size,
+                _ptr(out_offs), C.byref(n))
+        else:
+            rc = self._lib.marian_hip_translate_token_ids(
+                self._h, _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+                _ptr(lim), flags, _ptr(out), out.size, _ptr(out_offs), C.byref(n))
         if rc != _lib.OK:
             self._raise(rc)
         return BatchOutput(out[:n.value].copy(), out_offs.copy())
@@ -186,7 +249,7 @@ class HipEngine:
         out = np.zeros(max(cap, 1), np.int32)
         out_offs = np.zeros(max(offs.shape[0], 1), np.uint32)
         enc = np.zeros((max(toks.size, 1), g.dim), np.float32)
-        logits = np.zeros((max(B, 1), g.vocab), np.float32)
+        logits = np.zeros((max(B, 1), self.target_vocab), np.float32)
         active = np.zeros(max(B, 1), np.uint8)
         n = C.c_size_t(0)
         rc = self._lib.marian_hip_translate_probe(

@@ -112,6 +112,128 @@ def seeded_model(seed: int = DEFAULT_SEED, geometry: Geometry | None = None,
 
 
 # ---------------------------------------------------------------------------
+# The reference's own graph: Transformer encoder + SSRU decoder with one weight
+# multiplier and one static activation multiplier per dense layer
+# (crates/marian-cpu/src/q8_engine.rs:76-114, legacy_q8.rs:544-552).
+# ---------------------------------------------------------------------------
+@dataclass
+class SsruGeometry:
+    """Defaults: the reference's supported shape (crates/marian-model/src/
+    manifest.rs:27-36), 384 wide, 8 heads, 6 encoder and 4 SSRU decoder layers,
+    FFN 1536."""
+    source_vocab: int = 32000
+    target_vocab: int = 32000
+    dim: int = 384
+    heads: int = 8
+    ffn_dim: int = 1536
+    encoder_layers: int = 6
+    decoder_layers: int = 4
+
+
+@dataclass
+class SsruModel:
+    geometry: SsruGeometry
+    seed: int
+    encoder_embedding: np.ndarray = field(repr=False)
+    encoder_embedding_mult: float = field(repr=False)
+    decoder_embedding: np.ndarray = field(repr=False)
+    decoder_embedding_mult: float = field(repr=False)
+    output_act_mult: float = field(repr=False)
+    output_bias: np.ndarray = field(repr=False)
+    encoder: list = field(repr=False)
+    decoder: list = field(repr=False)
+
+
+def quantize_tensor(w: np.ndarray) -> tuple[np.ndarray, float]:
+    """One multiplier for the whole tensor: mult = 127 / max|w| (fp32),
+    q = clamp(rint(w * mult), -127, 127) (q8_fp32_artifact.rs:130-132)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    m = np.float32(np.abs(w).max())
+    mult = np.float32(127) / m if m > 0 else np.float32(1)
+    return np.clip(np.rint(w * mult), -127, 127).astype(np.int8), float(mult)
+
+
+def seeded_ssru_model(seed: int = DEFAULT_SEED, geometry: SsruGeometry | None = None,
+                      std: float = 0.02, shared_input_mults: bool = True) -> SsruModel:
+    """Random-init Transformer-SSRU model.  Draw order: encoder embedding
+    [Vs, d], decoder embedding [Vt, d], output bias [Vt]; per encoder layer
+    wq, wk, wv, wo, attn_ln, w1, w2, ffn_ln; per decoder layer ssru_w (no bias),
+    ssru_wf, ssru_ln, wq, wk, wv, wo, context_ln, w1, w2, ffn_ln; then the
+    static activation multipliers.  A multiplier is 127 / (the role's expected
+    largest |input|) times a draw from U(0.85, 1.15): LayerNorm outputs 4.5,
+    embedding + position 4 std sqrt(d) + 1, attention outputs and FFN hidden
+    4 std sqrt(d).  With shared_input_mults the layers that read the same input
+    (wq/wk/wv of an encoder layer, ssru_w/ssru_wf, a context layer's wk/wv)
+    share one multiplier, as calibration from the same activations gives."""
+    g = geometry or SsruGeometry()
+    rng = np.random.Generator(np.random.PCG64(seed))
+    d, f = g.dim, g.ffn_dim
+
+    def normal(*shape: int) -> np.ndarray:
+        return (rng.standard_normal(shape) * std).astype(np.float32)
+
+    def linear(out_dim: int, in_dim: int, bias: bool = True) -> dict:
+        q, mult = quantize_tensor(normal(out_dim, in_dim))
+        return {"weight": q, "weight_mult": mult, "act_mult": 1.0,
+                "bias": normal(out_dim) if bias else None}
+
+    def norm() -> dict:
+        return {"scale": (np.float32(1) + normal(d)).astype(np.float32), "bias": normal(d)}
+
+    enc_q, enc_mult = quantize_tensor(normal(g.source_vocab, d))
+    dec_q, dec_mult = quantize_tensor(normal(g.target_vocab, d))
+    out_bias = normal(g.target_vocab)
+    encoder = []
+    for _ in range(g.encoder_layers):
+        L = {k: linear(d, d) for k in ("wq", "wk", "wv", "wo")}
+        L["attn_ln"] = norm()
+        L["w1"] = linear(f, d)
+        L["w2"] = linear(d, f)
+        L["ffn_ln"] = norm()
+        encoder.append(L)
+    decoder = []
+    for _ in range(g.decoder_layers):
+        L = {"ssru_w": linear(d, d, bias=False), "ssru_wf": linear(d, d), "ssru_ln": norm()}
+        for k in ("wq", "wk", "wv", "wo"):
+            L[k] = linear(d, d)
+        L["context_ln"] = norm()
+        L["w1"] = linear(f, d)
+        L["w2"] = linear(d, f)
+        L["ffn_ln"] = norm()
+        decoder.append(L)
+
+    spread = 4.0 * std * math.sqrt(d)
+    ln_in, emb_in, proj_in = 4.5, spread + 1.0, spread
+
+    def mult(base: float) -> float:
+        return float(np.float32(127.0 / (base * rng.uniform(0.85, 1.15))))
+
+    def assign(layers, group, base):
+        if shared_input_mults:
+            m = mult(base)
+            for k in group:
+                layers[k]["act_mult"] = m
+        else:
+            for k in group:
+                layers[k]["act_mult"] = mult(base)
+
+    for i, L in enumerate(encoder):
+        assign(L, ("wq", "wk", "wv"), emb_in if i == 0 else ln_in)
+        L["wo"]["act_mult"] = mult(proj_in)
+        L["w1"]["act_mult"] = mult(ln_in)
+        L["w2"]["act_mult"] = mult(proj_in)
+    for i, L in enumerate(decoder):
+        assign(L, ("ssru_w", "ssru_wf"), emb_in if i == 0 else ln_in)
+        L["wq"]["act_mult"] = mult(ln_in)
+        assign(L, ("wk", "wv"), ln_in)
+        L["wo"]["act_mult"] = mult(proj_in)
+        L["w1"]["act_mult"] = mult(ln_in)
+        L["w2"]["act_mult"] = mult(proj_in)
+    out_act = mult(ln_in)
+    return SsruModel(g, seed, enc_q, enc_mult, dec_q, dec_mult, out_act, out_bias, encoder, decoder)
+
+
+# ---------------------------------------------------------------------------
 # Workloads.  A batch is (tokens int32[T], offsets uint32[B+1], limits
 # uint32[B]) plus the flags and work limits it is run with.
 # ---------------------------------------------------------------------------

@@ -587,15 +587,32 @@ bool encode_sentence(const oracle_model* m, const Geometry& g, const int32_t* to
 
 // Output scoring for one row: quantize the state, exact int8 dot per vocab
 // row, logit = acc * (1/(a*mult)) + bias, strict '>' argmax in ascending id
-// order (q8_engine.rs:749-790).  Optionally stores every logit.
+// order (q8_engine.rs:749-790), or over the candidate list in its order when
+// one is given (no generation mask then).  Optionally stores every logit.
 bool select_token(const oracle_model* m, const Geometry& g, const float* state, uint32_t flags,
-                  int32_t* token, float* logits_out) {
+                  int32_t* token, float* logits_out, const uint32_t* cands = nullptr,
+                  size_t n_cands = 0) {
   std::vector<int8_t> q(g.d);
   float a;
   if (!quantize_row(state, g.d, q.data(), &a)) return false;
   const bool avx2 = have_avx2();
   int32_t best = -1;
   float best_v = -INFINITY;
+  if (cands) {
+    for (size_t i = 0; i < n_cands; ++i) {
+      const size_t v = cands[i];
+      const int64_t acc = avx2 ? dot_i8_avx2(q.data(), m->embedding + v * g.d, g.d)
+                               : dot_i8_scalar(q.data(), m->embedding + v * g.d, g.d);
+      const float logit = (float)acc * (1.0f / (a * m->embedding_mult[v])) + m->output_bias[v];
+      if (best < 0) best = (int32_t)v;
+      if (logit > best_v) {
+        best_v = logit;
+        best = (int32_t)v;
+      }
+    }
+    *token = best;
+    return true;
+  }
   for (size_t v = 0; v < g.V; ++v) {
     const int64_t acc = avx2 ? dot_i8_avx2(q.data(), m->embedding + v * g.d, g.d)
                              : dot_i8_scalar(q.data(), m->embedding + v * g.d, g.d);
@@ -620,7 +637,8 @@ bool select_token(const oracle_model* m, const Geometry& g, const float* state, 
 bool decode_sentence(const oracle_model* m, const Geometry& g, const float* enc, size_t L,
                      uint32_t limit, uint32_t flags, int order, Pool* pool, Scratch& s,
                      std::vector<int32_t>& out, uint32_t stop_after, int64_t probe_step,
-                     float* probe_logits, bool* probed) {
+                     float* probe_logits, bool* probed, const uint32_t* cands = nullptr,
+                     size_t n_cands = 0) {
   const auto& pos = positions_for(m->dim);
   const size_t d = g.d;
   std::vector<std::vector<float>> ckv(g.Ld, std::vector<float>(L * 2 * d));
@@ -663,7 +681,8 @@ bool decode_sentence(const oracle_model* m, const Geometry& g, const float* enc,
     }
     int32_t token;
     const bool want_logits = probe_logits && (int64_t)t == probe_step;
-    if (!select_token(m, g, x.data(), flags, &token, want_logits ? probe_logits : nullptr))
+    if (!select_token(m, g, x.data(), flags, &token, want_logits ? probe_logits : nullptr, cands,
+                      n_cands))
       return false;
     if (want_logits && probed) *probed = true;
     out.push_back(token);
@@ -687,6 +706,198 @@ int pack_output(const std::vector<std::vector<int32_t>>& gen, int32_t* out_token
     out_offsets[b + 1] = (uint32_t)o;
   }
   return 0;
+}
+
+// ---------------------------------------------------------------------------
+// The Transformer-SSRU graph with static activation multipliers.
+// ---------------------------------------------------------------------------
+// Q8Linear::run_into (q8_gemm.rs:380-448): every element quantized with the
+// tensor's act_mult (quantize_symmetric_u8_into :569-590, non-finite input is
+// an error), exact GEMM, y = acc * (1 / (act_mult * weight_mult)) + bias, with
+// 0.0 added where the layer has no bias (:444).
+bool linear_static(Pool* pool, Scratch& s, const float* x, size_t M, size_t K,
+                   const oracle_static_linear* lin, size_t N, bool relu, float* y) {
+  s.q.resize(M * K);
+  s.acc.resize(M * N);
+  for (size_t i = 0; i < M * K; ++i) {
+    if (!std::isfinite(x[i])) return false;
+    s.q[i] = quantize_one(x[i], lin->act_mult);
+  }
+  if (!gemm_i8(pool, s.q.data(), M, K, lin->weight, N, s.acc.data())) return false;
+  const float inv = 1.0f / (lin->act_mult * lin->weight_mult);
+  for (size_t m = 0; m < M; ++m)
+    for (size_t n = 0; n < N; ++n) {
+      float v = (float)s.acc[m * N + n] * inv + (lin->bias ? lin->bias[n] : 0.0f);
+      if (relu) v = v > 0.0f ? v : 0.0f;  // relu_in_place after the layer (q8_engine.rs:639)
+      y[m * N + n] = v;
+    }
+  return true;
+}
+
+struct SsruGeometry {
+  size_t Vs, Vt, d, H, dh, F, Le, Ld;
+  float emb_scale;
+};
+
+SsruGeometry ssru_geometry(const oracle_ssru_model* m) {
+  SsruGeometry g;
+  g.Vs = m->source_vocab;
+  g.Vt = m->target_vocab;
+  g.d = m->dim;
+  g.H = m->heads;
+  g.dh = m->dim / m->heads;
+  g.F = m->ffn_dim;
+  g.Le = m->encoder_layers;
+  g.Ld = m->decoder_layers;
+  g.emb_scale = std::sqrt((float)m->dim);  // EMBEDDING_SCALE = sqrt(384) (q8_engine.rs:23)
+  return g;
+}
+
+// Q8Embedding::row_into (q8_engine.rs:53-74) then x * EMBEDDING_SCALE + pos.
+void embed_static(const int8_t* table, float mult, size_t d, float scale, int32_t token,
+                  const float* pos, float* out) {
+  const int8_t* e = table + (size_t)token * d;
+  for (size_t i = 0; i < d; ++i) {
+    const float v = (float)e[i] / mult;
+    out[i] = v * scale + pos[i];
+  }
+}
+
+// Attention of `rows` query rows over one sentence's keys, every head.
+void attend_rows(const float* q, const float* k, const float* v, size_t rows, size_t nk,
+                 const SsruGeometry& g, int order, float* out, std::vector<float>& sc) {
+  const float scale = 1.0f / std::sqrt((float)g.dh);
+  for (size_t i = 0; i < rows; ++i)
+    for (size_t h = 0; h < g.H; ++h)
+      attend_one(q + i * g.d + h * g.dh, k + h * g.dh, g.d, v + h * g.dh, g.d, nk, g.dh, scale,
+                 order, out + i * g.d + h * g.dh, sc);
+}
+
+// encode (q8_engine.rs:511-558) for one sentence: Q, K and V each from their
+// own layer and static multiplier.
+bool encode_sentence_ssru(const oracle_ssru_model* m, const SsruGeometry& g, const int32_t* tok,
+                          size_t L, int order, Pool* pool, Scratch& s, std::vector<float>& x) {
+  const auto& pos = positions_for(m->dim);
+  const size_t d = g.d;
+  x.resize(L * d);
+  for (size_t i = 0; i < L; ++i)
+    embed_static(m->encoder_embedding, m->encoder_embedding_mult, d, g.emb_scale, tok[i],
+                 pos.data() + i * d, x.data() + i * d);
+  std::vector<float> q(L * d), k(L * d), v(L * d), att(L * d), y(L * d), h(L * g.F), x2(L * d);
+  std::vector<float> sc;
+  for (size_t l = 0; l < g.Le; ++l) {
+    const oracle_ssru_encoder_layer& E = m->encoder[l];
+    if (!linear_static(pool, s, x.data(), L, d, &E.wq, d, false, q.data()) ||
+        !linear_static(pool, s, x.data(), L, d, &E.wk, d, false, k.data()) ||
+        !linear_static(pool, s, x.data(), L, d, &E.wv, d, false, v.data()))
+      return false;
+    attend_rows(q.data(), k.data(), v.data(), L, L, g, order, att.data(), sc);
+    if (!linear_static(pool, s, att.data(), L, d, &E.wo, d, false, y.data())) return false;
+    residual_ln(y.data(), x.data(), E.attn_ln_scale, E.attn_ln_bias, L, d, order, x2.data());
+    if (!linear_static(pool, s, x2.data(), L, d, &E.w1, g.F, true, h.data()) ||
+        !linear_static(pool, s, h.data(), L, g.F, &E.w2, d, false, y.data()))
+      return false;
+    residual_ln(y.data(), x2.data(), E.ffn_ln_scale, E.ffn_ln_bias, L, d, order, x.data());
+  }
+  return true;
+}
+
+// select_token (q8_engine.rs:749-790) with the static output multiplier: the
+// state quantized once, then a strict '>' scan from -inf over the candidates
+// in order (cands == nullptr: every target id ascending, masked ids skipped).
+bool select_static(const oracle_ssru_model* m, const SsruGeometry& g, const float* state,
+                   uint32_t flags, const uint32_t* cands, size_t n_cands, int32_t* token,
+                   float* logits_out) {
+  std::vector<int8_t> q(g.d);
+  for (size_t i = 0; i < g.d; ++i) {
+    if (!std::isfinite(state[i])) return false;
+    q[i] = quantize_one(state[i], m->output_act_mult);
+  }
+  const float inv = 1.0f / (m->output_act_mult * m->decoder_embedding_mult);
+  const bool avx2 = have_avx2();
+  auto logit_of = [&](size_t id) {
+    const int8_t* w = m->decoder_embedding + id * g.d;
+    const int64_t acc = avx2 ? dot_i8_avx2(q.data(), w, g.d) : dot_i8_scalar(q.data(), w, g.d);
+    return (float)acc * inv + m->output_bias[id];
+  };
+  if (logits_out)
+    for (size_t v = 0; v < g.Vt; ++v) logits_out[v] = -INFINITY;
+  int32_t best = -1;
+  float best_v = -INFINITY;
+  const size_t n = cands ? n_cands : g.Vt;
+  for (size_t i = 0; i < n; ++i) {
+    const size_t id = cands ? cands[i] : i;
+    if (!cands && generation_masked(id, flags)) continue;
+    const float lg = logit_of(id);
+    if (logits_out) logits_out[id] = lg;
+    if (best < 0) best = (int32_t)id;  // candidates[0] when nothing beats -inf
+    if (lg > best_v) {
+      best_v = lg;
+      best = (int32_t)id;
+    }
+  }
+  *token = best < 0 ? 0 : best;
+  return true;
+}
+
+// The greedy loop (q8_engine.rs:382-451) for one sentence with the SSRU
+// decoder: per layer the SSRU sublayer (W and Wf on the layer input, the gate
+// update and LayerNorm, :394-408), cross-attention over the sentence's
+// encoder rows (:410-432) and the FFN.  The recurrent state starts at zero.
+bool decode_sentence_ssru(const oracle_ssru_model* m, const SsruGeometry& g, const float* enc,
+                          size_t L, uint32_t limit, uint32_t flags, int order, Pool* pool,
+                          Scratch& s, const uint32_t* cands, size_t n_cands,
+                          std::vector<int32_t>& out, int64_t probe_step, float* probe_logits,
+                          bool* probed) {
+  const auto& pos = positions_for(m->dim);
+  const size_t d = g.d;
+  std::vector<std::vector<float>> ck(g.Ld, std::vector<float>(L * d)),
+      cv(g.Ld, std::vector<float>(L * d)), state(g.Ld, std::vector<float>(d, 0.0f));
+  for (size_t l = 0; l < g.Ld; ++l)
+    if (!linear_static(pool, s, enc, L, d, &m->decoder[l].wk, d, false, ck[l].data()) ||
+        !linear_static(pool, s, enc, L, d, &m->decoder[l].wv, d, false, cv[l].data()))
+      return false;
+  std::vector<float> x(d), u(d), f(d), x1(d), qc(d), att(d), y(d), x2(d), h(g.F), sc;
+  int32_t prev = -1;
+  for (uint32_t t = 0; t < limit; ++t) {
+    if (prev < 0)
+      std::memcpy(x.data(), pos.data() + (size_t)t * d, d * sizeof(float));
+    else
+      embed_static(m->decoder_embedding, m->decoder_embedding_mult, d, g.emb_scale, prev,
+                   pos.data() + (size_t)t * d, x.data());
+    for (size_t l = 0; l < g.Ld; ++l) {
+      const oracle_ssru_decoder_layer& D = m->decoder[l];
+      if (!linear_static(pool, s, x.data(), 1, d, &D.ssru_w, d, false, u.data()) ||
+          !linear_static(pool, s, x.data(), 1, d, &D.ssru_wf, d, false, f.data()))
+        return false;
+      oracle_ssru_layer_norm(u.data(), f.data(), state[l].data(), x.data(), D.ssru_ln_scale,
+                             D.ssru_ln_bias, 1, d, order, x1.data());
+      if (!linear_static(pool, s, x1.data(), 1, d, &D.wq, d, false, qc.data())) return false;
+      attend_rows(qc.data(), ck[l].data(), cv[l].data(), 1, L, g, order, att.data(), sc);
+      if (!linear_static(pool, s, att.data(), 1, d, &D.wo, d, false, y.data())) return false;
+      residual_ln(y.data(), x1.data(), D.context_ln_scale, D.context_ln_bias, 1, d, order, x2.data());
+      if (!linear_static(pool, s, x2.data(), 1, d, &D.w1, g.F, true, h.data()) ||
+          !linear_static(pool, s, h.data(), 1, g.F, &D.w2, d, false, y.data()))
+        return false;
+      residual_ln(y.data(), x2.data(), D.ffn_ln_scale, D.ffn_ln_bias, 1, d, order, x.data());
+    }
+    int32_t token;
+    const bool want = probe_logits && (int64_t)t == probe_step;
+    if (!select_static(m, g, x.data(), flags, cands, n_cands, &token, want ? probe_logits : nullptr))
+      return false;
+    if (want && probed) *probed = true;
+    out.push_back(token);
+    prev = token;
+    if (token == 0 && !(flags & ORACLE_FLAG_IGNORE_EOS)) break;
+  }
+  return true;
+}
+
+bool ssru_model_ok(const oracle_ssru_model* m) {
+  return m && m->dim && m->heads && m->dim % m->heads == 0 && m->dim % 2 == 0 && m->dim >= 4 &&
+         m->source_vocab > 0 && m->target_vocab > 0 && m->encoder_embedding &&
+         m->decoder_embedding && m->output_bias && m->decoder_layers > 0 && m->decoder &&
+         (m->encoder_layers == 0 || m->encoder);
 }
 
 bool model_ok(const oracle_model* m) {
@@ -880,13 +1091,14 @@ int oracle_translate(const oracle_model* model, const int32_t* tokens, size_t n_
                                 out_len, err, err_cap, UINT32_MAX, nullptr, nullptr, nullptr);
 }
 
-int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
-                           const uint32_t* offsets, size_t n_offsets,
-                           const uint32_t* max_output_tokens, const oracle_limits* limits,
-                           uint32_t flags, int order, int threads, int32_t* out_tokens,
-                           size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
-                           size_t err_cap, uint32_t probe_step, float* enc_out,
-                           float* logits_out, uint8_t* active_out) {
+static int translate_impl(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
+                          const uint32_t* offsets, size_t n_offsets,
+                          const uint32_t* max_output_tokens, const oracle_limits* limits,
+                          uint32_t flags, int order, int threads, const uint32_t* cands,
+                          const uint32_t* cand_offsets, int32_t* out_tokens, size_t out_cap,
+                          uint32_t* out_offsets, size_t* out_len, char* err, size_t err_cap,
+                          uint32_t probe_step, float* enc_out, float* logits_out,
+                          uint8_t* active_out) {
   Err e{err, err_cap};
   if (!model_ok(model)) return e.fail(-2, "invalid model description");
   std::vector<uint32_t> lim;
@@ -894,6 +1106,15 @@ int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, siz
   if (rc) return rc;
   const Geometry g = geometry(model);
   const size_t B = n_offsets - 1;
+  if (cands) {
+    if (!cand_offsets || cand_offsets[0] != 0) return e.fail(-1, "invalid candidate offsets");
+    for (size_t b = 0; b < B; ++b) {
+      if (cand_offsets[b + 1] <= cand_offsets[b])
+        return e.fail(-1, "cannot select from an empty candidate list");
+      for (uint32_t i = cand_offsets[b]; i < cand_offsets[b + 1]; ++i)
+        if (cands[i] >= g.V) return e.fail(-1, "output candidate %u exceeds vocabulary %zu", cands[i], g.V);
+    }
+  }
   std::vector<std::vector<int32_t>> gen(B);
   std::atomic<bool> ok{true};
   std::atomic<size_t> next{0};
@@ -915,7 +1136,9 @@ int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, siz
       if (enc_out) std::memcpy(enc_out + (size_t)offsets[b] * g.d, enc.data(), L * g.d * sizeof(float));
       bool probed = false;
       if (!decode_sentence(model, g, enc.data(), L, lim[b], flags, order, nullptr, s, gen[b], 0,
-                           probe_step, logits_out ? logits_out + b * g.V : nullptr, &probed))
+                           probe_step, logits_out ? logits_out + b * g.V : nullptr, &probed,
+                           cands ? cands + cand_offsets[b] : nullptr,
+                           cands ? cand_offsets[b + 1] - cand_offsets[b] : 0))
         ok = false;
       if (active_out) active_out[b] = probed ? 1 : 0;
     }
@@ -925,6 +1148,30 @@ int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, siz
   for (auto& w : workers) w.join();
   if (!ok) return e.fail(-2, "non-finite activation or accumulator overflow");
   return pack_output(gen, out_tokens, out_cap, out_offsets, out_len, e);
+}
+
+int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
+                           const uint32_t* offsets, size_t n_offsets,
+                           const uint32_t* max_output_tokens, const oracle_limits* limits,
+                           uint32_t flags, int order, int threads, int32_t* out_tokens,
+                           size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
+                           size_t err_cap, uint32_t probe_step, float* enc_out,
+                           float* logits_out, uint8_t* active_out) {
+  return translate_impl(model, tokens, n_tokens, offsets, n_offsets, max_output_tokens, limits, flags,
+                        order, threads, nullptr, nullptr, out_tokens, out_cap, out_offsets, out_len,
+                        err, err_cap, probe_step, enc_out, logits_out, active_out);
+}
+
+int oracle_translate_shortlisted(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
+                                 const uint32_t* offsets, size_t n_offsets,
+                                 const uint32_t* max_output_tokens, const oracle_limits* limits,
+                                 uint32_t flags, int order, int threads, const uint32_t* candidates,
+                                 const uint32_t* cand_offsets, int32_t* out_tokens, size_t out_cap,
+                                 uint32_t* out_offsets, size_t* out_len, char* err, size_t err_cap) {
+  if (!candidates) return Err{err, err_cap}.fail(-1, "candidate lists are required");
+  return translate_impl(model, tokens, n_tokens, offsets, n_offsets, max_output_tokens, limits, flags,
+                        order, threads, candidates, cand_offsets, out_tokens, out_cap, out_offsets,
+                        out_len, err, err_cap, UINT32_MAX, nullptr, nullptr, nullptr);
 }
 
 int oracle_encode(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
@@ -1112,6 +1359,69 @@ int oracle_translate_reference_schedule(
       if (token == 0 && !(flags & ORACLE_FLAG_IGNORE_EOS)) finished[b] = 1;
     }
   }
+  return pack_output(gen, out_tokens, out_cap, out_offsets, out_len, e);
+}
+
+
+int oracle_translate_ssru(const oracle_ssru_model* model, const int32_t* tokens, size_t n_tokens,
+                          const uint32_t* offsets, size_t n_offsets,
+                          const uint32_t* max_output_tokens, const oracle_limits* limits,
+                          uint32_t flags, int order, int threads, const uint32_t* candidates,
+                          const uint32_t* cand_offsets, int32_t* out_tokens, size_t out_cap,
+                          uint32_t* out_offsets, size_t* out_len, char* err, size_t err_cap,
+                          uint32_t probe_step, float* enc_out, float* logits_out,
+                          uint8_t* active_out) {
+  Err e{err, err_cap};
+  if (!ssru_model_ok(model)) return e.fail(-2, "invalid model description");
+  // validate_batch (q8_engine.rs:468-509) checks source ids against the
+  // source vocabulary; the shared checks take it from a transformer view.
+  oracle_model view{};
+  view.vocab = model->source_vocab;
+  std::vector<uint32_t> lim;
+  int rc = validate(&view, tokens, n_tokens, offsets, n_offsets, max_output_tokens, limits, lim, e);
+  if (rc) return rc;
+  const SsruGeometry g = ssru_geometry(model);
+  const size_t B = n_offsets - 1;
+  if (candidates) {
+    if (!cand_offsets || cand_offsets[0] != 0) return e.fail(-1, "invalid candidate offsets");
+    for (size_t b = 0; b < B; ++b) {
+      if (cand_offsets[b + 1] <= cand_offsets[b])
+        return e.fail(-1, "cannot select from an empty candidate list");
+      for (uint32_t i = cand_offsets[b]; i < cand_offsets[b + 1]; ++i)
+        if (candidates[i] >= g.Vt)
+          return e.fail(-1, "output candidate %u exceeds vocabulary %zu", candidates[i], g.Vt);
+    }
+  }
+  std::vector<std::vector<int32_t>> gen(B);
+  std::atomic<bool> ok{true};
+  std::atomic<size_t> next{0};
+  auto work = [&] {
+    Scratch s;
+    std::vector<float> enc;
+    for (;;) {
+      const size_t b = next.fetch_add(1);
+      if (b >= B) return;
+      const size_t L = offsets[b + 1] - offsets[b];
+      if (!encode_sentence_ssru(model, g, tokens + offsets[b], L, order, nullptr, s, enc)) {
+        ok = false;
+        continue;
+      }
+      if (enc_out) std::memcpy(enc_out + (size_t)offsets[b] * g.d, enc.data(), L * g.d * sizeof(float));
+      const uint32_t* c = candidates ? candidates + cand_offsets[b] : nullptr;
+      const size_t nc = candidates ? cand_offsets[b + 1] - cand_offsets[b] : 0;
+      bool probed = false;
+      if (!decode_sentence_ssru(model, g, enc.data(), L, lim[b], flags, order, nullptr, s, c, nc,
+                                gen[b], probe_step, logits_out ? logits_out + b * g.Vt : nullptr,
+                                &probed))
+        ok = false;
+      if (active_out) active_out[b] = probed ? 1 : 0;
+    }
+  };
+  std::vector<std::thread> workers;
+  for (int i = 1; i < std::max(1, threads); ++i) workers.emplace_back(work);
+  work();
+  for (auto& w : workers) w.join();
+  if (!ok) return e.fail(-2, "non-finite activation or accumulator overflow");
   return pack_output(gen, out_tokens, out_cap, out_offsets, out_len, e);
 }
 

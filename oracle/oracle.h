@@ -96,6 +96,50 @@ typedef struct {
   const oracle_decoder_layer* decoder;
 } oracle_model;
 
+/* The reference's own graph (q8_engine.rs:76-114): Transformer encoder, SSRU
+ * decoder, one weight multiplier and one static activation multiplier per
+ * dense layer, separate encoder/decoder embeddings (the decoder's is the tied
+ * output projection).  Same field order as marian_hip_ssru_model. */
+typedef struct {
+  const int8_t* weight; /* [out, in] */
+  float weight_mult;
+  float act_mult;
+  const float* bias; /* [out] or NULL */
+} oracle_static_linear;
+
+typedef struct {
+  oracle_static_linear wq, wk, wv, wo;
+  const float* attn_ln_scale;
+  const float* attn_ln_bias;
+  oracle_static_linear w1, w2;
+  const float* ffn_ln_scale;
+  const float* ffn_ln_bias;
+} oracle_ssru_encoder_layer;
+
+typedef struct {
+  oracle_static_linear ssru_w, ssru_wf;
+  const float* ssru_ln_scale;
+  const float* ssru_ln_bias;
+  oracle_static_linear wq, wk, wv, wo;
+  const float* context_ln_scale;
+  const float* context_ln_bias;
+  oracle_static_linear w1, w2;
+  const float* ffn_ln_scale;
+  const float* ffn_ln_bias;
+} oracle_ssru_decoder_layer;
+
+typedef struct {
+  uint32_t source_vocab, target_vocab, dim, heads, ffn_dim, encoder_layers, decoder_layers;
+  const int8_t* encoder_embedding;
+  float encoder_embedding_mult;
+  const int8_t* decoder_embedding;
+  float decoder_embedding_mult;
+  float output_act_mult;
+  const float* output_bias;
+  const oracle_ssru_encoder_layer* encoder;
+  const oracle_ssru_decoder_layer* decoder;
+} oracle_ssru_model;
+
 /* Work limits; 0 disables a cap (reference values in brackets). */
 typedef struct {
   uint32_t max_length_factor;    /* [2] limit <= len * factor */
@@ -192,6 +236,18 @@ int oracle_translate_probe(const oracle_model* model, const int32_t* tokens, siz
                            size_t err_cap, uint32_t probe_step, float* enc_out,
                            float* logits_out, uint8_t* active_out);
 
+/* oracle_translate with per-sentence output candidates (select_token over
+ * LexicalShortlist::candidates, q8_engine.rs:576-584, 749-790): sentence b
+ * scores candidates[cand_offsets[b] .. cand_offsets[b+1]) in list order, the
+ * first maximum winning, without the generation mask.  -1 for an empty list
+ * or an id out of the vocabulary. */
+int oracle_translate_shortlisted(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
+                                 const uint32_t* offsets, size_t n_offsets,
+                                 const uint32_t* max_output_tokens, const oracle_limits* limits,
+                                 uint32_t flags, int order, int threads, const uint32_t* candidates,
+                                 const uint32_t* cand_offsets, int32_t* out_tokens, size_t out_cap,
+                                 uint32_t* out_offsets, size_t* out_len, char* err, size_t err_cap);
+
 /* Same contract, executed the way the reference x86 engine schedules the work
  * (padded encoder batch, all rows every decode step, AVX2 madd GEMM row-split
  * over `threads` when rows>1 && rows*N >= 8192, scalar output scoring).  Its
@@ -213,6 +269,25 @@ int oracle_encode(const oracle_model* model, const int32_t* tokens, size_t n_tok
  * unless NO_GENERATION_MASK). */
 int oracle_last_step_logits(const oracle_model* model, const int32_t* tokens, size_t n_tokens,
                             uint32_t steps, uint32_t flags, int order, float* logits);
+
+/* Q8CpuEngine::translate_token_ids over the Transformer-SSRU graph
+ * (q8_engine.rs:353-466 with encode :511-574, the SSRU decoder layer
+ * :394-432, select_token :749-790).  candidates/cand_offsets[B+1] give each
+ * sentence's output candidates in scan order; NULL scores the whole target
+ * vocabulary in ascending order with the generation mask (what
+ * LexicalShortlist::from_bytes(None) yields).  enc_out, logits_out[B,
+ * target_vocab] (probe_step; ids not scored are -inf) and active_out as in
+ * oracle_translate_probe; each may be NULL.  Same return codes as
+ * oracle_translate, plus -1 for an empty candidate list or an id out of the
+ * target vocabulary. */
+int oracle_translate_ssru(const oracle_ssru_model* model, const int32_t* tokens, size_t n_tokens,
+                          const uint32_t* offsets, size_t n_offsets,
+                          const uint32_t* max_output_tokens, const oracle_limits* limits,
+                          uint32_t flags, int order, int threads, const uint32_t* candidates,
+                          const uint32_t* cand_offsets, int32_t* out_tokens, size_t out_cap,
+                          uint32_t* out_offsets, size_t* out_len, char* err, size_t err_cap,
+                          uint32_t probe_step, float* enc_out, float* logits_out,
+                          uint8_t* active_out);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,37 @@ class Model(C.Structure):
                 ("encoder", C.POINTER(EncoderLayer)), ("decoder", C.POINTER(DecoderLayer))]
 
 
+class StaticLinear(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("weight_mult", C.c_float), ("act_mult", C.c_float),
+                ("bias", C.c_void_p)]
+
+
+class SsruEncoderLayer(C.Structure):
+    _fields_ = [("wq", StaticLinear), ("wk", StaticLinear), ("wv", StaticLinear),
+                ("wo", StaticLinear), ("attn_ln_scale", C.c_void_p), ("attn_ln_bias", C.c_void_p),
+                ("w1", StaticLinear), ("w2", StaticLinear), ("ffn_ln_scale", C.c_void_p),
+                ("ffn_ln_bias", C.c_void_p)]
+
+
+class SsruDecoderLayer(C.Structure):
+    _fields_ = [("ssru_w", StaticLinear), ("ssru_wf", StaticLinear),
+                ("ssru_ln_scale", C.c_void_p), ("ssru_ln_bias", C.c_void_p),
+                ("wq", StaticLinear), ("wk", StaticLinear), ("wv", StaticLinear),
+                ("wo", StaticLinear), ("context_ln_scale", C.c_void_p),
+                ("context_ln_bias", C.c_void_p), ("w1", StaticLinear), ("w2", StaticLinear),
+                ("ffn_ln_scale", C.c_void_p), ("ffn_ln_bias", C.c_void_p)]
+
+
+class SsruModelStruct(C.Structure):
+    _fields_ = [("source_vocab", C.c_uint32), ("target_vocab", C.c_uint32), ("dim", C.c_uint32),
+                ("heads", C.c_uint32), ("ffn_dim", C.c_uint32), ("encoder_layers", C.c_uint32),
+                ("decoder_layers", C.c_uint32), ("encoder_embedding", C.c_void_p),
+                ("encoder_embedding_mult", C.c_float), ("decoder_embedding", C.c_void_p),
+                ("decoder_embedding_mult", C.c_float), ("output_act_mult", C.c_float),
+                ("output_bias", C.c_void_p), ("encoder", C.POINTER(SsruEncoderLayer)),
+                ("decoder", C.POINTER(SsruDecoderLayer))]
+
+
 class Limits(C.Structure):
     _fields_ = [("max_length_factor", C.c_uint32), ("max_generation_steps", C.c_uint32),
                 ("max_position", C.c_uint32), ("max_batch", C.c_uint32),
@@ -95,6 +126,13 @@ _SIG = {
                                          C.c_uint32, C.c_int, C.c_int, _P, _SZ, _P, C.POINTER(_SZ),
                                          C.c_char_p, _SZ, C.c_uint32, _P, _P, _P]),
     "oracle_encode": (C.c_int, [C.POINTER(Model), _P, _SZ, _P, _SZ, C.c_int, C.c_int, _P]),
+    "oracle_translate_shortlisted": (C.c_int, [C.POINTER(Model), _P, _SZ, _P, _SZ, _P,
+                                               C.POINTER(Limits), C.c_uint32, C.c_int, C.c_int, _P,
+                                               _P, _P, _SZ, _P, C.POINTER(_SZ), C.c_char_p, _SZ]),
+    "oracle_translate_ssru": (C.c_int, [C.POINTER(SsruModelStruct), _P, _SZ, _P, _SZ, _P,
+                                        C.POINTER(Limits), C.c_uint32, C.c_int, C.c_int, _P, _P,
+                                        _P, _SZ, _P, C.POINTER(_SZ), C.c_char_p, _SZ, C.c_uint32,
+                                        _P, _P, _P]),
     "oracle_last_step_logits": (C.c_int, [C.POINTER(Model), _P, _SZ, C.c_uint32, C.c_uint32,
                                           C.c_int, _P]),
 }
@@ -157,6 +195,86 @@ class OracleModel:
         self._keep = (keep, enc, dec)
 
 
+class OracleSsruModel:
+    """ctypes view of a Transformer-SSRU model (the SsruModel fields)."""
+
+    def __init__(self, m):
+        keep = []
+
+        def arr(a, dtype):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dtype)
+            keep.append(a)
+            return a.ctypes.data
+
+        def lin(d):
+            return StaticLinear(arr(d["weight"], np.int8), d["weight_mult"], d["act_mult"],
+                                arr(d["bias"], np.float32))
+
+        def ln(d):
+            return arr(d["scale"], np.float32), arr(d["bias"], np.float32)
+
+        g = m.geometry
+        enc = (SsruEncoderLayer * max(1, len(m.encoder)))()
+        for i, L in enumerate(m.encoder):
+            enc[i] = SsruEncoderLayer(lin(L["wq"]), lin(L["wk"]), lin(L["wv"]), lin(L["wo"]),
+                                      *ln(L["attn_ln"]), lin(L["w1"]), lin(L["w2"]),
+                                      *ln(L["ffn_ln"]))
+        dec = (SsruDecoderLayer * max(1, len(m.decoder)))()
+        for i, L in enumerate(m.decoder):
+            dec[i] = SsruDecoderLayer(lin(L["ssru_w"]), lin(L["ssru_wf"]), *ln(L["ssru_ln"]),
+                                      lin(L["wq"]), lin(L["wk"]), lin(L["wv"]), lin(L["wo"]),
+                                      *ln(L["context_ln"]), lin(L["w1"]), lin(L["w2"]),
+                                      *ln(L["ffn_ln"]))
+        self.struct = SsruModelStruct(
+            g.source_vocab, g.target_vocab, g.dim, g.heads, g.ffn_dim, len(m.encoder),
+            len(m.decoder), arr(m.encoder_embedding, np.int8), m.encoder_embedding_mult,
+            arr(m.decoder_embedding, np.int8), m.decoder_embedding_mult, m.output_act_mult,
+            arr(m.output_bias, np.float32), enc, dec)
+        self.geometry = g
+        self._keep = (keep, enc, dec)
+
+
+def translate_ssru(model: OracleSsruModel, tokens, offsets, max_output_tokens, limits: dict,
+                   flags=0, candidates=None, candidate_offsets=None, probe_step=None,
+                   order=REFERENCE, threads=8):
+    """Greedy translation over the Transformer-SSRU graph.  Returns the token
+    lists; with probe_step also the encoder states [T, d], the logits [B, Vt]
+    of that step (ids not scored are -inf) and the rows that reached it."""
+    lib = load()
+    toks = np.ascontiguousarray(tokens, np.int32)
+    offs = np.ascontiguousarray(offsets, np.uint32)
+    req = np.ascontiguousarray(max_output_tokens, np.uint32)
+    B = offs.size - 1
+    g = model.geometry
+    cap = int(np.minimum(req.astype(np.int64), 4096).sum()) + 1
+    out = np.zeros(cap, np.int32)
+    out_offs = np.zeros(offs.size, np.uint32)
+    n = C.c_size_t(0)
+    err = C.create_string_buffer(512)
+    lim = make_limits(limits)
+    cand = None if candidates is None else np.ascontiguousarray(candidates, np.uint32)
+    coff = None if candidate_offsets is None else np.ascontiguousarray(candidate_offsets, np.uint32)
+    enc = logits = active = None
+    if probe_step is not None:
+        enc = np.zeros((max(toks.size, 1), g.dim), np.float32)
+        logits = np.zeros((max(B, 1), g.target_vocab), np.float32)
+        active = np.zeros(max(B, 1), np.uint8)
+    rc = lib.oracle_translate_ssru(
+        C.byref(model.struct), _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+        _ptr(req), C.byref(lim), flags, order, threads, _ptr(cand), _ptr(coff), _ptr(out), cap,
+        _ptr(out_offs), C.byref(n), err, 512,
+        0xFFFFFFFF if probe_step is None else int(probe_step), _ptr(enc), _ptr(logits),
+        _ptr(active))
+    if rc != 0:
+        raise OracleError(rc, err.value.decode())
+    rows = [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(B)]
+    if probe_step is None:
+        return rows
+    return rows, enc[:toks.size], logits[:B], active[:B].astype(bool)
+
+
 def make_limits(d: dict) -> Limits:
     return Limits(d["max_length_factor"], d["max_generation_steps"], d["max_position"],
                   d["max_batch"], d["max_source_tokens"], d["max_padded_cells"])
@@ -185,6 +303,30 @@ def translate(model: OracleModel, tokens, offsets, max_output_tokens, limits: di
     rc = fn(C.byref(model.struct), _ptr(toks) if toks.size else None, toks.size, _ptr(offs),
             offs.size, _ptr(req), C.byref(lim), flags, order, threads, _ptr(out), cap,
             _ptr(out_offs), C.byref(n), err, 512)
+    if rc != 0:
+        raise OracleError(rc, err.value.decode())
+    return [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(offs.size - 1)]
+
+
+def translate_shortlisted(model: OracleModel, tokens, offsets, max_output_tokens, limits: dict,
+                          candidates, candidate_offsets, flags=0, order=REFERENCE, threads=8):
+    """translate() with each sentence scored over its candidate list."""
+    lib = load()
+    toks = np.ascontiguousarray(tokens, np.int32)
+    offs = np.ascontiguousarray(offsets, np.uint32)
+    req = np.ascontiguousarray(max_output_tokens, np.uint32)
+    cand = np.ascontiguousarray(candidates, np.uint32)
+    coff = np.ascontiguousarray(candidate_offsets, np.uint32)
+    cap = int(np.minimum(req.astype(np.int64), 4096).sum()) + 1
+    out = np.zeros(cap, np.int32)
+    out_offs = np.zeros(offs.size, np.uint32)
+    n = C.c_size_t(0)
+    err = C.create_string_buffer(512)
+    lim = make_limits(limits)
+    rc = lib.oracle_translate_shortlisted(
+        C.byref(model.struct), _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+        _ptr(req), C.byref(lim), flags, order, threads, _ptr(cand), _ptr(coff), _ptr(out), cap,
+        _ptr(out_offs), C.byref(n), err, 512)
     if rc != 0:
         raise OracleError(rc, err.value.decode())
     return [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(offs.size - 1)]

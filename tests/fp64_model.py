@@ -185,3 +185,145 @@ class Fp64Model:
             if tok == 0 and not flags & 1:
                 break
         return out, probed
+
+
+# ---------------------------------------------------------------------------
+# The reference's own graph: Transformer encoder + SSRU decoder with static
+# per-tensor activation multipliers (q8_engine.rs:76-114, 382-451, 511-574;
+# tensor.rs:184-218).
+#   linear         q = clamp(rint(x a), -127, 127), y = acc / (a w) + b
+#   embedding      x = (q / mult) sqrt(d) + pos, separate encoder/decoder tables
+#   encoder layer  Q, K, V each from its own layer (and multiplier)
+#   SSRU           c = W x, f = Wf x + bf, g = 1 / (1 + exp(-f)),
+#                  s = g s + (1 - g) c, x1 = LN(relu(s) + x)
+#   context        x2 = LN(Wo attn(Wq x1, Wk enc, Wv enc) + x1), then the FFN
+#   scoring        the state quantized with the output multiplier; candidates
+#                  scanned in order (or every id with the generation mask)
+# ---------------------------------------------------------------------------
+SSRU_MISTAKES = (
+    "gate_inverted",          # s = (1 - g) s + g c
+    "state_not_carried",      # the recurrent state restarts at zero every step
+    "ssru_no_relu",           # LN(s + x) instead of LN(relu(s) + x)
+    "ssru_no_residual",       # LN(relu(s)) without the layer input
+    "context_q_from_input",   # the context query from x instead of the SSRU output
+    "cross_from_embedding",   # context K/V from the encoder input
+    "decoder_table_swap",     # decoder input from the encoder embedding table
+    "output_mult_dynamic",    # output row quantized per row instead of statically
+    "kv_mult_swap",           # wk quantized with wv's multiplier and back
+    "ffn_residual_x",         # FFN residual from the SSRU output instead of x2
+    "no_sqrt_d",
+    "pos_off_by_one",
+)
+
+
+def slinear(x, lin, relu=False, act=None):
+    a = lin["act_mult"] if act is None else act
+    q = np.clip(np.rint(x * np.float64(a)), -127, 127)
+    acc = q @ lin["weight"].astype(np.float64).T
+    y = acc / (np.float64(a) * np.float64(lin["weight_mult"]))
+    if lin["bias"] is not None:
+        y = y + lin["bias"].astype(np.float64)
+    return np.maximum(y, 0.0) if relu else y
+
+
+class Fp64SsruModel:
+    def __init__(self, model, mistake=None):
+        assert mistake is None or mistake in SSRU_MISTAKES, mistake
+        self.m = model
+        self.g = model.geometry
+        self.mistake = mistake
+        self.pos = positions(self.g.dim, 4096)
+
+    def _embed(self, table, mult, tok):
+        e = table[tok].astype(np.float64) / np.float64(mult)
+        return e if self.mistake == "no_sqrt_d" else e * np.sqrt(self.g.dim)
+
+    def encode(self, tokens, offsets):
+        H = self.g.heads
+        toks = np.asarray(tokens)
+        p = np.concatenate([np.arange(offsets[i + 1] - offsets[i]) for i in range(len(offsets) - 1)])
+        x = self._embed(self.m.encoder_embedding, self.m.encoder_embedding_mult, toks) + self.pos[p]
+        for L in self.m.encoder:
+            q, k, v = slinear(x, L["wq"]), slinear(x, L["wk"]), slinear(x, L["wv"])
+            att = np.zeros_like(x)
+            for i in range(len(offsets) - 1):
+                sl = slice(int(offsets[i]), int(offsets[i + 1]))
+                att[sl] = attend(q[sl], k[sl], v[sl], H)
+            x1 = layer_norm(slinear(att, L["wo"]) + x, L["attn_ln"])
+            h = slinear(x1, L["w1"], relu=True)
+            x = layer_norm(slinear(h, L["w2"]) + x1, L["ffn_ln"])
+        return x
+
+    def logits(self, state, flags=0, candidates=None):
+        if self.mistake == "output_mult_dynamic":
+            q, a = quantize(state[None, :])
+            q, a = q[0], float(a[0, 0])
+        else:
+            a = np.float64(self.m.output_act_mult)
+            q = np.clip(np.rint(state * a), -127, 127)
+        acc = self.m.decoder_embedding.astype(np.float64) @ q
+        lg = acc / (a * np.float64(self.m.decoder_embedding_mult)) + self.m.output_bias.astype(np.float64)
+        out = np.full_like(lg, -np.inf)
+        if candidates is not None:
+            out[candidates] = lg[candidates]
+        else:
+            out[:] = lg
+            if not flags & 2:
+                out[1] = -np.inf
+                out[7:39] = -np.inf
+        return out
+
+    def decode(self, enc, tokens, steps, flags=1, candidates=None, probe_step=None):
+        d, H = self.g.dim, self.g.heads
+        src = enc
+        if self.mistake == "cross_from_embedding":
+            src = self._embed(self.m.encoder_embedding, self.m.encoder_embedding_mult,
+                              np.asarray(tokens)) + self.pos[:len(tokens)]
+        kv = []
+        for L in self.m.decoder:
+            if self.mistake == "kv_mult_swap":
+                kv.append((slinear(src, L["wk"], act=L["wv"]["act_mult"]),
+                           slinear(src, L["wv"], act=L["wk"]["act_mult"])))
+            else:
+                kv.append((slinear(src, L["wk"]), slinear(src, L["wv"])))
+        state = [np.zeros(d) for _ in self.m.decoder]
+        prev, out, probed = -1, [], None
+        cand = None if candidates is None else np.asarray(candidates, np.int64)
+        for t in range(steps):
+            p = self.pos[t + 1 if self.mistake == "pos_off_by_one" else t]
+            if prev < 0:
+                x = p.copy()
+            elif self.mistake == "decoder_table_swap":
+                x = self._embed(self.m.encoder_embedding, self.m.encoder_embedding_mult, prev) + p
+            else:
+                x = self._embed(self.m.decoder_embedding, self.m.decoder_embedding_mult, prev) + p
+            x = x[None, :]
+            for li, L in enumerate(self.m.decoder):
+                c = slinear(x, L["ssru_w"])
+                f = slinear(x, L["ssru_wf"])
+                gate = 1.0 / (1.0 + np.exp(-f))
+                if self.mistake == "gate_inverted":
+                    gate = 1.0 - gate
+                s0 = np.zeros(d) if self.mistake == "state_not_carried" else state[li]
+                s = gate * s0 + (1.0 - gate) * c
+                state[li] = s[0]
+                z = s if self.mistake == "ssru_no_relu" else np.maximum(s, 0.0)
+                x1 = layer_norm(z if self.mistake == "ssru_no_residual" else z + x, L["ssru_ln"])
+                qc = slinear(x if self.mistake == "context_q_from_input" else x1, L["wq"])
+                att = attend(qc, kv[li][0], kv[li][1], H)
+                x2 = layer_norm(slinear(att, L["wo"]) + x1, L["context_ln"])
+                h = slinear(x2, L["w1"], relu=True)
+                x = layer_norm(slinear(h, L["w2"]) + (x1 if self.mistake == "ffn_residual_x" else x2),
+                               L["ffn_ln"])
+            lg = self.logits(x[0], flags, cand)
+            if probe_step == t:
+                probed = lg
+            if cand is not None:
+                tok = int(cand[np.argmax(lg[cand])])
+            else:
+                tok = int(np.argmax(lg))
+            out.append(tok)
+            prev = tok
+            if tok == 0 and not flags & 1:
+                break
+        return out, probed

@@ -1,0 +1,137 @@
+"""GPU parity for the reference's own graph: Transformer encoder + SSRU decoder
+with static per-tensor activation multipliers (marian_hip_engine_create_ssru),
+and shortlisted scoring (marian_hip_translate_shortlisted) on both graphs.
+
+Every case is compared with the oracle (oracle_translate_ssru /
+oracle_translate_shortlisted) token for token; the probe cases also compare
+the encoder states and one step's logits bit for bit.  The geometries cover
+the reference's supported shape (d = 384, 8 heads of 48, FFN 1536, 6 encoder
+and 4 SSRU decoder layers, crates/marian-model/src/manifest.rs:27-36), a
+64-wide-head shape, layers whose inputs share one static multiplier (one
+quantization and one fused GEMM per group) and layers that do not (one per
+layer), and candidate lists from a lexical shortlist.
+"""
+
+import importlib
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ORACLE_THREADS = 16
+
+
+@pytest.fixture(scope="module")
+def sl(pkg):
+    return importlib.import_module(pkg.__name__ + ".shortlist")
+
+
+def shortlist_lists(sl, toks, offs, Vs, Vt, per_source=12, first=40, seed=3):
+    """A random lexical shortlist and the candidate lists of the batch."""
+    rng = np.random.default_rng(seed)
+    targets = rng.integers(0, Vt, size=per_source * Vs).astype(np.uint32)
+    offsets = np.arange(Vs + 1, dtype=np.uint64) * per_source
+    s = sl.LexicalShortlist.from_bytes(sl.LexicalShortlist.to_bytes(first, offsets, targets), Vs, Vt)
+    return sl.pack_candidates([s.candidates(toks[offs[b]:offs[b + 1]]) for b in range(len(offs) - 1)])
+
+
+def run_both(pkg, orc, engine, om, b, flags, cand=None, coff=None):
+    got = engine.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, flags,
+                                     candidates=cand, candidate_offsets=coff).rows()
+    want = orc.translate_ssru(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, flags,
+                              candidates=cand, candidate_offsets=coff, threads=ORACLE_THREADS)
+    return got, want
+
+
+SHAPES = {
+    "d384-dh48": dict(dim=384, heads=8, ffn_dim=1536),
+    "d256-dh64": dict(dim=256, heads=4, ffn_dim=1024),
+}
+
+
+@pytest.mark.parametrize("shared", [True, False], ids=["shared-mults", "own-mults"])
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_ssru_engine_token_exact(pkg, orc, sl, shape, shared):
+    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=2, decoder_layers=2,
+                         **SHAPES[shape])
+    model = pkg.seeded_ssru_model(seed=31, geometry=g, std=0.05, shared_input_mults=shared)
+    om = orc.OracleSsruModel(model)
+    b = pkg.ragged_batch(seed=19, n=12, vocab=g.source_vocab)
+    cand, coff, _ = shortlist_lists(sl, b.tokens, b.offsets, g.source_vocab, g.target_vocab)
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        for name, c, co in (("full vocabulary", None, None), ("shortlist", cand, coff)):
+            got, want = run_both(pkg, orc, e, om, b, 0, c, co)
+            print(f"{shape} {'shared' if shared else 'own'} {name}: {sum(map(len, got))} tokens",
+                  flush=True)
+            assert got == want
+        assert e.is_ready()
+
+
+@pytest.mark.parametrize("step", [0, 5, 17])
+def test_ssru_probe_bit_exact(pkg, orc, step):
+    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=2, decoder_layers=3)
+    model = pkg.seeded_ssru_model(seed=41, geometry=g, std=0.05)
+    om = orc.OracleSsruModel(model)
+    b = pkg.ragged_batch(seed=23, n=9, vocab=g.source_vocab)
+    lim = np.minimum(b.max_output_tokens.astype(np.int64), step + 1).astype(np.uint32)
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        out, enc, lg, act = e.translate_probe(b.tokens, b.offsets, lim, pkg.FLAG_IGNORE_EOS,
+                                              probe_step=step)
+    rows, enc_o, lg_o, act_o = orc.translate_ssru(om, b.tokens, b.offsets, lim, b.limits,
+                                                  pkg.FLAG_IGNORE_EOS, probe_step=step,
+                                                  threads=ORACLE_THREADS)
+    print(f"step {step}: {int(act.sum())} active rows", flush=True)
+    assert out.rows() == rows
+    assert np.array_equal(act, act_o)
+    assert np.array_equal(enc.view(np.uint32), enc_o.view(np.uint32))
+    assert np.array_equal(lg[act_o].view(np.uint32), lg_o[act_o].view(np.uint32))
+
+
+def test_ssru_reference_shape_ragged_64(pkg, orc, sl):
+    """The reference's supported shape at full size (32000-id vocabularies,
+    6 encoder / 4 SSRU decoder layers) on the 64-sentence ragged batch, with
+    and without a shortlist."""
+    g = pkg.SsruGeometry()
+    model = pkg.seeded_ssru_model(geometry=g)
+    om = orc.OracleSsruModel(model)
+    b = pkg.ragged_batch()
+    cand, coff, _ = shortlist_lists(sl, b.tokens, b.offsets, g.source_vocab, g.target_vocab,
+                                    per_source=40, first=100)
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        for name, c, co in (("full vocabulary", None, None), ("shortlist", cand, coff)):
+            got, want = run_both(pkg, orc, e, om, b, b.flags, c, co)
+            print(f"reference shape, {name}: {sum(map(len, got))} tokens", flush=True)
+            assert got == want
+
+
+def test_transformer_engine_shortlisted(pkg, orc, sl, small_model):
+    """Candidate scoring on the transformer graph (dynamic multipliers), at
+    step row counts that use the fused decode kernels and the generic ones."""
+    g = small_model.geometry
+    om = orc.OracleModel(small_model)
+    b = pkg.ragged_batch(seed=29, n=40, vocab=g.vocab)
+    cand, coff, _ = shortlist_lists(sl, b.tokens, b.offsets, g.vocab, g.vocab)
+    with pkg.HipEngine(small_model, limits=b.limits) as e:
+        got = e.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, b.flags,
+                                    candidates=cand, candidate_offsets=coff).rows()
+        want = orc.translate_shortlisted(om, b.tokens, b.offsets, b.max_output_tokens, b.limits,
+                                         cand, coff, b.flags, threads=ORACLE_THREADS)
+        print(f"transformer shortlisted: {sum(map(len, got))} tokens", flush=True)
+        assert got == want
+        assert e.is_ready()
+
+
+def test_shortlisted_input_errors_keep_the_engine_ready(pkg, small_model):
+    b = pkg.ragged_batch(seed=3, n=2, vocab=small_model.geometry.vocab)
+    with pkg.HipEngine(small_model, limits=b.limits) as e:
+        with pytest.raises(pkg.InvalidInput, match="empty candidate"):
+            e.translate_token_ids(b.tokens, b.offsets, [4, 4], candidates=[0, 5],
+                                  candidate_offsets=[0, 2, 2])
+        with pytest.raises(pkg.InvalidInput, match="exceeds vocabulary"):
+            e.translate_token_ids(b.tokens, b.offsets, [4, 4], candidates=[0, 5, 2048],
+                                  candidate_offsets=[0, 2, 3])
+        assert e.is_ready()
+        out = e.translate_token_ids(b.tokens, b.offsets, [4, 4], pkg.FLAG_IGNORE_EOS,
+                                    candidates=[7, 9], candidate_offsets=[0, 1, 2]).rows()
+        assert out == [[7] * 4, [9] * 4]

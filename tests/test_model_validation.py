@@ -78,3 +78,60 @@ def test_valid_tiny_model_passes_validation(pkg, tiny):
         pytest.skip("a GPU is visible: the engine would be created")
     with pytest.raises(pkg.DeviceError):
         pkg.HipEngine(tiny)
+
+
+# ---- the Transformer-SSRU graph (marian_hip_engine_create_ssru) ----
+@pytest.fixture(scope="module")
+def tiny_ssru(pkg):
+    g = pkg.SsruGeometry(source_vocab=90, target_vocab=96, dim=128, heads=2, ffn_dim=256,
+                         encoder_layers=1, decoder_layers=1)
+    return pkg.seeded_ssru_model(seed=3, geometry=g)
+
+
+@pytest.mark.parametrize("where", [("encoder", 0, "wk"), ("decoder", 0, "ssru_wf"),
+                                   ("decoder", 0, "wv"), ("decoder", 0, "w2")])
+@pytest.mark.parametrize("field", ["act_mult", "weight_mult"])
+@pytest.mark.parametrize("bad", [0.0, -2.0, float("nan"), float("inf")])
+def test_ssru_multipliers_must_be_finite_and_positive(pkg, tiny_ssru, where, field, bad):
+    m = copy.deepcopy(tiny_ssru)
+    part, idx, name = where
+    getattr(m, part)[idx][name][field] = bad
+    rejected(pkg, m, "multiplier")
+
+
+def test_ssru_weight_and_table_checks(pkg, tiny_ssru):
+    m = copy.deepcopy(tiny_ssru)
+    m.decoder[0]["ssru_w"]["weight"][1, 2] = -128
+    rejected(pkg, m, "[-127, 127]")
+    m = copy.deepcopy(tiny_ssru)
+    m.encoder_embedding[5, 5] = -128
+    rejected(pkg, m, "encoder embedding")
+    m = copy.deepcopy(tiny_ssru)
+    m.decoder_embedding_mult = 0.0
+    rejected(pkg, m, "decoder embedding")
+    m = copy.deepcopy(tiny_ssru)
+    m.output_act_mult = float("nan")
+    rejected(pkg, m, "output multiplier")
+    m = copy.deepcopy(tiny_ssru)
+    m.decoder[0]["context_ln"]["scale"] = None
+    rejected(pkg, m, "LayerNorm")
+
+
+@pytest.mark.parametrize("geom,needle", [
+    (dict(dim=576, heads=12), "heads"),
+    (dict(ffn_dim=100), "ffn_dim"),
+    (dict(decoder_layers=0), "decoder layer"),
+])
+def test_ssru_unsupported_geometry_is_a_model_error(pkg, geom, needle):
+    g = dict(source_vocab=90, target_vocab=96, dim=128, heads=2, ffn_dim=256, encoder_layers=1,
+             decoder_layers=1)
+    g.update(geom)
+    m = pkg.seeded_ssru_model(seed=4, geometry=pkg.SsruGeometry(**g))
+    rejected(pkg, m, needle)
+
+
+def test_valid_tiny_ssru_model_passes_validation(pkg, tiny_ssru):
+    if pkg._lib.load().marian_hip_device_count() > 0:
+        pytest.skip("a GPU is visible: the engine would be created")
+    with pytest.raises(pkg.DeviceError):
+        pkg.HipEngine(tiny_ssru)

@@ -90,3 +90,47 @@ def test_oracle_candidate_scoring(orc, sl):
     with pytest.raises(orc.OracleError):
         orc.candidate_argmax(xq, xa, emb, mult, bias, np.array([V], np.uint32),
                              np.array([0, 1], np.uint32))
+
+
+def _unmasked(V):
+    ids = np.arange(V, dtype=np.uint32)
+    return ids[(ids != 1) & ((ids < 7) | (ids > 38))]
+
+
+def test_oracle_translate_with_the_full_list_equals_masked_vocabulary(pkg, orc, sl):
+    """No shortlist (from_bytes(None)) gives every unmasked id ascending:
+    scoring that list must reproduce full-vocabulary scoring with the mask,
+    in both graphs."""
+    g = pkg.Geometry(vocab=400, dim=128, heads=2, ffn_dim=256, encoder_layers=1, decoder_layers=1)
+    m = pkg.seeded_model(seed=21, geometry=g, std=0.3)
+    b = pkg.ragged_batch(seed=2, n=4, vocab=400)
+    lim = np.minimum(b.max_output_tokens, 12)
+    full = sl.LexicalShortlist.from_bytes(None, 400, 400).candidates([3])
+    assert np.array_equal(full, _unmasked(400))
+    flat, offs, _ = sl.pack_candidates([full] * 4)
+    om = orc.OracleModel(m)
+    assert orc.translate_shortlisted(om, b.tokens, b.offsets, lim, b.limits, flat, offs) == \
+        orc.translate(om, b.tokens, b.offsets, lim, b.limits)
+    syn = importlib.import_module(pkg.__name__ + ".synthetic")
+    sg = syn.SsruGeometry(source_vocab=400, target_vocab=400, dim=128, heads=2, ffn_dim=256,
+                          encoder_layers=1, decoder_layers=1)
+    sm = orc.OracleSsruModel(syn.seeded_ssru_model(seed=22, geometry=sg, std=0.1))
+    assert orc.translate_ssru(sm, b.tokens, b.offsets, lim, b.limits, candidates=flat,
+                              candidate_offsets=offs) == \
+        orc.translate_ssru(sm, b.tokens, b.offsets, lim, b.limits)
+
+
+def test_oracle_translate_scores_only_the_candidates(pkg, orc, sl):
+    """A narrow list: every generated id is on the row's list, and a list that
+    is one id long makes the row emit that id at every step."""
+    g = pkg.Geometry(vocab=400, dim=128, heads=2, ffn_dim=256, encoder_layers=1, decoder_layers=1)
+    om = orc.OracleModel(pkg.seeded_model(seed=21, geometry=g, std=0.3))
+    b = pkg.ragged_batch(seed=2, n=3, vocab=400)
+    lists = [np.array([0, 50, 51, 300], np.uint32), np.array([77], np.uint32),
+             np.array([0, 2, 3, 4, 5, 6, 39], np.uint32)]
+    flat, offs, _ = sl.pack_candidates(lists)
+    rows = orc.translate_shortlisted(om, b.tokens, b.offsets, [10] * 3, b.limits, flat, offs,
+                                     flags=pkg.FLAG_IGNORE_EOS)
+    for r, c in zip(rows, lists):
+        assert set(r) <= set(c.tolist())
+    assert rows[1] == [77] * 10
