@@ -8,6 +8,8 @@ reference's token-level engine interface plus synthetic-model generators.
 from . import _lib
 from .engine import (BackendError, BatchOutput, BufferTooSmall, DeviceError, HipBackend,
                      HipEngine, InferenceError, InvalidInput, ModelError, make_limits)
+from .text import (HipTextBackend, HipTokenEngine, SegmentError, TextSegment, TranslationInput,
+                   TranslationOutput, UnsupportedDirection, segment_text, translate_with_engine)
 from .synthetic import (Batch, Geometry, LIFTED_LIMITS, REFERENCE_LIMITS, SeededModel,
                         SsruGeometry, SsruModel, attention_inputs, gemm_inputs, ragged_batch,
                         seeded_model, seeded_ssru_model, single_sentence_batch, stress_batch,
@@ -23,6 +25,8 @@ __all__ = [
     "seeded_ssru_model", "attention_inputs", "gemm_inputs",
     "ragged_batch", "seeded_model", "single_sentence_batch", "stress_batch", "GEMM_SHAPES",
     "GEMM_ROWS", "FLAG_IGNORE_EOS", "FLAG_NO_GENERATION_MASK", "load_library",
+    "HipTextBackend", "HipTokenEngine", "SegmentError", "TextSegment", "TranslationInput",
+    "TranslationOutput", "UnsupportedDirection", "segment_text", "translate_with_engine",
 ]
 
 
