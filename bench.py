@@ -287,12 +287,81 @@ def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
                 enc_ms=enc_ms, dec_ms=dec_ms, n_steps=n_steps)
 
 
+def ssru_bench(pkg, args):
+    """The reference's own graph (Transformer encoder + 4 SSRU decoder layers,
+    d = 384 with 8 heads of 48, FFN 1536, 32000-id vocabularies, static
+    per-tensor multipliers; seeded random weights) on the same 64-sentence
+    ragged batch, scored over lexical-shortlist candidates (the reference's
+    production mode) and over the full vocabulary.  Informational: the
+    headline metric is the default workload's."""
+    import importlib
+    sl = importlib.import_module(pkg.__name__ + ".shortlist")
+    g = pkg.SsruGeometry()
+    model = pkg.seeded_ssru_model(geometry=g)
+    batch = pkg.ragged_batch()
+    # A synthetic shortlist: 40 targets per source id, ids below 100 always allowed.
+    rng = np.random.Generator(np.random.PCG64(11))
+    per = 40
+    targets = rng.integers(0, g.target_vocab, size=per * g.source_vocab).astype(np.uint32)
+    shortlist = sl.LexicalShortlist.from_bytes(
+        sl.LexicalShortlist.to_bytes(100, np.arange(g.source_vocab + 1, dtype=np.uint64) * per, targets),
+        g.source_vocab, g.target_vocab)
+    offs = batch.offsets
+    cand, coff, maxc = sl.pack_candidates([shortlist.candidates(batch.tokens[offs[b]:offs[b + 1]])
+                                           for b in range(len(offs) - 1)])
+    eng = pkg.HipEngine(model, limits=batch.limits)
+
+    def run(with_shortlist):
+        kw = dict(candidates=cand, candidate_offsets=coff) if with_shortlist else {}
+        for _ in range(args.warmup):
+            eng.translate_token_ids(batch.tokens, batch.offsets, batch.max_output_tokens, batch.flags, **kw)
+        ms, ntok = [], 0
+        for _ in range(args.steps):
+            out = eng.translate_token_ids(batch.tokens, batch.offsets, batch.max_output_tokens,
+                                          batch.flags, **kw)
+            ms.append(eng.last_stats()["total_ms"])
+            ntok = int(out.tokens.size)
+        st = eng.last_stats()
+        return ntok, statistics.mean(ms), st
+
+    ntok, ms, st = run(True)
+    ntok_f, ms_f, _ = run(False)
+    line = {
+        "metric": "target tokens/sec, 64-sentence ragged greedy batch, reference Transformer-SSRU graph, 1 MI355X",
+        "value": round(ntok / (ms / 1000.0), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random-init weights, seeded token ids, synthetic shortlist)",
+        "config": {"workload": "64-sentence ragged greedy batch, shortlist scoring",
+                   "model": "transformer-ssru-q8 6 enc / 4 SSRU dec, d=384, 8 heads of 48, ffn 1536, "
+                            "vocab 32000/32000, static per-tensor multipliers",
+                   "shortlist": f"{per} targets per source id, first 100 ids; longest list {maxc}",
+                   "target_tokens": ntok, "decode_steps": st["decode_steps"]},
+        "encoder_ms": round(st["encoder_ms"], 4),
+        "decode_ms": round(st["decode_ms"], 4),
+        "full_vocabulary": {"value": round(ntok_f / (ms_f / 1000.0), 1), "ms_per_step": round(ms_f, 4),
+                            "target_tokens": ntok_f},
+        "device": eng.info()["device"],
+    }
+    eng.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["ragged", "stress", "single"], default="ragged")
+    ap.add_argument("--workload", choices=["ragged", "stress", "single", "reference-ssru"],
+                    default="ragged")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-cores", type=int, default=min(16, os.cpu_count() or 4))
     args = ap.parse_args(argv)
@@ -304,6 +373,8 @@ def main(argv=None):
         return 2
 
     pkg = load()
+    if args.workload == "reference-ssru":
+        return ssru_bench(pkg, args)
     model = pkg.seeded_model()
     batch = {"ragged": pkg.ragged_batch, "stress": pkg.stress_batch,
              "single": pkg.single_sentence_batch}[args.workload]()

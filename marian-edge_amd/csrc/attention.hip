@@ -235,6 +235,10 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   }
 
   if (lane < DH) a.out[(int64_t)r * a.ldo + h * DH + lane] = o;
+  if (a.qout) {  // static multiplier of the next layer (elementwise)
+    if (lane < DH) a.qout[(int64_t)r * a.ldqout + h * DH + lane] = (int8_t)quantize_one(o, a.qmult);
+    if (lane == 0 && h == 0) a.qa[r] = a.qmult;
+  }
   // |max| of this head's slice: the consumer derives the row's quantization
   // multiplier from the maxima of all heads.
   const bool bad = lane < DH && !isfinite(o);
@@ -439,6 +443,10 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   }
   if (!live) return;
   if (lane < DH) a.out[(int64_t)row * a.ldo + h * DH + lane] = o;
+  if (a.qout) {
+    if (lane < DH) a.qout[(int64_t)row * a.ldqout + h * DH + lane] = (int8_t)quantize_one(o, a.qmult);
+    if (lane == 0 && h == 0) a.qa[row] = a.qmult;
+  }
   const bool bad = lane < DH && !isfinite(o);
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
@@ -479,6 +487,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
   if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out || (a.head_dim != 64 && a.head_dim != 48) ||
       (int64_t)a.rows * a.heads > 0x7fffffff)
+    return hipErrorInvalidValue;
+  if (a.qout && (!a.qa || a.ldqout < (int64_t)a.heads * a.head_dim || !(a.qmult > 0.0f) ||
+                 !(a.qmult < __builtin_huge_valf())))
     return hipErrorInvalidValue;
   // Packed self-attention with a tile list: keys staged once per tile.
   if (a.mode == ATT_SEQ && a.tiles && a.tiles_cap > 0 && a.max_keys <= kTileMaxKeys) {

@@ -958,7 +958,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   const bool tiled = Lmax <= 256;
   if (tiled) MH_HIP(launch_seq_tiles(d_cu, Bi, TILES, tiles_cap, s));
   auto gemm = [&](const int8_t* A, const float* a, int M, const Lin& L, float* out, int relu,
-                  int64_t ldo = 0) {
+                  int64_t ldo = 0, int8_t* q = nullptr, float* qa = nullptr, float qmult = 0.0f) {
     GemmArgs g;
     g.A = A;
     g.a = a;
@@ -973,6 +973,11 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     e.out = out;
     e.ldo = ldo ? ldo : L.N;
     e.relu = relu;
+    e.out_q = q;
+    e.ldq = L.N;
+    e.out_qa = qa;
+    e.qmult = qmult;
+    if (q) g.err = E->err_flag;
     return launch_gemm_store(g, e, s);
   };
   auto qstatic = [&](const float* x, int64_t ldx, int M, int K, float mult, int8_t* q, float* a,
@@ -990,7 +995,8 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     }
     return hipSuccess;
   };
-  auto enc_attention = [&]() {
+  // q / qa / qmult: the output also quantized with a static multiplier.
+  auto enc_attention = [&](int8_t* q = nullptr, float* qa = nullptr, float qmult = 0.0f) {
     AttnArgs aa;
     aa.mode = ATT_SEQ;
     aa.q = QKV;
@@ -1011,6 +1017,10 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     aa.out = ATT;
     aa.ldo = d;
     aa.err = E->err_flag;
+    aa.qout = q;
+    aa.ldqout = d;
+    aa.qa = qa;
+    aa.qmult = qmult;
     return launch_attention(aa, s);
   };
   if (!E->ssru) {
@@ -1034,12 +1044,12 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     for (uint32_t l = 0; l < E->Le; ++l) {
       const SEncLayer& L = E->senc[l];
       MH_HIP(sgroup(L.qkv, X0, QKV));
-      MH_HIP(enc_attention());
-      MH_HIP(qstatic(ATT, d, T, d, L.ao, OQ, OA, nullptr));
+      // Static multipliers quantize elementwise, so the producers write the
+      // next layer's int8 input themselves.
+      MH_HIP(enc_attention(OQ, OA, L.ao));
       MH_HIP(gemm(OQ, OA, T, L.o, Y, 0));
       MH_HIP(launch_residual_ln(Y, X0, L.ln1_s, L.ln1_b, T, nullptr, d, X1, XQ, XA, E->err_flag, s, L.a1));
-      MH_HIP(gemm(XQ, XA, T, L.w1, Hb, 1));
-      MH_HIP(qstatic(Hb, F, T, F, L.a2, HQ, HA, nullptr));
+      MH_HIP(gemm(XQ, XA, T, L.w1, nullptr, 1, 0, HQ, HA, L.a2));
       MH_HIP(gemm(HQ, HA, T, L.w2, Y, 0));
       const SGroup* nx = l + 1 < E->Le ? &E->senc[l + 1].qkv : nullptr;
       MH_HIP(launch_residual_ln(Y, X1, L.ln2_s, L.ln2_b, T, nullptr, d, X0, nx && nx->shared ? XQ : nullptr,
@@ -1469,7 +1479,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     float* xres = DX0;
     float* xalt = DX1;
     auto dgemm = [&](const Lin& L, const int8_t* A, const float* a, float* out, int64_t ldo,
-                     int relu) {
+                     int relu, int8_t* q = nullptr, float* qa = nullptr, float qmult = 0.0f) {
       GemmArgs g;
       g.A = A;
       g.a = a;
@@ -1486,6 +1496,11 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       e.out = out;
       e.ldo = ldo;
       e.relu = relu;
+      e.out_q = q;
+      e.ldq = L.N;
+      e.out_qa = qa;
+      e.qmult = qmult;
+      if (q) g.err = E->err_flag;
       return launch_gemm_skinny(g, EPI_STORE, e, s);
     };
     auto qs = [&](const float* x, int K, float mult, int8_t* q, float* a) {
@@ -1542,17 +1557,18 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       ca.max_keys = (int)Lmax;
       ca.out = DATT;
       ca.ldo = d;
-      ca.amax = DAMAX;
       ca.err = E->err_flag;
+      ca.qout = DXQ;  // quantized for Wo with its static multiplier
+      ca.ldqout = d;
+      ca.qa = DXA;
+      ca.qmult = L.ao;
       MH_TRY(launch_attention(ca, s));
-      MH_TRY(qs(DATT, d, L.ao, DXQ, DXA));
       MH_TRY(dgemm(L.o, DXQ, DXA, DY, d, 0));
       MH_TRY(launch_residual_ln(DY, xres, L.ln1_s, L.ln1_b, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag, s,
                                 L.a1));
       std::swap(xres, xalt);
       // ---- feed-forward ----
-      MH_TRY(dgemm(L.w1, DXQ, DXA, DH, F, 1));
-      MH_TRY(qs(DH, F, L.a2, DHQ, DHA));
+      MH_TRY(dgemm(L.w1, DXQ, DXA, nullptr, F, 1, DHQ, DHA, L.a2));  // hidden quantized for W2
       MH_TRY(dgemm(L.w2, DHQ, DHA, DY, d, 0));
       // quantized for what reads it next: the next layer's SSRU inputs (when
       // they share a multiplier) or the output scoring

@@ -279,6 +279,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       } else {
         if (out) out[(int64_t)m * e.ldo + n] = y;
         if (e.out_i32) e.out_i32[(int64_t)m * e.ldi + n] = iv;
+        if (e.out_q) {  // int8 A only (no row offset r0)
+          e.out_q[(int64_t)m * e.ldq + n] = (int8_t)quantize_one(y, e.qmult);
+          if (n == 0) e.out_qa[m] = e.qmult;
+          if (!isfinite(y) && g.err) *g.err = 1;  // quantizing rejects non-finite input
+        }
       }
     }
     __syncthreads();
@@ -700,6 +705,16 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e, int t
         for (int t = 0; t < 4 && n + t < N; ++t) o[t] = si[t];
       }
     }
+    if (e.out_q) {
+      int8_t* o = e.out_q + (int64_t)m * e.ldq + n;
+      bool bad = false;
+      for (int t = 0; t < 4 && n + t < N; ++t) {
+        o[t] = (int8_t)quantize_one(so[t], e.qmult);
+        bad |= !isfinite(so[t]);
+      }
+      if (n == 0) e.out_qa[m] = e.qmult;
+      if (bad && g.err) *g.err = 1;  // quantizing rejects non-finite input
+    }
   }
 }
 
@@ -823,6 +838,9 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
 
 hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s) {
   if (g.K <= 0 || g.K % 64 || g.K > kSkinnyMaxK || g.N <= 0 || g.M <= 0) return hipErrorInvalidValue;
+  if (e.out_q && (mode != EPI_STORE || g.Af || !e.out_qa || e.ldq < g.N || !(e.qmult > 0.0f) ||
+                  !(e.qmult < __builtin_huge_valf())))
+    return hipErrorInvalidValue;
   switch (mode) {
     case EPI_STORE: return launch_skinny_mode<EPI_STORE>(g, e, s);
     case EPI_QKV_CACHE: return launch_skinny_mode<EPI_QKV_CACHE>(g, e, s);
@@ -852,6 +870,8 @@ hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t
 
 hipError_t launch_gemm_tile(const GemmArgs& g, const Epilogue& e, hipStream_t s) {
   if (g.K <= 0 || g.K % 64 || g.N <= 0 || g.M_dev || g.lda % 16) return hipErrorInvalidValue;
+  if (e.out_q && (!e.out_qa || e.ldq < g.N || !(e.qmult > 0.0f) || !(e.qmult < __builtin_huge_valf())))
+    return hipErrorInvalidValue;
   if (g.M <= 0) return hipSuccess;
   const int64_t tiles = (int64_t)((g.M + kTm - 1) / kTm) * ((g.N + kTm - 1) / kTm);
   if (tiles > (int64_t)INT32_MAX) return hipErrorInvalidValue;

@@ -87,6 +87,13 @@ struct Epilogue {
   float* logits = nullptr;  // optional [M, N]
   int64_t ldl = 0;
   uint32_t flags = 0;  // bit 1: no generation mask
+  // EPI_STORE, int8 A (skinny) or tile GEMM: the output also quantized with a
+  // static multiplier for the next layer, q = clamp(rne(y * qmult), -127, 127)
+  // into out_q [M, ldq], and out_qa[m] = qmult.
+  int8_t* out_q = nullptr;
+  int64_t ldq = 0;
+  float qmult = 0.0f;
+  float* out_qa = nullptr;
 };
 
 // Column groups of the skinny kernel, and the argmax partial count per row.
@@ -182,6 +189,12 @@ struct AttnArgs {
   int64_t ldo = 0;
   float* amax = nullptr;  // optional [rows, heads]: max |out| of each head's slice
   int* err = nullptr;
+  // Optional: the output also quantized with a static multiplier into qout
+  // [rows, ldqout] (head h at its columns), and qa[row] = qmult.
+  int8_t* qout = nullptr;
+  int64_t ldqout = 0;
+  float qmult = 0.0f;
+  float* qa = nullptr;
   // ATT_SEQ with max_keys <= 256: the query-tile list written by
   // launch_seq_tiles (tiles_cap = its bound) selects the tiled kernel (no amax).
   const uint32_t* tiles = nullptr;
