@@ -287,6 +287,32 @@ def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
                 enc_ms=enc_ms, dec_ms=dec_ms, n_steps=n_steps)
 
 
+def ssru_cpu_baseline(model, batch, cand, coff, cores: int):
+    """The oracle's Transformer-SSRU restatement over the same batch and
+    shortlist, sentences spread over `cores` threads (each sentence encoded and
+    decoded on its own, AVX2 int8 dots), timed on this host."""
+    import __graft_entry__ as ge
+
+    orc = ge.load_oracle()
+    om = orc.OracleSsruModel(model)
+    t0 = time.perf_counter()
+    out = orc.translate_ssru(om, batch.tokens, batch.offsets, batch.max_output_tokens, batch.limits,
+                             batch.flags, candidates=cand, candidate_offsets=coff, threads=cores)
+    wall = time.perf_counter() - t0
+    ntok = sum(map(len, out))
+    return {
+        "value": round(ntok / wall, 2),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"the full {len(out)}-sentence batch ({ntok} target tokens) with the same shortlist, "
+                   f"one sentence per thread on {cores} threads (encode, then greedy decode with "
+                   "shortlist scoring), AVX2 int8 dots; generation caps lifted as on the GPU"),
+        "wall_s": round(wall, 3),
+        "host": host_info(cores),
+    }
+
+
 def ssru_bench(pkg, args):
     """The reference's own graph (Transformer encoder + 4 SSRU decoder layers,
     d = 384 with 8 heads of 48, FFN 1536, 32000-id vocabularies, static
@@ -309,6 +335,9 @@ def ssru_bench(pkg, args):
     offs = batch.offsets
     cand, coff, maxc = sl.pack_candidates([shortlist.candidates(batch.tokens[offs[b]:offs[b + 1]])
                                            for b in range(len(offs) - 1)])
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = ssru_cpu_baseline(model, batch, cand, coff, args.cpu_cores)
     eng = pkg.HipEngine(model, limits=batch.limits)
 
     def run(with_shortlist):
@@ -350,6 +379,9 @@ def ssru_bench(pkg, args):
                             "target_tokens": ntok_f},
         "device": eng.info()["device"],
     }
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+        line["speedup_vs_cpu"] = round(line["value"] / cpu["value"], 1)
     eng.close()
     print(json.dumps(line), flush=True)
     return 0

@@ -873,11 +873,12 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   float* HA = (float*)E->get(B_HA, 4ull * T);
   float* CKV = (float*)E->get(B_CKV, 8ull * TR * d * LdA);
   // Self-attention caches (transformer graph); the SSRU graph keeps one
-  // recurrent state row per sequence and layer instead, and two projections
-  // per row for the SSRU's inputs.
+  // recurrent state row per sequence and layer instead (two buffers: step t
+  // reads buffer t % 2 and writes the other, so every head of a row can read
+  // the old state), and two projections per row for the SSRU's inputs.
   float* KC = (float*)E->get(B_KC, E->ssru ? 0 : 4ull * CR * d * LdA);
   float* VC = (float*)E->get(B_VC, E->ssru ? 0 : 4ull * CR * d * LdA);
-  float* STATE = (float*)E->get(B_STATE, E->ssru ? 4ull * R * d * LdA : 0);
+  float* STATE = (float*)E->get(B_STATE, E->ssru ? 2 * 4ull * R * d * LdA : 0);
   float* DUF = (float*)E->get(B_DUF, E->ssru ? 8ull * R * d : 0);
   float* DX0 = (float*)E->get(B_DX0, 4ull * R * d);
   float* DX1 = (float*)E->get(B_DX1, 4ull * R * d);
@@ -927,7 +928,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   MH_HIP(hipMemcpyAsync(ddec, dmeta_h.data(), dmeta_bytes, hipMemcpyHostToDevice, s));
   MH_HIP(hipMemsetAsync(E->err_flag, 0, sizeof(int), s));
   MH_HIP(hipMemsetAsync(COUNT, 0, 4 * B, s));
-  if (E->ssru) MH_HIP(hipMemsetAsync(STATE, 0, 4ull * R * d * LdA, s));  // states start at zero
+  if (E->ssru) MH_HIP(hipMemsetAsync(STATE, 0, 4ull * R * d * LdA, s));  // step 0 reads zero states
   // The timed region starts with the packed inputs resident in HBM.
   MH_HIP(hipEventRecord(E->ev[0], s));
 
@@ -1475,6 +1476,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   // layer input, gate, state update and LayerNorm), cross-attention over the
   // row's sentence and the FFN, every dense layer's input quantized with that
   // layer's static multiplier.  No fused blocks: the generic kernels.
+  const bool ssru_blk = E->ssru && ssru_block_supported(d, H, (int)Lmax);
   auto emit_step_ssru = [&](int rows, uint32_t t) -> hipError_t {
     float* xres = DX0;
     float* xalt = DX1;
@@ -1534,35 +1536,75 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
           MH_TRY(dgemm(L.uf.part(i), DXQ, DXA, DUF + (size_t)i * d, 2 * d, 0));
         }
       }
-      MH_TRY(launch_ssru_ln(DUF, DUF + d, STATE + (size_t)l * R * d, xres, L.ln0_s, L.ln0_b, rows, d, xalt,
-                            DXQ, DXA, E->err_flag, s, 2 * d, d_nact, rm.slot, L.aq));
-      std::swap(xres, xalt);
-      // ---- cross-attention over the row's sentence ----
-      MH_TRY(dgemm(L.q, DXQ, DXA, DQ, d, 0));
-      AttnArgs ca;
-      ca.mode = ATT_CROSS;
-      ca.q = DQ;
-      ca.ldq = d;
+      float* st_in = STATE + ((size_t)(t & 1) * LdA + l) * R * d;
+      float* st_out = STATE + ((size_t)((t + 1) & 1) * LdA + l) * R * d;
       const float* ckv = CKV + (size_t)l * TR * 2 * d;
-      ca.k = ckv;
-      ca.v = ckv + d;
-      ca.ldkv = 2 * d;
-      ca.heads = H;
-      ca.head_dim = d / H;
-      ca.rows = rows;
-      ca.rows_dev = d_nact;
-      ca.row_key0 = rm.src0;
-      ca.row_nk = rm.srcn;
-      ca.max_row = (int64_t)TR;
-      ca.max_keys = (int)Lmax;
-      ca.out = DATT;
-      ca.ldo = d;
-      ca.err = E->err_flag;
-      ca.qout = DXQ;  // quantized for Wo with its static multiplier
-      ca.ldqout = d;
-      ca.qa = DXA;
-      ca.qmult = L.ao;
-      MH_TRY(launch_attention(ca, s));
+      if (ssru_blk) {
+        // SSRU + LayerNorm, query projection and cross-attention in one launch.
+        SsruBlockArgs sb;
+        sb.cand = DUF;
+        sb.forget = DUF + d;
+        sb.ldc = 2 * d;
+        sb.state_in = st_in;
+        sb.state_out = st_out;
+        sb.state_row = rm.slot;
+        sb.state_rows = (int64_t)R;
+        sb.resid = xres;
+        sb.gamma = L.ln0_s;
+        sb.beta = L.ln0_b;
+        sb.x_out = xalt;
+        sb.xq_mult = L.aq;
+        sb.Wq = L.q.wf;
+        sb.wq_mult = L.q.mult;
+        sb.wq_bias = L.q.bias;
+        sb.k = ckv;
+        sb.v = ckv + d;
+        sb.ldkv = 2 * d;
+        sb.row_key0 = rm.src0;
+        sb.row_nk = rm.srcn;
+        sb.max_row = (int64_t)TR;
+        sb.max_keys = (int)Lmax;
+        sb.d = d;
+        sb.heads = H;
+        sb.rows = rows;
+        sb.rows_dev = d_nact;
+        sb.qout = DXQ;
+        sb.ldqout = d;
+        sb.qmult = L.ao;
+        sb.qa = DXA;
+        sb.err = E->err_flag;
+        MH_TRY(launch_ssru_block(sb, s));
+        std::swap(xres, xalt);
+      } else {
+        MH_TRY(launch_ssru_ln(DUF, DUF + d, st_in, xres, L.ln0_s, L.ln0_b, rows, d, xalt, DXQ, DXA,
+                              E->err_flag, s, 2 * d, d_nact, rm.slot, L.aq, st_out));
+        std::swap(xres, xalt);
+        // ---- cross-attention over the row's sentence ----
+        MH_TRY(dgemm(L.q, DXQ, DXA, DQ, d, 0));
+        AttnArgs ca;
+        ca.mode = ATT_CROSS;
+        ca.q = DQ;
+        ca.ldq = d;
+        ca.k = ckv;
+        ca.v = ckv + d;
+        ca.ldkv = 2 * d;
+        ca.heads = H;
+        ca.head_dim = d / H;
+        ca.rows = rows;
+        ca.rows_dev = d_nact;
+        ca.row_key0 = rm.src0;
+        ca.row_nk = rm.srcn;
+        ca.max_row = (int64_t)TR;
+        ca.max_keys = (int)Lmax;
+        ca.out = DATT;
+        ca.ldo = d;
+        ca.err = E->err_flag;
+        ca.qout = DXQ;  // quantized for Wo with its static multiplier
+        ca.ldqout = d;
+        ca.qa = DXA;
+        ca.qmult = L.ao;
+        MH_TRY(launch_attention(ca, s));
+      }
       MH_TRY(dgemm(L.o, DXQ, DXA, DY, d, 0));
       MH_TRY(launch_residual_ln(DY, xres, L.ln1_s, L.ln1_b, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag, s,
                                 L.a1));

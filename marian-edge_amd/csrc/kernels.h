@@ -130,12 +130,59 @@ hipError_t launch_quantize_rows_static(const float* x, int64_t ldx, int rows, in
 // gate = sigmoid(forget); out = LN(relu(state) + resid) (+ quantization, with
 // qmult when > 0).  cand/forget rows are ldc floats apart (0: d); row r's
 // state is state row state_row[r] when state_row is set; rows at or past
-// *rows_dev are skipped.
+// *rows_dev are skipped.  The new state goes to state_out when set (another
+// buffer than state), else over the old one.
 hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, const float* resid,
                           const float* g, const float* b, int rows, int d, float* out, int8_t* q,
                           float* a, int* err, hipStream_t s, int64_t ldc = 0,
                           const int* rows_dev = nullptr, const int* state_row = nullptr,
-                          float qmult = 0.0f);
+                          float qmult = 0.0f, float* state_out = nullptr);
+
+// Fused SSRU decode block (Transformer-SSRU graph, static multipliers): per
+// (row, head) one workgroup applies launch_ssru_ln's update and LayerNorm to
+// the row (the head-0 workgroup stores the new state to state_out and the
+// LayerNorm row to x_out), quantizes the row with the query projection's
+// static multiplier xq_mult, projects it onto the head's query with int8 MFMA
+// (static dequantization), attends over the row's encoder keys
+// row_key0[r] + [0, row_nk[r]) (at most kSsruBlockMaxKeys), and stores the
+// head's output quantized with the output projection's static multiplier
+// (qout [rows, ldqout], qa[r] = qmult).  One launch replaces the SSRU
+// LayerNorm, query projection and cross-attention kernels.  state_out must
+// not alias state_in: every head reads the old state.
+struct SsruBlockArgs {
+  const float* cand = nullptr;  // [rows, ldc] candidate inputs; forget at `forget`
+  const float* forget = nullptr;
+  int64_t ldc = 0;
+  const float* state_in = nullptr;  // [sequences, d]
+  float* state_out = nullptr;       // [sequences, d]
+  const int* state_row = nullptr;   // sequence of each row
+  int64_t state_rows = 0;           // sequences held by the state buffers
+  const float* resid = nullptr;     // [rows, d]
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float* x_out = nullptr;  // [rows, d] the LayerNorm rows
+  float xq_mult = 0.0f;    // the query projection's activation multiplier
+  const int8_t* Wq = nullptr;  // [d, d] in fragment order (frag_load)
+  const float* wq_mult = nullptr;
+  const float* wq_bias = nullptr;
+  const float* k = nullptr;  // encoder key / value rows, stride ldkv
+  const float* v = nullptr;
+  int64_t ldkv = 0;
+  const int64_t* row_key0 = nullptr;
+  const int32_t* row_nk = nullptr;
+  int64_t max_row = 0;  // key rows of k / v are < max_row
+  int max_keys = 0;     // upper bound on keys per row
+  int d = 0, heads = 0, rows = 0;
+  const int* rows_dev = nullptr;
+  int8_t* qout = nullptr;
+  int64_t ldqout = 0;
+  float qmult = 0.0f;
+  float* qa = nullptr;
+  int* err = nullptr;
+};
+constexpr int kSsruBlockMaxKeys = 128;
+bool ssru_block_supported(int d, int heads, int max_keys);
+hipError_t launch_ssru_block(const SsruBlockArgs& a, hipStream_t s);
 
 struct EmbedArgs {
   const int8_t* emb = nullptr;

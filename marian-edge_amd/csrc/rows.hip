@@ -172,8 +172,9 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
 // SSRU state update + LayerNorm (ssru_update_layer_norm_into, tensor.rs:184-218,
 // the reference's SSRU decoder, q8_engine.rs:394-408).  Per element: gate =
 // 1 / (1 + exp(-f)) with the C library's expf, s' = gate * s + (1 - gate) * c
-// (each product, the difference and the sum rounded on their own), the state
-// is overwritten with s'; then out = LN(relu(s') + residual) (relu_residual
+// (each product, the difference and the sum rounded on their own), s' is
+// stored to state_out (the state itself, or the other buffer of a pair); then
+// out = LN(relu(s') + residual) (relu_residual
 // :718-724, relu as max(x, 0) with NaN and -0.0 giving +0.0) with the
 // sequential folds of normalize_row.  One wave per row.  In the decode loop
 // the state of active row r is state row state_row[r] (its sequence), and
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float*
                                                  float* state, const float* resid, const float* gamma,
                                                  const float* beta, int rows, const int* rows_dev,
                                                  const int* state_row, float* out, int8_t* q,
-                                                 float* a, int* err, float qmult) {
+                                                 float* a, int* err, float qmult, float* state_out) {
   constexpr int D = PER * 64;
   __shared__ __attribute__((aligned(16))) float sZ[4][D];
   __shared__ uint64_t sTab[32];
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float*
     const float e = ref_expf(-f, sTab);
     const float gate = 1.0f / (1.0f + e);
     const float next = gate * st + (1.0f - gate) * c;
-    state[srow * D + e_] = next;
+    state_out[srow * D + e_] = next;
     z[j] = (next > 0.0f ? next : 0.0f) + r;
   }
   ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err, qmult);
@@ -609,13 +610,14 @@ hipError_t launch_quantize_rows_static(const float* x, int64_t ldx, int rows, in
 hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, const float* resid,
                           const float* g, const float* b, int rows, int d, float* out, int8_t* q,
                           float* a, int* err, hipStream_t s, int64_t ldc, const int* rows_dev,
-                          const int* state_row, float qmult) {
+                          const int* state_row, float qmult, float* state_out) {
   if (rows <= 0) return hipSuccess;
   if (d % 64) return hipErrorInvalidValue;
   const dim3 grid((rows + 3) / 4), block(256);
+  float* so = state_out ? state_out : state;
 #define MH_SSRU(P) \
   hipLaunchKernelGGL(k_ssru_ln<P>, grid, block, 0, s, cand, forget, ldc > 0 ? ldc : d, state, resid, g, b, rows, \
-                     rows_dev, state_row, out, q, a, err, qmult)
+                     rows_dev, state_row, out, q, a, err, qmult, so)
   MH_PER_DISPATCH_16(d / 64, MH_SSRU)
 #undef MH_SSRU
   return hipGetLastError();

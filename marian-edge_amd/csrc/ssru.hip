@@ -1,0 +1,254 @@
+// ssru.hip — fused decode block of the Transformer-SSRU graph (the
+// reference's own model, static per-tensor multipliers): one 256-thread
+// workgroup per (row, head) runs the SSRU update and LayerNorm of the row, the
+// head's query projection and the cross-attention over the row's sentence.
+// With static multipliers the quantized row needs nothing from other rows or
+// heads, so the three sublayers meet in one launch.
+//
+// Every value is produced by the same operations, in the same order, as the
+// separate kernels (and the reference):
+//   SSRU + LayerNorm  ssru_update_layer_norm_into, tensor.rs:184-218, and
+//                     normalize_row, tensor.rs:372-385 (sequential folds)
+//   quantization      quantize_static_into (legacy_q8.rs:544-552): q =
+//                     clamp(rne(x * act_mult), -127, 127)
+//   projection        exact i32 MFMA, y = acc * (1 / (act * w)) + b
+//                     (legacy_q8.rs:646-674)
+//   attention         attention_into, tensor.rs:251-318 (sequential dot from
+//                     -0.0, max, C-library expf, sequential sum from 0.0, PV in
+//                     key order from 0.0)
+//
+// Roles: wave 0 loads and normalizes the row; waves 1-3 stage the head's key
+// and value rows in LDS; wave t < head_dim / 16 projects one 16-column query
+// tile; wave 0 then attends alone (the dependent chains are per row).
+#include "device_common.h"
+#include "kernels.h"
+
+namespace mh {
+namespace {
+
+constexpr int kSbThreads = 256;
+constexpr int kSbLoaders = kSbThreads - 64;  // waves 1-3 stage keys and values
+
+__constant__ uint64_t kSbExp2Tab[32] = {MH_EXP2_TABLE_32};
+
+template <int PER, int DH>
+__global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
+  constexpr int D = PER * 64;
+  constexpr int T = DH / 16;  // query tiles of one head
+  constexpr int KS = D / 64;  // k-steps of the projection
+  constexpr int KR = DH + 4;  // padded LDS key row (floats), 16-byte aligned
+  constexpr int V4 = DH / 4;  // float4 per key row of one head
+  constexpr int NL = (kSsruBlockMaxKeys * V4 + kSbLoaders - 1) / kSbLoaders;
+  static_assert(T <= 4 && DH % 16 == 0, "one query tile per wave");
+  __shared__ __attribute__((aligned(16))) float sK[kSsruBlockMaxKeys * KR];
+  __shared__ __attribute__((aligned(16))) float sV[kSsruBlockMaxKeys * KR];
+  __shared__ __attribute__((aligned(16))) float sZ[D];
+  __shared__ __attribute__((aligned(16))) int8_t sX[D];
+  __shared__ __attribute__((aligned(16))) float sQ[DH];
+  __shared__ __attribute__((aligned(16))) float sP[kSsruBlockMaxKeys];
+  __shared__ uint64_t sTab[32];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
+  if (wave == 0 && lane < 32) sTab[lane] = kSbExp2Tab[lane];  // wave 0 alone reads it
+
+  // This row's key range, read before the device row count (a stale row's
+  // range is clamped into the buffer and its results are discarded).
+  int64_t key0 = a.row_key0[r];
+  int nk = max(a.row_nk[r], 1);
+  key0 = min(max(key0, (int64_t)0), a.max_row - 1);
+  nk = min(nk, kSsruBlockMaxKeys);
+  const int nk_ld = (int)min((int64_t)nk, a.max_row - key0);
+
+  // wave 0: the row's SSRU inputs, state, residual and LayerNorm parameters.
+  float cv[PER], fv[PER], sv[PER], rv[PER], gv[PER], bv[PER];
+  int64_t srow = r;
+  if (wave == 0) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      cv[j] = a.cand[(int64_t)r * a.ldc + e];
+      fv[j] = a.forget[(int64_t)r * a.ldc + e];
+      rv[j] = a.resid[(int64_t)r * D + e];
+      gv[j] = a.gamma[e];
+      bv[j] = a.beta[e];
+    }
+    // A stale row's sequence is clamped into the state buffer, like its keys.
+    srow = a.state_row ? min(max((int64_t)a.state_row[r], (int64_t)0), a.state_rows - 1) : r;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) sv[j] = a.state_in[srow * D + lane + 64 * j];
+  }
+  // Waves t < T: the weight fragments of query tile t of this head (columns
+  // h*DH + 16t ..) and the dequantization operands of lane t's column.
+  v4i bf[KS];
+  float wm = 1.0f, wb = 0.0f;
+  if (wave < T) {
+    const int tile = (h * DH >> 4) + wave;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bf[s] = frag_load(a.Wq, tile, KS, s, lane);
+    const int n = h * DH + 16 * wave + (lane & 15);
+    wm = a.wq_mult[n];
+    wb = a.wq_bias[n];
+  }
+  // Waves 1-3: this head's key and value rows (keys past the row's last
+  // reload that key, so every load is in bounds; they are not stored).
+  f4v kreg[NL], vreg[NL];
+  const int lt = tid - 64;
+  if (wave > 0) {
+    const int64_t base = key0 * a.ldkv + h * DH;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int idx = min(lt + kSbLoaders * i, nk_ld * V4 - 1);
+      const int64_t off = base + (int64_t)(idx / V4) * a.ldkv + 4 * (idx % V4);
+      kreg[i] = *(const f4v*)(a.k + off);
+      vreg[i] = *(const f4v*)(a.v + off);
+    }
+  }
+  const int n_rows = a.rows_dev ? *a.rows_dev : a.rows;
+  if (r >= n_rows) return;  // the whole workgroup alike
+
+  if (wave == 0) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the expf table is in LDS
+    __builtin_amdgcn_wave_barrier();
+    // SSRU update (k_ssru_ln's arithmetic), then LayerNorm(relu(s') + resid).
+    float z[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float e = ref_expf(-fv[j], sTab);
+      const float gate = 1.0f / (1.0f + e);
+      const float next = gate * sv[j] + (1.0f - gate) * cv[j];
+      if (h == 0) a.state_out[srow * D + lane + 64 * j] = next;
+      z[j] = (next > 0.0f ? next : 0.0f) + rv[j];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) sZ[lane + 64 * j] = z[j];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    const float mean = seq_fold_lds<D / 4>((const float4*)sZ, -0.0f) / (float)D;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float c = z[j] - mean;
+      sZ[lane + 64 * j] = c * c;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const float var = seq_fold_lds<D / 4>((const float4*)sZ, -0.0f) / (float)D;
+    const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      const float o = ((z[j] - mean) * inv) * gv[j] + bv[j];
+      bad |= !isfinite(o);
+      if (h == 0) a.x_out[(int64_t)r * D + e] = o;
+      sX[e] = (int8_t)quantize_one(o, a.xq_mult);
+    }
+    if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int idx = lt + kSbLoaders * i;
+      if (idx < nk * V4) {
+        const int so = (idx / V4) * KR + 4 * (idx % V4);
+        *(f4v*)(sK + so) = kreg[i];
+        *(f4v*)(sV + so) = vreg[i];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Query tile `wave`: row 0 of the MFMA A operand is the quantized row
+  // (lanes 0, 16, 32, 48 hold its 16-byte k-slices), the other rows zero;
+  // lane l < 16 ends with column l of row 0 in acc[0].
+  if (wave < T) {
+    v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const v4i x = (lane & 15) == 0 ? *(const v4i*)(sX + 64 * s + (lane >> 4) * 16) : v4i{0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x, bf[s], acc, 0, 0, 0);
+    }
+    if (lane < 16) sQ[16 * wave + lane] = dequant(acc[0], a.xq_mult, wm, wb);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // Scores: lane = key (keys lane and 64 + lane), DH-term dots in dimension
+  // order from -0.0, q read as an LDS broadcast.
+  const float scale = 1.0f / sqrtf((float)DH);
+  const bool two = nk > 64;
+  float d0 = -0.0f, d1 = -0.0f;
+  const float* k0 = sK + min(lane, nk - 1) * KR;
+  const float* k1 = sK + min(64 + lane, nk - 1) * KR;
+#pragma unroll
+  for (int i = 0; i < DH; i += 4) {
+    const f4v q = *(const f4v*)(sQ + i);
+    const f4v x = *(const f4v*)(k0 + i);
+    d0 = d0 + q.x * x.x;
+    d0 = d0 + q.y * x.y;
+    d0 = d0 + q.z * x.z;
+    d0 = d0 + q.w * x.w;
+    if (two) {
+      const f4v y = *(const f4v*)(k1 + i);
+      d1 = d1 + q.x * y.x;
+      d1 = d1 + q.y * y.y;
+      d1 = d1 + q.z * y.z;
+      d1 = d1 + q.w * y.w;
+    }
+  }
+  const float s0 = lane < nk ? d0 * scale : -INFINITY;
+  const float s1 = 64 + lane < nk ? d1 * scale : -INFINITY;
+  const float mx = wave_max(fmaxf(s0, s1));
+  const float p0 = lane < nk ? ref_expf(s0 - mx, sTab) : 0.0f;
+  const float p1 = 64 + lane < nk ? ref_expf(s1 - mx, sTab) : 0.0f;
+  sP[lane] = p0;
+  sP[64 + lane] = p1;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  // Denominator: the probabilities of the row's keys in key order from 0.0.
+  float sum = 0.0f;
+  for (int j = 0; j < nk; ++j) sum = sum + sP[j];
+  const float inv = 1.0f / sum;
+  // out_d = sum_j v[j][d] * (e_j * inv) in key order from 0.0; lane = d.
+  const int dl = min(lane, DH - 1);
+  float o = 0.0f;
+#pragma unroll 8
+  for (int j = 0; j < nk; ++j) o = o + sV[j * KR + dl] * (sP[j] * inv);
+
+  if (lane < DH) a.qout[(int64_t)r * a.ldqout + h * DH + lane] = (int8_t)quantize_one(o, a.qmult);
+  if (lane == 0 && h == 0) a.qa[r] = a.qmult;
+  if (__any(lane < DH && !isfinite(o)) && lane == 0 && a.err) *a.err = 1;
+}
+
+}  // namespace
+
+bool ssru_block_supported(int d, int heads, int max_keys) {
+  if (heads <= 0 || d % heads || max_keys <= 0 || max_keys > kSsruBlockMaxKeys) return false;
+  const int dh = d / heads;
+  return (d == 256 && dh == 64) || (d == 384 && (dh == 48 || dh == 64)) || (d == 512 && dh == 64);
+}
+
+hipError_t launch_ssru_block(const SsruBlockArgs& a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  if (!ssru_block_supported(a.d, a.heads, a.max_keys) || !a.cand || !a.forget || a.ldc < a.d ||
+      !a.state_in || !a.state_out || a.state_in == a.state_out || a.state_rows < a.rows ||
+      !a.resid || !a.gamma || !a.beta ||
+      !a.x_out || !a.Wq || !a.wq_mult || !a.wq_bias || !a.k || !a.v || a.ldkv < a.d || !a.row_key0 ||
+      !a.row_nk || a.max_row <= 0 || !a.qout || !a.qa || a.ldqout < a.d ||
+      (int64_t)a.rows * a.heads > 0x7fffffff)
+    return hipErrorInvalidValue;
+  for (const float m : {a.xq_mult, a.qmult})
+    if (!(m > 0.0f) || !(m < __builtin_huge_valf())) return hipErrorInvalidValue;
+  const dim3 grid(a.rows * a.heads), block(kSbThreads);
+  const int dh = a.d / a.heads;
+  if (a.d == 256)
+    hipLaunchKernelGGL((k_ssru_block<4, 64>), grid, block, 0, s, a);
+  else if (a.d == 384 && dh == 48)
+    hipLaunchKernelGGL((k_ssru_block<6, 48>), grid, block, 0, s, a);
+  else if (a.d == 384)
+    hipLaunchKernelGGL((k_ssru_block<6, 64>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((k_ssru_block<8, 64>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace mh

@@ -88,6 +88,25 @@ def test_ssru_probe_bit_exact(pkg, orc, step):
     assert np.array_equal(lg[act_o].view(np.uint32), lg_o[act_o].view(np.uint32))
 
 
+def test_ssru_long_sentences_token_exact(pkg, orc):
+    """Sentences longer than 128 tokens: every step's SSRU LayerNorm, query
+    projection and cross-attention run as separate kernels (the fused decode
+    block holds at most 128 encoder keys per row); shorter batches above use
+    the fused block.  Both read the recurrent state of step t from one buffer
+    and write it to the other."""
+    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=2, decoder_layers=2)
+    model = pkg.seeded_ssru_model(seed=37, geometry=g, std=0.05)
+    om = orc.OracleSsruModel(model)
+    rng = np.random.default_rng(13)
+    seqs = [rng.integers(3, g.source_vocab, size=L).astype(np.int32) for L in (150, 12, 131, 40)]
+    b = pkg.synthetic._pack("long", seqs, [30, 9, 25, 20], 0, dict(pkg.synthetic.LIFTED_LIMITS))
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        got, want = run_both(pkg, orc, e, om, b, pkg.FLAG_IGNORE_EOS)
+        print(f"long sentences: {sum(map(len, got))} tokens", flush=True)
+        assert got == want
+        assert e.is_ready()
+
+
 def test_ssru_reference_shape_ragged_64(pkg, orc, sl):
     """The reference's supported shape at full size (32000-id vocabularies,
     6 encoder / 4 SSRU decoder layers) on the 64-sentence ragged batch, with
