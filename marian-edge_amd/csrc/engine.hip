@@ -1477,6 +1477,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   // row's sentence and the FFN, every dense layer's input quantized with that
   // layer's static multiplier.  No fused blocks: the generic kernels.
   const bool ssru_blk = E->ssru && ssru_block_supported(d, H, (int)Lmax);
+  const bool ssru_lnf = E->ssru && ln_gemm_static_supported(d, F) && ln_gemm_static_supported(d, 2 * d);
   auto emit_step_ssru = [&](int rows, uint32_t t) -> hipError_t {
     float* xres = DX0;
     float* xalt = DX1;
@@ -1525,10 +1526,46 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     ea.qmult = uf0.shared ? uf0.act[0] : 0.0f;
     ea.err = E->err_flag;
     MH_TRY(launch_embed(ea, s));
+    // Residual LayerNorm + the linear that reads it, in one launch.
+    auto ln_gemm = [&](const float* y, const float* ln_s, const float* ln_b, const Lin& W, float a0,
+                       float a1, int part_n, int relu, float* out, int8_t* q, float* qa,
+                       float qmult) {
+      LnGemmStaticArgs lg;
+      lg.y = y;
+      lg.r = xres;
+      lg.gamma = ln_s;
+      lg.beta = ln_b;
+      lg.rows = rows;
+      lg.rows_dev = d_nact;
+      lg.x_out = xalt;
+      lg.xq_mult[0] = a0;
+      lg.xq_mult[1] = a1;
+      lg.part_n = part_n;
+      lg.W = W.wf;
+      lg.wmult = W.mult;
+      lg.bias = W.bias;
+      lg.K = W.K;
+      lg.N = W.N;
+      lg.relu = relu;
+      lg.out = out;
+      lg.ldo = W.N;
+      lg.out_q = q;
+      lg.ldq = W.N;
+      lg.qmult = qmult;
+      lg.out_qa = qa;
+      lg.err = E->err_flag;
+      const hipError_t rc = launch_ln_gemm_static(lg, s);
+      std::swap(xres, xalt);
+      return rc;
+    };
     for (uint32_t l = 0; l < E->Ld; ++l) {
       const SDecLayer& L = E->sdec[l];
       // ---- SSRU: candidate and forget-gate inputs side by side in DUF ----
-      if (L.uf.shared) {
+      if (ssru_lnf && l > 0) {  // with the previous layer's last LayerNorm
+        const SDecLayer& P = E->sdec[l - 1];
+        MH_TRY(ln_gemm(DY, P.ln2_s, P.ln2_b, L.uf.all, L.uf.act[0], L.uf.act[L.uf.shared ? 0 : 1],
+                       L.uf.shared ? 2 * d : d, 0, DUF, nullptr, nullptr, 0.0f));
+      } else if (L.uf.shared) {
         MH_TRY(dgemm(L.uf.all, DXQ, DXA, DUF, 2 * d, 0));
       } else {
         for (int i = 0; i < 2; ++i) {
@@ -1606,12 +1643,18 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
         MH_TRY(launch_attention(ca, s));
       }
       MH_TRY(dgemm(L.o, DXQ, DXA, DY, d, 0));
-      MH_TRY(launch_residual_ln(DY, xres, L.ln1_s, L.ln1_b, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag, s,
-                                L.a1));
-      std::swap(xres, xalt);
-      // ---- feed-forward ----
-      MH_TRY(dgemm(L.w1, DXQ, DXA, nullptr, F, 1, DHQ, DHA, L.a2));  // hidden quantized for W2
+      // ---- feed-forward (hidden quantized for W2) ----
+      if (ssru_lnf) {
+        MH_TRY(ln_gemm(DY, L.ln1_s, L.ln1_b, L.w1, L.a1, L.a1, F, 1, nullptr, DHQ, DHA, L.a2));
+      } else {
+        MH_TRY(launch_residual_ln(DY, xres, L.ln1_s, L.ln1_b, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag,
+                                  s, L.a1));
+        std::swap(xres, xalt);
+        MH_TRY(dgemm(L.w1, DXQ, DXA, nullptr, F, 1, DHQ, DHA, L.a2));
+      }
       MH_TRY(dgemm(L.w2, DHQ, DHA, DY, d, 0));
+      // The next layer's SSRU projections build this LayerNorm themselves.
+      if (ssru_lnf && l + 1 < E->Ld) continue;
       // quantized for what reads it next: the next layer's SSRU inputs (when
       // they share a multiplier) or the output scoring
       const SGroup* nx = l + 1 < E->Ld ? &E->sdec[l + 1].uf : nullptr;

@@ -181,6 +181,40 @@ struct SsruBlockArgs {
   int* err = nullptr;
 };
 constexpr int kSsruBlockMaxKeys = 128;
+
+// Residual LayerNorm + static-multiplier Q8 linear (Transformer-SSRU graph):
+// out[m] = (relu of) Q8Linear(LN(y[m] + r[m])) with the row quantized by
+// xq_mult[0] for output columns below part_n and xq_mult[1] from it (a row
+// group of two layers with their own multipliers; part_n = N: one).
+// Optional outputs: fp32 `out`, and/or `out_q` quantized with qmult (the next
+// layer's static multiplier, out_qa[m] = qmult); x_out receives the
+// LayerNorm rows.  Eight rows and 128 output columns per workgroup;
+// K = 256, 384 or 512, N a multiple of 128.
+struct LnGemmStaticArgs {
+  const float* y = nullptr;  // [rows, K]
+  const float* r = nullptr;  // [rows, K]
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  int rows = 0;
+  const int* rows_dev = nullptr;
+  float* x_out = nullptr;  // optional [rows, K]
+  float xq_mult[2] = {0.0f, 0.0f};
+  int part_n = 0;
+  const int8_t* W = nullptr;  // [N, K] in fragment order (frag_load)
+  const float* wmult = nullptr;
+  const float* bias = nullptr;
+  int K = 0, N = 0;
+  int relu = 0;
+  float* out = nullptr;
+  int64_t ldo = 0;
+  int8_t* out_q = nullptr;
+  int64_t ldq = 0;
+  float qmult = 0.0f;
+  float* out_qa = nullptr;
+  int* err = nullptr;
+};
+bool ln_gemm_static_supported(int K, int N);
+hipError_t launch_ln_gemm_static(const LnGemmStaticArgs& a, hipStream_t s);
 bool ssru_block_supported(int d, int heads, int max_keys);
 hipError_t launch_ssru_block(const SsruBlockArgs& a, hipStream_t s);
 

@@ -31,6 +31,32 @@ constexpr int kSbLoaders = kSbThreads - 64;  // waves 1-3 stage keys and values
 
 __constant__ uint64_t kSbExp2Tab[32] = {MH_EXP2_TABLE_32};
 
+// LayerNorm of the row z (lane l holds elements l + 64j) by one wave with
+// normalize_row's sequential folds (tensor.rs:372-385); zr is the wave's LDS
+// row (D floats).  Returns the normalized row in o.
+template <int PER>
+__device__ __forceinline__ void ln_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
+                                        const float (&bv)[PER], int lane, float (&o)[PER]) {
+  constexpr int D = PER * 64;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) zr[lane + 64 * j] = z[j];
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  const float mean = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const float c = z[j] - mean;
+    zr[lane + 64 * j] = c * c;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  const float var = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
+  const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];
+}
+
 template <int PER, int DH>
 __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   constexpr int D = PER * 64;
@@ -119,29 +145,15 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
       if (h == 0) a.state_out[srow * D + lane + 64 * j] = next;
       z[j] = (next > 0.0f ? next : 0.0f) + rv[j];
     }
-#pragma unroll
-    for (int j = 0; j < PER; ++j) sZ[lane + 64 * j] = z[j];
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
-    const float mean = seq_fold_lds<D / 4>((const float4*)sZ, -0.0f) / (float)D;
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const float c = z[j] - mean;
-      sZ[lane + 64 * j] = c * c;
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    const float var = seq_fold_lds<D / 4>((const float4*)sZ, -0.0f) / (float)D;
-    const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+    float o[PER];
+    ln_wave<PER>(z, sZ, gv, bv, lane, o);
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int e = lane + 64 * j;
-      const float o = ((z[j] - mean) * inv) * gv[j] + bv[j];
-      bad |= !isfinite(o);
-      if (h == 0) a.x_out[(int64_t)r * D + e] = o;
-      sX[e] = (int8_t)quantize_one(o, a.xq_mult);
+      bad |= !isfinite(o[j]);
+      if (h == 0) a.x_out[(int64_t)r * D + e] = o[j];
+      sX[e] = (int8_t)quantize_one(o[j], a.xq_mult);
     }
     if (__any(bad) && lane == 0 && a.err) *a.err = 1;
   } else {
@@ -219,7 +231,125 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   if (__any(lane < DH && !isfinite(o)) && lane == 0 && a.err) *a.err = 1;
 }
 
+// ---------------------------------------------------------------------------
+// Residual LayerNorm + static-multiplier Q8 linear: out = (relu of)
+// Q8Linear(LN(y + r)) for kLgsRows rows and kLgsCols output columns per
+// workgroup.  Wave w builds row w of the group (LayerNorm as
+// launch_residual_ln), quantizes it with the activation multiplier of the
+// column block it feeds (xq_mult[0] below part_n, xq_mult[1] from it: the
+// two parts of a row-block group with their own multipliers) into LDS, then
+// runs the MFMA chain of column tile w over the group's rows.  Slice-0
+// workgroups also store the LayerNorm rows (the next residual).
+// ---------------------------------------------------------------------------
+constexpr int kLgsRows = 8;
+constexpr int kLgsWaves = 8;
+constexpr int kLgsCols = 16 * kLgsWaves;
+
+template <int PER>
+__global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticArgs a) {
+  constexpr int D = PER * 64;
+  constexpr int KS = D / 64;
+  __shared__ __attribute__((aligned(16))) float sZ[kLgsWaves][D];
+  __shared__ __attribute__((aligned(16))) int8_t sX[kLgsRows][D];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int slices = a.N / kLgsCols;
+  const int slice = blockIdx.x % slices, grp = blockIdx.x / slices;
+  const int r = grp * kLgsRows + wave;  // this wave's row
+  const int n0 = slice * kLgsCols;
+  const float am = n0 < a.part_n ? a.xq_mult[0] : a.xq_mult[1];
+  // Row loads (rows below the host bound are backed by memory).
+  float yv[PER], rv[PER], gv[PER], bv[PER];
+  const bool row_mem = r < a.rows;
+  if (row_mem) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      yv[j] = a.y[(int64_t)r * D + e];
+      rv[j] = a.r[(int64_t)r * D + e];
+      gv[j] = a.gamma[e];
+      bv[j] = a.beta[e];
+    }
+  }
+  // Tile `wave` of this slice: weight fragments, dequantization operands.
+  const int col = n0 + 16 * wave + (lane & 15);
+  v4i bf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) bf[s] = frag_load(a.W, (n0 >> 4) + wave, KS, s, lane);
+  const float wm = a.wmult[col], wb = a.bias[col];
+  const int n_rows = a.rows_dev ? min(*a.rows_dev, a.rows) : a.rows;
+  if (grp * kLgsRows >= n_rows) return;  // the whole workgroup alike
+  const bool live = r < n_rows;
+  if (live) {
+    float z[PER], o[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) z[j] = yv[j] + rv[j];
+    ln_wave<PER>(z, sZ[wave], gv, bv, lane, o);
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      bad |= !isfinite(o[j]);
+      if (slice == 0 && a.x_out) a.x_out[(int64_t)r * D + e] = o[j];
+      sX[wave][e] = (int8_t)quantize_one(o[j], am);
+    }
+    if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+  }
+  __syncthreads();
+  // Rows 0..7 of the A operand are the group's rows (zero past the device
+  // count), rows 8..15 zero.  Lane l ends with rows 4(l/16)+i of column l%16.
+  const int ar = lane & 15;
+  const bool a_live = ar < kLgsRows && grp * kLgsRows + ar < n_rows;
+  v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const v4i x = a_live ? *(const v4i*)(&sX[ar][64 * s + (lane >> 4) * 16]) : v4i{0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x, bf[s], acc, 0, 0, 0);
+  }
+  if (lane >= 32) return;  // rows 8..15
+  const float inv = dequant_scale(am, wm);
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = grp * kLgsRows + 4 * (lane >> 4) + i;
+    if (m >= n_rows) continue;
+    float y = dequant_apply(acc[i], inv, wb);
+    if (a.relu) y = y > 0.0f ? y : 0.0f;
+    if (a.out) a.out[(int64_t)m * a.ldo + col] = y;
+    if (a.out_q) {
+      a.out_q[(int64_t)m * a.ldq + col] = (int8_t)quantize_one(y, a.qmult);
+      if (col == 0) a.out_qa[m] = a.qmult;
+      bad |= !isfinite(y);  // quantizing rejects non-finite input
+    }
+  }
+  if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+}
+
 }  // namespace
+
+bool ln_gemm_static_supported(int K, int N) {
+  return (K == 256 || K == 384 || K == 512) && N > 0 && N % kLgsCols == 0;
+}
+
+hipError_t launch_ln_gemm_static(const LnGemmStaticArgs& a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  if (!ln_gemm_static_supported(a.K, a.N) || !a.y || !a.r || !a.gamma || !a.beta || !a.W ||
+      !a.wmult || !a.bias || (!a.out && !a.out_q) || (a.out && a.ldo < a.N) ||
+      (a.out_q && (!a.out_qa || a.ldq < a.N)) || a.part_n < 0 || a.part_n % kLgsCols)
+    return hipErrorInvalidValue;
+  for (const float m : {a.xq_mult[0], a.xq_mult[1]})
+    if (!(m > 0.0f) || !(m < __builtin_huge_valf())) return hipErrorInvalidValue;
+  if (a.out_q && (!(a.qmult > 0.0f) || !(a.qmult < __builtin_huge_valf()))) return hipErrorInvalidValue;
+  const int groups = (a.rows + kLgsRows - 1) / kLgsRows;
+  if ((int64_t)groups * (a.N / kLgsCols) > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 grid(groups * (a.N / kLgsCols)), block(64 * kLgsWaves);
+  if (a.K == 256)
+    hipLaunchKernelGGL(k_ln_gemm_static<4>, grid, block, 0, s, a);
+  else if (a.K == 384)
+    hipLaunchKernelGGL(k_ln_gemm_static<6>, grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL(k_ln_gemm_static<8>, grid, block, 0, s, a);
+  return hipGetLastError();
+}
 
 bool ssru_block_supported(int d, int heads, int max_keys) {
   if (heads <= 0 || d % heads || max_keys <= 0 || max_keys > kSsruBlockMaxKeys) return false;

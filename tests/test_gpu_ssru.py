@@ -89,12 +89,16 @@ def test_ssru_probe_bit_exact(pkg, orc, step):
 
 
 def test_ssru_long_sentences_token_exact(pkg, orc):
-    """Sentences longer than 128 tokens: every step's SSRU LayerNorm, query
-    projection and cross-attention run as separate kernels (the fused decode
-    block holds at most 128 encoder keys per row); shorter batches above use
-    the fused block.  Both read the recurrent state of step t from one buffer
-    and write it to the other."""
-    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=2, decoder_layers=2)
+    """Sentences longer than 128 tokens and an FFN width that is not a
+    multiple of 128: every step's SSRU LayerNorm, query projection and
+    cross-attention run as separate kernels (the fused decode block holds at
+    most 128 encoder keys per row), and so do the residual LayerNorms and the
+    linears that read them (the fused LayerNorm + linear kernel takes 128
+    output columns per workgroup).  The other cases use the fused kernels.
+    Both read the recurrent state of step t from one buffer and write it to
+    the other."""
+    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=2, decoder_layers=2,
+                         ffn_dim=960)
     model = pkg.seeded_ssru_model(seed=37, geometry=g, std=0.05)
     om = orc.OracleSsruModel(model)
     rng = np.random.default_rng(13)
