@@ -335,6 +335,97 @@ __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, f
   return s;
 }
 
+// ---- speculative exact fold by one wave ---------------------------------------
+// The sequential fold init + p[0] + ... + p[128 NC - 1] with a dependent chain
+// of 128 additions instead of 128 NC: the values are cut into NC chunks of 128,
+// stored in LDS 132 floats apart (chunk c at p + kSwStride c, so the lane
+// groups' broadcast reads fall in different banks).  Lanes [0, kSwLead) fold
+// chunk 0 from init; the kSwCand(NC) lanes of group c >= 1 fold chunk c from
+// consecutive floats (by key, as in spec_fold_chunk) around est[c], an
+// estimate of the prefix p[0] + ... + p[128c - 1].  Then the true start of
+// each chunk (the end of the one before) picks its lane's chain end when it
+// lies in the window, and otherwise chunk c is folded again from the true
+// start.  Every step is the sequential fold's own float addition, so the
+// result is exactly the sequential fold's; the estimates only decide how often
+// a refold happens.  All lanes return the result.
+constexpr int kSwStride = 132;
+template <int NC>
+constexpr int kSwCand = NC == 2 ? 32 : NC == 3 ? 24 : 16;
+template <int NC>
+constexpr int kSwLead = 64 - (NC - 1) * kSwCand<NC>;
+
+template <int NC>
+__device__ __forceinline__ float spec_fold_wave(const float* p, const float (&est)[NC], float init,
+                                                int lane) {
+  static_assert(NC >= 2 && NC <= 4, "two to four chunks");
+  constexpr int W = kSwCand<NC>, L0 = kSwLead<NC>;
+  const int c = lane < L0 ? 0 : 1 + (lane - L0) / W;
+  int base[NC];
+#pragma unroll
+  for (int k = 1; k < NC; ++k)
+    base[k] = min(max(float_key(est[k]), INT32_MIN + W / 2), INT32_MAX - W / 2 + 1) - W / 2;
+  float st = init;
+#pragma unroll
+  for (int k = 1; k < NC; ++k)
+    if (c == k) st = key_float(base[k] + (lane - L0 - (k - 1) * W));
+  const float* pc = p + kSwStride * c;
+  const int ek = float_key(seq_fold_lds<kSpecChunk / 4, 4>((const float4*)pc, st));
+  int ks = __builtin_amdgcn_readfirstlane(ek);  // lane 0: the end of chunk 0
+#pragma unroll
+  for (int k = 1; k < NC; ++k) {
+    const uint32_t d = (uint32_t)ks - (uint32_t)__builtin_amdgcn_readfirstlane(base[k]);
+    if (d < (uint32_t)W) {
+      ks = __builtin_amdgcn_readlane(ek, L0 + (k - 1) * W + (int)d);
+    } else {  // the start lies outside the window: fold chunk k again from it
+      const float s = seq_fold_lds<kSpecChunk / 4, 4>((const float4*)(p + kSwStride * k), key_float(ks));
+      ks = __builtin_amdgcn_readfirstlane(float_key(s));
+    }
+  }
+  return key_float(ks);
+}
+
+// LDS floats of one wave's LayerNorm row (room for the chunked layout).
+template <int PER>
+constexpr bool kLnSpec = PER == 4 || PER == 6 || PER == 8;
+template <int PER>
+constexpr int kLnRow = kLnSpec<PER> ? kSwStride * (PER / 2) : PER * 64;
+
+// The sequential fold -0.0 + v[0] + v[1] + ... of a row held by one wave
+// (lane l: elements l + 64j in v[j]) through its LDS row zr.  Rows of 256,
+// 384 or 512 elements fold as 2, 3 or 4 speculative chunks (spec_fold_wave,
+// the estimates being float sums of the chunks), others strictly in order.
+template <int PER>
+__device__ __forceinline__ float fold_row_wave(const float (&v)[PER], float* zr, int lane) {
+  if constexpr (kLnSpec<PER>) {
+    constexpr int NC = PER / 2;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) zr[kSwStride * (j >> 1) + lane + 64 * (j & 1)] = v[j];
+    // Prefix estimates: est[c] = sum of chunks 0 .. c-1.
+    float cs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c + 1 < NC; ++c) cs[c] = v[2 * c] + v[2 * c + 1];
+    wave_sum2(cs[0], cs[1]);
+    if constexpr (NC == 4) wave_sum2(cs[2], cs[3]);
+    float est[NC];
+    est[0] = 0.0f;
+#pragma unroll
+    for (int c = 1; c < NC; ++c) est[c] = est[c - 1] + cs[c - 1];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the row is in LDS
+    __builtin_amdgcn_wave_barrier();
+    const float r = spec_fold_wave<NC>(zr, est, -0.0f, lane);
+    __builtin_amdgcn_wave_barrier();
+    return r;
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) zr[lane + 64 * j] = v[j];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const float r = seq_fold_lds<PER * 16>((const float4*)zr, -0.0f);
+    __builtin_amdgcn_wave_barrier();
+    return r;
+  }
+}
+
 // q = clamp(round_half_even(x * a), -127, 127)  (q8_gemm.rs:584-587)
 __device__ __forceinline__ int quantize_one(float x, float a) {
   float v = rintf(x * a);

@@ -93,29 +93,23 @@ __global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_
 // LayerNorm of one row z (lane holds z[lane + 64 j]) by one wave, stored to
 // out (and quantized into q / a when q is set, with the row's own multiplier
 // or, when qmult > 0, the next layer's static one): normalize_row
-// (tensor.rs:372-385) sums the row strictly left to right, so the wave parks z
-// in LDS (zr, D floats) and every lane folds the row sequentially; the centred
-// squares are formed lane-parallel and parked the same way.
+// (tensor.rs:372-385) sums the row strictly left to right: the wave parks z in
+// LDS (zr, kLnRow<PER> floats) and folds it with fold_row_wave (speculative
+// 128-element chunks for even PER, with the sequential fold's exact result);
+// the centred squares are formed lane-parallel and folded the same way.
 template <int PER>
 __device__ __forceinline__ void ln_row_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
                                             const float (&bv)[PER], int row, int lane, float* out,
                                             int8_t* q, float* a, int* err, float qmult) {
   constexpr int D = PER * 64;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) zr[lane + 64 * j] = z[j];
-  // The wave's LDS writes complete before its reads below.
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  const float mean = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
-  __builtin_amdgcn_wave_barrier();
+  const float mean = fold_row_wave<PER>(z, zr, lane) / (float)D;
+  float t[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const float c = z[j] - mean;
-    zr[lane + 64 * j] = c * c;
+    t[j] = c * c;
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
-  const float var = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
+  const float var = fold_row_wave<PER>(t, zr, lane) / (float)D;
   const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
   float o[PER];
   float m = 0.0f;
@@ -145,7 +139,7 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
                                                      int rows, const int* rows_dev, float* out,
                                                      int8_t* q, float* a, int* err, float qmult) {
   constexpr int D = PER * 64;
-  __shared__ __attribute__((aligned(16))) float sZ[4][D];
+  __shared__ __attribute__((aligned(16))) float sZ[4][kLnRow<PER>];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + wave;
   if (row >= rows) return;  // uniform per wave; the waves share no barrier
@@ -187,7 +181,7 @@ __global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float*
                                                  const int* state_row, float* out, int8_t* q,
                                                  float* a, int* err, float qmult, float* state_out) {
   constexpr int D = PER * 64;
-  __shared__ __attribute__((aligned(16))) float sZ[4][D];
+  __shared__ __attribute__((aligned(16))) float sZ[4][kLnRow<PER>];
   __shared__ uint64_t sTab[32];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (threadIdx.x < 32) sTab[threadIdx.x] = kRowsExp2Tab[threadIdx.x];

@@ -33,25 +33,19 @@ __constant__ uint64_t kSbExp2Tab[32] = {MH_EXP2_TABLE_32};
 
 // LayerNorm of the row z (lane l holds elements l + 64j) by one wave with
 // normalize_row's sequential folds (tensor.rs:372-385); zr is the wave's LDS
-// row (D floats).  Returns the normalized row in o.
+// row (kLnRow<PER> floats).  Returns the normalized row in o.
 template <int PER>
 __device__ __forceinline__ void ln_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
                                         const float (&bv)[PER], int lane, float (&o)[PER]) {
   constexpr int D = PER * 64;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) zr[lane + 64 * j] = z[j];
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  const float mean = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
-  __builtin_amdgcn_wave_barrier();
+  const float mean = fold_row_wave<PER>(z, zr, lane) / (float)D;
+  float t[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const float c = z[j] - mean;
-    zr[lane + 64 * j] = c * c;
+    t[j] = c * c;
   }
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
-  const float var = seq_fold_lds<D / 4>((const float4*)zr, -0.0f) / (float)D;
+  const float var = fold_row_wave<PER>(t, zr, lane) / (float)D;
   const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
 #pragma unroll
   for (int j = 0; j < PER; ++j) o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];
@@ -68,7 +62,7 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   static_assert(T <= 4 && DH % 16 == 0, "one query tile per wave");
   __shared__ __attribute__((aligned(16))) float sK[kSsruBlockMaxKeys * KR];
   __shared__ __attribute__((aligned(16))) float sV[kSsruBlockMaxKeys * KR];
-  __shared__ __attribute__((aligned(16))) float sZ[D];
+  __shared__ __attribute__((aligned(16))) float sZ[kLnRow<PER>];
   __shared__ __attribute__((aligned(16))) int8_t sX[D];
   __shared__ __attribute__((aligned(16))) float sQ[DH];
   __shared__ __attribute__((aligned(16))) float sP[kSsruBlockMaxKeys];
@@ -249,7 +243,7 @@ template <int PER>
 __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticArgs a) {
   constexpr int D = PER * 64;
   constexpr int KS = D / 64;
-  __shared__ __attribute__((aligned(16))) float sZ[kLgsWaves][D];
+  __shared__ __attribute__((aligned(16))) float sZ[kLgsWaves][kLnRow<PER>];
   __shared__ __attribute__((aligned(16))) int8_t sX[kLgsRows][D];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int slices = a.N / kLgsCols;

@@ -121,9 +121,9 @@ def _ln_edge_rows(rng, d=512):
     windows miss and chunks are refolded), exact zeros and negative zeros,
     constants, wide and tiny magnitudes."""
     rows = []
-    for _ in range(8):  # cancellation at 128, 256 and 384
+    for _ in range(8):  # cancellation at every 128-element chunk boundary
         z = rng.standard_normal(d).astype(np.float32) * np.float32(rng.uniform(0.5, 20))
-        for k in (128, 256, 384):
+        for k in range(128, d, 128):
             s = np.float32(-0.0)
             for v in z[:k - 1]:
                 s = np.float32(s + v)
@@ -137,6 +137,45 @@ def _ln_edge_rows(rng, d=512):
     alt = np.where(np.arange(d) % 2 == 0, 1e4, -1e4).astype(np.float32)
     rows.append(alt + (rng.standard_normal(d) * 1e-3).astype(np.float32))
     return np.stack(rows)
+
+
+@pytest.mark.parametrize("d", [256, 384])
+def test_residual_layer_norm_single_wave_speculative_edges(pkg, orc, dev, d):
+    """Rows of 256 and 384 fold as two or three speculative 128-element chunks
+    inside one wave (the SSRU graph's LayerNorms): chunk boundaries where the
+    prefix cancels to near zero force refolds; the result is the sequential
+    fold's, bit for bit, and non-finite rows keep their NaN positions."""
+    rng = np.random.default_rng(23 + d)
+    z = np.concatenate([_ln_edge_rows(rng, d), rng.standard_normal((21, d)).astype(np.float32) * 3])
+    y = (z * np.float32(0.75)).astype(np.float32)
+    r = (z - y).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(d)).astype(np.float32)
+    ref = orc.residual_layer_norm(y, r, g, b)
+    q_ref, a_ref = orc.quantize_rows(ref)
+    out = dev.DeviceArray.zeros(y.shape, np.float32)
+    q = dev.DeviceArray.zeros(y.shape, np.int8)
+    a = dev.DeviceArray.zeros(y.shape[0], np.float32)
+    dev.residual_layer_norm(dev.DeviceArray.from_host(y), dev.DeviceArray.from_host(r),
+                            dev.DeviceArray.from_host(g), dev.DeviceArray.from_host(b), out, q, a)
+    dev.synchronize()
+    assert np.array_equal(out.host().view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(q.host(), q_ref) and np.array_equal(a.host(), a_ref)
+    y2 = y[:3].copy()
+    y2[0, 130] = np.nan
+    y2[1, 257 % d] = np.inf
+    y2[2, 5] = -np.inf
+    ref2 = orc.residual_layer_norm(y2, r[:3], g, b)
+    out2 = dev.DeviceArray.zeros(y2.shape, np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.residual_layer_norm(dev.DeviceArray.from_host(y2), dev.DeviceArray.from_host(r[:3]),
+                            dev.DeviceArray.from_host(g), dev.DeviceArray.from_host(b), out2, err=err)
+    dev.synchronize()
+    got2 = out2.host()
+    assert np.array_equal(np.isnan(got2), np.isnan(ref2))
+    fin = ~np.isnan(ref2)
+    assert np.array_equal(got2[fin], ref2[fin])
+    assert err.host()[0] == 1
 
 
 def test_residual_layer_norm_few_rows_edge_cases(pkg, orc, dev):
