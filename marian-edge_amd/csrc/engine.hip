@@ -1510,22 +1510,26 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       return launch_quantize_rows_static(x, K, rows, K, mult, q, K, a, E->err_flag, s, d_nact);
     };
     const SGroup& uf0 = E->sdec[0].uf;
-    EmbedArgs ea;
-    ea.emb = E->emb.w;
-    ea.emb_mult = E->emb.mult;
-    ea.pos = E->pos;
-    ea.scale = E->emb_scale;
-    ea.d = d;
-    ea.row_prev = rm.prev;
-    ea.step = (int)t;
-    ea.rows = rows;
-    ea.rows_dev = d_nact;
-    ea.x = xres;
-    ea.xq = uf0.shared ? DXQ : nullptr;
-    ea.xa = DXA;
-    ea.qmult = uf0.shared ? uf0.act[0] : 0.0f;
-    ea.err = E->err_flag;
-    MH_TRY(launch_embed(ea, s));
+    // With the fused SSRU kernels the first layer's input kernel builds the
+    // embedding itself.
+    if (!ssru_blk) {
+      EmbedArgs ea;
+      ea.emb = E->emb.w;
+      ea.emb_mult = E->emb.mult;
+      ea.pos = E->pos;
+      ea.scale = E->emb_scale;
+      ea.d = d;
+      ea.row_prev = rm.prev;
+      ea.step = (int)t;
+      ea.rows = rows;
+      ea.rows_dev = d_nact;
+      ea.x = xres;
+      ea.xq = uf0.shared ? DXQ : nullptr;
+      ea.xa = DXA;
+      ea.qmult = uf0.shared ? uf0.act[0] : 0.0f;
+      ea.err = E->err_flag;
+      MH_TRY(launch_embed(ea, s));
+    }
     // Residual LayerNorm + the linear that reads it, in one launch.
     auto ln_gemm = [&](const float* y, const float* ln_s, const float* ln_b, const Lin& W, float a0,
                        float a1, int part_n, int relu, float* out, int8_t* q, float* qa,
@@ -1560,33 +1564,46 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     };
     for (uint32_t l = 0; l < E->Ld; ++l) {
       const SDecLayer& L = E->sdec[l];
-      // ---- SSRU: candidate and forget-gate inputs side by side in DUF ----
-      if (ssru_lnf && l > 0) {  // with the previous layer's last LayerNorm
-        const SDecLayer& P = E->sdec[l - 1];
-        MH_TRY(ln_gemm(DY, P.ln2_s, P.ln2_b, L.uf.all, L.uf.act[0], L.uf.act[L.uf.shared ? 0 : 1],
-                       L.uf.shared ? 2 * d : d, 0, DUF, nullptr, nullptr, 0.0f));
-      } else if (L.uf.shared) {
-        MH_TRY(dgemm(L.uf.all, DXQ, DXA, DUF, 2 * d, 0));
-      } else {
-        for (int i = 0; i < 2; ++i) {
-          MH_TRY(qs(xres, d, L.uf.act[i], DXQ, DXA));
-          MH_TRY(dgemm(L.uf.part(i), DXQ, DXA, DUF + (size_t)i * d, 2 * d, 0));
-        }
-      }
       float* st_in = STATE + ((size_t)(t & 1) * LdA + l) * R * d;
       float* st_out = STATE + ((size_t)((t + 1) & 1) * LdA + l) * R * d;
       const float* ckv = CKV + (size_t)l * TR * 2 * d;
       if (ssru_blk) {
-        // SSRU + LayerNorm, query projection and cross-attention in one launch.
+        // ---- SSRU: the layer input, its candidate and forget-gate
+        // projections and the state update (z = relu(state') + x in DUF) ----
+        SsruInputArgs si;
+        if (l == 0) {
+          si.pro.kind = PRO_EMB;
+          si.pro.emb = E->emb.w;
+          si.pro.emb_mult = E->emb.mult;
+          si.pro.pos = E->pos;
+          si.pro.scale = E->emb_scale;
+          si.pro.row_prev = rm.prev;
+          si.step = (int)t;
+        } else {  // the previous layer's last residual LayerNorm
+          si.pro.kind = PRO_LN;
+          si.pro.y = DY;
+          si.pro.r = xres;
+          si.pro.gamma = E->sdec[l - 1].ln2_s;
+          si.pro.beta = E->sdec[l - 1].ln2_b;
+        }
+        si.rows = rows;
+        si.rows_dev = d_nact;
+        si.d = d;
+        si.act_c = L.uf.act[0];
+        si.act_f = L.uf.act[L.uf.shared ? 0 : 1];
+        si.W = L.uf.all.wf;
+        si.wmult = L.uf.all.mult;
+        si.bias = L.uf.all.bias;
+        si.state_in = st_in;
+        si.state_out = st_out;
+        si.state_row = rm.slot;
+        si.state_rows = (int64_t)R;
+        si.z = DUF;
+        si.err = E->err_flag;
+        MH_TRY(launch_ssru_input(si, s));
+        // ---- SSRU LayerNorm, query projection and cross-attention ----
         SsruBlockArgs sb;
-        sb.cand = DUF;
-        sb.forget = DUF + d;
-        sb.ldc = 2 * d;
-        sb.state_in = st_in;
-        sb.state_out = st_out;
-        sb.state_row = rm.slot;
-        sb.state_rows = (int64_t)R;
-        sb.resid = xres;
+        sb.z = DUF;
         sb.gamma = L.ln0_s;
         sb.beta = L.ln0_b;
         sb.x_out = xalt;
@@ -1613,6 +1630,19 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
         MH_TRY(launch_ssru_block(sb, s));
         std::swap(xres, xalt);
       } else {
+        // ---- SSRU: candidate and forget-gate inputs side by side in DUF ----
+        if (ssru_lnf && l > 0) {  // with the previous layer's last LayerNorm
+          const SDecLayer& P = E->sdec[l - 1];
+          MH_TRY(ln_gemm(DY, P.ln2_s, P.ln2_b, L.uf.all, L.uf.act[0], L.uf.act[L.uf.shared ? 0 : 1],
+                         L.uf.shared ? 2 * d : d, 0, DUF, nullptr, nullptr, 0.0f));
+        } else if (L.uf.shared) {
+          MH_TRY(dgemm(L.uf.all, DXQ, DXA, DUF, 2 * d, 0));
+        } else {
+          for (int i = 0; i < 2; ++i) {
+            MH_TRY(qs(xres, d, L.uf.act[i], DXQ, DXA));
+            MH_TRY(dgemm(L.uf.part(i), DXQ, DXA, DUF + (size_t)i * d, 2 * d, 0));
+          }
+        }
         MH_TRY(launch_ssru_ln(DUF, DUF + d, st_in, xres, L.ln0_s, L.ln0_b, rows, d, xalt, DXQ, DXA,
                               E->err_flag, s, 2 * d, d_nact, rm.slot, L.aq, st_out));
         std::swap(xres, xalt);
@@ -1654,7 +1684,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       }
       MH_TRY(dgemm(L.w2, DHQ, DHA, DY, d, 0));
       // The next layer's SSRU projections build this LayerNorm themselves.
-      if (ssru_lnf && l + 1 < E->Ld) continue;
+      if ((ssru_blk || ssru_lnf) && l + 1 < E->Ld) continue;
       // quantized for what reads it next: the next layer's SSRU inputs (when
       // they share a multiplier) or the output scoring
       const SGroup* nx = l + 1 < E->Ld ? &E->sdec[l + 1].uf : nullptr;

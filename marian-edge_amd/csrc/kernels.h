@@ -138,26 +138,45 @@ hipError_t launch_ssru_ln(const float* cand, const float* forget, float* state, 
                           const int* rows_dev = nullptr, const int* state_row = nullptr,
                           float qmult = 0.0f, float* state_out = nullptr);
 
-// Fused SSRU decode block (Transformer-SSRU graph, static multipliers): per
-// (row, head) one workgroup applies launch_ssru_ln's update and LayerNorm to
-// the row (the head-0 workgroup stores the new state to state_out and the
-// LayerNorm row to x_out), quantizes the row with the query projection's
+// SSRU input (Transformer-SSRU decoder, static multipliers): the layer input
+// x of each row (pro: PRO_LN, LayerNorm(y + r), the previous layer's last
+// sublayer; PRO_EMB, the decoder input embedding at position `step`), its
+// candidate and forget-gate projections (W [2d, d] in fragment order: rows
+// [0, d) the candidate, [d, 2d) the forget gate, each input quantized with its
+// own static multiplier act_c / act_f), and the SSRU update of each state
+// column: state_out[seq] = gate * state_in[seq] + (1 - gate) * c with gate =
+// 1 / (1 + exp(-f)), z = relu(state') + x.  d = 256, 384 or 512; state_out
+// must not alias state_in.
+struct SsruInputArgs {
+  RowPrologue pro;
+  int step = 0;  // PRO_EMB: the position row
+  int rows = 0;
+  const int* rows_dev = nullptr;
+  int d = 0;
+  float act_c = 0.0f, act_f = 0.0f;
+  const int8_t* W = nullptr;
+  const float* wmult = nullptr;  // [2d]
+  const float* bias = nullptr;   // [2d]
+  const float* state_in = nullptr;  // [sequences, d]
+  float* state_out = nullptr;
+  const int* state_row = nullptr;   // sequence of each row
+  int64_t state_rows = 0;           // sequences held by the state buffers
+  float* z = nullptr;               // [rows, d]
+  int* err = nullptr;
+};
+hipError_t launch_ssru_input(const SsruInputArgs& a, hipStream_t s);
+
+// SSRU decode block: per (row, head) one workgroup takes z (from
+// launch_ssru_input), applies the SSRU LayerNorm (the head-0 workgroup stores
+// the LayerNorm row to x_out), quantizes the row with the query projection's
 // static multiplier xq_mult, projects it onto the head's query with int8 MFMA
 // (static dequantization), attends over the row's encoder keys
 // row_key0[r] + [0, row_nk[r]) (at most kSsruBlockMaxKeys), and stores the
 // head's output quantized with the output projection's static multiplier
-// (qout [rows, ldqout], qa[r] = qmult).  One launch replaces the SSRU
-// LayerNorm, query projection and cross-attention kernels.  state_out must
-// not alias state_in: every head reads the old state.
+// (qout [rows, ldqout], qa[r] = qmult).  One launch replaces the LayerNorm,
+// query projection and cross-attention kernels.
 struct SsruBlockArgs {
-  const float* cand = nullptr;  // [rows, ldc] candidate inputs; forget at `forget`
-  const float* forget = nullptr;
-  int64_t ldc = 0;
-  const float* state_in = nullptr;  // [sequences, d]
-  float* state_out = nullptr;       // [sequences, d]
-  const int* state_row = nullptr;   // sequence of each row
-  int64_t state_rows = 0;           // sequences held by the state buffers
-  const float* resid = nullptr;     // [rows, d]
+  const float* z = nullptr;  // [rows, d]
   const float* gamma = nullptr;
   const float* beta = nullptr;
   float* x_out = nullptr;  // [rows, d] the LayerNorm rows
