@@ -727,43 +727,75 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e, int t
 // against the row's quantized state on the matrix cores (every row of the A
 // tile is the state, so output row 0 is the dot products).  Keys (logit,
 // inverted id) give the first maximum in candidate order, as the strict '>'
-// scan does; one key per workgroup goes to partials[m * nparts + chunk].
+// scan does; one key per workgroup goes to partials[m * nparts + chunk]
+// (0 from the workgroups past a shorter list, which exit at once).
 // ---------------------------------------------------------------------------
 constexpr int kCandChunk = 128;
+constexpr int kCandKs = 8;  // k-steps requested together (K <= 512: all of them)
 __global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
   __shared__ uint64_t sKey[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = blockIdx.y, chunk = blockIdx.x;
-  if (c.rows_dev && m >= *c.rows_dev) return;  // uniform per workgroup
   const int ksteps = c.K >> 6, kq = (lane >> 4) * 16;
+  // The first k-steps are requested before the device row count is known
+  // (rows below the host bound are backed by memory; a finished row's list is
+  // another sequence's, still in bounds), all of them at once.
   const int b = c.row_slot ? c.row_slot[m] : m;
   const int64_t c0 = c.off[b], n = (int64_t)c.off[b + 1] - c0;
-  const int8_t* xr = c.xq + (int64_t)m * c.K;
+  if ((int64_t)chunk * kCandChunk >= n) {  // past the row's list (the grid fits the longest)
+    if (tid == 0 && !(c.rows_dev && m >= *c.rows_dev)) c.partials[(int64_t)m * c.nparts + chunk] = 0;
+    return;
+  }
+  const int8_t* xr = c.xq + (int64_t)m * c.K + kq;
   const float am = c.xa[m];
-  uint64_t best = 0;
-  bool bad = false;
+  bool live[2], bad = false;
+  uint32_t id[2];
+  const int8_t* er[2];
+  float wm[2], wb[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int64_t i = (int64_t)chunk * kCandChunk + wave * 32 + t * 16 + (lane & 15);
-    bool live = i < n;
-    uint32_t id = live ? c.cand[c0 + i] : 0u;
-    if (id >= (uint32_t)c.V) {  // not a vocabulary id: reported, never scored
+    live[t] = i < n;
+    id[t] = live[t] ? c.cand[c0 + i] : 0u;
+    if (id[t] >= (uint32_t)c.V) {  // not a vocabulary id: reported, never scored
       bad = true;
-      live = false;
-      id = 0u;
+      live[t] = false;
+      id[t] = 0u;
     }
-    const int8_t* er = c.emb + (int64_t)id * c.K + kq;
-    v4i acc = zero4();
-    for (int s = 0; s < ksteps; ++s) {
-      const v4i a = *(const v4i*)(xr + kq + s * 64);
-      const v4i b = *(const v4i*)(er + s * 64);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+    er[t] = c.emb + (int64_t)id[t] * c.K + kq;
+    wm[t] = c.mult[id[t]];
+    wb[t] = c.bias[id[t]];
+  }
+  v4i xa[kCandKs], bw[2][kCandKs];
+  auto load = [&](int s0) {
+#pragma unroll
+    for (int s = 0; s < kCandKs; ++s) {
+      const int64_t o = 64 * min(s0 + s, ksteps - 1);
+      xa[s] = *(const v4i*)(xr + o);
+      bw[0][s] = *(const v4i*)(er[0] + o);
+      bw[1][s] = *(const v4i*)(er[1] + o);
     }
-    // Lanes 0-15 hold row 0 (register 0) for candidates 16t + lane.
-    if (lane < 16 && live) {
-      const float y = dequant(acc[0], am, c.mult[id], c.bias[id]);
-      if (c.logits) c.logits[c0 + i] = y;
-      const uint64_t k = argmax_key(y, id);
+  };
+  load(0);
+  if (c.rows_dev && m >= *c.rows_dev) return;  // uniform per workgroup
+  v4i acc[2] = {zero4(), zero4()};
+  for (int s0 = 0; s0 < ksteps; s0 += kCandKs) {
+    if (s0 > 0) load(s0);
+#pragma unroll
+    for (int s = 0; s < kCandKs; ++s)
+      if (s0 + s < ksteps) {  // uniform
+        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s], bw[0][s], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s], bw[1][s], acc[1], 0, 0, 0);
+      }
+  }
+  uint64_t best = 0;
+  // Lanes 0-15 hold row 0 (register 0) for candidates 16t + lane.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (lane < 16 && live[t]) {
+      const float y = dequant(acc[t][0], am, wm[t], wb[t]);
+      if (c.logits) c.logits[c0 + chunk * kCandChunk + wave * 32 + t * 16 + lane] = y;
+      const uint64_t k = argmax_key(y, id[t]);
       best = k > best ? k : best;
     }
   }
