@@ -1531,11 +1531,19 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       MH_TRY(launch_embed(ea, s));
     }
     // Residual LayerNorm + the linear that reads it, in one launch.
+    // y == nullptr: y is the static linear Wy of the int8 rows DXQ (ya_mult).
     auto ln_gemm = [&](const float* y, const float* ln_s, const float* ln_b, const Lin& W, float a0,
                        float a1, int part_n, int relu, float* out, int8_t* q, float* qa,
-                       float qmult) {
+                       float qmult, const Lin* Wy = nullptr, float ya_mult = 0.0f) {
       LnGemmStaticArgs lg;
       lg.y = y;
+      if (!y) {
+        lg.ya = DXQ;
+        lg.ya_mult = ya_mult;
+        lg.Wy = Wy->wf;
+        lg.ymult = Wy->mult;
+        lg.ybias = Wy->bias;
+      }
       lg.r = xres;
       lg.gamma = ln_s;
       lg.beta = ln_b;
@@ -1672,11 +1680,13 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
         ca.qmult = L.ao;
         MH_TRY(launch_attention(ca, s));
       }
-      MH_TRY(dgemm(L.o, DXQ, DXA, DY, d, 0));
-      // ---- feed-forward (hidden quantized for W2) ----
-      if (ssru_lnf) {
-        MH_TRY(ln_gemm(DY, L.ln1_s, L.ln1_b, L.w1, L.a1, L.a1, F, 1, nullptr, DHQ, DHA, L.a2));
+      // ---- output projection, context LayerNorm, feed-forward (hidden
+      // quantized for W2) ----
+      if (ssru_lnf) {  // every workgroup projects its rows itself
+        MH_TRY(ln_gemm(nullptr, L.ln1_s, L.ln1_b, L.w1, L.a1, L.a1, F, 1, nullptr, DHQ, DHA, L.a2, &L.o,
+                       L.ao));
       } else {
+        MH_TRY(dgemm(L.o, DXQ, DXA, DY, d, 0));
         MH_TRY(launch_residual_ln(DY, xres, L.ln1_s, L.ln1_b, rows, d_nact, d, xalt, DXQ, DXA, E->err_flag,
                                   s, L.a1));
         std::swap(xres, xalt);

@@ -210,7 +210,15 @@ constexpr int kSsruBlockMaxKeys = 128;
 // LayerNorm rows.  Eight rows and 128 output columns per workgroup;
 // K = 256, 384 or 512, N a multiple of 128.
 struct LnGemmStaticArgs {
-  const float* y = nullptr;  // [rows, K]
+  const float* y = nullptr;  // [rows, K], or computed from ya:
+  // y = the static Q8 linear of the int8 rows ya [rows, K] with multiplier
+  // ya_mult and Wy [K, K] in fragment order (ymult, ybias): the attention
+  // output projection, computed by every workgroup for its rows.
+  const int8_t* ya = nullptr;
+  float ya_mult = 0.0f;
+  const int8_t* Wy = nullptr;
+  const float* ymult = nullptr;
+  const float* ybias = nullptr;
   const float* r = nullptr;  // [rows, K]
   const float* gamma = nullptr;
   const float* beta = nullptr;

@@ -394,18 +394,24 @@ constexpr int kLgsRows = 8;
 constexpr int kLgsWaves = 8;
 constexpr int kLgsCols = 16 * kLgsWaves;
 
-template <int PER>
+// YP: y is not read but computed here, the static Q8 linear of the int8 rows
+// a.ya with Wy (the attention-output projection): wave w takes its column
+// tiles w, w + 8, ... over the group's rows, and the rows meet in LDS.
+template <int PER, bool YP>
 __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticArgs a) {
   constexpr int D = PER * 64;
   constexpr int KS = D / 64;
+  constexpr int YT = YP ? D / 16 / kLgsWaves : 1;  // y tiles per wave
   __shared__ __attribute__((aligned(16))) float sZ[kLgsWaves][kLnRow<PER>];
   __shared__ __attribute__((aligned(16))) int8_t sX[kLgsRows][D];
+  __shared__ __attribute__((aligned(16))) float sY[YP ? kLgsRows : 1][YP ? D : 1];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int slices = a.N / kLgsCols;
   const int slice = blockIdx.x % slices, grp = blockIdx.x / slices;
   const int r = grp * kLgsRows + wave;  // this wave's row
   const int n0 = slice * kLgsCols;
   const float am = n0 < a.part_n ? a.xq_mult[0] : a.xq_mult[1];
+  const int ar = lane & 15;  // MFMA A-operand row of this lane
   // Row loads (rows below the host bound are backed by memory).
   float yv[PER], rv[PER], gv[PER], bv[PER];
   const bool row_mem = r < a.rows;
@@ -413,10 +419,26 @@ __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticA
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int e = lane + 64 * j;
-      yv[j] = a.y[(int64_t)r * D + e];
+      if (!YP) yv[j] = a.y[(int64_t)r * D + e];
       rv[j] = a.r[(int64_t)r * D + e];
       gv[j] = a.gamma[e];
       bv[j] = a.beta[e];
+    }
+  }
+  // YP: the group's int8 rows (A fragments) and this wave's Wy tiles.
+  v4i ya[YP ? KS : 1], by[YT][YP ? KS : 1];
+  float ym[YT], yb[YT];
+  if constexpr (YP) {
+    const int m = min(grp * kLgsRows + (ar & (kLgsRows - 1)), a.rows - 1);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) ya[s] = *(const v4i*)(a.ya + (int64_t)m * D + 64 * s + (lane >> 4) * 16);
+#pragma unroll
+    for (int i = 0; i < YT; ++i) {
+      const int t = wave + kLgsWaves * i;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) by[i][s] = frag_load(a.Wy, t, KS, s, lane);
+      ym[i] = a.ymult[16 * t + ar];
+      yb[i] = a.ybias[16 * t + ar];
     }
   }
   // Tile `wave` of this slice: weight fragments, dequantization operands.
@@ -428,6 +450,29 @@ __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticA
   const int n_rows = a.rows_dev ? min(*a.rows_dev, a.rows) : a.rows;
   if (grp * kLgsRows >= n_rows) return;  // the whole workgroup alike
   const bool live = r < n_rows;
+  if constexpr (YP) {
+    // y rows 0..7 = the group's rows (zero past the device count); lane l
+    // ends with rows 4(l/16)+i of column l%16 of each tile.
+    const bool y_live = ar < kLgsRows && grp * kLgsRows + ar < n_rows;
+#pragma unroll
+    for (int i = 0; i < YT; ++i) {
+      v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(y_live ? ya[s] : v4i{0, 0, 0, 0}, by[i][s], acc, 0, 0, 0);
+      if (lane < 32) {
+        const float inv = dequant_scale(a.ya_mult, ym[i]);
+        const int t = wave + kLgsWaves * i;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sY[4 * (lane >> 4) + k][16 * t + ar] = dequant_apply(acc[k], inv, yb[i]);
+      }
+    }
+    wg_lds_barrier();
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) yv[j] = sY[wave][lane + 64 * j];
+    }
+  }
   if (live) {
     float z[PER], o[PER];
 #pragma unroll
@@ -446,7 +491,6 @@ __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticA
   wg_lds_barrier();  // LDS only: the LayerNorm row stores stay in flight
   // Rows 0..7 of the A operand are the group's rows (zero past the device
   // count), rows 8..15 zero.  Lane l ends with rows 4(l/16)+i of column l%16.
-  const int ar = lane & 15;
   const bool a_live = ar < kLgsRows && grp * kLgsRows + ar < n_rows;
   v4i acc = v4i{0, 0, 0, 0};
 #pragma unroll
@@ -481,22 +525,31 @@ bool ln_gemm_static_supported(int K, int N) {
 
 hipError_t launch_ln_gemm_static(const LnGemmStaticArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
-  if (!ln_gemm_static_supported(a.K, a.N) || !a.y || !a.r || !a.gamma || !a.beta || !a.W ||
+  const bool yp = a.ya != nullptr;
+  if (!ln_gemm_static_supported(a.K, a.N) || (yp ? !(a.Wy && a.ymult && a.ybias) : !a.y) || !a.r ||
+      !a.gamma || !a.beta || !a.W ||
       !a.wmult || !a.bias || (!a.out && !a.out_q) || (a.out && a.ldo < a.N) ||
       (a.out_q && (!a.out_qa || a.ldq < a.N)) || a.part_n < 0 || a.part_n % kLgsCols)
     return hipErrorInvalidValue;
-  for (const float m : {a.xq_mult[0], a.xq_mult[1]})
+  for (const float m : {a.xq_mult[0], a.xq_mult[1], yp ? a.ya_mult : 1.0f})
     if (!(m > 0.0f) || !(m < __builtin_huge_valf())) return hipErrorInvalidValue;
   if (a.out_q && (!(a.qmult > 0.0f) || !(a.qmult < __builtin_huge_valf()))) return hipErrorInvalidValue;
   const int groups = (a.rows + kLgsRows - 1) / kLgsRows;
   if ((int64_t)groups * (a.N / kLgsCols) > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid(groups * (a.N / kLgsCols)), block(64 * kLgsWaves);
-  if (a.K == 256)
-    hipLaunchKernelGGL(k_ln_gemm_static<4>, grid, block, 0, s, a);
-  else if (a.K == 384)
-    hipLaunchKernelGGL(k_ln_gemm_static<6>, grid, block, 0, s, a);
-  else
-    hipLaunchKernelGGL(k_ln_gemm_static<8>, grid, block, 0, s, a);
+#define MH_LG(P)                                                          \
+  if (yp)                                                                 \
+    hipLaunchKernelGGL((k_ln_gemm_static<P, true>), grid, block, 0, s, a); \
+  else                                                                    \
+    hipLaunchKernelGGL((k_ln_gemm_static<P, false>), grid, block, 0, s, a);
+  if (a.K == 256) {
+    MH_LG(4)
+  } else if (a.K == 384) {
+    MH_LG(6)
+  } else {
+    MH_LG(8)
+  }
+#undef MH_LG
   return hipGetLastError();
 }
 
