@@ -426,6 +426,26 @@ __device__ __forceinline__ float fold_row_wave(const float (&v)[PER], float* zr,
   }
 }
 
+// LayerNorm of the row z (lane l holds elements l + 64j) by one wave with
+// normalize_row's sequential folds (tensor.rs:372-385); zr is the wave's LDS
+// row (kLnRow<PER> floats).  Returns the normalized row in o.
+template <int PER>
+__device__ __forceinline__ void ln_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
+                                        const float (&bv)[PER], int lane, float (&o)[PER]) {
+  constexpr int D = PER * 64;
+  const float mean = fold_row_wave<PER>(z, zr, lane) / (float)D;
+  float t[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const float c = z[j] - mean;
+    t[j] = c * c;
+  }
+  const float var = fold_row_wave<PER>(t, zr, lane) / (float)D;
+  const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];
+}
+
 // q = clamp(round_half_even(x * a), -127, 127)  (q8_gemm.rs:584-587)
 __device__ __forceinline__ int quantize_one(float x, float a) {
   float v = rintf(x * a);

@@ -1133,7 +1133,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
     P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
     P.ffn_af = rows <= kFfnAfMaxRows;
-    P.vocab_ln = rows <= kVocabLnMaxRows && vocab_ln_supported(d) && !cand;
+    P.vocab_ln = cand ? cand_ln_supported(d) : rows <= kVocabLnMaxRows && vocab_ln_supported(d);
     return P;
   };
 
@@ -1148,11 +1148,19 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   // the stop rules and the compaction of the active set.  With candidates
   // every row scores its sentence's list (select_token, q8_engine.rs:749-790);
   // without, the whole vocabulary under the generation mask.
-  auto score = [&](int rows, uint32_t t, RowPrologue& pend) -> hipError_t {
+  // A pending LayerNorm (pend.kind == PRO_LN) is built by the scoring kernel
+  // itself and quantized with qmult (> 0: static) or the row's own multiplier.
+  auto score = [&](int rows, uint32_t t, RowPrologue& pend, float qmult = 0.0f) -> hipError_t {
     if (cand) {
       CandArgs c;
       c.xq = DXQ;
       c.xa = DXA;
+      if (pend.kind == PRO_LN) {  // its fp32 output is not needed
+        c.pro = pend;
+        c.pro.out = nullptr;
+        c.qmult = qmult;
+        pend.kind = PRO_NONE;
+      }
       c.M = rows;
       c.K = d;
       c.V = (int)E->V;
@@ -1693,8 +1701,19 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
         MH_TRY(dgemm(L.w1, DXQ, DXA, nullptr, F, 1, DHQ, DHA, L.a2));
       }
       MH_TRY(dgemm(L.w2, DHQ, DHA, DY, d, 0));
-      // The next layer's SSRU projections build this LayerNorm themselves.
+      // The next layer's SSRU projections build this LayerNorm themselves, and
+      // so does the candidate scoring after the last layer.
       if ((ssru_blk || ssru_lnf) && l + 1 < E->Ld) continue;
+      if (l + 1 == E->Ld && cand && cand_ln_supported(d)) {
+        RowPrologue pend;
+        pend.kind = PRO_LN;
+        pend.y = DY;
+        pend.r = xres;
+        pend.gamma = L.ln2_s;
+        pend.beta = L.ln2_b;
+        pend.err = E->err_flag;
+        return score(rows, t, pend, E->out_act);
+      }
       // quantized for what reads it next: the next layer's SSRU inputs (when
       // they share a multiplier) or the output scoring
       const SGroup* nx = l + 1 < E->Ld ? &E->sdec[l + 1].uf : nullptr;

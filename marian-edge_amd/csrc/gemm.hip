@@ -60,12 +60,6 @@ __device__ __forceinline__ v4i quantize_frag16(const float4 (&f)[4], float a) {
            ((quantize_one(f[w].z, a) & 0xFF) << 16) | ((quantize_one(f[w].w, a) & 0xFF) << 24);
   return r;
 }
-__device__ __forceinline__ v4i quantize_frag16(const float* x, float a) {
-  float4 f[4];
-#pragma unroll
-  for (int w = 0; w < 4; ++w) f[w] = *(const float4*)(x + 4 * w);
-  return quantize_frag16(f, a);
-}
 constexpr int kAfRows = 16;  // fp32 A source: one MFMA row tile per workgroup
 
 // A sources of the skinny kernel: int8 rows with their multipliers, or fp32
@@ -732,22 +726,42 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e, int t
 // ---------------------------------------------------------------------------
 constexpr int kCandChunk = 128;
 constexpr int kCandKs = 8;  // k-steps requested together (K <= 512: all of them)
+// LNP > 0: the row is LayerNorm(pro.y + pro.r) of width 64 LNP, built by wave
+// 0 while the candidates' embedding rows are in flight, and quantized with
+// c.qmult (> 0, static) or its own multiplier.
+template <int LNP>
 __global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
   __shared__ uint64_t sKey[4];
+  __shared__ __attribute__((aligned(16))) float sZ[LNP ? kLnRow<LNP> : 1];
+  __shared__ __attribute__((aligned(16))) int8_t sX[LNP ? 64 * LNP : 16];
+  __shared__ float sA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = blockIdx.y, chunk = blockIdx.x;
   const int ksteps = c.K >> 6, kq = (lane >> 4) * 16;
   // The first k-steps are requested before the device row count is known
   // (rows below the host bound are backed by memory; a finished row's list is
   // another sequence's, still in bounds), all of them at once.
+  float ly[LNP ? LNP : 1], lr[LNP ? LNP : 1], lg[LNP ? LNP : 1], lb[LNP ? LNP : 1];
+  if constexpr (LNP > 0) {
+    if (wave == 0) {
+#pragma unroll
+      for (int j = 0; j < LNP; ++j) {
+        const int e = lane + 64 * j;
+        ly[j] = c.pro.y[(int64_t)m * c.K + e];
+        lr[j] = c.pro.r[(int64_t)m * c.K + e];
+        lg[j] = c.pro.gamma[e];
+        lb[j] = c.pro.beta[e];
+      }
+    }
+  }
   const int b = c.row_slot ? c.row_slot[m] : m;
   const int64_t c0 = c.off[b], n = (int64_t)c.off[b + 1] - c0;
   if ((int64_t)chunk * kCandChunk >= n) {  // past the row's list (the grid fits the longest)
     if (tid == 0 && !(c.rows_dev && m >= *c.rows_dev)) c.partials[(int64_t)m * c.nparts + chunk] = 0;
     return;
   }
-  const int8_t* xr = c.xq + (int64_t)m * c.K + kq;
-  const float am = c.xa[m];
+  const int8_t* xr = LNP ? nullptr : c.xq + (int64_t)m * c.K + kq;
+  float am = LNP ? 0.0f : c.xa[m];
   bool live[2], bad = false;
   uint32_t id[2];
   const int8_t* er[2];
@@ -771,13 +785,37 @@ __global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
 #pragma unroll
     for (int s = 0; s < kCandKs; ++s) {
       const int64_t o = 64 * min(s0 + s, ksteps - 1);
-      xa[s] = *(const v4i*)(xr + o);
+      if (!LNP) xa[s] = *(const v4i*)(xr + o);
       bw[0][s] = *(const v4i*)(er[0] + o);
       bw[1][s] = *(const v4i*)(er[1] + o);
     }
   };
   load(0);
   if (c.rows_dev && m >= *c.rows_dev) return;  // uniform per workgroup
+  if constexpr (LNP > 0) {
+    if (wave == 0) {
+      float z[LNP], o[LNP];
+#pragma unroll
+      for (int j = 0; j < LNP; ++j) z[j] = ly[j] + lr[j];
+      ln_wave<LNP>(z, sZ, lg, lb, lane, o);
+      float mx = 0.0f;
+      bool nf = false;
+#pragma unroll
+      for (int j = 0; j < LNP; ++j) {
+        nf |= !isfinite(o[j]);
+        mx = fmaxf(mx, fabsf(o[j]));
+      }
+      const float sc = c.qmult > 0.0f ? c.qmult : row_multiplier(wave_max(mx));
+#pragma unroll
+      for (int j = 0; j < LNP; ++j) sX[lane + 64 * j] = (int8_t)quantize_one(o[j], sc);
+      if (lane == 0) sA = sc;
+      if (__any(nf) && lane == 0 && c.err) *c.err = 1;
+    }
+    wg_lds_barrier();
+    am = sA;
+#pragma unroll
+    for (int s = 0; s < kCandKs; ++s) xa[s] = *(const v4i*)(sX + 64 * min(s, ksteps - 1) + kq);
+  }
   v4i acc[2] = {zero4(), zero4()};
   for (int s0 = 0; s0 < ksteps; s0 += kCandKs) {
     if (s0 > 0) load(s0);
@@ -815,10 +853,25 @@ hipError_t launch_cand_argmax(const CandArgs& c, hipStream_t s) {
     return hipErrorInvalidValue;
   const int chunks = cand_groups(c.max_cands);
   if (c.nparts < chunks) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_cand_argmax, dim3(chunks, c.M), dim3(256), 0, s, c);
+  const dim3 grid(chunks, c.M), block(256);
+  if (c.pro.kind == PRO_LN) {
+    if (!cand_ln_supported(c.K) || !c.pro.y || !c.pro.r || !c.pro.gamma || !c.pro.beta ||
+        !(c.qmult >= 0.0f) || !(c.qmult < __builtin_huge_valf()))
+      return hipErrorInvalidValue;
+    if (c.K == 256)
+      hipLaunchKernelGGL(k_cand_argmax<4>, grid, block, 0, s, c);
+    else if (c.K == 384)
+      hipLaunchKernelGGL(k_cand_argmax<6>, grid, block, 0, s, c);
+    else
+      hipLaunchKernelGGL(k_cand_argmax<8>, grid, block, 0, s, c);
+  } else {
+    if (!c.xq || !c.xa) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_cand_argmax<0>, grid, block, 0, s, c);
+  }
   return hipGetLastError();
 }
 int cand_groups(int max_cands) { return (max_cands + kCandChunk - 1) / kCandChunk; }
+bool cand_ln_supported(int K) { return K == 256 || K == 384 || K == 512; }
 
 // Columns per skinny workgroup: wide enough that the vocabulary projection
 // does not re-read the activations too often, narrow enough that the small

@@ -425,8 +425,14 @@ struct CandArgs {
   int nparts = 0;
   float* logits = nullptr;
   int* err = nullptr;
+  // pro.kind == PRO_LN (K = 256, 384 or 512): the rows are LayerNorm(pro.y +
+  // pro.r), built in the kernel and quantized with qmult (> 0, static) or each
+  // row's own multiplier (0); xq / xa are not read.
+  RowPrologue pro;
+  float qmult = 0.0f;
 };
 int cand_groups(int max_cands);
+bool cand_ln_supported(int K);
 hipError_t launch_cand_argmax(const CandArgs& c, hipStream_t s);
 
 // Reduces argmax partials to token ids (op-level argmax).

@@ -37,26 +37,6 @@ constexpr int kSbLoaders = kSbThreads - 64;  // waves 1-3 stage keys and values
 
 __constant__ uint64_t kSbExp2Tab[32] = {MH_EXP2_TABLE_32};
 
-// LayerNorm of the row z (lane l holds elements l + 64j) by one wave with
-// normalize_row's sequential folds (tensor.rs:372-385); zr is the wave's LDS
-// row (kLnRow<PER> floats).  Returns the normalized row in o.
-template <int PER>
-__device__ __forceinline__ void ln_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
-                                        const float (&bv)[PER], int lane, float (&o)[PER]) {
-  constexpr int D = PER * 64;
-  const float mean = fold_row_wave<PER>(z, zr, lane) / (float)D;
-  float t[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const float c = z[j] - mean;
-    t[j] = c * c;
-  }
-  const float var = fold_row_wave<PER>(t, zr, lane) / (float)D;
-  const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
-#pragma unroll
-  for (int j = 0; j < PER; ++j) o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];
-}
-
 // ---------------------------------------------------------------------------
 // SSRU LayerNorm + query projection + cross-attention, one 256-thread
 // workgroup per (row, head).  Wave 0 loads z and normalizes it; waves 1-3
