@@ -918,6 +918,9 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
   if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1, A_I8>(g, e, s);
   if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2, A_I8>(g, e, s);
   if (ksteps <= 16) return launch_skinny_k<MODE, 4, 4, A_I8>(g, e, s);
+  // K = 1536 (the FFN down-projection of a 1536-wide FFN): 16 waves of two
+  // k-steps beat 8 of four (measured); K = 2048 the other way round.
+  if (ksteps <= 24) return launch_skinny_k<MODE, 16, 2, A_I8>(g, e, s);
   return launch_skinny_k<MODE, 8, 4, A_I8>(g, e, s);
 }
 
