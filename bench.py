@@ -13,7 +13,9 @@ head projection + attention, four launches per decode step), the roofline of
 the vocabulary projection + fused argmax (the decode GEMM with the largest
 weight stream), both timed with HIP events that each launch's own dispatch
 records on the engine's stream during the timed steps, and the CPU baseline
-(the oracle's reference-schedule port, timed on this host's cores).
+(the oracle's reference-schedule port, timed on this host's cores).  For
+information, `reference_ssru` gives the same batch through the reference's
+own graph (`--workload reference-ssru` prints its full line).
 """
 
 from __future__ import annotations
@@ -314,6 +316,11 @@ def ssru_cpu_baseline(model, batch, cand, coff, cores: int):
 
 
 def ssru_bench(pkg, args):
+    print(json.dumps(ssru_line(pkg, args)), flush=True)
+    return 0
+
+
+def ssru_line(pkg, args):
     """The reference's own graph (Transformer encoder + 4 SSRU decoder layers,
     d = 384 with 8 heads of 48, FFN 1536, 32000-id vocabularies, static
     per-tensor multipliers; seeded random weights) on the same 64-sentence
@@ -383,8 +390,7 @@ def ssru_bench(pkg, args):
         line["cpu_baseline"] = cpu
         line["speedup_vs_cpu"] = round(line["value"] / cpu["value"], 1)
     eng.close()
-    print(json.dumps(line), flush=True)
-    return 0
+    return line
 
 
 def main(argv=None):
@@ -395,6 +401,8 @@ def main(argv=None):
     ap.add_argument("--workload", choices=["ragged", "stress", "single", "reference-ssru"],
                     default="ragged")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference-ssru", action="store_true",
+                    help="skip the informational Transformer-SSRU run on the default workload")
     ap.add_argument("--cpu-cores", type=int, default=min(16, os.cpu_count() or 4))
     args = ap.parse_args(argv)
 
@@ -497,6 +505,17 @@ def main(argv=None):
     }
     if cpu:
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    if args.workload == "ragged" and not args.no_reference_ssru:
+        # The reference's own graph on the same batch, for information.
+        sr = ssru_line(pkg, args)
+        line["reference_ssru"] = {
+            "metric": sr["metric"], "value": sr["value"], "unit": sr["unit"],
+            "ms_per_step": sr["ms_per_step"], "config": sr["config"],
+            "full_vocabulary": sr["full_vocabulary"],
+            "cpu_baseline": ({"value": sr["cpu_baseline"]["value"], "unit": "tokens/s",
+                              "cores": sr["cpu_baseline"]["cores"], "kind": "port",
+                              "sample": sr["cpu_baseline"]["sample"]} if "cpu_baseline" in sr else None),
+        }
     print(json.dumps(line), flush=True)
     return 0
 
