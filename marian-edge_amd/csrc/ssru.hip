@@ -191,34 +191,37 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   // hold +0.0, which leaves the non-negative sum unchanged), 16 at a time.
   const float inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, (nk + 15) >> 4, 0.0f);
   // out_d = sum_j v[j][d] * (e_j * inv) in key order from 0.0; lane = d.
-  // Eight keys per batch, the next batch read before this one is added; keys
-  // past the last have e = +0.0 and finite value rows, so their +-0.0
-  // products leave the sum unchanged.
+  // Sixteen keys per batch in two alternating register sets: the next batch
+  // is read while this one is added.  Keys past the last have e = +0.0 and
+  // finite value rows, so their +-0.0 products leave the sum unchanged.
+  constexpr int PB = 16;
   const int dl = min(lane, DH - 1);
   const float* vc = sV + dl;
-  const int nb = (nk + 7) >> 3;
+  const int nb = (nk + PB - 1) / PB;
   float o = 0.0f;
-  f4v pa[2], pb[2];
-  float va[8], vb[8];
-  pa[0] = *(const f4v*)(sP);
-  pa[1] = *(const f4v*)(sP + 4);
+  f4v pA[PB / 4], pB[PB / 4];
+  float vA[PB], vB[PB];
+  auto read = [&](int b, f4v (&p)[PB / 4], float (&v)[PB]) {
 #pragma unroll
-  for (int u = 0; u < 8; ++u) va[u] = vc[u * KR];
+    for (int i = 0; i < PB / 4; ++i) p[i] = *(const f4v*)(sP + PB * b + 4 * i);
+#pragma unroll
+    for (int u = 0; u < PB; ++u) v[u] = vc[(PB * b + u) * KR];
+  };
+  auto add = [&](const f4v (&p)[PB / 4], const float (&v)[PB]) {
+#pragma unroll
+    for (int u = 0; u < PB; ++u) o = o + v[u] * (p[u / 4][u % 4] * inv);
+  };
+  read(0, pA, vA);
 #pragma unroll 1
-  for (int b = 0; b < nb; ++b) {
-    const int bn = min(b + 1, nb - 1);  // past the last batch: re-read it, unused
-    pb[0] = *(const f4v*)(sP + 8 * bn);
-    pb[1] = *(const f4v*)(sP + 8 * bn + 4);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) vb[u] = vc[(8 * bn + u) * KR];
+  for (int b = 0;;) {
+    read(min(b + 1, nb - 1), pB, vB);  // past the last batch: re-read it, unused
     __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the adds
-    const float pr[8] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w};
-#pragma unroll
-    for (int u = 0; u < 8; ++u) o = o + va[u] * (pr[u] * inv);
-    pa[0] = pb[0];
-    pa[1] = pb[1];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) va[u] = vb[u];
+    add(pA, vA);
+    if (++b >= nb) break;
+    read(min(b + 1, nb - 1), pA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    add(pB, vB);
+    if (++b >= nb) break;
   }
 
   if (lane < DH) a.qout[(int64_t)r * a.ldqout + h * DH + lane] = (int8_t)quantize_one(o, a.qmult);
