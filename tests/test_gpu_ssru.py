@@ -111,6 +111,22 @@ def test_ssru_long_sentences_token_exact(pkg, orc):
         assert e.is_ready()
 
 
+def test_ssru_many_rows_token_exact(pkg, orc, sl):
+    """200 sentences: the fused SSRU kernels over 25 row groups and 800
+    (row, head) workgroups, with the active set shrinking step by step."""
+    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=1, decoder_layers=2,
+                         dim=256, heads=4, ffn_dim=1024)
+    model = pkg.seeded_ssru_model(seed=43, geometry=g, std=0.05)
+    om = orc.OracleSsruModel(model)
+    b = pkg.ragged_batch(seed=31, n=200, vocab=g.source_vocab)
+    cand, coff, _ = shortlist_lists(sl, b.tokens, b.offsets, g.source_vocab, g.target_vocab)
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        for name, c, co in (("full vocabulary", None, None), ("shortlist", cand, coff)):
+            got, want = run_both(pkg, orc, e, om, b, 0, c, co)
+            print(f"200 rows, {name}: {sum(map(len, got))} tokens", flush=True)
+            assert got == want
+
+
 def test_ssru_reference_shape_ragged_64(pkg, orc, sl):
     """The reference's supported shape at full size (32000-id vocabularies,
     6 encoder / 4 SSRU decoder layers) on the 64-sentence ragged batch, with
