@@ -335,11 +335,35 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     }
   }
 
+  // Weight fragments for the wave's columns over all of K, issued first.
+  v4i bf[kVocabCT][kVocabMaxK / 64];
+  int ncol[kVocabCT];
+#pragma unroll
+  for (int ct = 0; ct < kVocabCT; ++ct) {
+    ncol[ct] = nbase + ct * 16 + (lane & 15);
+    const int tile = min((nbase >> 4) + ct, ((g.N + 15) >> 4) - 1);
+    const int8_t* wb = g.Wf ? g.Wf + ((int64_t)tile * ksteps * 64 + lane) * 16
+                            : g.W + (int64_t)min(ncol[ct], g.N - 1) * g.K + kq;
+    const int wstep = g.Wf ? 1024 : 64;  // fragment order: 1 KB per k-step
+#pragma unroll
+    for (int s = 0; s < kVocabMaxK / 64; ++s) {
+      const v4i v = *(const v4i*)(wb + (int64_t)min(s, ksteps - 1) * wstep);
+      bf[ct][s] = FULL || s < ksteps ? v : zero4();
+    }
+  }
+  // Epilogue operands of this lane's columns.
+  float wm[kVocabCT], bi[kVocabCT];
+  bool live[kVocabCT];
+#pragma unroll
+  for (int ct = 0; ct < kVocabCT; ++ct) {
+    const int n = min(ncol[ct], g.N - 1);
+    wm[ct] = g.wmult[n];
+    bi[ct] = g.bias[n];
+    live[ct] = ncol[ct] < g.N && ((e.flags & 2u) || !generation_masked((uint32_t)ncol[ct]));
+  }
   // Activation rows of a 64-row chunk: thread t holds 16-byte pieces
-  // t + 256 j (row = piece / 32, piece % 32 < K / 16), all requested at once,
-  // before the weights: loads complete in issue order, so rows requested
-  // after the weights could only be used once every weight had arrived.  The
-  // first chunk is requested for the rows below the host bound g.M (all
+  // t + 256 j (row = piece / 32, piece % 32 < K / 16), all requested at once.
+  // The first chunk is requested for the rows below the host bound g.M (all
   // allocated) before the device row count arrives.
   constexpr int kStage = kSkinnyRows * (kVocabMaxK / 16) / 256;
   const int cpr = g.K >> 4;
@@ -354,37 +378,6 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
                                          : zero4();
     }
     if (tid < rows_h) sa = g.a[tid];
-  }
-  // Weight fragments for the wave's columns over all of K, in k-step order
-  // (the order the matrix cores consume them, so each k-step waits only for
-  // its own fragments).
-  v4i bf[kVocabCT][kVocabMaxK / 64];
-  int ncol[kVocabCT];
-  const int8_t* wb[kVocabCT];
-  const int wstep = g.Wf ? 1024 : 64;  // fragment order: 1 KB per k-step
-#pragma unroll
-  for (int ct = 0; ct < kVocabCT; ++ct) {
-    ncol[ct] = nbase + ct * 16 + (lane & 15);
-    const int tile = min((nbase >> 4) + ct, ((g.N + 15) >> 4) - 1);
-    wb[ct] = g.Wf ? g.Wf + ((int64_t)tile * ksteps * 64 + lane) * 16
-                  : g.W + (int64_t)min(ncol[ct], g.N - 1) * g.K + kq;
-  }
-#pragma unroll
-  for (int s = 0; s < kVocabMaxK / 64; ++s)
-#pragma unroll
-    for (int ct = 0; ct < kVocabCT; ++ct) {
-      const v4i v = *(const v4i*)(wb[ct] + (int64_t)min(s, ksteps - 1) * wstep);
-      bf[ct][s] = FULL || s < ksteps ? v : zero4();
-    }
-  // Epilogue operands of this lane's columns.
-  float wm[kVocabCT], bi[kVocabCT];
-  bool live[kVocabCT];
-#pragma unroll
-  for (int ct = 0; ct < kVocabCT; ++ct) {
-    const int n = min(ncol[ct], g.N - 1);
-    wm[ct] = g.wmult[n];
-    bi[ct] = g.bias[n];
-    live[ct] = ncol[ct] < g.N && ((e.flags & 2u) || !generation_masked((uint32_t)ncol[ct]));
   }
   const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
   if constexpr (LNP) {
@@ -428,20 +421,9 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     }
   }
 
-  // The first chunk goes to LDS here, outside the chunk loop: a later
-  // chunk's rows are requested after every weight, and a store shared with
-  // that path would wait for all outstanding loads.
-  if constexpr (!LNP) {
-#pragma unroll
-    for (int j = 0; j < kStage; ++j) {
-      const int c = tid + 256 * j;
-      *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
-    }
-    if (tid < kSkinnyRows) sAm[tid] = sa;
-  }
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
-    if (!LNP && m0 > 0) {
+    if (m0 > 0) {
 #pragma unroll
       for (int j = 0; j < kStage; ++j) {
         const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
@@ -450,6 +432,8 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
                     : zero4();
       }
       sa = tid < rows ? g.a[m0 + tid] : 0.0f;
+    }
+    if constexpr (!LNP) {
 #pragma unroll
       for (int j = 0; j < kStage; ++j) {
         const int c = tid + 256 * j;
