@@ -223,16 +223,9 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   __shared__ float sS[64];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  int h, r;  // r < b.rows (host bound)
-  if (b.row_local) {  // id = 8 * (8 * row block + head) + XCD; row = 8 * row block + XCD
-    const int slot = blockIdx.x >> 3;
-    h = slot % b.heads;
-    r = (slot / b.heads) * 8 + (blockIdx.x & 7);
-    if (r >= b.rows) return;  // padding of the grid: the whole workgroup, before any barrier
-  } else {
-    h = blockIdx.x % b.heads;
-    r = blockIdx.x / b.heads;
-  }
+  // Row-major ids: workgroups are dealt to the 8 XCDs in turn, so head h of
+  // every row runs on XCD h and each XCD reads one head's weights.
+  const int h = blockIdx.x % b.heads, r = blockIdx.x / b.heads;  // r < b.rows (host bound)
   const int n = b.rows_dev ? *b.rows_dev : b.rows;
   const int step = b.step;
   // Key range of this row (read before the device row count is known; rows
@@ -554,7 +547,7 @@ hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s, hipEvent_t ev_st
                            b.step >= 0 && b.step < kMaxPosition))
     return hipErrorInvalidValue;
   if (b.mode == ATT_CROSS && p.kind != PRO_LN) return hipErrorInvalidValue;
-  const dim3 grid((b.row_local ? (b.rows + 7) / 8 * 8 : b.rows) * b.heads), block(kBlkThreads);
+  const dim3 grid(b.rows * b.heads), block(kBlkThreads);
   auto kern = b.mode == ATT_CROSS ? k_attn_block<ATT_CROSS, PRO_LN>
                : p.kind == PRO_LN  ? k_attn_block<ATT_SELF, PRO_LN>
                                    : k_attn_block<ATT_SELF, PRO_EMB>;

@@ -1115,7 +1115,6 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   constexpr int kBlkMaxRows = 64;  // steps up to this many rows use attention blocks
   constexpr int kLnFfnMaxRows = 32;  // ... and the LayerNorm + FFN up-projection block
   constexpr int kFfnAfMaxRows = 8;   // ... and the FFN down-projection quantizing its fp32 rows
-  constexpr int kRowLocalMaxRows = 8;  // ... and attention blocks with a row's heads on one XCD
 
   // What one decode step launches is decided on the host: the row bound
   // (grid sizes; rows at or past the device row count exit early), the path
@@ -1331,7 +1330,6 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       ba.ldo = d;
       ba.amax = DAMAX;
       ba.err = E->err_flag;
-      ba.row_local = rows <= kRowLocalMaxRows;
       return launch_attn_block(ba, s, ev[0], ev[1]);
     };
     if (P.blk_self) {

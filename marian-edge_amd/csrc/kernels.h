@@ -345,13 +345,6 @@ struct BlockArgs {
   int64_t ldo = 0;
   float* amax = nullptr;  // [rows, heads]
   int* err = nullptr;
-  // Workgroup placement.  Workgroups are dealt to the 8 XCDs in turn, so by
-  // default (row-major ids) head h runs on XCD h for every row and each XCD
-  // fetches every row's inputs.  row_local puts all heads of a row on one
-  // XCD (the grid is padded to a multiple of 64 workgroups), so the row's
-  // inputs are fetched once; the heads' weights then reach every XCD that
-  // holds a row, which is cheaper only for few rows.
-  int row_local = 0;
 };
 bool attn_block_supported(int d, int heads, int max_keys);
 
