@@ -20,7 +20,7 @@ CSRC = PKG / "csrc"
 INCLUDE = PKG.parent / "include"
 BUILD_DIR = PKG / "_build"
 LIB = PKG / "libmarian_hip.so"
-SOURCES = ["gemm.hip", "attention.hip", "block.hip", "rows.hip", "ssru.hip", "engine.hip", "ops.hip"]
+SOURCES = ["gemm.hip", "attention.hip", "block.hip", "rows.hip", "ssru.hip", "lngemm.hip", "engine.hip", "ops.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

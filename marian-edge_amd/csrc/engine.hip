@@ -1121,7 +1121,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   // of each attention sublayer and the key bounds that pick kernel variants.
   struct StepPlan {
     int rows, self_keys, cross_keys;
-    bool blk_self, blk_cross, ln_ffn, ffn_af, vocab_ln;
+    bool blk_self, blk_cross, ln_ffn, ln_rows, ffn_af, vocab_ln;
   };
   auto make_plan = [&](int rows, int self_keys, int cross_keys) {
     StepPlan P;
@@ -1131,6 +1131,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     P.blk_self = rows <= kBlkMaxRows && attn_block_supported(d, H, self_keys);
     P.blk_cross = rows <= kBlkMaxRows && attn_block_supported(d, H, cross_keys);
     P.ln_ffn = rows <= kLnFfnMaxRows && ln_gemm_block_supported(d, F);
+    P.ln_rows = !P.ln_ffn && ln_gemm_rows_supported(d, F);
     P.ffn_af = rows <= kFfnAfMaxRows;
     P.vocab_ln = cand ? cand_ln_supported(d) : rows <= kVocabLnMaxRows && vocab_ln_supported(d);
     return P;
@@ -1430,8 +1431,30 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       }
       MH_TRY(agemm(L.cross_out, store_epi(DY, d, 0)));
       // ---- feed-forward; its LayerNorm inside the up-projection block ----
-      MH_TRY(layer_norm(DY, L.ln2_s, L.ln2_b, P.ln_ffn));
-      if (P.ln_ffn) {
+      MH_TRY(layer_norm(DY, L.ln2_s, L.ln2_b, P.ln_ffn || P.ln_rows));
+      if (P.ln_rows) {  // more rows: eight rows per workgroup
+        LnGemmRowsArgs lg;
+        lg.y = pend.y;
+        lg.r = pend.r;
+        lg.gamma = pend.gamma;
+        lg.beta = pend.beta;
+        lg.x_out = pend.out;
+        pend.kind = PRO_NONE;
+        lg.rows = rows;
+        lg.rows_dev = d_nact;
+        lg.dyn = 1;
+        lg.part_n = F;
+        lg.W = L.ffn1.wf;
+        lg.wmult = L.ffn1.mult;
+        lg.bias = L.ffn1.bias;
+        lg.K = L.ffn1.K;
+        lg.N = L.ffn1.N;
+        lg.relu = 1;
+        lg.out = DH;
+        lg.ldo = F;
+        lg.err = E->err_flag;
+        MH_TRY(launch_ln_gemm_rows(lg, s));
+      } else if (P.ln_ffn) {
         LnGemmArgs lg;
         lg.pro = pend;
         pend.kind = PRO_NONE;
@@ -1481,9 +1504,9 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   // the decoder input, then per layer the SSRU sublayer (W and Wf on the
   // layer input, gate, state update and LayerNorm), cross-attention over the
   // row's sentence and the FFN, every dense layer's input quantized with that
-  // layer's static multiplier.  No fused blocks: the generic kernels.
+  // layer's static multiplier.
   const bool ssru_blk = E->ssru && ssru_block_supported(d, H, (int)Lmax);
-  const bool ssru_lnf = E->ssru && ln_gemm_static_supported(d, F) && ln_gemm_static_supported(d, 2 * d);
+  const bool ssru_lnf = E->ssru && ln_gemm_rows_supported(d, F) && ln_gemm_rows_supported(d, 2 * d);
   auto emit_step_ssru = [&](int rows, uint32_t t) -> hipError_t {
     float* xres = DX0;
     float* xalt = DX1;
@@ -1541,7 +1564,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     auto ln_gemm = [&](const float* y, const float* ln_s, const float* ln_b, const Lin& W, float a0,
                        float a1, int part_n, int relu, float* out, int8_t* q, float* qa,
                        float qmult, const Lin* Wy = nullptr, float ya_mult = 0.0f) {
-      LnGemmStaticArgs lg;
+      LnGemmRowsArgs lg;
       lg.y = y;
       if (!y) {
         lg.ya = DXQ;
@@ -1572,7 +1595,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
       lg.qmult = qmult;
       lg.out_qa = qa;
       lg.err = E->err_flag;
-      const hipError_t rc = launch_ln_gemm_static(lg, s);
+      const hipError_t rc = launch_ln_gemm_rows(lg, s);
       std::swap(xres, xalt);
       return rc;
     };

@@ -201,15 +201,16 @@ struct SsruBlockArgs {
 };
 constexpr int kSsruBlockMaxKeys = 128;
 
-// Residual LayerNorm + static-multiplier Q8 linear (Transformer-SSRU graph):
-// out[m] = (relu of) Q8Linear(LN(y[m] + r[m])) with the row quantized by
-// xq_mult[0] for output columns below part_n and xq_mult[1] from it (a row
-// group of two layers with their own multipliers; part_n = N: one).
+// Residual LayerNorm + Q8 linear for groups of eight rows: out[m] = (relu of)
+// Q8Linear(LN(y[m] + r[m])) with the row quantized by xq_mult[0] for output
+// columns below part_n and xq_mult[1] from it (a row group of two layers with
+// their own static multipliers; part_n = N: one), or with each row's own
+// multiplier when dyn is set (xq_mult unused).
 // Optional outputs: fp32 `out`, and/or `out_q` quantized with qmult (the next
 // layer's static multiplier, out_qa[m] = qmult); x_out receives the
 // LayerNorm rows.  Eight rows and 128 output columns per workgroup;
 // K = 256, 384 or 512, N a multiple of 128.
-struct LnGemmStaticArgs {
+struct LnGemmRowsArgs {
   const float* y = nullptr;  // [rows, K], or computed from ya:
   // y = the static Q8 linear of the int8 rows ya [rows, K] with multiplier
   // ya_mult and Wy [K, K] in fragment order (ymult, ybias): the attention
@@ -227,6 +228,7 @@ struct LnGemmStaticArgs {
   float* x_out = nullptr;  // optional [rows, K]
   float xq_mult[2] = {0.0f, 0.0f};
   int part_n = 0;
+  int dyn = 0;
   const int8_t* W = nullptr;  // [N, K] in fragment order (frag_load)
   const float* wmult = nullptr;
   const float* bias = nullptr;
@@ -240,8 +242,8 @@ struct LnGemmStaticArgs {
   float* out_qa = nullptr;
   int* err = nullptr;
 };
-bool ln_gemm_static_supported(int K, int N);
-hipError_t launch_ln_gemm_static(const LnGemmStaticArgs& a, hipStream_t s);
+bool ln_gemm_rows_supported(int K, int N);
+hipError_t launch_ln_gemm_rows(const LnGemmRowsArgs& a, hipStream_t s);
 bool ssru_block_supported(int d, int heads, int max_keys);
 hipError_t launch_ssru_block(const SsruBlockArgs& a, hipStream_t s);
 

@@ -10,8 +10,8 @@
 //                     query projection and the cross-attention over the row's
 //                     sentence, quantized for the output projection;
 //   (output projection: the skinny GEMM)
-//   k_ln_gemm_static  the context block's residual LayerNorm and the FFN
-//                     up-projection (also used for any LayerNorm + linear);
+//   k_ln_gemm_rows    (lngemm.hip) the output projection, the context
+//                     block's residual LayerNorm and the FFN up-projection;
 //   (FFN down-projection: the skinny GEMM).
 //
 // Every value is produced by the same operations, in the same order, as the
@@ -363,178 +363,7 @@ __global__ __launch_bounds__(512) void k_ssru_input(SsruInputArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Residual LayerNorm + static-multiplier Q8 linear: out = (relu of)
-// Q8Linear(LN(y + r)) for kLgsRows rows and kLgsCols output columns per
-// workgroup.  Wave w builds row w of the group (LayerNorm as
-// launch_residual_ln), quantizes it with the activation multiplier of the
-// column block it feeds (xq_mult[0] below part_n, xq_mult[1] from it: the
-// two parts of a row-block group with their own multipliers) into LDS, then
-// runs the MFMA chain of column tile w over the group's rows.  Slice-0
-// workgroups also store the LayerNorm rows (the next residual).
-// ---------------------------------------------------------------------------
-constexpr int kLgsRows = 8;
-constexpr int kLgsWaves = 8;
-constexpr int kLgsCols = 16 * kLgsWaves;
-
-// YP: y is not read but computed here, the static Q8 linear of the int8 rows
-// a.ya with Wy (the attention-output projection): wave w takes its column
-// tiles w, w + 8, ... over the group's rows, and the rows meet in LDS.
-template <int PER, bool YP>
-__global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_static(LnGemmStaticArgs a) {
-  constexpr int D = PER * 64;
-  constexpr int KS = D / 64;
-  constexpr int YT = YP ? D / 16 / kLgsWaves : 1;  // y tiles per wave
-  __shared__ __attribute__((aligned(16))) float sZ[kLgsWaves][kLnRow<PER>];
-  __shared__ __attribute__((aligned(16))) int8_t sX[kLgsRows][D];
-  __shared__ __attribute__((aligned(16))) float sY[YP ? kLgsRows : 1][YP ? D : 1];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int slices = a.N / kLgsCols;
-  const int slice = blockIdx.x % slices, grp = blockIdx.x / slices;
-  const int r = grp * kLgsRows + wave;  // this wave's row
-  const int n0 = slice * kLgsCols;
-  const float am = n0 < a.part_n ? a.xq_mult[0] : a.xq_mult[1];
-  const int ar = lane & 15;  // MFMA A-operand row of this lane
-  // Row loads (rows below the host bound are backed by memory).
-  float yv[PER], rv[PER], gv[PER], bv[PER];
-  const bool row_mem = r < a.rows;
-  if (row_mem) {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = lane + 64 * j;
-      if (!YP) yv[j] = a.y[(int64_t)r * D + e];
-      rv[j] = a.r[(int64_t)r * D + e];
-      gv[j] = a.gamma[e];
-      bv[j] = a.beta[e];
-    }
-  }
-  // YP: the group's int8 rows (A fragments) and this wave's Wy tiles.
-  v4i ya[YP ? KS : 1], by[YT][YP ? KS : 1];
-  float ym[YT], yb[YT];
-  if constexpr (YP) {
-    const int m = min(grp * kLgsRows + (ar & (kLgsRows - 1)), a.rows - 1);
-#pragma unroll
-    for (int s = 0; s < KS; ++s) ya[s] = *(const v4i*)(a.ya + (int64_t)m * D + 64 * s + (lane >> 4) * 16);
-#pragma unroll
-    for (int i = 0; i < YT; ++i) {
-      const int t = wave + kLgsWaves * i;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) by[i][s] = frag_load(a.Wy, t, KS, s, lane);
-      ym[i] = a.ymult[16 * t + ar];
-      yb[i] = a.ybias[16 * t + ar];
-    }
-  }
-  // Tile `wave` of this slice: weight fragments, dequantization operands.
-  const int col = n0 + 16 * wave + (lane & 15);
-  v4i bf[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) bf[s] = frag_load(a.W, (n0 >> 4) + wave, KS, s, lane);
-  const float wm = a.wmult[col], wb = a.bias[col];
-  const int n_rows = a.rows_dev ? min(*a.rows_dev, a.rows) : a.rows;
-  if (grp * kLgsRows >= n_rows) return;  // the whole workgroup alike
-  const bool live = r < n_rows;
-  if constexpr (YP) {
-    // y rows 0..7 = the group's rows (zero past the device count); lane l
-    // ends with rows 4(l/16)+i of column l%16 of each tile.
-    const bool y_live = ar < kLgsRows && grp * kLgsRows + ar < n_rows;
-#pragma unroll
-    for (int i = 0; i < YT; ++i) {
-      v4i acc = v4i{0, 0, 0, 0};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(y_live ? ya[s] : v4i{0, 0, 0, 0}, by[i][s], acc, 0, 0, 0);
-      if (lane < 32) {
-        const float inv = dequant_scale(a.ya_mult, ym[i]);
-        const int t = wave + kLgsWaves * i;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) sY[4 * (lane >> 4) + k][16 * t + ar] = dequant_apply(acc[k], inv, yb[i]);
-      }
-    }
-    wg_lds_barrier();
-    if (live) {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) yv[j] = sY[wave][lane + 64 * j];
-    }
-  }
-  if (live) {
-    float z[PER], o[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) z[j] = yv[j] + rv[j];
-    ln_wave<PER>(z, sZ[wave], gv, bv, lane, o);
-    bool bad = false;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = lane + 64 * j;
-      bad |= !isfinite(o[j]);
-      if (slice == 0 && a.x_out) a.x_out[(int64_t)r * D + e] = o[j];
-      sX[wave][e] = (int8_t)quantize_one(o[j], am);
-    }
-    if (__any(bad) && lane == 0 && a.err) *a.err = 1;
-  }
-  wg_lds_barrier();  // LDS only: the LayerNorm row stores stay in flight
-  // Rows 0..7 of the A operand are the group's rows (zero past the device
-  // count), rows 8..15 zero.  Lane l ends with rows 4(l/16)+i of column l%16.
-  const bool a_live = ar < kLgsRows && grp * kLgsRows + ar < n_rows;
-  v4i acc = v4i{0, 0, 0, 0};
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const v4i x = a_live ? *(const v4i*)(&sX[ar][64 * s + (lane >> 4) * 16]) : v4i{0, 0, 0, 0};
-    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x, bf[s], acc, 0, 0, 0);
-  }
-  if (lane >= 32) return;  // rows 8..15
-  const float inv = dequant_scale(am, wm);
-  bool bad = false;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = grp * kLgsRows + 4 * (lane >> 4) + i;
-    if (m >= n_rows) continue;
-    float y = dequant_apply(acc[i], inv, wb);
-    if (a.relu) y = y > 0.0f ? y : 0.0f;
-    if (a.out) a.out[(int64_t)m * a.ldo + col] = y;
-    if (a.out_q) {
-      a.out_q[(int64_t)m * a.ldq + col] = (int8_t)quantize_one(y, a.qmult);
-      if (col == 0) a.out_qa[m] = a.qmult;
-      bad |= !isfinite(y);  // quantizing rejects non-finite input
-    }
-  }
-  if (__any(bad) && lane == 0 && a.err) *a.err = 1;
-}
-
 }  // namespace
-
-bool ln_gemm_static_supported(int K, int N) {
-  return (K == 256 || K == 384 || K == 512) && N > 0 && N % kLgsCols == 0;
-}
-
-hipError_t launch_ln_gemm_static(const LnGemmStaticArgs& a, hipStream_t s) {
-  if (a.rows <= 0) return hipSuccess;
-  const bool yp = a.ya != nullptr;
-  if (!ln_gemm_static_supported(a.K, a.N) || (yp ? !(a.Wy && a.ymult && a.ybias) : !a.y) || !a.r ||
-      !a.gamma || !a.beta || !a.W ||
-      !a.wmult || !a.bias || (!a.out && !a.out_q) || (a.out && a.ldo < a.N) ||
-      (a.out_q && (!a.out_qa || a.ldq < a.N)) || a.part_n < 0 || a.part_n % kLgsCols)
-    return hipErrorInvalidValue;
-  for (const float m : {a.xq_mult[0], a.xq_mult[1], yp ? a.ya_mult : 1.0f})
-    if (!(m > 0.0f) || !(m < __builtin_huge_valf())) return hipErrorInvalidValue;
-  if (a.out_q && (!(a.qmult > 0.0f) || !(a.qmult < __builtin_huge_valf()))) return hipErrorInvalidValue;
-  const int groups = (a.rows + kLgsRows - 1) / kLgsRows;
-  if ((int64_t)groups * (a.N / kLgsCols) > 0x7fffffff) return hipErrorInvalidValue;
-  const dim3 grid(groups * (a.N / kLgsCols)), block(64 * kLgsWaves);
-#define MH_LG(P)                                                          \
-  if (yp)                                                                 \
-    hipLaunchKernelGGL((k_ln_gemm_static<P, true>), grid, block, 0, s, a); \
-  else                                                                    \
-    hipLaunchKernelGGL((k_ln_gemm_static<P, false>), grid, block, 0, s, a);
-  if (a.K == 256) {
-    MH_LG(4)
-  } else if (a.K == 384) {
-    MH_LG(6)
-  } else {
-    MH_LG(8)
-  }
-#undef MH_LG
-  return hipGetLastError();
-}
 
 hipError_t launch_ssru_input(const SsruInputArgs& a, hipStream_t s) {
   if (a.rows <= 0) return hipSuccess;
