@@ -127,6 +127,29 @@ def test_ssru_many_rows_token_exact(pkg, orc, sl):
             assert got == want
 
 
+@pytest.mark.parametrize("ffn_dim", [1536, 960], ids=["fused", "generic"])
+def test_ssru_non_finite_activation_is_an_inference_error(pkg, orc, ffn_dim):
+    """A decoder FFN whose weight multiplier makes its output overflow: the
+    quantization of the hidden rows rejects the infinities, as the oracle's
+    static quantization does (error -2); the call fails with an inference
+    error and the engine stays ready.  FFN 1536 runs the fused kernels, 960
+    the generic ones."""
+    g = pkg.SsruGeometry(source_vocab=3000, target_vocab=3200, encoder_layers=1, decoder_layers=2,
+                         ffn_dim=ffn_dim)
+    model = pkg.seeded_ssru_model(seed=47, geometry=g, std=0.05)
+    model.decoder[1]["w1"]["weight_mult"] = 1e-37  # acc / (act * 1e-37) overflows
+    om = orc.OracleSsruModel(model)
+    b = pkg.ragged_batch(seed=5, n=6, vocab=g.source_vocab)
+    with pytest.raises(orc.OracleError) as ei:
+        orc.translate_ssru(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, 0,
+                           threads=ORACLE_THREADS)
+    assert ei.value.code == -2
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        with pytest.raises(pkg.InferenceError, match="not finite"):
+            e.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, 0)
+        assert e.is_ready()
+
+
 def test_ssru_reference_shape_ragged_64(pkg, orc, sl):
     """The reference's supported shape at full size (32000-id vocabularies,
     6 encoder / 4 SSRU decoder layers) on the 64-sentence ragged batch, with
