@@ -47,6 +47,8 @@ def run_both(pkg, orc, engine, om, b, flags, cand=None, coff=None):
 SHAPES = {
     "d384-dh48": dict(dim=384, heads=8, ffn_dim=1536),
     "d256-dh64": dict(dim=256, heads=4, ffn_dim=1024),
+    "d384-dh64": dict(dim=384, heads=6, ffn_dim=1536),
+    "d512-dh64": dict(dim=512, heads=8, ffn_dim=2048),
 }
 
 
