@@ -69,6 +69,9 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   int64_t key0 = a.row_key0[r];
   int nk = max(a.row_nk[r], 1);
   key0 = min(max(key0, (int64_t)0), a.max_row - 1);
+  // More keys than the block stages: attend over the first 128 (flagged
+  // below for live rows; the host bound max_keys rules it out).
+  const bool too_long = nk > kSsruBlockMaxKeys;
   nk = min(nk, kSsruBlockMaxKeys);
   const int nk_ld = (int)min((int64_t)nk, a.max_row - key0);
 
@@ -111,6 +114,7 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   }
   const int n_rows = a.rows_dev ? *a.rows_dev : a.rows;
   if (r >= n_rows) return;  // the whole workgroup alike
+  if (too_long && tid == 0 && a.err) *a.err = 2;
 
   if (wave == 0) {
     // LayerNorm(z): the SSRU LayerNorm (ssru_update_layer_norm_into).
