@@ -116,14 +116,15 @@ def test_residual_layer_norm_matches_oracle(pkg, orc, dev):
 
 
 def _ln_edge_rows(rng, d=512):
-    """Rows whose sequential sums stress the four-chunk speculative folds:
+    """Rows whose sequential sums stress the speculative folds (chunks of 64
+    or 128):
     prefixes cancelling to near zero at the chunk boundaries (the candidate
     windows miss and chunks are refolded), exact zeros and negative zeros,
     constants, wide and tiny magnitudes."""
     rows = []
-    for _ in range(8):  # cancellation at every 128-element chunk boundary
+    for _ in range(8):  # cancellation at every 64-element chunk boundary
         z = rng.standard_normal(d).astype(np.float32) * np.float32(rng.uniform(0.5, 20))
-        for k in range(128, d, 128):
+        for k in range(64, d, 64):
             s = np.float32(-0.0)
             for v in z[:k - 1]:
                 s = np.float32(s + v)
@@ -179,7 +180,8 @@ def test_residual_layer_norm_single_wave_speculative_edges(pkg, orc, dev, d):
 
 
 def test_residual_layer_norm_few_rows_edge_cases(pkg, orc, dev):
-    """Few rows of width 512 take the four-wave kernel (speculative folds)."""
+    """Rows of width 512 take the four-wave kernel (eight-chunk speculative
+    folds)."""
     rng = np.random.default_rng(17)
     z = _ln_edge_rows(rng)
     base = rng.standard_normal((48, 512)).astype(np.float32) * 2
