@@ -141,12 +141,20 @@ def cpu_baseline(pkg, model, batch, cores: int, threads: int = 4):
 # ---------------------------------------------------------------------------
 # GPU leg
 # ---------------------------------------------------------------------------
+# Steps with at most this many rows build the last residual LayerNorm inside
+# the vocabulary kernel (kVocabLnMaxRows in csrc/kernels.h).
+VOCAB_LN_MAX_ROWS = 4
+
+
 def vocab_bytes(V, K, rows):
     """Algorithmic bytes of one vocabulary launch over `rows` active rows:
-    int8 weights + fp32 multipliers + fp32 bias + int8 activations + fp32 row
-    multipliers + the 8-byte argmax partial per row and 128-column workgroup."""
+    int8 weights + fp32 multipliers + fp32 bias + the 8-byte argmax partial
+    per row and 128-column workgroup + the rows: int8 activations and fp32
+    row multipliers, or, on steps that build the LayerNorm in the kernel, the
+    fp32 sublayer output and residual rows and the fp32 scale and bias."""
     groups = (V + 127) // 128
-    return V * K + 8 * V + rows * (K + 4 + 8 * groups)
+    row_in = rows * 8 * K + 8 * K if rows <= VOCAB_LN_MAX_ROWS else rows * (K + 4)
+    return V * K + 8 * V + rows * 8 * groups + row_in
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_kernels_ragged64_traffic.json"

@@ -299,39 +299,37 @@ constexpr int kVocabMaxK = 512;                   // K held in registers
 constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 
 // FULL: K = 512, every k-step live, unconditional weight loads.  LNP: the
-// rows (at most kVocabLnMaxRows) are the residual LayerNorm of g.pro, built by
-// wave pair p (waves 2p, 2p + 1) for row p with the speculative folds while
-// the weight loads are in flight; their loads are issued before the weights'.
-// Each wave of the pair normalizes the whole row, takes its maximum and
-// quantizes its half into the LDS rows the matrix cores read.
+// rows (at most kVocabLnMaxRows = 4, K = 512) are the residual LayerNorm of
+// g.pro: wave w builds row w with the one-wave speculative folds (ln_wave)
+// while the weight loads are in flight (the row's loads are issued before
+// the weights'), takes its maximum and quantizes it into the LDS row the
+// matrix cores read.
 template <bool FULL, bool LNP>
 __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
-  static_assert(!LNP || 4 / kSpecWaves >= kVocabLnMaxRows, "a wave pair per prologue row");
+  static_assert(kVocabLnMaxRows <= 4, "a wave per prologue row");
+  constexpr int PER = kVocabMaxK / 64;  // prologue rows: lane l holds elements l + 64j
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
   __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
   __shared__ float sAm[kSkinnyRows];
-  __shared__ __attribute__((aligned(16))) float sZ[LNP ? kVocabLnMaxRows * kVocabMaxK : 4];
-  __shared__ __attribute__((aligned(16))) float sT[LNP ? kVocabLnMaxRows * kVocabMaxK : 4];
-  __shared__ SpecFoldLds sFm[LNP ? kVocabLnMaxRows : 1], sFv[LNP ? kVocabLnMaxRows : 1];
+  __shared__ __attribute__((aligned(16))) float sZ[LNP ? 4 * kLnRow<PER> : 4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kq = (lane >> 4) * 16;
   const int ksteps = g.K >> 6;
   const int nbase = blockIdx.x * kVocabCols + wave * 16 * kVocabCT;
 
-  // LayerNorm prologue: this wave pair's row (rows below the host bound are
+  // LayerNorm prologue: this wave's row (rows below the host bound are
   // allocated), requested before the weights.
-  const int pr = wave / kSpecWaves, pw = wave % kSpecWaves;
-  const bool prow = LNP && pr < g.M;
-  f4v lz[2], lg[2], lb[2];
+  float wy[LNP ? PER : 1], wr[LNP ? PER : 1], wgm[LNP ? PER : 1], wbt[LNP ? PER : 1];
   if constexpr (LNP) {
+    const int64_t ro = (int64_t)min(wave, g.M - 1) * kVocabMaxK;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = 4 * lane + 256 * j;
-      const int64_t off = (int64_t)min(pr, g.M - 1) * kVocabMaxK + c;
-      lz[j] = *(const f4v*)(g.pro.y + off) + *(const f4v*)(g.pro.r + off);  // add_slices
-      lg[j] = *(const f4v*)(g.pro.gamma + c);
-      lb[j] = *(const f4v*)(g.pro.beta + c);
+    for (int j = 0; j < PER; ++j) {
+      const int c = lane + 64 * j;
+      wy[j] = g.pro.y[ro + c];
+      wr[j] = g.pro.r[ro + c];
+      wgm[j] = g.pro.gamma[c];
+      wbt[j] = g.pro.beta[c];
     }
   }
 
@@ -381,43 +379,24 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   }
   const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
   if constexpr (LNP) {
-    // normalize_row (tensor.rs:372-385) with speculative folds; every wave
-    // passes both fold barriers.
-    float* zr = sZ + pr * kVocabMaxK;
-    float* tr = sT + pr * kVocabMaxK;
-    if (prow) spec_fold_chunk(lz, zr, -0.0f, sFm[pr], pw, lane);
-    wg_lds_barrier();
-    f4v lt[2];
-    float mean = 0.0f;
-    if (prow) {
-      mean = spec_fold_resolve(zr, sFm[pr], lane) / (float)kVocabMaxK;
+    // normalize_row (tensor.rs:372-385), one wave per row.
+    if (wave < g.M) {
+      float z[PER], o[PER];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const f4v c = lz[j] - mean;
-        lt[j] = c * c;
-      }
-      spec_fold_chunk(lt, tr, -0.0f, sFv[pr], pw, lane);
-    }
-    wg_lds_barrier();
-    if (prow) {
-      const float var = spec_fold_resolve(tr, sFv[pr], lane) / (float)kVocabMaxK;
-      const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
-      f4v o[2];
+      for (int j = 0; j < PER; ++j) z[j] = wy[j] + wr[j];  // add_slices
+      ln_wave<PER>(z, sZ + wave * kLnRow<PER>, wgm, wbt, lane, o);
       float mx = 0.0f;
       bool bad = false;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        o[j] = ((lz[j] - mean) * inv) * lg[j] + lb[j];
-        bad |= !isfinite(o[j].x) || !isfinite(o[j].y) || !isfinite(o[j].z) || !isfinite(o[j].w);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
+      for (int j = 0; j < PER; ++j) {
+        bad |= !isfinite(o[j]);
+        mx = fmaxf(mx, fabsf(o[j]));
       }
       const float a_row = row_multiplier(wave_max(mx));
-      const f4v h = pw == 0 ? o[0] : o[1];
-      *(uint32_t*)(sA + pr * kVocabLds + 4 * lane + 256 * pw) =
-          (uint32_t)(quantize_one(h.x, a_row) & 0xFF) | ((uint32_t)(quantize_one(h.y, a_row) & 0xFF) << 8) |
-          ((uint32_t)(quantize_one(h.z, a_row) & 0xFF) << 16) | ((uint32_t)(quantize_one(h.w, a_row) & 0xFF) << 24);
-      if (pw == 0 && lane == 0) sAm[pr] = a_row;
-      if (__any(bad) && lane == 0 && pr < M && g.pro.err) *g.pro.err = 1;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) sA[wave * kVocabLds + lane + 64 * j] = (int8_t)quantize_one(o[j], a_row);
+      if (lane == 0) sAm[wave] = a_row;
+      if (__any(bad) && lane == 0 && wave < M && g.pro.err) *g.pro.err = 1;
     }
   }
 

@@ -61,7 +61,7 @@ struct GemmArgs {
   // kernel instead of read from A (pro.out is not written).
   RowPrologue pro;
 };
-constexpr int kVocabLnMaxRows = 2;
+constexpr int kVocabLnMaxRows = 4;
 // Whether the vocabulary kernel can build LayerNorm rows of width K itself.
 bool vocab_ln_supported(int K);
 

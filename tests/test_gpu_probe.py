@@ -9,8 +9,8 @@ embedding prologues, the LayerNorm + FFN up-projection block, the FFN
 down-projection that quantizes its fp32 input, the attention-output
 projection with its 16-row groups, and the vocabulary kernel with and without
 its LayerNorm prologue.  The cases straddle every row and key threshold at
-which the engine switches kernels: 1, 2, 3, 8, 9, 16, 17, 32, 33, 64 and 65
-active rows; 128 and 129 cached keys; 128 and 129 source tokens.
+which the engine switches kernels: 1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64 and
+65 active rows; 128 and 129 cached keys; 128 and 129 source tokens.
 
 Limits are capped at probe_step + 1 on both sides: a row is active at the
 probed step, and its logits there are the same, whatever happens afterwards.
@@ -62,7 +62,7 @@ def small(pkg, orc, small_model):
         yield e, orc.OracleModel(small_model), small_model.geometry.vocab
 
 
-@pytest.mark.parametrize("rows", [1, 2, 3, 8, 9, 16, 17, 32, 33, 64, 65])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64, 65])
 def test_probe_row_thresholds(pkg, orc, small, rows):
     engine, om, V = small
     rng = np.random.default_rng(100 + rows)
