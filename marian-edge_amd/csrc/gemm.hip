@@ -64,16 +64,18 @@ constexpr int kAfRows = 16;  // fp32 A source: one MFMA row tile per workgroup
 
 // A sources of the skinny kernel: int8 rows with their multipliers, or fp32
 // rows quantized while loading, with the row maxima of the producer (A_F32)
-// or found here over all of K (A_F32_MAX).
-enum ASrc { A_I8 = 0, A_F32 = 1, A_F32_MAX = 2 };
+// or found here over all of K (A_F32_MAX).  A_I8_RG: int8 rows in 16-row
+// groups over blockIdx.y, as the fp32 sources are (plain stores only).
+enum ASrc { A_I8 = 0, A_F32 = 1, A_F32_MAX = 2, A_I8_RG = 3 };
 
 // FULL: K is exactly NW x KSW k-steps (every shape the engine uses), so no
 // k-step needs a guard and every prologue load is unconditional (guarded
 // loads become branches that the compiler waits on one by one).
 template <int MODE, int CT, int NW, int KSW, int ASRC, bool FULL>
 __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
-  constexpr bool AF = ASRC != A_I8;        // fp32 A, quantized while loading
+  constexpr bool AF = ASRC == A_F32 || ASRC == A_F32_MAX;  // fp32 A, quantized while loading
   constexpr bool AX = ASRC == A_F32_MAX;   // ... with the row maxima found here
+  constexpr bool RG = ASRC != A_I8;        // one 16-row group per workgroup
   constexpr int NT = NW * 64;
   constexpr int COLS = CT * 16;
   constexpr int LDC = COLS + 1;          // padded LDS row (i32)
@@ -86,14 +88,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   const int ksteps = g.K >> 6;
   // An fp32 A source is split into 16-row groups over blockIdx.y: each
   // workgroup quantizes only its own rows (one MFMA row tile).
-  const int r0 = AF ? (int)blockIdx.y * kAfRows : 0;
+  const int r0 = RG ? (int)blockIdx.y * kAfRows : 0;
   const float* Af = AF ? g.Af + (int64_t)r0 * g.ldaf : nullptr;
+  const int8_t* Ai = AF ? nullptr : g.A + (int64_t)r0 * g.lda;
+  const float* ai = AF ? nullptr : g.a + r0;
   const float* Aamax = ASRC == A_F32 ? g.Aamax + (int64_t)r0 * g.amax_parts : nullptr;
   float* out = e.out ? e.out + (int64_t)r0 * e.ldo : nullptr;
   // g.M bounds the rows on the host side; every row below it is allocated,
   // so the first row chunk's activations are loaded before the device row
   // count (g.M_dev) is known.
-  const int Mh = AF ? min(g.M - r0, kAfRows) : g.M;
+  const int Mh = RG ? min(g.M - r0, kAfRows) : g.M;
 
   // Every weight fragment of this wave (k-steps wave, wave+NW, ...).
   v4i bf[KSW][CT];
@@ -165,7 +169,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int m = min(mt * 16 + (lane & 15), Mh - 1);
-      const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
+      const int8_t* ar = Ai + (int64_t)m * g.lda + kq;
 #pragma unroll
       for (int i = 0; i < KSW; ++i) {
         const int s = wave + NW * i;
@@ -189,12 +193,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + m]);
       am[k] = row_multiplier(rm);
     } else {
-      am[k] = AF ? af_row_mult(Aamax, m, g.amax_parts) : g.a[m];
+      am[k] = AF ? af_row_mult(Aamax, m, g.amax_parts) : ai[m];
     }
     if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
   const int Md = g.M_dev ? min(*g.M_dev, g.M) : g.M;
-  const int M = AF ? min(Md - r0, kAfRows) : Md;  // this workgroup's rows
+  const int M = RG ? min(Md - r0, kAfRows) : Md;  // this workgroup's rows
   // Non-finite values count only in rows below the device row count, as in
   // the row quantization.
   if constexpr (AX)
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         const int m = min(m0 + mt * 16 + (lane & 15), M - 1);
-        const int8_t* ar = g.A + (int64_t)m * g.lda + kq;
+        const int8_t* ar = Ai + (int64_t)m * g.lda + kq;
 #pragma unroll
         for (int i = 0; i < KSW; ++i) {
           const int s = wave + NW * i;
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
       for (int k = 0; k < ROWS_PER_THREAD; ++k) {
         const int m = min(m0 + tid / COLS + k * (NT / COLS), M - 1);
-        am[k] = g.a[m];
+        am[k] = ai[m];
         if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
       }
     }
@@ -884,9 +888,13 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
   if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2, A_I8>(g, e, s);
   if (ksteps <= 16) return launch_skinny_k<MODE, 4, 4, A_I8>(g, e, s);
   // K = 1536 (the FFN down-projection of a 1536-wide FFN): 16 waves of two
-  // k-steps beat 8 of four (measured); K = 2048 the other way round.
-  if (ksteps <= 24) return launch_skinny_k<MODE, 16, 2, A_I8>(g, e, s);
-  return launch_skinny_k<MODE, 8, 4, A_I8>(g, e, s);
+  // k-steps beat 8 of four (measured); K = 2048 the other way round.  Above
+  // 16 rows, plain stores take one 16-row group per workgroup: a 64-row
+  // chunk of these K is 96-128 KB of activations per workgroup.
+  const bool rg = MODE == EPI_STORE && !e.out_i32 && !e.out_q && g.M > kAfRows && g.M <= 65535 * kAfRows;
+  if (ksteps <= 24)
+    return rg ? launch_skinny_k<MODE, 16, 2, A_I8_RG>(g, e, s) : launch_skinny_k<MODE, 16, 2, A_I8>(g, e, s);
+  return rg ? launch_skinny_k<MODE, 8, 4, A_I8_RG>(g, e, s) : launch_skinny_k<MODE, 8, 4, A_I8>(g, e, s);
 }
 
 hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hipStream_t s) {
