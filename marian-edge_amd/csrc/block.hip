@@ -20,7 +20,7 @@
 namespace mh {
 namespace {
 
-constexpr int kBlkRowWaves = 4;   // waves 0-3: the input row (0-1 fold, 2-3 exit)
+constexpr int kBlkRowWaves = 4;   // waves 0-3: the input row (wave 0; 1-3 exit)
 constexpr int kBlkLoadWaves = 4;  // waves 4-7 load weights and keys, then project
 constexpr int kBlkThreads = 64 * (kBlkRowWaves + kBlkLoadWaves);
 constexpr int kBlkD = 512;             // model width handled (8 heads x 64)
@@ -28,7 +28,6 @@ constexpr int kBlkMaxKeys = 128;       // keys staged in LDS
 constexpr int kBlkRow = kHeadDim + 4;  // padded LDS key row (floats)
 constexpr int kPvRow = kBlkMaxKeys + 4;  // padded LDS row of one dimension's PV products
 static_assert(kHeadDim * kPvRow <= kBlkMaxKeys * kBlkRow, "the PV products fit in the key rows");
-static_assert(kBlkRowWaves >= kSpecWaves && kBlkD == kSpecChunks * kSpecChunk, "the LayerNorm folds: two of the row waves, four chunks");
 
 __constant__ uint64_t kBlkExp2Tab[32] = {MH_EXP2_TABLE_32};
 
@@ -75,32 +74,6 @@ __device__ __forceinline__ void row_load(const RowPrologue& p, int r, int step, 
     }
     L.mu = p.emb_mult[tk];
   }
-}
-
-// LayerNorm(y + r) built by the two fold waves together (each loaded the
-// whole row): the mean and variance folds run as speculative four-chunk folds
-// (bit-identical to the sequential folds) over LDS copies of z and of the
-// squared deviations.  Both waves return the normalized row.
-__device__ __forceinline__ void row_build_ln_spec(const RowLoads<PRO_LN>& L, float* sZ, float* sT,
-                                              SpecFoldLds& fm, SpecFoldLds& fv, int w, int lane,
-                                              f4v (&o)[2]) {
-  f4v z[2], t[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) z[j] = L.a[j] + L.b[j];  // add_slices
-  spec_fold_chunk(z, sZ, -0.0f, fm, w, lane);
-  wg_lds_barrier();
-  const float mean = spec_fold_resolve(sZ, fm, lane) / (float)kBlkD;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const f4v c = z[j] - mean;
-    t[j] = c * c;
-  }
-  spec_fold_chunk(t, sT, -0.0f, fv, w, lane);
-  wg_lds_barrier();
-  const float var = spec_fold_resolve(sT, fv, lane) / (float)kBlkD;
-  const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) o[j] = ((z[j] - mean) * inv) * L.g[j] + L.bb[j];
 }
 
 // The row's values built by one wave: LayerNorm(y + r) with its two
@@ -195,12 +168,11 @@ __device__ __forceinline__ void row_tiles_mfma(const int8_t* sX, const v4i (&bf)
   for (int i = 0; i < T; ++i) out[i] = CH == 2 ? acc[i][0][0] + acc[i][1][0] : acc[i][0][0];
 }
 
-// Work split: waves 0-1 build the input row (a LayerNorm's two speculative
-// fold waves; an embedding row by wave 0 alone), waves 2-3 exit at once;
-// waves 4-7 meanwhile load this head's weight rows and stage the row's keys
-// and values in LDS, passing the folds' two workgroup barriers with their
-// loads in flight, then run the projection; wave 0 attends, helped by waves
-// 4-7 (wave 5: a second chunk of scores; all four: the PV products).
+// Work split: wave 0 builds the input row (a LayerNorm with the one-wave
+// speculative folds, or the embedding row), waves 1-3 exit at once; waves
+// 4-7 meanwhile load this head's weight rows and stage the row's keys and
+// values in LDS, then run the projection; wave 0 attends, helped by waves 4-7
+// (wave 5: a second chunk of scores; all four: the PV products).
 constexpr int kBlkLoaders = 64 * kBlkLoadWaves;
 static_assert(kBlkRow % 4 == 0 && kBlkMaxKeys * (kBlkRow / 4) % 64 == 0, "key staging by wave instructions");
 
@@ -212,9 +184,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   static_assert(NT % kBlkLoadWaves == 0, "every loader wave owns whole tiles");
   __shared__ __attribute__((aligned(16))) float sK[kBlkMaxKeys * kBlkRow];
   __shared__ __attribute__((aligned(16))) float sV[kBlkMaxKeys * kBlkRow];
-  __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
-  __shared__ __attribute__((aligned(16))) float sT[PK == PRO_LN ? kBlkD : 4];
-  __shared__ SpecFoldLds sFm, sFv;
+  constexpr int PER = kBlkD / 64;  // LayerNorm row: lane l holds elements l + 64j
+  __shared__ __attribute__((aligned(16))) float sZ[PK == PRO_LN ? kLnRow<PER> : kBlkD];
   __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
   __shared__ __attribute__((aligned(16))) float sQ[kHeadDim];
   __shared__ __attribute__((aligned(16))) float sP[kBlkMaxKeys];
@@ -239,23 +210,51 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 
   if (wave < kBlkRowWaves) {
     // ---- the input row ----------------------------------------------------------
-    if (wave >= (PK == PRO_LN ? kSpecWaves : 1)) return;  // an embedding row has no folds
+    if (wave != 0) return;  // wave 0 builds the row
     const uint64_t tab_v = kBlkExp2Tab[lane & 31];
-    RowLoads<PK> in;
-    row_load<PK>(b.pro, r, step, lane, in);
-    if (r >= n) return;
-    f4v o[2];
-    if constexpr (PK == PRO_LN) {
-      row_build_ln_spec(in, sZ, sT, sFm, sFv, wave, lane, o);
-      if (wave != 0) return;
-    } else {
-      row_build<PK>(b.pro, in, sZ, lane, o);
-    }
     bool bad;
-    const float a_row = row_quantize(o, sX, lane, bad);
-    if (h == 0 && b.pro.out) {
+    float a_row;
+    if constexpr (PK == PRO_LN) {
+      // LayerNorm(y + r) with the one-wave speculative folds (ln_wave).
+      float y[PER], rr[PER], gv[PER], bv[PER];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) *(f4v*)(b.pro.out + (int64_t)r * kBlkD + 4 * lane + 256 * j) = o[j];
+      for (int j = 0; j < PER; ++j) {
+        const int64_t e = (int64_t)r * kBlkD + lane + 64 * j;
+        y[j] = b.pro.y[e];
+        rr[j] = b.pro.r[e];
+        gv[j] = b.pro.gamma[lane + 64 * j];
+        bv[j] = b.pro.beta[lane + 64 * j];
+      }
+      if (r >= n) return;
+      float z[PER], o[PER];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) z[j] = y[j] + rr[j];  // add_slices
+      ln_wave<PER>(z, sZ, gv, bv, lane, o);
+      bad = false;
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        bad |= !isfinite(o[j]);
+        mx = fmaxf(mx, fabsf(o[j]));
+      }
+      a_row = row_multiplier(wave_max(mx));
+#pragma unroll
+      for (int j = 0; j < PER; ++j) sX[lane + 64 * j] = (int8_t)quantize_one(o[j], a_row);
+      if (h == 0 && b.pro.out) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) b.pro.out[(int64_t)r * kBlkD + lane + 64 * j] = o[j];
+      }
+    } else {
+      RowLoads<PK> in;
+      row_load<PK>(b.pro, r, step, lane, in);
+      if (r >= n) return;
+      f4v o[2];
+      row_build<PK>(b.pro, in, sZ, lane, o);
+      a_row = row_quantize(o, sX, lane, bad);
+      if (h == 0 && b.pro.out) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) *(f4v*)(b.pro.out + (int64_t)r * kBlkD + 4 * lane + 256 * j) = o[j];
+      }
     }
     if (lane == 0) sA = a_row;
     if (lane < 32) sTab[lane] = tab_v;
@@ -300,10 +299,6 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     if (r >= n) {
       __builtin_amdgcn_s_waitcnt(0);  // no LDS write may land after the workgroup ends
       return;
-    }
-    if constexpr (PK == PRO_LN) {  // the row waves' two fold barriers, loads still in flight
-      wg_lds_barrier();
-      wg_lds_barrier();
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's key and value rows are in LDS
     // Value rows from the last key up to the next multiple of 16 are zero, so
@@ -453,9 +448,9 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
 
 // ---------------------------------------------------------------------------
 // LayerNorm + up-projection block (the FFN's first layer on steps with few
-// rows): one 512-thread workgroup per (row, 128-column slice).  Waves 0-1
-// build the row's residual LayerNorm (speculative four-chunk folds) and wave
-// 0 quantizes it, as in the attention block; waves 4-7 meanwhile load the
+// rows): one 512-thread workgroup per (row, 128-column slice).  Wave 0
+// builds the row's residual LayerNorm (one-wave speculative folds) and
+// quantizes it, as in the attention block; waves 4-7 meanwhile load the
 // slice's weight rows into registers, then run the projection on MFMA (row 0
 // of a 16-row tile), dequantize, apply ReLU and store.  Replaces the
 // LayerNorm kernel and the skinny GEMM that followed it.
@@ -466,9 +461,8 @@ constexpr int kLgTpw = kLgTiles / kBlkLoadWaves;  // tiles per loader wave
 static_assert(kLgTiles % kBlkLoadWaves == 0, "every loader wave owns whole tiles");
 
 __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
-  __shared__ __attribute__((aligned(16))) float sZ[kBlkD];
-  __shared__ __attribute__((aligned(16))) float sT[kBlkD];
-  __shared__ SpecFoldLds sFm, sFv;
+  constexpr int PER = kBlkD / 64;  // lane l holds row elements l + 64j
+  __shared__ __attribute__((aligned(16))) float sZ[kLnRow<PER>];
   __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
   __shared__ float sA;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -476,18 +470,34 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   const int slice = blockIdx.x % slices, r = blockIdx.x / slices;  // r < a.rows (host bound)
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
   if (wave < kBlkRowWaves) {
-    if (wave >= kSpecWaves) return;  // the two fold waves build the row
-    RowLoads<PRO_LN> in;
-    row_load<PRO_LN>(a.pro, r, 0, lane, in);
+    if (wave != 0) return;  // wave 0 builds the row with the one-wave folds
+    float y[PER], rr[PER], gv[PER], bv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int64_t e = (int64_t)r * kBlkD + lane + 64 * j;
+      y[j] = a.pro.y[e];
+      rr[j] = a.pro.r[e];
+      gv[j] = a.pro.gamma[lane + 64 * j];
+      bv[j] = a.pro.beta[lane + 64 * j];
+    }
     if (r >= n) return;
-    f4v o[2];
-    row_build_ln_spec(in, sZ, sT, sFm, sFv, wave, lane, o);
-    if (wave != 0) return;
-    bool bad;
-    const float a_row = row_quantize(o, sX, lane, bad);
+    float z[PER], o[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) z[j] = y[j] + rr[j];  // add_slices
+    ln_wave<PER>(z, sZ, gv, bv, lane, o);
+    bool bad = false;
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      bad |= !isfinite(o[j]);
+      mx = fmaxf(mx, fabsf(o[j]));
+    }
+    const float a_row = row_multiplier(wave_max(mx));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) sX[lane + 64 * j] = (int8_t)quantize_one(o[j], a_row);
     if (slice == 0 && a.pro.out) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) *(f4v*)(a.pro.out + (int64_t)r * kBlkD + 4 * lane + 256 * j) = o[j];
+      for (int j = 0; j < PER; ++j) a.pro.out[(int64_t)r * kBlkD + lane + 64 * j] = o[j];
     }
     if (lane == 0) sA = a_row;
     if (__any(bad) && lane == 0 && a.err) *a.err = 1;
@@ -508,8 +518,6 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     bi[i] = a.bias[col];
   }
   if (r >= n) return;
-  wg_lds_barrier();  // the row waves' two fold barriers, weight loads still in flight
-  wg_lds_barrier();
   __syncthreads();  // the quantized row is in LDS
   const float a_row = sA;
   float inv[kLgTpw];
