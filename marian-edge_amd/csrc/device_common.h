@@ -164,39 +164,11 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
   return s;
 }
 
-// ---- speculative exact fold over 512 values ------------------------------------
-// The sequential fold init + p[0] + p[1] + ... + p[511], run by two waves at
-// once with the same result bits.  The row is cut into four 128-term chunks;
-// wave w folds chunks 2w (lanes 0-31) and 2w + 1 (lanes 32-63) in one
-// instruction stream.  Chunk 0 starts from init; chunk c >= 1 starts from each
-// of 32 consecutive floats (one per lane of its half-wave) centred on an
-// estimate of the prefix sum p[0] + ... + p[128c - 1] (a float tree sum).
-// Floats are consecutive when their keys are (the key is the bit pattern with
-// the magnitude bits of negative values flipped: a monotone, self-inverse map
-// onto the 32-bit integers, with -0.0 just below +0.0).  The true start of
-// chunk c is the end of chunk c - 1: when its key lies in chunk c's window,
-// that candidate's chain is chunk c's exact end; otherwise chunk c is folded
-// again from the true start.  Every step is the sequential fold's own float
-// addition, so the result is the sequential fold's whatever the estimates
-// are: they only decide how often a 128-term refold is needed.  Chunk ends of
-// sums of non-negative terms stay within a few units in the last place of the
-// exact prefix; a prefix near zero after cancellation can fall outside the
-// window (a few percent of folds of centred normal rows).
-//
-// Protocol: each of the two fold waves (w = 0, 1) holds the whole row (lane l:
-// elements 4l..4l+3 in v[0], 256+4l..256+4l+3 in v[1]) and calls
-// spec_fold_chunk, which stores v[w] (its two chunks) to p (LDS, 512 floats)
-// and folds them; then every wave of the workgroup passes wg_lds_barrier; then
-// the fold waves call spec_fold_resolve (each gets the result).  p and L stay
-// unchanged until both have resolved.
-constexpr int kSpecChunk = 128;
-constexpr int kSpecChunks = 4;
-constexpr int kSpecCand = 32;  // candidate starts per chunk: half a wave
-constexpr int kSpecWaves = 2;  // fold waves
-struct SpecFoldLds {
-  int end[kSpecChunks][kSpecCand];  // keys of the chain ends (chunk 0: every lane the same)
-  int base[kSpecChunks];            // key of each window's first candidate
-};
+// ---- float keys ---------------------------------------------------------------
+// The key of a float is its bit pattern with the magnitude bits of negative
+// values flipped: a monotone, self-inverse map onto the 32-bit integers, with
+// -0.0 just below +0.0, so consecutive floats have consecutive keys.
+constexpr int kSpecChunk = 128;  // terms per chunk of the speculative folds
 
 __device__ __forceinline__ int float_key(float f) {
   const uint32_t b = __float_as_uint(f);
@@ -231,68 +203,6 @@ __device__ __forceinline__ void wave_sum2(float& a, float& b) {
       (__int_as_float(__builtin_amdgcn_readlane(ia, 32)) + __int_as_float(__builtin_amdgcn_readlane(ia, 48)));
   b = (__int_as_float(__builtin_amdgcn_readlane(ib, 0)) + __int_as_float(__builtin_amdgcn_readlane(ib, 16))) +
       (__int_as_float(__builtin_amdgcn_readlane(ib, 32)) + __int_as_float(__builtin_amdgcn_readlane(ib, 48)));
-}
-
-__device__ __forceinline__ void spec_fold_chunk(const f4v (&v)[2], float* p, float init,
-                                                SpecFoldLds& L, int w, int lane) {
-  const int h = lane >> 5, c = 2 * w + h, cl = lane & 31;
-  *(f4v*)(p + 256 * w + 4 * lane) = v[w];  // chunks 2w and 2w + 1
-  // Prefix estimates: x = chunk 0 (w = 0) or chunks 0-1 (w = 1); y = chunk 2.
-  const float f0 = (v[0].x + v[0].y) + (v[0].z + v[0].w);
-  const float f1 = (v[1].x + v[1].y) + (v[1].z + v[1].w);
-  float x = (w == 1 || lane < 32) ? f0 : 0.0f;
-  float y = (w == 1 && lane < 32) ? f1 : 0.0f;
-  wave_sum2(x, y);
-  const float est = (w == 1 && h == 1) ? x + y : x;
-  // Window base (key of candidate 0), kept where base + 31 cannot overflow.
-  const int base = min(max(float_key(est), INT32_MIN + kSpecCand / 2), INT32_MAX - kSpecCand / 2 + 1) - kSpecCand / 2;
-  const float st = c == 0 ? init : key_float(base + cl);
-  if (cl == 0) L.base[c] = base;
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's chunks are in LDS
-  __builtin_amdgcn_wave_barrier();
-  const float e = seq_fold_lds<kSpecChunk / 4, 4>((const float4*)(p + kSpecChunk * c), st);
-  L.end[c][cl] = float_key(e);
-}
-
-__device__ __forceinline__ float spec_fold_resolve(const float* p, const SpecFoldLds& L, int lane) {
-  int en[kSpecChunks - 1], bs[kSpecChunks - 1];
-#pragma unroll
-  for (int k = 1; k < kSpecChunks; ++k) {
-    en[k - 1] = L.end[k][lane & (kSpecCand - 1)];
-    bs[k - 1] = L.base[k];
-  }
-  const int e0 = L.end[0][0];
-  // All of them requested here, one LDS round trip in all (left to itself the
-  // compiler sinks each read into the step that uses it).
-  asm volatile("" ::: "memory");
-  // The running key and the window bases are the same in every lane: the
-  // lookups run on the scalar unit, without branches while they hit; `miss`
-  // marks the chunks whose start was outside the window.  With the base at
-  // most INT32_MAX - 31, d < 32 exactly when the key is in the window.
-  int ks = __builtin_amdgcn_readfirstlane(e0);
-  uint32_t miss = 0;
-#pragma unroll
-  for (int k = 1; k < kSpecChunks; ++k) {
-    const uint32_t d = (uint32_t)ks - (uint32_t)__builtin_amdgcn_readfirstlane(bs[k - 1]);
-    const int t = __builtin_amdgcn_readlane(en[k - 1], (int)(d & (kSpecCand - 1)));
-    miss |= d < (uint32_t)kSpecCand ? 0u : 1u << k;
-    ks = miss ? ks : t;
-  }
-  if (miss) {  // from the first miss on: fold again where a start is outside the window
-    const int km = __builtin_ctz(miss);
-    float s = key_float(ks);  // the true start of chunk km
-#pragma unroll 1
-    for (int k = km; k < kSpecChunks; ++k) {
-      const uint32_t d = (uint32_t)float_key(s) - (uint32_t)__builtin_amdgcn_readfirstlane(L.base[k]);
-      if (k > km && d < (uint32_t)kSpecCand)
-        s = key_float(__builtin_amdgcn_readfirstlane(L.end[k][d]));
-      else
-        s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(
-            seq_fold_lds<kSpecChunk / 4, 4>((const float4*)(p + kSpecChunk * k), s))));
-    }
-    return s;
-  }
-  return key_float(ks);
 }
 
 // The same fold over the first nb batches of NB float4 (nb >= 1, a value
@@ -341,7 +251,7 @@ __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, f
 // stored in LDS 132 floats apart (chunk c at p + kSwStride c, so the lane
 // groups' broadcast reads fall in different banks).  Lanes [0, kSwLead) fold
 // chunk 0 from init; the kSwCand(NC) lanes of group c >= 1 fold chunk c from
-// consecutive floats (by key, as in spec_fold_chunk) around est[c], an
+// consecutive floats (by key) around est[c], an
 // estimate of the prefix p[0] + ... + p[128c - 1].  Then the true start of
 // each chunk (the end of the one before) picks its lane's chain end when it
 // lies in the window, and otherwise chunk c is folded again from the true

@@ -206,68 +206,6 @@ __global__ __launch_bounds__(256) void k_ssru_ln(const float* cand, const float*
   ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err, qmult);
 }
 
-// The same LayerNorm for rows of width 512 (decode and encoder): one two-wave
-// workgroup per row, the mean and variance folds as speculative four-chunk
-// folds (bit-identical to the sequential folds, a quarter of the dependent
-// chain); wave 0 then normalizes, stores and quantizes the row.  Lane l holds
-// elements 4l..4l+3 and 256+4l..256+4l+3.
-constexpr int kLnSpecD = kSpecChunks * kSpecChunk;  // 512
-__global__ __launch_bounds__(64 * kSpecWaves) void k_residual_ln_spec(const float* y, const float* r,
-                                                          const float* gamma, const float* beta,
-                                                          const int* rows_dev, float* out, int8_t* q,
-                                                          float* a, int* err, float qmult) {
-  __shared__ __attribute__((aligned(16))) float sZ[kLnSpecD];
-  __shared__ __attribute__((aligned(16))) float sT[kLnSpecD];
-  __shared__ SpecFoldLds sFm, sFv;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row = blockIdx.x;  // below the host bound: backed by memory (rows_dev: the device count)
-  f4v z[2], t[2], gv[2], bv[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e = 4 * lane + 256 * j;
-    z[j] = *(const f4v*)(y + (int64_t)row * kLnSpecD + e) + *(const f4v*)(r + (int64_t)row * kLnSpecD + e);
-    if (w == 0) {
-      gv[j] = *(const f4v*)(gamma + e);
-      bv[j] = *(const f4v*)(beta + e);
-    }
-  }
-  const int n = rows_dev ? *rows_dev : 0;
-  if (rows_dev && row >= n) return;  // every wave of the workgroup alike
-  spec_fold_chunk(z, sZ, -0.0f, sFm, w, lane);
-  wg_lds_barrier();
-  const float mean = spec_fold_resolve(sZ, sFm, lane) / (float)kLnSpecD;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const f4v c = z[j] - mean;
-    t[j] = c * c;
-  }
-  spec_fold_chunk(t, sT, -0.0f, sFv, w, lane);
-  wg_lds_barrier();
-  const float var = spec_fold_resolve(sT, sFv, lane) / (float)kLnSpecD;
-  if (w != 0) return;
-  const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
-  f4v o[2];
-  float m = 0.0f;
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];
-    bad |= !isfinite(o[j].x) || !isfinite(o[j].y) || !isfinite(o[j].z) || !isfinite(o[j].w);
-    m = fmaxf(m, fmaxf(fmaxf(fabsf(o[j].x), fabsf(o[j].y)), fmaxf(fabsf(o[j].z), fabsf(o[j].w))));
-    *(f4v*)(out + (int64_t)row * kLnSpecD + 4 * lane + 256 * j) = o[j];
-  }
-  if (q) {
-    const float sc = qmult > 0.0f ? qmult : row_multiplier(wave_max(m));
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *(uint32_t*)(q + (int64_t)row * kLnSpecD + 4 * lane + 256 * j) =
-          (uint32_t)(quantize_one(o[j].x, sc) & 0xFF) | ((uint32_t)(quantize_one(o[j].y, sc) & 0xFF) << 8) |
-          ((uint32_t)(quantize_one(o[j].z, sc) & 0xFF) << 16) | ((uint32_t)(quantize_one(o[j].w, sc) & 0xFF) << 24);
-    if (lane == 0) a[row] = sc;
-  }
-  if (__any(bad) && lane == 0 && err) *err = 1;
-}
-
 // x = (q/mult)*sqrt(d) + pos[p] (q8_engine.rs:53-74, 586-630); token < 0 gives
 // pos[p] alone (the decoder's first step).  Fused quantization of x with its
 // own multiplier or, when a.qmult > 0, the next layer's static one; none
@@ -639,13 +577,8 @@ hipError_t launch_residual_ln(const float* y, const float* r, const float* g, co
                               float* a, int* err, hipStream_t s, float qmult) {
   if (rows <= 0) return hipSuccess;
   if (d % 64) return hipErrorInvalidValue;
-  // Width 512 (decode and encoder): two waves share each row's speculative
-  // folds.  Other widths (op level): one wave per row, sequential folds.
-  if (d == kLnSpecD) {
-    hipLaunchKernelGGL(k_residual_ln_spec, dim3(rows), dim3(64 * kSpecWaves), 0, s, y, r, g, b, rows_dev, out, q, a, err,
-                       qmult);
-    return hipGetLastError();
-  }
+  // One wave per row, four rows per workgroup: widths of 256, 384 and 512
+  // fold with the one-wave speculative folds, others sequentially.
   const dim3 grid((rows + 3) / 4), block(256);
 #define MH_LN(P) \
   hipLaunchKernelGGL(k_residual_ln<P>, grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err, qmult)

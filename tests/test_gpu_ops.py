@@ -140,12 +140,13 @@ def _ln_edge_rows(rng, d=512):
     return np.stack(rows)
 
 
-@pytest.mark.parametrize("d", [256, 384])
+@pytest.mark.parametrize("d", [256, 384, 512])
 def test_residual_layer_norm_single_wave_speculative_edges(pkg, orc, dev, d):
-    """Rows of 256 and 384 fold as two or three speculative 128-element chunks
-    inside one wave (the SSRU graph's LayerNorms): chunk boundaries where the
-    prefix cancels to near zero force refolds; the result is the sequential
-    fold's, bit for bit, and non-finite rows keep their NaN positions."""
+    """Rows of 256, 384 and 512 fold as two, three or four speculative
+    128-element chunks inside one wave (the LayerNorms of both graphs):
+    chunk boundaries where the prefix cancels to near zero force refolds; the
+    result is the sequential fold's, bit for bit, and non-finite rows keep
+    their NaN positions."""
     rng = np.random.default_rng(23 + d)
     z = np.concatenate([_ln_edge_rows(rng, d), rng.standard_normal((21, d)).astype(np.float32) * 3])
     y = (z * np.float32(0.75)).astype(np.float32)
@@ -180,8 +181,8 @@ def test_residual_layer_norm_single_wave_speculative_edges(pkg, orc, dev, d):
 
 
 def test_residual_layer_norm_few_rows_edge_cases(pkg, orc, dev):
-    """Rows of width 512 take the four-wave kernel (eight-chunk speculative
-    folds)."""
+    """Rows of width 512 (four speculative 128-element chunks in one wave):
+    the edge rows among ordinary ones, with their quantization."""
     rng = np.random.default_rng(17)
     z = _ln_edge_rows(rng)
     base = rng.standard_normal((48, 512)).astype(np.float32) * 2
