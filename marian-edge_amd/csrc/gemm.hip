@@ -297,8 +297,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 // per workgroup in LDS.  Each row's best (logit, id) key over the workgroup's
 // columns is written as one partial; the step finalizer reduces the partials.
 // ---------------------------------------------------------------------------
-constexpr int kVocabCT = 2;                       // column tiles per wave
-constexpr int kVocabCols = 4 * 16 * kVocabCT;     // 128 columns per workgroup
+constexpr int kVocabCols = 128;                   // columns per workgroup
+// Waves per workgroup: 8 of one column tile when the kernel builds the rows'
+// LayerNorm (at most 4 rows: 7.8 against 9.1 µs per launch with 4 waves), 4
+// of two tiles otherwise (10.1 against 10.8 µs at 5-64 rows).
+template <bool LNP>
+constexpr int kVocabWaves = LNP ? 8 : 4;
 constexpr int kVocabMaxK = 512;                   // K held in registers
 constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 
@@ -309,9 +313,12 @@ constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 // the weights'), takes its maximum and quantizes it into the LDS row the
 // matrix cores read.
 template <bool FULL, bool LNP>
-__global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
-  constexpr int KEYS = 4 * 16;  // per row: one key per (wave, lane column)
-  static_assert(kVocabLnMaxRows <= 4, "a wave per prologue row");
+__global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs g, Epilogue e) {
+  constexpr int kVocabThreads = 64 * kVocabWaves<LNP>;
+  constexpr int kVocabCT = kVocabCols / (16 * kVocabWaves<LNP>);  // column tiles per wave
+  constexpr int KEYS = kVocabWaves<LNP> * 16;  // per row: one key per (wave, lane column)
+  static_assert(kVocabCT * 16 * kVocabWaves<LNP> == kVocabCols, "whole tiles per wave");
+  static_assert(!LNP || (kVocabLnMaxRows <= kVocabWaves<LNP> && kVocabLnMaxRows <= 4), "a wave per prologue row");
   constexpr int PER = kVocabMaxK / 64;  // prologue rows: lane l holds elements l + 64j
   __shared__ __attribute__((aligned(16))) int8_t sA[kSkinnyRows * kVocabLds];
   __shared__ uint64_t sK[kSkinnyRows * (KEYS + 1)];
@@ -364,10 +371,11 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     live[ct] = ncol[ct] < g.N && ((e.flags & 2u) || !generation_masked((uint32_t)ncol[ct]));
   }
   // Activation rows of a 64-row chunk: thread t holds 16-byte pieces
-  // t + 256 j (row = piece / 32, piece % 32 < K / 16), all requested at once.
+  // t + kVocabThreads j (row = piece / 32, piece % 32 < K / 16), all
+  // requested at once.
   // The first chunk is requested for the rows below the host bound g.M (all
   // allocated) before the device row count arrives.
-  constexpr int kStage = kSkinnyRows * (kVocabMaxK / 16) / 256;
+  constexpr int kStage = kSkinnyRows * (kVocabMaxK / 16) / kVocabThreads;
   const int cpr = g.K >> 4;
   v4i st[kStage];
   float sa = 0.0f;
@@ -375,7 +383,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   if constexpr (!LNP) {
 #pragma unroll
     for (int j = 0; j < kStage; ++j) {
-      const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
+      const int c = tid + kVocabThreads * j, row = c >> 5, cc = c & 31;
       st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
                                          : zero4();
     }
@@ -409,7 +417,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     if (m0 > 0) {
 #pragma unroll
       for (int j = 0; j < kStage; ++j) {
-        const int c = tid + 256 * j, row = c >> 5, cc = c & 31;
+        const int c = tid + kVocabThreads * j, row = c >> 5, cc = c & 31;
         st[j] = (row < rows && cc < cpr)
                     ? *(const v4i*)(g.A + (int64_t)(m0 + row) * g.lda + cc * 16)
                     : zero4();
@@ -419,7 +427,7 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
     if constexpr (!LNP) {
 #pragma unroll
       for (int j = 0; j < kStage; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + kVocabThreads * j;
         *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
       }
       if (tid < kSkinnyRows) sAm[tid] = sa;
@@ -498,19 +506,22 @@ __global__ __launch_bounds__(256) void k_vocab_argmax(GemmArgs g, Epilogue e) {
       }
     }
     __syncthreads();
-    // 4 threads per row reduce its 64 parked keys.
+    // P threads per row reduce its KEYS parked keys.
     {
-      const int row = tid >> 2, part = tid & 3;
+      constexpr int P = kVocabThreads / kSkinnyRows;
+      static_assert(P == 4 || P == 8, "4 or 8 threads per row");
+      const int row = tid / P, part = tid % P;
       uint64_t best = 0;
       if (row < rows) {
 #pragma unroll
-        for (int j = 0; j < KEYS / 4; ++j) {
-          const uint64_t k = sK[row * (KEYS + 1) + part * (KEYS / 4) + j];
+        for (int j = 0; j < KEYS / P; ++j) {
+          const uint64_t k = sK[row * (KEYS + 1) + part * (KEYS / P) + j];
           best = k > best ? k : best;
         }
       }
       best = umax64(best, xor_lane_u64<1>(best));
       best = umax64(best, xor_lane_u64<2>(best));
+      if constexpr (P == 8) best = umax64(best, xor_lane_u64<4>(best));
       if (row < rows && part == 0)
         e.partials[(int64_t)(m0 + row) * e.partial_ld + blockIdx.x] = best;
     }
@@ -914,8 +925,9 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, int mode, const Epilogue& e, hi
 hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t s,
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
-  const dim3 grid((g.N + kVocabCols - 1) / kVocabCols), block(256);
   const RowPrologue& p = g.pro;
+  const dim3 grid((g.N + kVocabCols - 1) / kVocabCols),
+      block(64 * (p.kind == PRO_LN ? kVocabWaves<true> : kVocabWaves<false>));
   if (p.kind != PRO_NONE &&
       (p.kind != PRO_LN || g.K != kVocabMaxK || g.M > kVocabLnMaxRows || !p.y || !p.r || !p.gamma || !p.beta))
     return hipErrorInvalidValue;
