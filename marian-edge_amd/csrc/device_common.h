@@ -260,7 +260,7 @@ __device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, f
 // a refold happens.  All lanes return the result.
 constexpr int kSwStride = 132;
 template <int NC>
-constexpr int kSwCand = NC == 2 ? 32 : NC == 3 ? 24 : 16;
+constexpr int kSwCand = 63 / (NC - 1);  // chunk 0's start is known: its group needs one lane
 template <int NC>
 constexpr int kSwLead = 64 - (NC - 1) * kSwCand<NC>;
 
@@ -273,7 +273,7 @@ __device__ __forceinline__ float spec_fold_wave(const float* p, const float (&es
   int base[NC];
 #pragma unroll
   for (int k = 1; k < NC; ++k)
-    base[k] = min(max(float_key(est[k]), INT32_MIN + W / 2), INT32_MAX - W / 2 + 1) - W / 2;
+    base[k] = min(max(float_key(est[k]), INT32_MIN + W / 2), INT32_MAX - (W - 1) + W / 2) - W / 2;
   float st = init;
 #pragma unroll
   for (int k = 1; k < NC; ++k)
