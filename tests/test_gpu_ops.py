@@ -48,6 +48,25 @@ def test_q8_linear_sweep(pkg, orc, dev, M, K, N):
     assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), "dequant not bit-identical"
 
 
+@pytest.mark.parametrize("K,N", [(2048, 512), (1536, 384)])
+@pytest.mark.parametrize("M", [17, 33, 50, 64])
+def test_q8_linear_long_k_row_groups(pkg, orc, dev, M, K, N):
+    """fp32-only outputs above 16 rows at K = 1536 or 2048 run the skinny
+    kernel with one 16-row group per workgroup (the decode FFN
+    down-projection's path); ragged row counts leave a partial last group.
+    Bit-identical to the oracle."""
+    print(f"q8_linear row groups M={M} K={K} N={N}", flush=True)
+    a, w, mult, bias = pkg.gemm_inputs(M, K, N)
+    y_ref, _, _, _ = orc.linear_forward(a, w, mult, bias, threads=16)
+    da, dw, dm, db = (dev.DeviceArray.from_host(x) for x in (a, w, mult, bias))
+    df = dev.DeviceArray.zeros((M, N), np.float32)
+    err = dev.DeviceArray.zeros(1, np.int32)
+    dev.q8_linear(da, dw, dm, db, None, df, err=err)
+    dev.synchronize()
+    assert err.host()[0] == 0
+    assert np.array_equal(df.host().view(np.uint32), y_ref.view(np.uint32))
+
+
 def test_quantize_rows_matches_oracle(pkg, orc, dev):
     rng = np.random.default_rng(11)
     x = (rng.standard_normal((300, 2048)) * rng.uniform(0.01, 50, size=(300, 1))).astype(np.float32)
