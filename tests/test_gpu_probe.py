@@ -129,6 +129,30 @@ def test_probe_ragged_64(pkg, orc, full, step):
     check(f"ragged-64, step {step}", res)
 
 
+def test_vocabulary_over_32768_ids_token_exact(pkg, orc):
+    """A 40000-id vocabulary: 313 argmax partials per row, more than the
+    finalizer's first pass of 4 x 64 per lane requests.  70 sentences, so the
+    steps run every finalizer (the workgroup scan above 64 rows, one wave per
+    8 rows up to 64, the 4- and 8-row single waves); tokens and one step's
+    logits against the oracle."""
+    g = pkg.Geometry(vocab=40000, dim=256, heads=4, ffn_dim=1024, encoder_layers=1,
+                     decoder_layers=2)
+    model = pkg.seeded_model(seed=17, geometry=g)
+    om = orc.OracleModel(model)
+    b = pkg.ragged_batch(seed=41, n=70, vocab=g.vocab)
+    with pkg.HipEngine(model, limits=b.limits) as e:
+        got = e.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, b.flags).rows()
+        want = orc.translate(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, b.flags,
+                             threads=ORACLE_THREADS)
+        print(f"vocabulary 40000: {sum(map(len, got))} tokens", flush=True)
+        assert got == want
+        sub = b.subset(range(20))
+        res = probe_both(pkg, orc, e, om, sub.tokens, sub.offsets, [4] * 20, pkg.FLAG_IGNORE_EOS,
+                         3, b.limits)
+        assert check("vocabulary 40000, 20 rows", res) == 20
+        assert e.is_ready()
+
+
 @pytest.mark.parametrize("geom", [dict(dim=256, heads=4, ffn_dim=1024),
                                   dict(dim=512, heads=8, ffn_dim=1536),
                                   dict(dim=128, heads=2, ffn_dim=320),
