@@ -1150,6 +1150,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   // without, the whole vocabulary under the generation mask.
   // A pending LayerNorm (pend.kind == PRO_LN) is built by the scoring kernel
   // itself and quantized with qmult (> 0: static) or the row's own multiplier.
+  int* host_active = nullptr;  // pinned host slot for this step's active count (poll steps)
   auto score = [&](int rows, uint32_t t, RowPrologue& pend, float qmult = 0.0f) -> hipError_t {
     if (cand) {
       CandArgs c;
@@ -1223,6 +1224,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
     f.step = (int)t;
     f.flags = flags;
     f.active_hist = HIST;
+    f.host_active = host_active;
     return launch_finalize(f, s);
   };
 
@@ -1748,14 +1750,18 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   };
 
   // Poll the active count without blocking; stop launching once it has
-  // reached zero (rows can end early on EOS).
+  // reached zero (rows can end early on EOS).  On every kPoll-th step the
+  // finalizer also stores the new count in a pinned host slot (no copy in
+  // the stream); the slot is read once the event after that step has
+  // completed.  A slot starts at -1, and a count read late is an older,
+  // larger one: polling only ever stops the loop late, never early.
   constexpr uint32_t kPoll = 8;
   int poll_slot = 0;
   uint32_t polls = 0;
   bool done = n_active0 == 0;
+  E->pinned[0] = E->pinned[1] = -1;
   auto poll = [&]() -> hipError_t {
-    // issue a new poll, then look at the previous one if it has landed
-    MH_TRY(hipMemcpyAsync(E->pinned + poll_slot, d_nact, sizeof(int), hipMemcpyDeviceToHost, s));
+    // this step's count is on its way; look at the previous one if it has landed
     MH_TRY(hipEventRecord(E->ev[3 + poll_slot], s));
     const int other = poll_slot ^ 1;
     if (polls > 0 && hipEventQuery(E->ev[3 + other]) == hipSuccess && E->pinned[other] == 0) done = true;
@@ -1767,6 +1773,7 @@ static int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_token
   for (uint32_t t = 0; t < gen_limit && !done; ++t) {
     const int rows = (int)remaining[t];
     if (rows == 0) break;
+    host_active = (t + 1) % kPoll == 0 ? E->pinned + poll_slot : nullptr;
     MH_HIP(E->ssru ? emit_step_ssru(rows, t) : emit_step(make_plan(rows, (int)t + 1, (int)Lmax), t));
     if (time_steps) MH_HIP(hipEventRecord(E->step_ev[t], s));
     ++steps;

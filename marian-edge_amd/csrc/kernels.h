@@ -395,6 +395,7 @@ struct FinalizeArgs {
   int step = 0;
   uint32_t flags = 0;
   uint32_t* active_hist = nullptr;  // optional: active_hist[step] = rows this step ran on
+  int* host_active = nullptr;       // optional, pinned host memory: the new active count
 };
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 

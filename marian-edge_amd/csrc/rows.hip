@@ -389,6 +389,7 @@ __global__ __launch_bounds__(W * 64) void k_finalize_wave(FinalizeArgs f) {
     if (n_dev > ub && f.err) *f.err = 3;
     if (f.active_hist) f.active_hist[f.step] = (uint32_t)n;
     *f.n_active = total;
+    if (f.host_active) *f.host_active = total;
   }
 }
 
@@ -506,6 +507,7 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
     if (n_dev > ub && f.err) *f.err = 3;
     if (f.active_hist) f.active_hist[f.step] = (uint32_t)n;
     *f.n_active = s_total;
+    if (f.host_active) *f.host_active = s_total;
   }
 }
 
