@@ -28,6 +28,15 @@
  *   marian_hip_translate_shortlisted
  *                              translate_token_ids with the lexical shortlist's
  *                              candidates, q8_engine.rs:361-362, 576-584, 749-790
+ *   marian_hip_warmup          Q8CpuEngine::warmup q8_engine.rs:349-351 (called by
+ *                              the backends at load, marian-cpu/src/backend.rs:448,
+ *                              812, 853, 896)
+ *   marian_hip_validate_batch  Q8CpuEngine::validate_batch q8_engine.rs:468-509 and
+ *                              validate_work_shape :1103-1119, host only
+ *   marian_hip_reserve         no counterpart: sizes the engine's grow-only decode
+ *                              buffers (the reference's pooled scratch,
+ *                              q8_engine.rs:733-747) for a serving worker's
+ *                              largest batch at load time
  *
  * Op-level entry points (device pointers, caller's stream) replace the
  * reference's building blocks and exist so each kernel can be checked and timed
@@ -68,8 +77,10 @@
 extern "C" {
 #endif
 
-#define MARIAN_HIP_ABI_VERSION 3 /* 2: marian_hip_attention takes head_dim;
-                                    3: the Transformer-SSRU engine, shortlisted translate */
+#define MARIAN_HIP_ABI_VERSION 4 /* 2: marian_hip_attention takes head_dim;
+                                    3: the Transformer-SSRU engine, shortlisted translate;
+                                    4: warmup, reserve, validate_batch, stats
+                                       launched_steps and allocations */
 
 enum {
   MARIAN_HIP_OK = 0,
@@ -270,8 +281,9 @@ int marian_hip_engine_create_ssru(const marian_hip_ssru_model* model,
  * in list order, the first maximum winning (select_token over
  * LexicalShortlist::candidates: prepare_candidates, q8_engine.rs:576-584, and
  * :749-790).  The lists come from the caller (the reference builds them from
- * the source ids with its shortlist, shortlist.rs:150-198); no generation mask
- * is applied to them.  An empty list or an id >= the target vocabulary is
+ * the source ids with its shortlist, shortlist.rs:150-198, sorted and without
+ * repeats); no generation mask is applied to them.  An empty list, a list that
+ * is not strictly ascending or an id >= the target vocabulary is
  * MARIAN_HIP_ERR_INVALID_INPUT.  Works on either engine kind. */
 int marian_hip_translate_shortlisted(marian_hip_engine* engine, const int32_t* tokens,
                                      size_t n_tokens, const uint32_t* offsets, size_t n_offsets,
@@ -279,6 +291,46 @@ int marian_hip_translate_shortlisted(marian_hip_engine* engine, const int32_t* t
                                      const uint32_t* candidates,
                                      const uint32_t* candidate_offsets, int32_t* out_tokens,
                                      size_t out_cap, uint32_t* out_offsets, size_t* out_len);
+
+/* Q8CpuEngine::warmup (crates/marian-cpu/src/q8_engine.rs:349-351): translates
+ * the one-sentence batch [2, 0] with at most 4 output tokens, so the first
+ * request does not pay for loading the kernels' code objects or allocating
+ * the decode buffers.  The reference's backends call it once after loading
+ * (crates/marian-cpu/src/backend.rs:448, 812, 853, 896); a failure there is
+ * BackendError::Inference.  Needs a vocabulary of at least 3 ids. */
+int marian_hip_warmup(marian_hip_engine* engine);
+
+/* Capacity of a serving worker's largest call, for marian_hip_reserve. */
+typedef struct {
+  uint32_t sentences;      /* sentences (packed rows) of one call, 1..4096 */
+  uint32_t source_tokens;  /* source tokens of one call (sum over sentences) */
+  uint32_t output_tokens;  /* sum over sentences of the generation limits */
+  uint32_t steps;          /* longest generation limit */
+  uint32_t candidate_ids;  /* shortlisted calls: candidate ids of one call (0: none) */
+  uint32_t max_candidates; /* shortlisted calls: longest candidate list */
+} marian_hip_capacity;
+/* No counterpart in the reference (its scratch is pooled per call,
+ * q8_engine.rs:733-747, and grows on the heap as needed): sizes the engine's
+ * grow-only device buffers and pinned host staging for calls up to
+ * `capacity`, so that such calls allocate nothing (marian_hip_stats.allocations
+ * = 0) and a serving worker never allocates in the middle of a request.
+ * Larger calls still work and grow the buffers.  Buffers never shrink. */
+int marian_hip_reserve(marian_hip_engine* engine, const marian_hip_capacity* capacity);
+
+/* The host checks marian_hip_translate_token_ids and
+ * marian_hip_translate_shortlisted run before they touch the device, with no
+ * engine or device: Q8CpuEngine::validate_batch (q8_engine.rs:468-509) and
+ * validate_work_shape (:1103-1119) under `limits` (NULL: the reference's
+ * values; 0 disables a cap), source ids below source_vocab, and, when
+ * candidate_offsets is given, candidate lists that are non-empty, strictly
+ * ascending (as LexicalShortlist::candidates returns them,
+ * shortlist.rs:150-198) and below target_vocab.  Returns MARIAN_HIP_OK or
+ * MARIAN_HIP_ERR_INVALID_INPUT with the reason written to msg (may be NULL). */
+int marian_hip_validate_batch(const marian_hip_limits* limits, uint32_t source_vocab,
+                              uint32_t target_vocab, const int32_t* tokens, size_t n_tokens,
+                              const uint32_t* offsets, size_t n_offsets,
+                              const uint32_t* candidates, const uint32_t* candidate_offsets,
+                              char* msg, size_t msg_cap);
 
 int marian_hip_is_ready(const marian_hip_engine* engine);
 /* Last error message of this engine ("" if none); valid until the next call. */
@@ -288,10 +340,15 @@ const char* marian_hip_last_error(const marian_hip_engine* engine);
 int marian_hip_info(const marian_hip_engine* engine, char* buf, size_t cap);
 
 /* Timing of the last translate call, in milliseconds (events on the engine's
- * stream): total (packed inputs resident in HBM to generated tokens in host
- * memory), encoder, decode loop, the
- * summed device time of the vocabulary projection + argmax kernel and the
- * number of its launches, and the number of decode steps run. */
+ * stream): total (from the upload of the packed batch to the generated tokens
+ * in host memory), encoder (upload included), decode loop, the summed device
+ * time of the vocabulary projection + argmax kernel and the number of its
+ * launches, and the number of decode steps that ran on rows.
+ * launched_steps counts the steps enqueued: rows that end on EOS are seen by
+ * the host a few steps late, and steps enqueued after the last row finished
+ * run on no rows.  allocations counts the device and pinned host buffers the
+ * call had to (re)allocate: 0 once marian_hip_reserve (or an earlier call)
+ * sized them for the batch. */
 typedef struct {
   double total_ms, encoder_ms, decode_ms;
   double vocab_kernel_ms;
@@ -299,13 +356,15 @@ typedef struct {
   uint32_t decode_steps;
   uint32_t max_active_rows;
   uint64_t generated_tokens;
+  uint32_t launched_steps;
+  uint32_t allocations;
 } marian_hip_stats;
 int marian_hip_last_stats(const marian_hip_engine* engine, marian_hip_stats* stats);
 /* Timing of later translate calls (default 0: none).
  * MARIAN_HIP_TIME_STEPS: one event at the end of every decode step
  *   (marian_hip_last_step_trace reports the times); cheap.
- * MARIAN_HIP_TIME_KERNELS: the vocabulary and attention-block launches record
- *   events from their own dispatches (marian_hip_stats.vocab_kernel_ms and
+ * MARIAN_HIP_TIME_KERNELS: the vocabulary, attention-block and decode
+ *   attention launches record events from their own dispatches (marian_hip_stats.vocab_kernel_ms and
  *   marian_hip_last_kernel_trace are filled); this adds several microseconds
  *   of device time per timed launch, so throughput is measured without it. */
 #define MARIAN_HIP_TIME_STEPS 1u
@@ -315,6 +374,8 @@ int marian_hip_set_timing(marian_hip_engine* engine, uint32_t flags);
 #define MARIAN_HIP_KERNEL_VOCAB 0       /* vocabulary projection + argmax partials */
 #define MARIAN_HIP_KERNEL_SELF_BLOCK 1  /* decoder self-attention block */
 #define MARIAN_HIP_KERNEL_CROSS_BLOCK 2 /* decoder cross-attention block */
+#define MARIAN_HIP_KERNEL_SELF_ATTN 3   /* decoder self-attention kernel (steps the blocks do not cover) */
+#define MARIAN_HIP_KERNEL_CROSS_ATTN 4  /* decoder cross-attention kernel (likewise) */
 /* With MARIAN_HIP_TIME_KERNELS: one record per timed decode launch of the last
  * translate call, in launch order: its kind, decode step, decoder layer and
  * device duration in microseconds (from events its own dispatch recorded).

@@ -7,7 +7,8 @@ reference's token-level engine interface plus synthetic-model generators.
 
 from . import _lib
 from .engine import (BackendError, BatchOutput, BufferTooSmall, DeviceError, HipBackend,
-                     HipEngine, InferenceError, InvalidInput, ModelError, make_limits)
+                     HipEngine, InferenceError, InvalidInput, ModelError, capacity_for, make_limits,
+                     validate_batch)
 from .text import (HipTextBackend, HipTokenEngine, SegmentError, TextSegment, TranslationInput,
                    TranslationOutput, UnsupportedDirection, segment_text, translate_with_engine)
 from .synthetic import (Batch, Geometry, LIFTED_LIMITS, REFERENCE_LIMITS, SeededModel,
@@ -20,7 +21,8 @@ FLAG_NO_GENERATION_MASK = _lib.FLAG_NO_GENERATION_MASK
 
 __all__ = [
     "BackendError", "BatchOutput", "BufferTooSmall", "DeviceError", "HipBackend", "HipEngine",
-    "InferenceError", "InvalidInput", "ModelError", "make_limits", "Batch", "Geometry",
+    "InferenceError", "InvalidInput", "ModelError", "make_limits", "capacity_for", "validate_batch",
+    "Batch", "Geometry",
     "LIFTED_LIMITS", "REFERENCE_LIMITS", "SeededModel", "SsruGeometry", "SsruModel",
     "seeded_ssru_model", "attention_inputs", "gemm_inputs",
     "ragged_batch", "seeded_model", "single_sentence_batch", "stress_batch", "GEMM_SHAPES",

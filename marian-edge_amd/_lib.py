@@ -106,7 +106,15 @@ class Stats(C.Structure):
         ("total_ms", C.c_double), ("encoder_ms", C.c_double), ("decode_ms", C.c_double),
         ("vocab_kernel_ms", C.c_double), ("vocab_kernel_launches", C.c_uint32),
         ("decode_steps", C.c_uint32), ("max_active_rows", C.c_uint32),
-        ("generated_tokens", C.c_uint64),
+        ("generated_tokens", C.c_uint64), ("launched_steps", C.c_uint32),
+        ("allocations", C.c_uint32),
+    ]
+
+
+class Capacity(C.Structure):
+    _fields_ = [
+        ("sentences", C.c_uint32), ("source_tokens", C.c_uint32), ("output_tokens", C.c_uint32),
+        ("steps", C.c_uint32), ("candidate_ids", C.c_uint32), ("max_candidates", C.c_uint32),
     ]
 
 
@@ -126,6 +134,10 @@ SIGNATURES = {
                                                  C.POINTER(_P)]),
     "marian_hip_translate_shortlisted": (C.c_int, [_P, _P, _SZ, _P, _SZ, _P, C.c_uint32, _P, _P, _P, _SZ,
                                                    _P, C.POINTER(_SZ)]),
+    "marian_hip_warmup": (C.c_int, [_P]),
+    "marian_hip_reserve": (C.c_int, [_P, C.POINTER(Capacity)]),
+    "marian_hip_validate_batch": (C.c_int, [C.POINTER(Limits), C.c_uint32, C.c_uint32, _P, _SZ, _P, _SZ, _P, _P,
+                                            C.c_char_p, _SZ]),
     "marian_hip_is_ready": (C.c_int, [_P]),
     "marian_hip_last_error": (C.c_char_p, [_P]),
     "marian_hip_info": (C.c_int, [_P, C.c_char_p, _SZ]),

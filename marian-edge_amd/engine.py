@@ -156,13 +156,53 @@ def make_limits(limits: dict | None) -> _lib.Limits:
                        d["max_batch"], d["max_source_tokens"], d["max_padded_cells"])
 
 
+def capacity_for(batches) -> dict:
+    """The marian_hip_reserve capacity that covers every batch in `batches`
+    (objects with tokens, offsets and max_output_tokens, e.g. synthetic.Batch),
+    with the generation limits as requested (caps may only lower them)."""
+    cap = dict(sentences=0, source_tokens=0, output_tokens=0, steps=0)
+    for b in batches:
+        lim = np.asarray(b.max_output_tokens, np.int64)
+        cap["sentences"] = max(cap["sentences"], len(b.offsets) - 1)
+        cap["source_tokens"] = max(cap["source_tokens"], int(np.asarray(b.tokens).size))
+        cap["output_tokens"] = max(cap["output_tokens"], int(np.minimum(lim, 4096).sum()))
+        cap["steps"] = max(cap["steps"], int(np.minimum(lim, 4096).max(initial=0)))
+    return cap
+
+
+def validate_batch(tokens, offsets, limits: dict | None = None, source_vocab: int = 32000,
+                   target_vocab: int = 32000, candidates=None, candidate_offsets=None) -> None:
+    """The library's host-only batch checks (marian_hip_validate_batch, the
+    reference's validate_batch, q8_engine.rs:468-509); raises InvalidInput
+    with the reference's message.  Needs no device."""
+    lib = _lib.load()
+    toks = np.ascontiguousarray(tokens, np.int32)
+    offs = np.ascontiguousarray(offsets, np.uint32)
+    lim = make_limits(limits)
+    cand = coff = None
+    if candidates is not None or candidate_offsets is not None:
+        cand = np.ascontiguousarray(candidates, np.uint32)
+        coff = np.ascontiguousarray(candidate_offsets, np.uint32)
+    msg = C.create_string_buffer(512)
+    rc = lib.marian_hip_validate_batch(
+        C.byref(lim), source_vocab, target_vocab, _ptr(toks) if toks.size else None, toks.size,
+        _ptr(offs) if offs.size else None, offs.size,
+        _ptr(cand) if cand is not None and cand.size else None,
+        _ptr(coff) if coff is not None and coff.size else None, msg, len(msg))
+    if rc != _lib.OK:
+        raise _ERRORS.get(rc, BackendError)(msg.value.decode(errors="replace"))
+
+
 class HipEngine:
     """Owns one marian_hip_engine (one device, one stream, one owner thread)."""
 
-    def __init__(self, model: SeededModel | SsruModel, limits: dict | None = None, device: int = 0):
+    def __init__(self, model: SeededModel | SsruModel, limits: dict | None = None, device: int = 0,
+                 capacity: dict | None = None):
         """A SeededModel gives the transformer-decoder engine
         (marian_hip_engine_create), an SsruModel the reference's
-        Transformer-SSRU graph (marian_hip_engine_create_ssru)."""
+        Transformer-SSRU graph (marian_hip_engine_create_ssru).  `capacity`
+        (marian_hip_capacity fields, e.g. from capacity_for) sizes the decode
+        buffers at creation, so calls within it allocate nothing."""
         self._lib = _lib.load()
         self._limits = make_limits(limits)
         handle = C.c_void_p()
@@ -180,6 +220,24 @@ class HipEngine:
                 f"engine creation failed ({rc}): {self._lib.marian_hip_last_op_error().decode(errors='replace')}")
         self._h = handle
         self.geometry = model.geometry
+        if capacity:
+            self.reserve(**capacity)
+
+    def reserve(self, sentences: int, source_tokens: int, output_tokens: int, steps: int,
+                candidate_ids: int = 0, max_candidates: int = 0) -> None:
+        """marian_hip_reserve: size the buffers for calls up to this capacity."""
+        cap = _lib.Capacity(int(sentences), int(source_tokens), int(output_tokens), int(steps),
+                            int(candidate_ids), int(max_candidates))
+        rc = self._lib.marian_hip_reserve(self._h, C.byref(cap))
+        if rc != _lib.OK:
+            self._raise(rc)
+
+    def warmup(self) -> None:
+        """Q8CpuEngine::warmup (q8_engine.rs:349-351): the batch [2, 0], at
+        most 4 output tokens."""
+        rc = self._lib.marian_hip_warmup(self._h)
+        if rc != _lib.OK:
+            self._raise(rc)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -285,7 +343,7 @@ class HipEngine:
         self._lib.marian_hip_last_step_trace(self._h, _ptr(rows), _ptr(ms), n.value, C.byref(n))
         return rows[:n.value], ms[:n.value]
 
-    KERNEL_VOCAB, KERNEL_SELF_BLOCK, KERNEL_CROSS_BLOCK = 0, 1, 2
+    KERNEL_VOCAB, KERNEL_SELF_BLOCK, KERNEL_CROSS_BLOCK, KERNEL_SELF_ATTN, KERNEL_CROSS_ATTN = 0, 1, 2, 3, 4
 
     def last_kernel_trace(self) -> dict:
         """Per timed decode launch of the last call (kernel timing on):
@@ -321,11 +379,18 @@ class HipBackend:
     materializes none: a decode step here costs about the same from 1 to 4 rows
     and more above, so copies of a row only add work."""
 
-    def __init__(self, engine: HipEngine, duplicate_batch_width: int = 1):
+    def __init__(self, engine: HipEngine, duplicate_batch_width: int = 1, warmup: bool = True):
+        """Like the reference's backends, warms the engine up once at load
+        (backend.rs:448); a failure there is an InferenceError."""
         if duplicate_batch_width < 1:
             raise InvalidInput("duplicate_batch_width must be at least 1")
         self.engine = engine
         self.duplicate_batch_width = int(duplicate_batch_width)
+        if warmup:
+            try:
+                engine.warmup()
+            except BackendError as e:
+                raise InferenceError(f"HIP warmup failed: {e}") from e
 
     def info(self) -> dict:
         return self.engine.info()

@@ -64,6 +64,9 @@ pub struct HipBackend {
 }
 
 impl HipBackend {
+    /// Builds the backend and warms its engine up once, as the reference's
+    /// backends do at load (Q8CpuBackend, crates/marian-cpu/src/backend.rs:810-813);
+    /// a warmup failure is BackendError::Inference.
     #[allow(clippy::too_many_arguments)]
     pub fn new(
         engine: HipEngine,
@@ -74,8 +77,11 @@ impl HipBackend {
         target_lang: impl Into<String>,
         model_id: impl Into<String>,
         eos_id: i32,
-    ) -> Self {
-        Self {
+    ) -> Result<Self, BackendError> {
+        engine
+            .warmup()
+            .map_err(|error| BackendError::Inference(format!("HIP warmup failed: {error}")))?;
+        Ok(Self {
             engine: HipTokenEngine { engine, shortlist },
             source,
             target,
@@ -84,7 +90,7 @@ impl HipBackend {
             model_id: model_id.into(),
             eos_id,
             duplicate_batch_width: 1,
-        }
+        })
     }
 
     pub fn with_duplicate_batch_width(mut self, width: usize) -> Self {
@@ -166,5 +172,24 @@ impl TranslationBackend for HipBackend {
             )));
         }
         Ok(first_copy.into_iter().map(|i| outputs[i].clone()).collect())
+    }
+}
+
+/// Scheduler settings for a HIP worker (marian-core's `SchedulerConfig`,
+/// crates/marian-core/src/scheduler.rs:22-44).  Measured on one MI355X with
+/// batches of 1 to 256 sentences of the 64-sentence ragged distribution: a
+/// decode step costs nearly the same from 1 to 64 rows, so throughput grows
+/// from 11.7k target tokens/s at 1 sentence to 267k at 64 and 498k at 256
+/// (profiles/batch_sweep_ragged.md).  A model of `worker_loop` over those
+/// batch times gives the lowest median latency at 10/50/90% load with 256
+/// requests per batch and a 100 us window; the CLI's 16 and 750 us saturate
+/// the worker at about a fifth of that load.  The length-bucket cap is raised
+/// so that it never limits a batch below 256 (the engine does not pad).
+pub fn recommended_scheduler_config() -> marian_core::SchedulerConfig {
+    marian_core::SchedulerConfig {
+        max_batch_size: 256,
+        max_padded_source_chars: 256 * 1024,
+        batch_window: std::time::Duration::from_micros(100),
+        ..marian_core::SchedulerConfig::default()
     }
 }

@@ -19,6 +19,9 @@ use crate::{
 /// Work limits (crates/marian-cpu/src/limits.rs:3-7); 0 disables a cap.
 pub type Limits = ffi::marian_hip_limits;
 
+/// The largest call a serving worker will make, for `HipEngine::reserve`.
+pub type Capacity = ffi::marian_hip_capacity;
+
 /// The reference's caps.
 pub const REFERENCE_LIMITS: Limits = Limits {
     max_length_factor: 2,
@@ -73,6 +76,27 @@ impl HipEngine {
             (ffi::OK, Some(raw)) => Ok(Self { raw, _owner_thread: PhantomData }),
             (ffi::OK, None) => Err(creation_error(ffi::ERR_DEVICE)),
             (code, _) => Err(creation_error(code)),
+        }
+    }
+
+    /// Q8CpuEngine::warmup (crates/marian-cpu/src/q8_engine.rs:349-351): the
+    /// batch [2, 0] with at most 4 output tokens, so the first request does not
+    /// pay for code-object loading or the first buffer allocations.
+    pub fn warmup(&self) -> Result<(), String> {
+        // SAFETY: self.raw is a live engine handle.
+        match unsafe { ffi::marian_hip_warmup(self.raw.as_ptr()) } {
+            ffi::OK => Ok(()),
+            _ => Err(self.last_error()),
+        }
+    }
+
+    /// Sizes the engine's decode buffers for calls up to `capacity`, so that
+    /// such calls allocate nothing (`last_stats().allocations == 0`).
+    pub fn reserve(&self, capacity: &Capacity) -> Result<(), String> {
+        // SAFETY: self.raw is a live engine handle; capacity is read during the call.
+        match unsafe { ffi::marian_hip_reserve(self.raw.as_ptr(), capacity) } {
+            ffi::OK => Ok(()),
+            _ => Err(self.last_error()),
         }
     }
 

@@ -6,7 +6,7 @@
 
 use std::ffi::{c_char, c_int};
 
-pub const MARIAN_HIP_ABI_VERSION: u32 = 3;
+pub const MARIAN_HIP_ABI_VERSION: u32 = 4;
 
 pub const OK: c_int = 0;
 pub const ERR_INVALID_INPUT: c_int = -1;
@@ -157,6 +157,19 @@ pub struct marian_hip_stats {
     pub decode_steps: u32,
     pub max_active_rows: u32,
     pub generated_tokens: u64,
+    pub launched_steps: u32,
+    pub allocations: u32,
+}
+
+#[repr(C)]
+#[derive(Clone, Copy, Default, Debug)]
+pub struct marian_hip_capacity {
+    pub sentences: u32,
+    pub source_tokens: u32,
+    pub output_tokens: u32,
+    pub steps: u32,
+    pub candidate_ids: u32,
+    pub max_candidates: u32,
 }
 
 /// Opaque engine handle.
@@ -206,6 +219,21 @@ extern "C" {
         out_cap: usize,
         out_offsets: *mut u32,
         out_len: *mut usize,
+    ) -> c_int;
+    pub fn marian_hip_warmup(engine: *mut marian_hip_engine) -> c_int;
+    pub fn marian_hip_reserve(engine: *mut marian_hip_engine, capacity: *const marian_hip_capacity) -> c_int;
+    pub fn marian_hip_validate_batch(
+        limits: *const marian_hip_limits,
+        source_vocab: u32,
+        target_vocab: u32,
+        tokens: *const i32,
+        n_tokens: usize,
+        offsets: *const u32,
+        n_offsets: usize,
+        candidates: *const u32,
+        candidate_offsets: *const u32,
+        msg: *mut c_char,
+        msg_cap: usize,
     ) -> c_int;
     pub fn marian_hip_is_ready(engine: *const marian_hip_engine) -> c_int;
     pub fn marian_hip_last_error(engine: *const marian_hip_engine) -> *const c_char;

@@ -10,8 +10,8 @@ pub mod engine;
 pub mod ffi;
 pub mod model;
 
-pub use backend::{HipBackend, HipTokenEngine};
-pub use engine::{HipEngine, Limits, REFERENCE_LIMITS};
+pub use backend::{HipBackend, HipTokenEngine, recommended_scheduler_config};
+pub use engine::{Capacity, HipEngine, Limits, REFERENCE_LIMITS};
 pub use model::{
     DecoderLayer, EncoderLayer, Linear, Norm, SsruDecoderLayer, SsruEncoderLayer, SsruModel, StaticLinear,
     TransformerModel,

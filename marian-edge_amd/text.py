@@ -571,10 +571,15 @@ class HipTextBackend:
 
     def __init__(self, engine, source: TextTokenizer, target: TextTokenizer, source_lang: str,
                  target_lang: str, eos_id: int = 0, shortlist=None, model_id: str = "marian-q8",
-                 duplicate_batch_width: int = 1):
+                 duplicate_batch_width: int = 1, warmup: bool = True):
         if duplicate_batch_width < 1:
             raise InvalidInput("duplicate_batch_width must be at least 1")
         self.engine = engine
+        if warmup:  # Q8CpuBackend warms its engine at load (backend.rs:810-814)
+            try:
+                engine.warmup()
+            except BackendError as e:
+                raise InferenceError(f"HIP warmup failed: {e}") from e
         self.token_engine = HipTokenEngine(engine, shortlist)
         self.source, self.target = source, target
         self.source_lang, self.target_lang = source_lang, target_lang

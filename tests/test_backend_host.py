@@ -12,9 +12,16 @@ import pytest
 
 
 class StubEngine:
-    def __init__(self, pkg):
+    def __init__(self, pkg, warmup_error=None):
         self.pkg = pkg
         self.calls = []
+        self.warmups = 0
+        self.warmup_error = warmup_error
+
+    def warmup(self):
+        self.warmups += 1
+        if self.warmup_error:
+            raise self.warmup_error
 
     def translate_token_ids(self, toks, offs, limits, flags=0):
         self.calls.append((np.asarray(toks).copy(), np.asarray(offs).copy(), list(limits), flags))
@@ -50,3 +57,17 @@ def test_malformed_repetitions_are_invalid_input(pkg, reps):
     be = pkg.HipBackend(StubEngine(pkg))
     with pytest.raises(pkg.InvalidInput):
         be.translate_token_batch([[5], [6]], [1, 1], repetitions=reps)
+
+
+def test_backend_warms_its_engine_up_once_at_load(pkg):
+    """Q8CpuBackend warms its engine at load (crates/marian-cpu/src/backend.rs:810-813)."""
+    eng = StubEngine(pkg)
+    be = pkg.HipBackend(eng)
+    assert eng.warmups == 1
+    be.translate_token_batch([[5]], [2])
+    assert eng.warmups == 1 and len(eng.calls) == 1
+
+
+def test_warmup_failure_is_an_inference_error(pkg):
+    with pytest.raises(pkg.InferenceError, match="HIP warmup failed"):
+        pkg.HipBackend(StubEngine(pkg, warmup_error=pkg.DeviceError("no device")))

@@ -157,7 +157,10 @@ def test_vocabulary_over_32768_ids_token_exact(pkg, orc):
                                   dict(dim=512, heads=8, ffn_dim=1536),
                                   dict(dim=128, heads=2, ffn_dim=320),
                                   dict(dim=384, heads=8, ffn_dim=1536),
-                                  dict(dim=192, heads=4, ffn_dim=768)])
+                                  dict(dim=192, heads=4, ffn_dim=768),
+                                  dict(dim=64, heads=1, ffn_dim=256),
+                                  dict(dim=320, heads=5, ffn_dim=1280),
+                                  dict(dim=448, heads=7, ffn_dim=1792)])
 def test_other_geometries_token_exact(pkg, orc, geom):
     g = pkg.Geometry(vocab=3000, encoder_layers=2, decoder_layers=2, **geom)
     model = pkg.seeded_model(seed=13, geometry=g)

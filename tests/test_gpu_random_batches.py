@@ -60,8 +60,8 @@ def test_rows_ending_on_eos_stop_the_launches(pkg, orc):
     """A model whose output bias makes id 0 (EOS) every row's argmax: all
     rows end at step 0.  The decode loop learns it from the count the
     finalizer stores in pinned host memory every 8 steps and stops
-    launching within a few poll periods, far below the step limit; the
-    tokens match the oracle."""
+    launching within a few poll periods (the engine's launched-step count),
+    far below the step limit; the tokens match the oracle."""
     g = pkg.Geometry(vocab=2048, dim=256, heads=4, ffn_dim=1024, encoder_layers=1, decoder_layers=1)
     model = pkg.seeded_model(seed=9, geometry=g)
     model.output_bias = model.output_bias.copy()
@@ -72,15 +72,18 @@ def test_rows_ending_on_eos_stop_the_launches(pkg, orc):
     with pkg.HipEngine(model, limits=pkg.LIFTED_LIMITS) as e:
         e.translate_token_ids(b.tokens, b.offsets, mo, 0)  # warm-up
         got = e.translate_token_ids(b.tokens, b.offsets, mo, 0).rows()
-        eos_ms = e.last_stats()["decode_ms"]
+        eos = e.last_stats()
         forced = e.translate_token_ids(b.tokens, b.offsets, mo, pkg.FLAG_IGNORE_EOS).rows()
-        full_ms = e.last_stats()["decode_ms"]
+        full = e.last_stats()
     want = orc.translate(orc.OracleModel(model), b.tokens, b.offsets, mo, pkg.LIFTED_LIMITS, 0,
                          threads=ORACLE_THREADS)
-    print(f"EOS at step 0: decode {eos_ms:.3f} ms; all {limit} steps (EOS ignored) {full_ms:.3f} ms",
-          flush=True)
+    print(f"EOS at step 0: {eos['decode_steps']} step on rows, {eos['launched_steps']} launched, "
+          f"decode {eos['decode_ms']:.3f} ms; all {limit} steps (EOS ignored): "
+          f"{full['launched_steps']} launched, {full['decode_ms']:.3f} ms", flush=True)
     assert got == want
     assert all(len(r) <= 1 for r in got) and all(len(r) == limit for r in forced)
-    # the launches stop within a few poll periods (a few dozen of the 200 steps)
-    assert eos_ms < 0.3 * full_ms
+    assert eos["decode_steps"] == 1 and full["decode_steps"] == full["launched_steps"] == limit
+    # the launches stop within a few poll periods of 8 steps (count stored at
+    # step 7, seen when step 15 or a later poll step is enqueued)
+    assert eos["launched_steps"] <= 5 * 8
 

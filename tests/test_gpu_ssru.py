@@ -49,6 +49,8 @@ SHAPES = {
     "d256-dh64": dict(dim=256, heads=4, ffn_dim=1024),
     "d384-dh64": dict(dim=384, heads=6, ffn_dim=1536),
     "d512-dh64": dict(dim=512, heads=8, ffn_dim=2048),
+    "d128-dh64": dict(dim=128, heads=2, ffn_dim=512),
+    "d192-dh48": dict(dim=192, heads=4, ffn_dim=768),
 }
 
 
@@ -194,6 +196,9 @@ def test_shortlisted_input_errors_keep_the_engine_ready(pkg, small_model):
                                   candidate_offsets=[0, 2, 2])
         with pytest.raises(pkg.InvalidInput, match="exceeds vocabulary"):
             e.translate_token_ids(b.tokens, b.offsets, [4, 4], candidates=[0, 5, 2048],
+                                  candidate_offsets=[0, 2, 3])
+        with pytest.raises(pkg.InvalidInput, match="not strictly ascending"):
+            e.translate_token_ids(b.tokens, b.offsets, [4, 4], candidates=[5, 0, 2],
                                   candidate_offsets=[0, 2, 3])
         assert e.is_ready()
         out = e.translate_token_ids(b.tokens, b.offsets, [4, 4], pkg.FLAG_IGNORE_EOS,
