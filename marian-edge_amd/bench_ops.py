@@ -137,7 +137,7 @@ def copy_calibration(mb: int, reps: int) -> None:
 
 
 def pmc_summary(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_csv: str,
-                copy_mb: int) -> dict:
+                copy_mb: int, workload: str) -> dict:
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the decode kernels from
     two rocprofv3 --pmc runs of bench.py, scaled by what the same counters
     read for the copy kernel per byte it moves."""
@@ -161,8 +161,7 @@ def pmc_summary(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_
 
     ff, fw = copy_factor(cf), copy_factor(cw)
     res = {
-        "workload": "64-sentence ragged greedy batch (bench.py --steps 2 --warmup 1 --no-cpu-baseline: "
-                    "5 translations)",
+        "workload": workload,
         "counters": "FETCH_SIZE and WRITE_SIZE (KiB per dispatch), one rocprofv3 --pmc run each",
         "calibration": {
             "copy_mib": copy_mb,
@@ -279,7 +278,7 @@ def step_breakdown(trace_csv: str, steps_per_batch: int, batches: int, rows_at: 
             steps.append(cur)
             cur = []
     enc = ("k_gemm_tile", "k_attn_tiles", "k_seq_tiles", "k_embed", "k_quantize_rows_v4<2>")
-    groups = [(1, 1), (2, 4), (5, 8), (9, 16), (17, 32), (33, 64), (65, 4096)]
+    groups = [(1, 1), (2, 4), (5, 8), (9, 16), (17, 32), (33, 64), (65, 128), (129, 256), (257, 4096)]
     agg: dict = {}
     for b in range(first_batch, first_batch + batches):
         for t in range(steps_per_batch):
@@ -359,13 +358,18 @@ def main(argv=None) -> int:
     pm.add_argument("copy_fetch_csv")
     pm.add_argument("copy_write_csv")
     pm.add_argument("--copy-mb", type=int, default=64)
+    pm.add_argument("--workload", default="64-sentence ragged greedy batch (bench.py --steps 2 --warmup 1 "
+                                          "--no-cpu-baseline: 5 translations)",
+                    help="what the counted command ran")
     st = sub.add_parser("stats")
     st.add_argument("stats_csv")
     st.add_argument("--batches", type=int, required=True)
     st.add_argument("--json", action="store_true", help="per-kernel calls and averages as JSON")
-    sb = sub.add_parser("steps", help="per-step kernel breakdown of a bench.py trace (ragged batch)")
+    sb = sub.add_parser("steps", help="per-step kernel breakdown of a bench.py trace")
     sb.add_argument("trace_csv")
     sb.add_argument("--batches", type=int, default=6, help="untimed-event batches at the start")
+    sb.add_argument("--workload", choices=["ragged", "stress"], default="ragged",
+                    help="the bench.py workload the trace ran (its forced stops give the row counts)")
     cc = sub.add_parser("counters")
     cc.add_argument("csv", nargs="+")
     cc.add_argument("--trace", default=None)
@@ -376,13 +380,13 @@ def main(argv=None) -> int:
         copy_calibration(a.mb, a.reps)
     elif a.cmd == "pmc":
         print(json.dumps(pmc_summary(a.fetch_csv, a.write_csv, a.copy_fetch_csv, a.copy_write_csv,
-                                     a.copy_mb), indent=1))
+                                     a.copy_mb, a.workload), indent=1))
     elif a.cmd == "stats":
         print(json.dumps(stats_json(a.stats_csv, a.batches), indent=1) if a.json
               else stats_table(a.stats_csv, a.batches))
     elif a.cmd == "steps":
         pkg = _load_package()
-        b = pkg.ragged_batch()
+        b = pkg.ragged_batch() if a.workload == "ragged" else pkg.stress_batch()
         lim = b.max_output_tokens.astype(np.int64)
         n = int(lim.max())
         print(step_breakdown(a.trace_csv, n, a.batches, [int((lim > t).sum()) for t in range(n)]))

@@ -21,6 +21,7 @@
 // (decoder self-attention over steps 0..t).
 #include "device_common.h"
 #include "kernels.h"
+#include <hip/hip_ext.h>
 
 namespace mh {
 namespace {
@@ -451,18 +452,20 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
+// ev_start / ev_stop (optional) are recorded by the launch's own dispatch.
 template <int CH, typename T, bool PRE>
-hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
-  if (a.head_dim == 48)
-    hipLaunchKernelGGL((k_attention<CH, T, PRE, 48>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
+hipError_t launch_t(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  auto kern = a.head_dim == 48 ? k_attention<CH, T, PRE, 48> : k_attention<CH, T, PRE, 64>;
+  if (ev0 || ev1)
+    hipExtLaunchKernelGGL(kern, dim3(a.heads * a.rows), dim3(64), 0, s, ev0, ev1, 0, a);
   else
-    hipLaunchKernelGGL((k_attention<CH, T, PRE, 64>), dim3(a.heads * a.rows), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3(a.heads * a.rows), dim3(64), 0, s, a);
   return hipGetLastError();
 }
 
 template <int CH, bool PRE = false>
-hipError_t launch_ch(const AttnArgs& a, hipStream_t s) {
-  return a.bf16 ? launch_t<CH, uint16_t, PRE>(a, s) : launch_t<CH, float, PRE>(a, s);
+hipError_t launch_ch(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  return a.bf16 ? launch_t<CH, uint16_t, PRE>(a, s, ev0, ev1) : launch_t<CH, float, PRE>(a, s, ev0, ev1);
 }
 
 template <typename T>
@@ -483,7 +486,7 @@ hipError_t launch_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles, int c
   return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (a.rows <= 0) return hipSuccess;
   if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out || (a.head_dim != 64 && a.head_dim != 48) ||
       (int64_t)a.rows * a.heads > 0x7fffffff)
@@ -503,10 +506,12 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   }
   // Decode launches cover few rows: one round trip per row matters more
   // than occupancy.  Encoder launches keep the lighter register budget.
-  if (a.max_keys <= 128) return a.mode == ATT_SEQ ? launch_ch<2>(a, s) : launch_ch<2, true>(a, s);
-  if (a.max_keys <= 512) return launch_ch<8>(a, s);
-  if (a.max_keys <= 1024) return launch_ch<16>(a, s);
-  if (a.max_keys <= 4096) return launch_ch<64>(a, s);
+  hipEvent_t e0 = ev_start, e1 = ev_stop;
+  if (a.max_keys <= 128)
+    return a.mode == ATT_SEQ ? launch_ch<2>(a, s, e0, e1) : launch_ch<2, true>(a, s, e0, e1);
+  if (a.max_keys <= 512) return launch_ch<8>(a, s, e0, e1);
+  if (a.max_keys <= 1024) return launch_ch<16>(a, s, e0, e1);
+  if (a.max_keys <= 4096) return launch_ch<64>(a, s, e0, e1);
   return hipErrorInvalidValue;
 }
 

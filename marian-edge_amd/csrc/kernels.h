@@ -310,7 +310,9 @@ struct AttnArgs {
   const uint32_t* tiles = nullptr;
   int tiles_cap = 0;
 };
-hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+// ev_start / ev_stop as in launch_vocab_argmax (single-wave kernel only).
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s, hipEvent_t ev_start = nullptr,
+                            hipEvent_t ev_stop = nullptr);
 // Query tiles of packed sequences cu[0..nseq] for the tiled ATT_SEQ kernel:
 // at most seq_tiles_bound(rows, nseq) entries; tiles needs 1 + 2 * cap words.
 int seq_tiles_bound(int rows, int nseq);
