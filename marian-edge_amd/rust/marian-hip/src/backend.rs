@@ -17,7 +17,9 @@ use crate::engine::HipEngine;
 /// (Q8CpuEngine::prepare_candidates, crates/marian-cpu/src/q8_engine.rs:576-584).
 pub struct HipTokenEngine {
     pub engine: HipEngine,
-    pub shortlist: Option<LexicalShortlist>,
+    /// None scores the whole vocabulary under the generation mask, which is
+    /// what the reference's engine does without a shortlist file.
+    pub shortlist: Option<Arc<LexicalShortlist>>,
 }
 
 impl CpuTokenEngine for HipTokenEngine {
@@ -70,7 +72,7 @@ impl HipBackend {
     #[allow(clippy::too_many_arguments)]
     pub fn new(
         engine: HipEngine,
-        shortlist: Option<LexicalShortlist>,
+        shortlist: Option<Arc<LexicalShortlist>>,
         source: Arc<dyn TextTokenizer>,
         target: Arc<dyn TextTokenizer>,
         source_lang: impl Into<String>,

@@ -108,6 +108,73 @@ pub struct SsruModel<'a> {
     pub decoder: Vec<SsruDecoderLayer<'a>>,
 }
 
+impl<'a> SsruModel<'a> {
+    /// The loaded Q8 model of marian-cpu (`Q8CpuEngine::weights_view`, added by
+    /// marian-edge-wiring.patch), one to one: `encoder_Wemb` / `decoder_Wemb`,
+    /// `decoder_output_activation_mult`, and per layer the Q8Linear weights
+    /// ([out, in] int8), weight and activation multipliers and optional bias,
+    /// with the LayerNorms in the graph's order (q8_engine.rs:76-114).
+    pub fn from_q8_view(view: &marian_cpu::Q8ModelView<'a>) -> Self {
+        fn st<'a>(l: &'a marian_cpu::Q8Linear) -> StaticLinear<'a> {
+            StaticLinear {
+                weight: l.weights(),
+                weight_mult: l.weight_quant_mult(),
+                act_mult: l.activation_quant_mult(),
+                bias: l.bias(),
+            }
+        }
+        fn nm<'a>(n: &marian_cpu::Q8LayerNormView<'a>) -> Norm<'a> {
+            Norm { scale: n.scale, bias: n.bias }
+        }
+        let ffn_dim = view.encoder.first().map_or(0, |l| l.w1.output_dim());
+        let dim = view.dim.max(1);
+        SsruModel {
+            source_vocab: (view.encoder_embedding.len() / dim) as u32,
+            target_vocab: (view.decoder_embedding.len() / dim) as u32,
+            dim: view.dim as u32,
+            heads: view.heads as u32,
+            ffn_dim: ffn_dim as u32,
+            encoder_embedding: view.encoder_embedding,
+            encoder_embedding_mult: view.encoder_embedding_mult,
+            decoder_embedding: view.decoder_embedding,
+            decoder_embedding_mult: view.decoder_embedding_mult,
+            output_act_mult: view.decoder_output_activation_mult,
+            output_bias: view.output_bias,
+            encoder: view
+                .encoder
+                .iter()
+                .map(|l| SsruEncoderLayer {
+                    wq: st(l.wq),
+                    wk: st(l.wk),
+                    wv: st(l.wv),
+                    wo: st(l.wo),
+                    attn_ln: nm(&l.attention_norm),
+                    w1: st(l.w1),
+                    w2: st(l.w2),
+                    ffn_ln: nm(&l.ffn_norm),
+                })
+                .collect(),
+            decoder: view
+                .decoder
+                .iter()
+                .map(|l| SsruDecoderLayer {
+                    ssru_w: st(l.ssru_w),
+                    ssru_wf: st(l.ssru_wf),
+                    ssru_ln: nm(&l.ssru_norm),
+                    wq: st(l.wq),
+                    wk: st(l.wk),
+                    wv: st(l.wv),
+                    wo: st(l.wo),
+                    context_ln: nm(&l.context_norm),
+                    w1: st(l.w1),
+                    w2: st(l.w2),
+                    ffn_ln: nm(&l.ffn_norm),
+                })
+                .collect(),
+        }
+    }
+}
+
 fn lin(l: &Linear<'_>) -> ffi::marian_hip_linear {
     ffi::marian_hip_linear { weight: l.weight.as_ptr(), mult: l.mult.as_ptr(), bias: l.bias.as_ptr() }
 }

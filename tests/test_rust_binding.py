@@ -17,7 +17,8 @@ HEADERS = [ROOT / "include" / "marian_hip.h", ROOT / "include" / "marian_hip_uti
 ENGINE_LEVEL = {
     "marian_hip_engine_create", "marian_hip_engine_create_ssru", "marian_hip_engine_destroy",
     "marian_hip_translate_token_ids", "marian_hip_translate_shortlisted", "marian_hip_is_ready",
-    "marian_hip_last_error", "marian_hip_info", "marian_hip_last_stats",
+    "marian_hip_last_error", "marian_hip_info", "marian_hip_last_stats", "marian_hip_warmup",
+    "marian_hip_reserve",
 }
 
 
