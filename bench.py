@@ -370,7 +370,46 @@ def run_translate_bench(pkg, model, batch, steps, warmup, extra_passes=2):
     info = eng.info()
     eng.close()
     return dict(dev_ms=dev_ms, wall_ms=wall_ms, lat=lat, ntok=ntok, info=info, families=fam,
-                enc_ms=enc_ms, dec_ms=dec_ms, n_steps=n_steps, step_table=table)
+                enc_ms=enc_ms, dec_ms=dec_ms, n_steps=n_steps, step_table=table, rows=out.rows())
+
+
+def fast_mode(pkg, model, batch, steps, warmup, exact_rows, probe_steps=(0, 20, 60)):
+    """The same batch with MARIAN_HIP_FLAG_FAST_REDUCTIONS (the decoder's
+    LayerNorm and softmax sums in the tree order): tokens/s over `steps`
+    timed translations, how many sentences equal the exact mode's, and the
+    relative L2 difference of the logits from the exact mode's at a few
+    decode steps (over the rows active there, masked ids excluded)."""
+    flags = batch.flags | pkg.FLAG_FAST_REDUCTIONS
+    eng = pkg.HipEngine(model, limits=batch.limits)
+    for _ in range(warmup):
+        eng.translate_token_ids(batch.tokens, batch.offsets, batch.max_output_tokens, flags)
+    ms, rows = [], None
+    for _ in range(steps):
+        out = eng.translate_token_ids(batch.tokens, batch.offsets, batch.max_output_tokens, flags)
+        ms.append(eng.last_stats()["total_ms"])
+        rows = out.rows()
+    same = sum(a == b for a, b in zip(rows, exact_rows))
+    rel = []
+    for step in probe_steps:
+        lim = np.minimum(batch.max_output_tokens.astype(np.int64), step + 1).astype(np.uint32)
+        _, _, lf, act = eng.translate_probe(batch.tokens, batch.offsets, lim, flags, probe_step=step)
+        _, _, le, _ = eng.translate_probe(batch.tokens, batch.offsets, lim, batch.flags, probe_step=step)
+        if not act.any():
+            continue
+        f, e = lf[act], le[act]
+        fin = np.isfinite(e)
+        rel.append(float(np.linalg.norm(np.where(fin, f, 0.0) - np.where(fin, e, 0.0)) /
+                         np.linalg.norm(np.where(fin, e, 0.0))))
+    eng.close()
+    ntok = sum(map(len, rows))
+    m = statistics.mean(ms)
+    return {"value": round(ntok / (m / 1000.0), 1), "unit": "tokens/s", "ms_per_step": round(m, 4),
+            "identical_sentences": f"{same}/{len(rows)}",
+            "max_logit_rel_l2": round(max(rel), 6) if rel else None,
+            "probe_steps": list(probe_steps),
+            "note": "opt-in MARIAN_HIP_FLAG_FAST_REDUCTIONS: the decoder's LayerNorm sums and softmax "
+                    "denominators as lane partials + xor butterfly (bit-exact with the oracle's restatement "
+                    "of that order); compared here with the exact mode of the same build"}
 
 
 def roofline_of(family, f, tag, timing_note):
@@ -583,6 +622,8 @@ def main(argv=None):
                     help="translations with step events and with launch events (each); 0 skips "
                          "the p50, step table and rooflines (for counter runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fast-mode", action="store_true",
+                    help="skip the opt-in fast-reduction mode's line items")
     ap.add_argument("--no-reference-ssru", action="store_true",
                     help="skip the informational Transformer-SSRU run on the default workload")
     ap.add_argument("--cpu-cores", type=int, default=min(16, os.cpu_count() or 4))
@@ -664,6 +705,8 @@ def main(argv=None):
         "cpu_baseline": cpu,
         "device": r["info"]["device"],
     }
+    if not args.no_fast_mode:
+        line["fast_reductions"] = fast_mode(pkg, model, batch, args.steps, args.warmup, r["rows"])
     if cpu:
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
     if args.workload == "ragged" and not args.no_reference_ssru:

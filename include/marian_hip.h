@@ -95,8 +95,18 @@ enum {
 /* Translate flags. */
 enum {
   MARIAN_HIP_FLAG_IGNORE_EOS = 1u << 0,         /* token 0 does not finish a row */
-  MARIAN_HIP_FLAG_NO_GENERATION_MASK = 1u << 1  /* also score ids 1 and 7..38
+  MARIAN_HIP_FLAG_NO_GENERATION_MASK = 1u << 1, /* also score ids 1 and 7..38
                                                    (shortlist.rs:169-176 masks them) */
+  /* Opt-in, no counterpart in the reference: the decoder's LayerNorm sums and
+   * softmax denominators as 64 lane partials (lane l: elements l, l + 64, ...
+   * in order from 0.0) combined by an xor butterfly over lane distances 32,
+   * 16, ..., 1, instead of the reference's left-to-right folds
+   * (tensor.rs:372-385, 745-754).  The encoder, every other sum, exp and the
+   * integer work are unchanged.  Results then differ from the reference in the
+   * last bits of those sums; greedy outputs are compared with the exact mode in
+   * tests/test_gpu_fast.py.  Transformer graph only (the SSRU engine rejects
+   * it). */
+  MARIAN_HIP_FLAG_FAST_REDUCTIONS = 1u << 2
 };
 
 /* One Q8 dense layer.  weight is [out, in] int8, input-contiguous (the

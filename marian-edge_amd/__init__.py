@@ -18,6 +18,7 @@ from .synthetic import (Batch, Geometry, LIFTED_LIMITS, REFERENCE_LIMITS, Seeded
 
 FLAG_IGNORE_EOS = _lib.FLAG_IGNORE_EOS
 FLAG_NO_GENERATION_MASK = _lib.FLAG_NO_GENERATION_MASK
+FLAG_FAST_REDUCTIONS = _lib.FLAG_FAST_REDUCTIONS
 
 __all__ = [
     "BackendError", "BatchOutput", "BufferTooSmall", "DeviceError", "HipBackend", "HipEngine",
@@ -26,7 +27,7 @@ __all__ = [
     "LIFTED_LIMITS", "REFERENCE_LIMITS", "SeededModel", "SsruGeometry", "SsruModel",
     "seeded_ssru_model", "attention_inputs", "gemm_inputs",
     "ragged_batch", "seeded_model", "single_sentence_batch", "stress_batch", "GEMM_SHAPES",
-    "GEMM_ROWS", "FLAG_IGNORE_EOS", "FLAG_NO_GENERATION_MASK", "load_library",
+    "GEMM_ROWS", "FLAG_IGNORE_EOS", "FLAG_NO_GENERATION_MASK", "FLAG_FAST_REDUCTIONS", "load_library",
     "HipTextBackend", "HipTokenEngine", "SegmentError", "TextSegment", "TranslationInput",
     "TranslationOutput", "UnsupportedDirection", "segment_text", "translate_with_engine",
 ]

@@ -21,6 +21,7 @@ ERR_NOT_READY = -6
 
 FLAG_IGNORE_EOS = 1 << 0
 FLAG_NO_GENERATION_MASK = 1 << 1
+FLAG_FAST_REDUCTIONS = 1 << 2
 
 
 class Linear(C.Structure):

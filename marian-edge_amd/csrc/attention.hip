@@ -184,19 +184,29 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   // Denominator in key order from 0.0 (softmax_in_place): the probabilities
   // pass through the tile and every lane folds them sequentially.  Keys past
   // the last hold +0.0, which leaves the (non-negative) sum unchanged.
-  __syncthreads();  // the last K chunk has been read
-#pragma unroll
-  for (int c = 0; c < CH; ++c)
-    if (c < nch) tile[c * 64 + lane] = s[c];
-  __syncthreads();
+  // With a.fast (decode only) the denominator takes the fast-reduction tree
+  // order instead: lane l's keys l, 64 + l, ... in order from 0.0, then the
+  // xor butterfly (tree_combine_wave).
   float sum = 0.0f;
+  if (a.fast) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      if (c < nch) sum = sum + s[c];
+    sum = tree_combine_wave(sum);
+  } else {
+    __syncthreads();  // the last K chunk has been read
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      if (c < nch) tile[c * 64 + lane] = s[c];
+    __syncthreads();
 #pragma unroll 4
-  for (int j = 0; j < nch * 64; j += 4) {
-    const float4 v = *(const float4*)(tile + j);
-    sum = sum + v.x;
-    sum = sum + v.y;
-    sum = sum + v.z;
-    sum = sum + v.w;
+    for (int j = 0; j < nch * 64; j += 4) {
+      const float4 v = *(const float4*)(tile + j);
+      sum = sum + v.x;
+      sum = sum + v.y;
+      sum = sum + v.z;
+      sum = sum + v.w;
+    }
   }
   const float inv = 1.0f / sum;
 #pragma unroll
@@ -488,6 +498,7 @@ hipError_t launch_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles, int c
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (a.rows <= 0) return hipSuccess;
+  if (a.fast && a.mode == ATT_SEQ) return hipErrorInvalidValue;  // the encoder keeps the reference order
   if (a.heads <= 0 || a.heads > 16 || a.max_keys <= 0 || !a.out || (a.head_dim != 64 && a.head_dim != 48) ||
       (int64_t)a.rows * a.heads > 0x7fffffff)
     return hipErrorInvalidValue;

@@ -176,7 +176,9 @@ __device__ __forceinline__ void row_tiles_mfma(const int8_t* sX, const v4i (&bf)
 constexpr int kBlkLoaders = 64 * kBlkLoadWaves;
 static_assert(kBlkRow % 4 == 0 && kBlkMaxKeys * (kBlkRow / 4) % 64 == 0, "key staging by wave instructions");
 
-template <int MODE, int PK>
+// FAST: the LayerNorm sums and the softmax denominator in the fast-reduction
+// tree order (tree_sum_wave / tree_combine_wave) instead of the folds.
+template <int MODE, int PK, bool FAST>
 __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   constexpr bool SELF = MODE == ATT_SELF;
   constexpr int NT = SELF ? 12 : 4;        // 16-column projection tiles: Q (+ K, V)
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       float z[PER], o[PER];
 #pragma unroll
       for (int j = 0; j < PER; ++j) z[j] = y[j] + rr[j];  // add_slices
-      ln_wave<PER>(z, sZ, gv, bv, lane, o);
+      ln_wave<PER, FAST>(z, sZ, gv, bv, lane, o);
       bad = false;
       float mx = 0.0f;
 #pragma unroll
@@ -390,15 +392,22 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     const float mx = wave_max(fmaxf(sc, sc1));
     const float e0 = lane < nkey ? ref_expf(sc - mx, sTab) : 0.0f;
     const float e1 = 64 + lane < nkey ? ref_expf(sc1 - mx, sTab) : 0.0f;
-    sP[lane] = e0;
-    sP[64 + lane] = e1;
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
-    __builtin_amdgcn_wave_barrier();
-    // Denominator: keys in order from 0.0 (softmax_in_place), folded over
-    // whole batches of 16 entries: past the last key they hold +0.0, which
-    // leaves the (non-negative) sum unchanged.
-    const float inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, n16, 0.0f);
-    __builtin_amdgcn_wave_barrier();
+    float inv;
+    if constexpr (FAST) {
+      // Lane l's keys l and 64 + l in order from 0.0 (0.0 + e0 is e0), then
+      // the butterfly; +0.0 past the last key leaves the sums unchanged.
+      inv = 1.0f / tree_combine_wave(e0 + e1);
+    } else {
+      sP[lane] = e0;
+      sP[64 + lane] = e1;
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+      __builtin_amdgcn_wave_barrier();
+      // Denominator: keys in order from 0.0 (softmax_in_place), folded over
+      // whole batches of 16 entries: past the last key they hold +0.0, which
+      // leaves the (non-negative) sum unchanged.
+      inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, n16, 0.0f);
+      __builtin_amdgcn_wave_barrier();
+    }
     // p_k = e_k * inv (scale_in_place)
     sP[lane] = e0 * inv;
     sP[64 + lane] = e1 * inv;
@@ -460,6 +469,7 @@ constexpr int kLgTiles = kLgCols / 16;                            // MFMA column
 constexpr int kLgTpw = kLgTiles / kBlkLoadWaves;  // tiles per loader wave
 static_assert(kLgTiles % kBlkLoadWaves == 0, "every loader wave owns whole tiles");
 
+template <bool FAST>
 __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   constexpr int PER = kBlkD / 64;  // lane l holds row elements l + 64j
   __shared__ __attribute__((aligned(16))) float sZ[kLnRow<PER>];
@@ -484,7 +494,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     float z[PER], o[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) z[j] = y[j] + rr[j];  // add_slices
-    ln_wave<PER>(z, sZ, gv, bv, lane, o);
+    ln_wave<PER, FAST>(z, sZ, gv, bv, lane, o);
     bool bad = false;
     float mx = 0.0f;
 #pragma unroll
@@ -556,9 +566,12 @@ hipError_t launch_attn_block(const BlockArgs& b, hipStream_t s, hipEvent_t ev_st
     return hipErrorInvalidValue;
   if (b.mode == ATT_CROSS && p.kind != PRO_LN) return hipErrorInvalidValue;
   const dim3 grid(b.rows * b.heads), block(kBlkThreads);
-  auto kern = b.mode == ATT_CROSS ? k_attn_block<ATT_CROSS, PRO_LN>
-               : p.kind == PRO_LN  ? k_attn_block<ATT_SELF, PRO_LN>
-                                   : k_attn_block<ATT_SELF, PRO_EMB>;
+  auto kern = b.fast ? (b.mode == ATT_CROSS ? k_attn_block<ATT_CROSS, PRO_LN, true>
+                        : p.kind == PRO_LN  ? k_attn_block<ATT_SELF, PRO_LN, true>
+                                            : k_attn_block<ATT_SELF, PRO_EMB, true>)
+                     : (b.mode == ATT_CROSS ? k_attn_block<ATT_CROSS, PRO_LN, false>
+                        : p.kind == PRO_LN  ? k_attn_block<ATT_SELF, PRO_LN, false>
+                                            : k_attn_block<ATT_SELF, PRO_EMB, false>);
   // With events the dispatch itself records them at its start and end.
   if (ev_start || ev_stop)
     hipExtLaunchKernelGGL(kern, grid, block, 0, s, ev_start, ev_stop, 0, b);
@@ -575,7 +588,8 @@ hipError_t launch_ln_gemm_block(const LnGemmArgs& a, hipStream_t s) {
   if (!ln_gemm_block_supported(a.K, a.N) || p.kind != PRO_LN || !p.y || !p.r || !p.gamma ||
       !p.beta || !a.W || !a.wmult || !a.bias || !a.out || a.ldo < a.N)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_ln_gemm_block, dim3(a.rows * (a.N / kLgCols)), dim3(kBlkThreads), 0, s, a);
+  hipLaunchKernelGGL(p.fast ? k_ln_gemm_block<true> : k_ln_gemm_block<false>, dim3(a.rows * (a.N / kLgCols)),
+                     dim3(kBlkThreads), 0, s, a);
   return hipGetLastError();
 }
 

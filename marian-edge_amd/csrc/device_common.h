@@ -336,21 +336,50 @@ __device__ __forceinline__ float fold_row_wave(const float (&v)[PER], float* zr,
   }
 }
 
+// ---- the opt-in fast-reduction order (decoder only) -----------------------------
+// With MARIAN_HIP_FLAG_FAST_REDUCTIONS the decoder's LayerNorm sums and
+// softmax denominators are not the reference's left-to-right folds but a
+// tree: 64 lane partials (lane l adds elements l, l + 64, l + 128, ... in
+// order, from 0.0), then an xor butterfly over lane distances 32, 16, 8, 4, 2
+// and 1 (lane l adds lane l ^ dist's value to its own; addition commutes, so
+// every lane ends with the same sum).  One wave, no LDS.
+
+// The partial p (this lane's in-order sum) combined over the wave.
+__device__ __forceinline__ float tree_combine_wave(float p) {
+  p = p + __shfl_xor(p, 32, 64);
+  p = p + xor_lane_f<16>(p);
+  p = p + xor_lane_f<8>(p);
+  p = p + xor_lane_f<4>(p);
+  p = p + xor_lane_f<2>(p);
+  p = p + xor_lane_f<1>(p);
+  return p;
+}
+
+// The tree sum of a row held by one wave (lane l: elements l + 64j in v[j]).
+template <int PER>
+__device__ __forceinline__ float tree_sum_wave(const float (&v)[PER]) {
+  float p = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) p = p + v[j];
+  return tree_combine_wave(p);
+}
+
 // LayerNorm of the row z (lane l holds elements l + 64j) by one wave with
 // normalize_row's sequential folds (tensor.rs:372-385); zr is the wave's LDS
-// row (kLnRow<PER> floats).  Returns the normalized row in o.
-template <int PER>
+// row (kLnRow<PER> floats).  Returns the normalized row in o.  FAST: the two
+// sums in the tree order above instead (zr unused).
+template <int PER, bool FAST = false>
 __device__ __forceinline__ void ln_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
                                         const float (&bv)[PER], int lane, float (&o)[PER]) {
   constexpr int D = PER * 64;
-  const float mean = fold_row_wave<PER>(z, zr, lane) / (float)D;
+  const float mean = (FAST ? tree_sum_wave<PER>(z) : fold_row_wave<PER>(z, zr, lane)) / (float)D;
   float t[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const float c = z[j] - mean;
     t[j] = c * c;
   }
-  const float var = fold_row_wave<PER>(t, zr, lane) / (float)D;
+  const float var = (FAST ? tree_sum_wave<PER>(t) : fold_row_wave<PER>(t, zr, lane)) / (float)D;
   const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
 #pragma unroll
   for (int j = 0; j < PER; ++j) o[j] = ((z[j] - mean) * inv) * gv[j] + bv[j];

@@ -959,6 +959,7 @@ struct Translation {
   size_t cache_rows = 1;
   int n_active0 = 0, nparts = 0;
   bool tiled = false;
+  bool fast = false;  // MARIAN_HIP_FLAG_FAST_REDUCTIONS: the decoder's sums in the tree order
   MetaLayout L{};
   CallBufs b{};
   // device views of the metadata
@@ -1426,7 +1427,8 @@ hipError_t Translation::emit_step(const StepPlan& P, uint32_t t) {
   auto layer_norm = [&](const float* y, const float* gm, const float* bt, bool defer) -> hipError_t {
     hipError_t rc = hipSuccess;
     if (!defer) {
-      rc = launch_residual_ln(y, xres, gm, bt, rows, d_nact, d, xalt, b.DXQ, b.DXA, E->err_flag, s);
+      rc = launch_residual_ln(y, xres, gm, bt, rows, d_nact, d, xalt, b.DXQ, b.DXA, E->err_flag, s, 0.0f,
+                              fast);
     } else {
       pend = RowPrologue();
       pend.kind = PRO_LN;
@@ -1436,6 +1438,7 @@ hipError_t Translation::emit_step(const StepPlan& P, uint32_t t) {
       pend.beta = bt;
       pend.out = xalt;
       pend.err = E->err_flag;
+      pend.fast = fast;
     }
     std::swap(xres, xalt);
     return rc;
@@ -1470,6 +1473,7 @@ hipError_t Translation::emit_step(const StepPlan& P, uint32_t t) {
     ba.ldo = d;
     ba.amax = b.DAMAX;
     ba.err = E->err_flag;
+    ba.fast = fast;
     return launch_attn_block(ba, s, ev[0], ev[1]);
   };
   if (P.blk_self) {
@@ -1536,6 +1540,7 @@ hipError_t Translation::emit_step(const StepPlan& P, uint32_t t) {
       sa.ldo = d;
       sa.amax = b.DAMAX;
       sa.err = E->err_flag;
+      sa.fast = fast;
       hipEvent_t ev[2];
       MH_TRY(timer(MARIAN_HIP_KERNEL_SELF_ATTN, t, l, ev));
       MH_TRY(launch_attention(sa, s, ev[0], ev[1]));
@@ -1567,6 +1572,7 @@ hipError_t Translation::emit_step(const StepPlan& P, uint32_t t) {
       ca.ldo = d;
       ca.amax = b.DAMAX;
       ca.err = E->err_flag;
+      ca.fast = fast;
       hipEvent_t ev[2];
       MH_TRY(timer(MARIAN_HIP_KERNEL_CROSS_ATTN, t, l, ev));
       MH_TRY(launch_attention(ca, s, ev[0], ev[1]));
@@ -1585,6 +1591,7 @@ hipError_t Translation::emit_step(const StepPlan& P, uint32_t t) {
       lg.rows = rows;
       lg.rows_dev = d_nact;
       lg.dyn = 1;
+      lg.fast = fast;
       lg.part_n = F;
       lg.W = L.ffn1.wf;
       lg.wmult = L.ffn1.mult;
@@ -2057,6 +2064,9 @@ int translate(marian_hip_engine* E, const int32_t* tokens, size_t n_tokens, cons
   c.cand = cand;
   c.cand_off = cand_off;
   c.pr = pr;
+  c.fast = flags & MARIAN_HIP_FLAG_FAST_REDUCTIONS;
+  if (c.fast && E->ssru)
+    return E->fail(MARIAN_HIP_ERR_INVALID_INPUT, "fast reductions are implemented for the transformer graph only");
 
   const hipError_t he = hipSetDevice(E->device);
   if (he != hipSuccess) return E->hip_fail(he, "hipSetDevice");

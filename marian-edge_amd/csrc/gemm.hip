@@ -312,7 +312,8 @@ constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 // while the weight loads are in flight (the row's loads are issued before
 // the weights'), takes its maximum and quantizes it into the LDS row the
 // matrix cores read.
-template <bool FULL, bool LNP>
+// FAST (with LNP): the LayerNorm sums in the fast-reduction tree order.
+template <bool FULL, bool LNP, bool FAST = false>
 __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs g, Epilogue e) {
   constexpr int kVocabThreads = 64 * kVocabWaves<LNP>;
   constexpr int kVocabCT = kVocabCols / (16 * kVocabWaves<LNP>);  // column tiles per wave
@@ -396,7 +397,7 @@ __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs
       float z[PER], o[PER];
 #pragma unroll
       for (int j = 0; j < PER; ++j) z[j] = wy[j] + wr[j];  // add_slices
-      ln_wave<PER>(z, sZ + wave * kLnRow<PER>, wgm, wbt, lane, o);
+      ln_wave<PER, FAST>(z, sZ + wave * kLnRow<PER>, wgm, wbt, lane, o);
       float mx = 0.0f;
       bool bad = false;
 #pragma unroll
@@ -707,7 +708,8 @@ constexpr int kCandKs = 8;  // k-steps requested together (K <= 512: all of them
 // LNP > 0: the row is LayerNorm(pro.y + pro.r) of width 64 LNP, built by wave
 // 0 while the candidates' embedding rows are in flight, and quantized with
 // c.qmult (> 0, static) or its own multiplier.
-template <int LNP>
+// FAST (with LNP): the LayerNorm sums in the fast-reduction tree order.
+template <int LNP, bool FAST = false>
 __global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
   __shared__ uint64_t sKey[4];
   __shared__ __attribute__((aligned(16))) float sZ[LNP ? kLnRow<LNP> : 1];
@@ -775,7 +777,7 @@ __global__ __launch_bounds__(256) void k_cand_argmax(CandArgs c) {
       float z[LNP], o[LNP];
 #pragma unroll
       for (int j = 0; j < LNP; ++j) z[j] = ly[j] + lr[j];
-      ln_wave<LNP>(z, sZ, lg, lb, lane, o);
+      ln_wave<LNP, FAST>(z, sZ, lg, lb, lane, o);
       float mx = 0.0f;
       bool nf = false;
 #pragma unroll
@@ -836,12 +838,13 @@ hipError_t launch_cand_argmax(const CandArgs& c, hipStream_t s) {
     if (!cand_ln_supported(c.K) || !c.pro.y || !c.pro.r || !c.pro.gamma || !c.pro.beta ||
         !(c.qmult >= 0.0f) || !(c.qmult < __builtin_huge_valf()))
       return hipErrorInvalidValue;
+    const bool f = c.pro.fast;
     if (c.K == 256)
-      hipLaunchKernelGGL(k_cand_argmax<4>, grid, block, 0, s, c);
+      hipLaunchKernelGGL((f ? k_cand_argmax<4, true> : k_cand_argmax<4>), grid, block, 0, s, c);
     else if (c.K == 384)
-      hipLaunchKernelGGL(k_cand_argmax<6>, grid, block, 0, s, c);
+      hipLaunchKernelGGL((f ? k_cand_argmax<6, true> : k_cand_argmax<6>), grid, block, 0, s, c);
     else
-      hipLaunchKernelGGL(k_cand_argmax<8>, grid, block, 0, s, c);
+      hipLaunchKernelGGL((f ? k_cand_argmax<8, true> : k_cand_argmax<8>), grid, block, 0, s, c);
   } else {
     if (!c.xq || !c.xa) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_cand_argmax<0>, grid, block, 0, s, c);
@@ -931,7 +934,7 @@ hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t
   if (p.kind != PRO_NONE &&
       (p.kind != PRO_LN || g.K != kVocabMaxK || g.M > kVocabLnMaxRows || !p.y || !p.r || !p.gamma || !p.beta))
     return hipErrorInvalidValue;
-  auto kern = p.kind == PRO_LN      ? k_vocab_argmax<true, true>
+  auto kern = p.kind == PRO_LN      ? (p.fast ? k_vocab_argmax<true, true, true> : k_vocab_argmax<true, true>)
               : g.K == kVocabMaxK ? k_vocab_argmax<true, false>
                                   : k_vocab_argmax<false, false>;
   if (ev_start || ev_stop)

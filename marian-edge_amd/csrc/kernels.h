@@ -29,6 +29,7 @@ struct RowPrologue {
   const int32_t* row_prev = nullptr;  // position row: the consumer's step
   float* out = nullptr;  // fp32 [M, K], or nullptr when nothing reads the rows again
   int* err = nullptr;    // set to 1 on a non-finite row value
+  int fast = 0;          // PRO_LN: the LayerNorm sums in the fast-reduction tree order
 };
 
 // Quantized activations times an int8 weight matrix [N, K] (K-contiguous).
@@ -116,9 +117,11 @@ hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int
 
 // qmult > 0: q is quantized with that static multiplier (the next layer's)
 // instead of each row's own.
+// fast: the LayerNorm sums in the fast-reduction tree order (decoder only).
 hipError_t launch_residual_ln(const float* y, const float* r, const float* g, const float* b,
                               int rows, const int* rows_dev, int d, float* out, int8_t* q,
-                              float* a, int* err, hipStream_t s, float qmult = 0.0f);
+                              float* a, int* err, hipStream_t s, float qmult = 0.0f,
+                              bool fast = false);
 
 // Quantization with one static activation multiplier for every row (a[row] =
 // mult); rejects a multiplier that is not finite and positive.
@@ -241,6 +244,7 @@ struct LnGemmRowsArgs {
   float qmult = 0.0f;
   float* out_qa = nullptr;
   int* err = nullptr;
+  int fast = 0;  // dyn only: the LayerNorm sums in the fast-reduction tree order
 };
 bool ln_gemm_rows_supported(int K, int N);
 hipError_t launch_ln_gemm_rows(const LnGemmRowsArgs& a, hipStream_t s);
@@ -309,6 +313,7 @@ struct AttnArgs {
   // launch_seq_tiles (tiles_cap = its bound) selects the tiled kernel (no amax).
   const uint32_t* tiles = nullptr;
   int tiles_cap = 0;
+  int fast = 0;  // ATT_CROSS / ATT_SELF: the softmax denominator in the fast-reduction tree order
 };
 // ev_start / ev_stop as in launch_vocab_argmax (single-wave kernel only).
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s, hipEvent_t ev_start = nullptr,
@@ -349,6 +354,7 @@ struct BlockArgs {
   int64_t ldo = 0;
   float* amax = nullptr;  // [rows, heads]
   int* err = nullptr;
+  int fast = 0;  // the softmax denominator (and, with pro.fast, the LayerNorm) in the tree order
 };
 bool attn_block_supported(int d, int heads, int max_keys);
 

@@ -30,7 +30,8 @@ constexpr int kLgsCols = 16 * kLgsWaves;
 // YP: y is not read but computed here, the static Q8 linear of the int8 rows
 // a.ya with Wy (the attention-output projection): wave w takes its column
 // tiles w, w + 8, ... over the group's rows, and the rows meet in LDS.
-template <int PER, bool YP, bool DYN>
+// FAST (DYN only): the LayerNorm sums in the fast-reduction tree order.
+template <int PER, bool YP, bool DYN, bool FAST = false>
 __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_rows(LnGemmRowsArgs a) {
   constexpr int D = PER * 64;
   constexpr int KS = D / 64;
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(64 * kLgsWaves) void k_ln_gemm_rows(LnGemmRowsArgs 
     float z[PER], o[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) z[j] = yv[j] + rv[j];
-    ln_wave<PER>(z, sZ[wave], gv, bv, lane, o);
+    ln_wave<PER, FAST>(z, sZ[wave], gv, bv, lane, o);
     bool bad = false;
     float mx = 0.0f;
 #pragma unroll
@@ -174,15 +175,17 @@ hipError_t launch_ln_gemm_rows(const LnGemmRowsArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
   for (const float m : {a.dyn ? 1.0f : a.xq_mult[0], a.dyn ? 1.0f : a.xq_mult[1], yp ? a.ya_mult : 1.0f})
     if (!(m > 0.0f) || !(m < __builtin_huge_valf())) return hipErrorInvalidValue;
-  if (a.dyn && yp) return hipErrorInvalidValue;
+  if ((a.dyn && yp) || (a.fast && !a.dyn)) return hipErrorInvalidValue;
   if (a.out_q && (!(a.qmult > 0.0f) || !(a.qmult < __builtin_huge_valf()))) return hipErrorInvalidValue;
   const int groups = (a.rows + kLgsRows - 1) / kLgsRows;
   if ((int64_t)groups * (a.N / kLgsCols) > 0x7fffffff) return hipErrorInvalidValue;
   const dim3 grid(groups * (a.N / kLgsCols)), block(64 * kLgsWaves);
-#define MH_LG(P)                                                                 \
-  if (a.dyn)                                                                     \
-    hipLaunchKernelGGL((k_ln_gemm_rows<P, false, true>), grid, block, 0, s, a);  \
-  else if (yp)                                                                   \
+#define MH_LG(P)                                                                       \
+  if (a.dyn && a.fast)                                                                 \
+    hipLaunchKernelGGL((k_ln_gemm_rows<P, false, true, true>), grid, block, 0, s, a);  \
+  else if (a.dyn)                                                                      \
+    hipLaunchKernelGGL((k_ln_gemm_rows<P, false, true>), grid, block, 0, s, a);        \
+  else if (yp)                                                                         \
     hipLaunchKernelGGL((k_ln_gemm_rows<P, true, false>), grid, block, 0, s, a);  \
   else                                                                           \
     hipLaunchKernelGGL((k_ln_gemm_rows<P, false, false>), grid, block, 0, s, a);

@@ -97,19 +97,20 @@ __global__ __launch_bounds__(256) void k_quantize_rows_v4(const float* x, int64_
 // LDS (zr, kLnRow<PER> floats) and folds it with fold_row_wave (speculative
 // 128-element chunks for even PER, with the sequential fold's exact result);
 // the centred squares are formed lane-parallel and folded the same way.
-template <int PER>
+// FAST: both sums in the fast-reduction tree order instead (tree_sum_wave).
+template <int PER, bool FAST = false>
 __device__ __forceinline__ void ln_row_wave(const float (&z)[PER], float* zr, const float (&gv)[PER],
                                             const float (&bv)[PER], int row, int lane, float* out,
                                             int8_t* q, float* a, int* err, float qmult) {
   constexpr int D = PER * 64;
-  const float mean = fold_row_wave<PER>(z, zr, lane) / (float)D;
+  const float mean = (FAST ? tree_sum_wave<PER>(z) : fold_row_wave<PER>(z, zr, lane)) / (float)D;
   float t[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const float c = z[j] - mean;
     t[j] = c * c;
   }
-  const float var = fold_row_wave<PER>(t, zr, lane) / (float)D;
+  const float var = (FAST ? tree_sum_wave<PER>(t) : fold_row_wave<PER>(t, zr, lane)) / (float)D;
   const float inv = 1.0f / sqrtf(var + kLayerNormEpsilon);
   float o[PER];
   float m = 0.0f;
@@ -133,7 +134,7 @@ __device__ __forceinline__ void ln_row_wave(const float (&z)[PER], float* zr, co
 }
 
 // out = LN(y + r), optionally quantized for the next GEMM.  One wave per row.
-template <int PER>
+template <int PER, bool FAST = false>
 __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float* r,
                                                      const float* gamma, const float* beta,
                                                      int rows, const int* rows_dev, float* out,
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(256) void k_residual_ln(const float* y, const float
   float z[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) z[j] = yv[j] + rv[j];
-  ln_row_wave<PER>(z, sZ[wave], gv, bv, row, lane, out, q, a, err, qmult);
+  ln_row_wave<PER, FAST>(z, sZ[wave], gv, bv, row, lane, out, q, a, err, qmult);
 }
 
 // SSRU state update + LayerNorm (ssru_update_layer_norm_into, tensor.rs:184-218,
@@ -576,15 +577,24 @@ hipError_t launch_quantize_rows(const float* x, int64_t ldx, int rows, const int
 
 hipError_t launch_residual_ln(const float* y, const float* r, const float* g, const float* b,
                               int rows, const int* rows_dev, int d, float* out, int8_t* q,
-                              float* a, int* err, hipStream_t s, float qmult) {
+                              float* a, int* err, hipStream_t s, float qmult, bool fast) {
   if (rows <= 0) return hipSuccess;
   if (d % 64) return hipErrorInvalidValue;
   // One wave per row, four rows per workgroup: widths of 256, 384 and 512
-  // fold with the one-wave speculative folds, others sequentially.
+  // fold with the one-wave speculative folds, others sequentially; with
+  // `fast` (the decoder's widths) the sums take the tree order.
   const dim3 grid((rows + 3) / 4), block(256);
 #define MH_LN(P) \
   hipLaunchKernelGGL(k_residual_ln<P>, grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err, qmult)
-  MH_PER_DISPATCH_16(d / 64, MH_LN)
+#define MH_LNF(P)                                                                                            \
+  hipLaunchKernelGGL((k_residual_ln<P, true>), grid, block, 0, s, y, r, g, b, rows, rows_dev, out, q, a, err, \
+                     qmult)
+  if (fast) {
+    MH_PER_DISPATCH(d / 64, MH_LNF)
+  } else {
+    MH_PER_DISPATCH_16(d / 64, MH_LN)
+  }
+#undef MH_LNF
 #undef MH_LN
   return hipGetLastError();
 }

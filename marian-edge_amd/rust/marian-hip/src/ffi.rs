@@ -18,6 +18,7 @@ pub const ERR_NOT_READY: c_int = -6;
 
 pub const FLAG_IGNORE_EOS: u32 = 1 << 0;
 pub const FLAG_NO_GENERATION_MASK: u32 = 1 << 1;
+pub const FLAG_FAST_REDUCTIONS: u32 = 1 << 2;
 
 #[repr(C)]
 #[derive(Clone, Copy)]

@@ -175,7 +175,12 @@ inline float row_sum(const float* x, size_t n, int order) {
 }
 
 inline float exp_op(float x, int order) {
-  return order == ORACLE_ORDER_REFERENCE ? std::exp(x) : canon_expf(x);
+  return order == ORACLE_ORDER_CANONICAL ? canon_expf(x) : std::exp(x);
+}
+
+// The encoder's order: FAST_DECODER keeps the reference's there.
+inline int encoder_order(int order) {
+  return order == ORACLE_ORDER_FAST_DECODER ? ORACLE_ORDER_REFERENCE : order;
 }
 
 // Sequential fp32 dot (tensor.rs:479 on x86: map(a*b).sum()).
@@ -1129,7 +1134,7 @@ static int translate_impl(const oracle_model* model, const int32_t* tokens, size
       const size_t b = next.fetch_add(1);
       if (b >= B) return;
       const size_t L = offsets[b + 1] - offsets[b];
-      if (!encode_sentence(model, g, tokens + offsets[b], L, order, nullptr, s, enc)) {
+      if (!encode_sentence(model, g, tokens + offsets[b], L, encoder_order(order), nullptr, s, enc)) {
         ok = false;
         continue;
       }
@@ -1188,7 +1193,7 @@ int oracle_encode(const oracle_model* model, const int32_t* tokens, size_t n_tok
       const size_t b = next.fetch_add(1);
       if (b >= B) return;
       const size_t L = offsets[b + 1] - offsets[b];
-      if (!encode_sentence(model, g, tokens + offsets[b], L, order, nullptr, s, enc)) ok = false;
+      if (!encode_sentence(model, g, tokens + offsets[b], L, encoder_order(order), nullptr, s, enc)) ok = false;
       else std::memcpy(out + (size_t)offsets[b] * g.d, enc.data(), L * g.d * sizeof(float));
     }
   };
@@ -1206,7 +1211,7 @@ int oracle_last_step_logits(const oracle_model* model, const int32_t* tokens, si
   Scratch s;
   std::vector<float> enc;
   std::vector<int32_t> out;
-  if (!encode_sentence(model, g, tokens, n_tokens, order, nullptr, s, enc)) return -2;
+  if (!encode_sentence(model, g, tokens, n_tokens, encoder_order(order), nullptr, s, enc)) return -2;
   if (!decode_sentence(model, g, enc.data(), n_tokens, steps, flags | ORACLE_FLAG_IGNORE_EOS,
                        order, nullptr, s, out, steps, (int64_t)steps - 1, logits, nullptr))
     return -2;
@@ -1402,7 +1407,7 @@ int oracle_translate_ssru(const oracle_ssru_model* model, const int32_t* tokens,
       const size_t b = next.fetch_add(1);
       if (b >= B) return;
       const size_t L = offsets[b + 1] - offsets[b];
-      if (!encode_sentence_ssru(model, g, tokens + offsets[b], L, order, nullptr, s, enc)) {
+      if (!encode_sentence_ssru(model, g, tokens + offsets[b], L, encoder_order(order), nullptr, s, enc)) {
         ok = false;
         continue;
       }

@@ -33,8 +33,12 @@
  *     xor butterfly, exp via a double-precision Cody-Waite/Taylor routine),
  *     kept to measure how sensitive greedy outputs are to the fp32 summation
  *     order.
+ *   ORACLE_ORDER_FAST_DECODER (2): the order of the HIP engine's opt-in
+ *     MARIAN_HIP_FLAG_FAST_REDUCTIONS: the encoder exactly as REFERENCE; in
+ *     the decoder the LayerNorm sums and softmax denominators as 64 strided
+ *     lane partials + xor butterfly (canon_sum), exp still the C library's.
  * Everything else (dot products, PV accumulation, dequant, LN affine, embedding)
- * uses the reference's sequential op order in both modes.
+ * uses the reference's sequential op order in every mode.
  */
 #ifndef MARIAN_ORACLE_H
 #define MARIAN_ORACLE_H
@@ -46,7 +50,7 @@
 extern "C" {
 #endif
 
-enum { ORACLE_ORDER_CANONICAL = 0, ORACLE_ORDER_REFERENCE = 1 };
+enum { ORACLE_ORDER_CANONICAL = 0, ORACLE_ORDER_REFERENCE = 1, ORACLE_ORDER_FAST_DECODER = 2 };
 
 /* Translate flags (same values as MARIAN_HIP_FLAG_*). */
 enum {

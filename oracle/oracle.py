@@ -18,9 +18,12 @@ LIB_PATH = HERE / "liboracle.so"
 
 # Reduction orders (oracle.h).  REFERENCE, the reference's own order, is the
 # default and the one the HIP kernels reproduce; CANONICAL is kept to measure
-# how sensitive greedy outputs are to the fp32 summation order.
+# how sensitive greedy outputs are to the fp32 summation order; FAST_DECODER is
+# the order of the engine's opt-in fast-reduction flag (encoder as REFERENCE,
+# the decoder's LayerNorm and softmax sums as lane partials + butterfly).
 CANONICAL = 0
 REFERENCE = 1
+FAST_DECODER = 2
 FLAG_IGNORE_EOS = 1
 FLAG_NO_GENERATION_MASK = 2
 
