@@ -74,18 +74,42 @@ def _reference_sub_batches(lengths, cell_cap=65536, batch_cap=256):
 
 
 def _cpu_worker(rows):
-    orc, om, batch, threads = (_CPU_STATE[k] for k in ("orc", "om", "batch", "threads"))
+    """One process's share of the batch, in the reference's padded
+    sub-batches, translated by _CPU_STATE["run"](sub_batch, batch_rows)."""
+    run, batch = _CPU_STATE["run"], _CPU_STATE["batch"]
     sub = batch.subset(rows)
     t0 = time.perf_counter()
     done_ms, ntok = [], 0
     for part in _reference_sub_batches(sub.lengths):
-        b = sub.subset(part)
-        out = orc.translate(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, b.flags,
-                            threads=threads, schedule="reference")
+        out = run(sub.subset(part), [rows[i] for i in part])
         ntok += sum(map(len, out))
         t = (time.perf_counter() - t0) * 1000.0
         done_ms += [t] * len(part)
     return ntok, time.perf_counter() - t0, done_ms
+
+
+def _reference_schedule_port(batch, cores: int, threads: int, run):
+    """The batch spread over cores // threads processes (greedy partition by
+    expected work: source plus forced output length), each running `run` on
+    its padded sub-batches with `threads` threads.  Returns the generated
+    tokens, the slowest process's wall time, the sentences' completion times
+    and the process count."""
+    procs = max(1, cores // threads)
+    lens = batch.lengths
+    work = [(int(lens[i]) + int(batch.max_output_tokens[i]), i) for i in range(len(lens))]
+    parts = [[] for _ in range(procs)]
+    load_ = [0] * procs
+    for w, i in sorted(work, reverse=True):
+        j = int(np.argmin(load_))
+        parts[j].append(i)
+        load_[j] += w
+    parts = [sorted(p) for p in parts if p]
+    _CPU_STATE.update(run=run, batch=batch)
+    ctx = mp.get_context("fork")
+    with ctx.Pool(len(parts)) as pool:
+        res = pool.map(_cpu_worker, parts)
+    return (sum(r[0] for r in res), max(r[1] for r in res), [t for r in res for t in r[2]],
+            len(parts))
 
 
 def host_info(cores_used: int) -> dict:
@@ -112,31 +136,21 @@ def cpu_baseline(pkg, model, batch, cores: int, threads: int = 4):
     import __graft_entry__ as ge
 
     orc = ge.load_oracle()
-    procs = max(1, cores // threads)
+    om = orc.OracleModel(model)
+
+    def run(b, _rows):
+        return orc.translate(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, b.flags,
+                             threads=threads, schedule="reference")
+
+    tokens, wall, lat, nproc = _reference_schedule_port(batch, cores, threads, run)
     lens = batch.lengths
-    # greedy partition by expected work (source + forced output length)
-    work = [(int(lens[i]) + int(batch.max_output_tokens[i]), i) for i in range(len(lens))]
-    parts = [[] for _ in range(procs)]
-    load_ = [0] * procs
-    for w, i in sorted(work, reverse=True):
-        j = int(np.argmin(load_))
-        parts[j].append(i)
-        load_[j] += w
-    parts = [sorted(p) for p in parts if p]
-    _CPU_STATE.update(orc=orc, om=orc.OracleModel(model), batch=batch, threads=threads)
-    ctx = mp.get_context("fork")
-    with ctx.Pool(len(parts)) as pool:
-        res = pool.map(_cpu_worker, parts)
-    tokens = sum(r[0] for r in res)
-    wall = max(r[1] for r in res)
-    lat = [t for r in res for t in r[2]]
     return {
         "value": round(tokens / wall, 2),
         "unit": "tokens/s",
-        "cores": len(parts) * threads,
+        "cores": nproc * threads,
         "kind": "port",
         "sample": (f"the full {len(lens)}-sentence batch ({tokens} target tokens) on "
-                   f"{len(parts)} processes x {threads} threads; reference schedule: padded "
+                   f"{nproc} processes x {threads} threads; reference schedule: padded "
                    "sub-batches (batch*Lmax^2 <= 65536), all rows every step, AVX2 madd "
                    "GEMM, scalar output scoring; generation caps lifted as on the GPU"),
         "p50_ms": round(statistics.median(lat), 2),
@@ -260,8 +274,8 @@ def block_bytes(kind, step, layer, src_lens, d, heads):
 
 
 def attn_bytes(kind, step, src_lens, d, heads):
-    """Algorithmic bytes of one decode attention launch (k_attention, the
-    steps the blocks do not cover) over the active rows whose source lengths
+    """Algorithmic bytes of one decode attention launch (k_attention or
+    k_attn_long, the steps the blocks do not cover) over the active rows whose source lengths
     are `src_lens`: per row the fp32 query, the keys and values it reads
     (self: the `step` + 1 cached rows, this step's written by the projection
     before; cross: the sentence's encoder rows), d floats each, the fp32
@@ -277,7 +291,8 @@ def attn_bytes(kind, step, src_lens, d, heads):
 FAMILIES = {
     "vocab": ((0,), "k_vocab_argmax", "k_vocab_argmax (vocab projection + bias + mask + argmax partials)"),
     "block": ((1, 2), "k_attn_block", "k_attn_block (LayerNorm/embedding + head projection + attention)"),
-    "attention": ((3, 4), "k_attention", "k_attention (decode self- and cross-attention over fp32 K/V rows)"),
+    "attention": ((3, 4), ("k_attention", "k_attn_long"),
+                  "k_attention / k_attn_long (decode self- and cross-attention over fp32 K/V rows)"),
 }
 
 # Active-row buckets of the step table.
@@ -435,29 +450,40 @@ def roofline_of(family, f, tag, timing_note):
     }
 
 
-def ssru_cpu_baseline(model, batch, cand, coff, cores: int):
-    """The oracle's Transformer-SSRU restatement over the same batch and
-    shortlist, sentences spread over `cores` threads (each sentence encoded and
-    decoded on its own, AVX2 int8 dots), timed on this host."""
+def ssru_cpu_baseline(model, batch, cand, coff, cores: int, threads: int = 4):
+    """The oracle's Transformer-SSRU restatement on the reference x86
+    schedule over the same batch and shortlist: one process per `threads`
+    cores, each translating its sentences in the reference's padded
+    sub-batches (every row decoded every step, keys masked by length, u8 AVX2
+    GEMMs split over `threads` threads, scalar scoring of the unfinished rows
+    over their candidates), timed on this host."""
     import __graft_entry__ as ge
 
     orc = ge.load_oracle()
     om = orc.OracleSsruModel(model)
-    t0 = time.perf_counter()
-    out = orc.translate_ssru(om, batch.tokens, batch.offsets, batch.max_output_tokens, batch.limits,
-                             batch.flags, candidates=cand, candidate_offsets=coff, threads=cores)
-    wall = time.perf_counter() - t0
-    ntok = sum(map(len, out))
+    lists = [np.asarray(cand[coff[b]:coff[b + 1]], np.uint32) for b in range(len(coff) - 1)]
+
+    def run(b, rows):
+        c = np.concatenate([lists[r] for r in rows])
+        co = np.zeros(len(rows) + 1, np.uint32)
+        co[1:] = np.cumsum([lists[r].size for r in rows])
+        return orc.translate_ssru(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, b.flags,
+                                  candidates=c, candidate_offsets=co, threads=threads,
+                                  schedule="reference")
+
+    tokens, wall, lat, nproc = _reference_schedule_port(batch, cores, threads, run)
     return {
-        "value": round(ntok / wall, 2),
+        "value": round(tokens / wall, 2),
         "unit": "tokens/s",
-        "cores": cores,
+        "cores": nproc * threads,
         "kind": "port",
-        "sample": (f"the full {len(out)}-sentence batch ({ntok} target tokens) with the same shortlist, "
-                   f"one sentence per thread on {cores} threads (encode, then greedy decode with "
-                   "shortlist scoring), AVX2 int8 dots; generation caps lifted as on the GPU"),
+        "sample": (f"the full {len(batch.lengths)}-sentence batch ({tokens} target tokens) with the same "
+                   f"shortlist on {nproc} processes x {threads} threads; reference schedule: padded "
+                   "sub-batches (batch*Lmax^2 <= 65536), all rows every step, AVX2 madd GEMM, scalar "
+                   "shortlist scoring; generation caps lifted as on the GPU"),
+        "p50_ms": round(statistics.median(lat), 2),
         "wall_s": round(wall, 3),
-        "host": host_info(cores),
+        "host": host_info(nproc * threads),
     }
 
 

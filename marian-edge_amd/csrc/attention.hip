@@ -462,6 +462,140 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   if (__any(bad) && lane == 0 && a.err) *a.err = 1;
 }
 
+// ---------------------------------------------------------------------------
+// Decode attention over long key ranges (ATT_CROSS / ATT_SELF, 129 to 512
+// keys): one workgroup of W = blockDim.x / 64 waves (3 to 8, the launch's key
+// bound in 64-key chunks) per (row, head); wave w owns the keys
+// [64w, 64w + 64) of the row.  Every wave requests its keys' K rows (lane =
+// key, the head's 64 values in 16 float4) and V values (lane = dimension, one
+// value per key) before anything else, so a row's whole key range is one
+// memory round trip instead of one per 64-key chunk.  The arithmetic is
+// k_attention's, in the reference order:
+//   * scores: lane = key, the 64-term dot in dimension order from -0.0, the
+//     query broadcast from its lanes;
+//   * max over the workgroup (waves' maxima through LDS), the C library's
+//     expf, the denominator folded in key order from 0.0 by wave 0 over the
+//     exponentials in LDS (with FAST: the tree order, as in k_attention);
+//   * PV: out_d = sum_k p_k v_k[d] in key order.  Each wave forms its keys'
+//     products (lane = dimension, p broadcast from the score lanes), then the
+//     running sums pass from wave to wave in key order through LDS, one
+//     barrier per 64-key chunk, each wave adding its 64 products in order.
+// Keys past the row's count have p = 0 (their values reloaded from its last
+// key), so their products are +-0 and leave the sums unchanged.
+// The workgroup holds its waves through these dependent phases, so it pays
+// where few (row, head) pairs leave the chip idle; with many, the one-wave
+// kernel keeps more loads in flight per CU (launch_attention chooses).
+// ---------------------------------------------------------------------------
+constexpr int kLongWaves = 8;  // the most waves per workgroup
+constexpr int kLongMaxKeys = 64 * kLongWaves;
+constexpr int kLongMaxPairs = 512;  // (row, head) pairs up to which it runs
+
+template <int DH, bool FAST>
+__global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
+  static_assert(DH == 64 || DH == 48, "head widths");
+  __shared__ __attribute__((aligned(16))) float sE[kLongMaxKeys];  // exponentials of the keys
+  __shared__ float sO[64];                                          // the PV relay
+  __shared__ float sMax[kLongWaves];
+  __shared__ float sInv;
+  __shared__ uint64_t sTab[32];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int nw = blockDim.x >> 6;  // 3..kLongWaves, set by the launch
+  const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
+  const uint64_t tab_v = kExp2Tab[lane & 31];
+
+  // This row's key range, read before the device row count (rows past it
+  // read clamped stale ranges and are discarded below).
+  int64_t key0 = a.row_key0[r];
+  int nk = a.mode == ATT_CROSS ? a.row_nk[r] : a.step + 1;
+  nk = max(nk, 1);
+  key0 = min(max(key0, (int64_t)0), a.max_row - 1);
+  const bool too_long = nk > 64 * nw;
+  if (too_long) nk = 64 * nw;
+  const int nk_ld = (int)min((int64_t)nk, a.max_row - key0);  // readable rows
+  const int nch = (nk + 63) >> 6;
+  const int kc = 64 * w;         // this wave's first key
+  const bool mine = kc < nk;     // uniform per wave
+  const int64_t kbase = key0 * a.ldkv + h * DH;
+
+  f4v kr[DH / 4];
+  float vv[64];
+  if (mine) {
+    const int key = min(kc + lane, nk_ld - 1);
+#pragma unroll
+    for (int i = 0; i < DH / 4; ++i) kr[i] = *(const f4v*)((const float*)a.k + kbase + (int64_t)key * a.ldkv + 4 * i);
+    const int d = min(lane, DH - 1);
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const int kj = min(kc + j, nk_ld - 1);
+      vv[j] = ((const float*)a.v)[kbase + (int64_t)kj * a.ldkv + d];
+    }
+  }
+  const int qv = __float_as_int(((const float*)a.q)[(int64_t)r * a.ldq + h * DH + min(lane, DH - 1)]);
+  const int n = a.rows_dev ? *a.rows_dev : a.rows;
+  if (r >= n) return;  // the whole workgroup alike
+  if (too_long && tid == 0 && a.err) *a.err = 2;
+  if (tid < 32) sTab[tid] = tab_v;
+
+  // ---- scores and the row maximum ----
+  const float scale = 1.0f / sqrtf((float)DH);
+  const bool valid = mine && kc + lane < nk;
+  float sc = -INFINITY;
+  if (mine) {
+    float dot = -0.0f;
+#pragma unroll
+    for (int i = 0; i < DH; ++i)
+      dot = dot + __int_as_float(__builtin_amdgcn_readlane(qv, i)) * kr[i >> 2][i & 3];
+    if (valid) sc = dot * scale;
+  }
+  const float wmax = wave_max(sc);
+  if (lane == 0) sMax[w] = wmax;
+  __syncthreads();  // also publishes sTab
+  float mx = sMax[0];
+  for (int i = 1; i < nw; ++i) mx = fmaxf(mx, sMax[i]);
+  const float e = valid ? ref_expf(sc - mx, sTab) : 0.0f;
+  if (mine) sE[kc + lane] = e;
+
+  // ---- denominator (wave 0) ----
+  __syncthreads();  // every exponential is in LDS
+  if (w == 0) {
+    float sum;
+    if constexpr (FAST) {
+      sum = 0.0f;  // lane l: keys l, 64 + l, ... in order from 0.0, then the butterfly
+      for (int c = 0; c < nch; ++c) sum = sum + sE[64 * c + lane];
+      sum = tree_combine_wave(sum);
+    } else {
+      // keys in order from 0.0, whole batches of 16 (zeros past the last key)
+      sum = seq_fold_lds_batches<4>((const float4*)sE, (nk + 15) >> 4, 0.0f);
+    }
+    if (lane == 0) sInv = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = sInv;
+
+  // ---- PV: products, then the in-order relay across the waves ----
+  float o = 0.0f;
+  if (mine) {
+    const int pc = __float_as_int(e * inv);  // p of key kc + lane
+#pragma unroll
+    for (int j = 0; j < 64; ++j) vv[j] = vv[j] * __int_as_float(__builtin_amdgcn_readlane(pc, j));
+  }
+  for (int c = 0; c < nch; ++c) {  // nch is uniform over the workgroup
+    if (w == c) {
+      o = c == 0 ? 0.0f : sO[lane];
+#pragma unroll
+      for (int j = 0; j < 64; ++j) o = o + vv[j];
+      if (c + 1 < nch) sO[lane] = o;
+    }
+    if (c + 1 < nch) __syncthreads();
+  }
+  if (w != nch - 1) return;
+  if (lane < DH) a.out[(int64_t)r * a.ldo + h * DH + lane] = o;
+  const bool bad = lane < DH && !isfinite(o);
+  const float m = wave_max(lane < DH ? fabsf(o) : 0.0f);
+  if (lane == 0 && a.amax) a.amax[(int64_t)r * a.heads + h] = m;
+  if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+}
+
 // ev_start / ev_stop (optional) are recorded by the launch's own dispatch.
 template <int CH, typename T, bool PRE>
 hipError_t launch_t(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
@@ -476,6 +610,15 @@ hipError_t launch_t(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t
 template <int CH, bool PRE = false>
 hipError_t launch_ch(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   return a.bf16 ? launch_t<CH, uint16_t, PRE>(a, s, ev0, ev1) : launch_t<CH, float, PRE>(a, s, ev0, ev1);
+}
+
+template <int DH, bool FAST>
+hipError_t launch_long(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+  if (ev0 || ev1)
+    hipExtLaunchKernelGGL((k_attn_long<DH, FAST>), grid, block, 0, s, ev0, ev1, 0, a);
+  else
+    hipLaunchKernelGGL((k_attn_long<DH, FAST>), grid, block, 0, s, a);
+  return hipGetLastError();
 }
 
 template <typename T>
@@ -520,6 +663,13 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s, hipEvent_t ev_star
   hipEvent_t e0 = ev_start, e1 = ev_stop;
   if (a.max_keys <= 128)
     return a.mode == ATT_SEQ ? launch_ch<2>(a, s, e0, e1) : launch_ch<2, true>(a, s, e0, e1);
+  if (a.max_keys <= kLongMaxKeys && a.mode != ATT_SEQ && !a.bf16 && !a.qout &&
+      a.rows * a.heads <= kLongMaxPairs) {
+    const dim3 grid(a.rows * a.heads), block(64 * ((a.max_keys + 63) / 64));
+    if (a.head_dim == 64)
+      return a.fast ? launch_long<64, true>(a, grid, block, s, e0, e1) : launch_long<64, false>(a, grid, block, s, e0, e1);
+    return a.fast ? launch_long<48, true>(a, grid, block, s, e0, e1) : launch_long<48, false>(a, grid, block, s, e0, e1);
+  }
   if (a.max_keys <= 512) return launch_ch<8>(a, s, e0, e1);
   if (a.max_keys <= 1024) return launch_ch<16>(a, s, e0, e1);
   if (a.max_keys <= 4096) return launch_ch<64>(a, s, e0, e1);

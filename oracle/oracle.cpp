@@ -739,6 +739,29 @@ bool linear_static(Pool* pool, Scratch& s, const float* x, size_t M, size_t K,
   return true;
 }
 
+// Reference-schedule static linear (timed CPU baseline): the elements
+// quantized with act_mult as u8 (q + 127, quantize_symmetric_u8_into
+// q8_gemm.rs:569-590) into the AVX2 kernel (q8_avx2.rs:125-229), then the
+// same dequantization as linear_static.
+bool linear_static_reference(Pool* pool, Scratch& s, const float* x, size_t M, size_t K,
+                             const oracle_static_linear* lin, size_t N, bool relu, float* y) {
+  s.qu.resize(M * K);
+  s.acc.resize(M * N);
+  for (size_t i = 0; i < M * K; ++i) {
+    if (!std::isfinite(x[i])) return false;
+    s.qu[i] = (uint8_t)((int)quantize_one(x[i], lin->act_mult) + 127);
+  }
+  if (!gemm_u8_reference(pool, s.qu.data(), M, K, lin->weight, N, 127, s.acc.data())) return false;
+  const float inv = 1.0f / (lin->act_mult * lin->weight_mult);
+  for (size_t m = 0; m < M; ++m)
+    for (size_t n = 0; n < N; ++n) {
+      float v = (float)s.acc[m * N + n] * inv + (lin->bias ? lin->bias[n] : 0.0f);
+      if (relu) v = v > 0.0f ? v : 0.0f;
+      y[m * N + n] = v;
+    }
+  return true;
+}
+
 struct SsruGeometry {
   size_t Vs, Vt, d, H, dh, F, Le, Ld;
   float emb_scale;
@@ -1427,6 +1450,156 @@ int oracle_translate_ssru(const oracle_ssru_model* model, const int32_t* tokens,
   work();
   for (auto& w : workers) w.join();
   if (!ok) return e.fail(-2, "non-finite activation or accumulator overflow");
+  return pack_output(gen, out_tokens, out_cap, out_offsets, out_len, e);
+}
+
+// ---------------------------------------------------------------------------
+// The Transformer-SSRU graph on the reference schedule (timed CPU baseline).
+// Mirrors Q8CpuEngine::translate_token_ids (q8_engine.rs:353-466): the batch
+// padded to [batch x Lmax] with token 0 (encode, :511-558), every encoder and
+// cross-projection GEMM over all padded rows, keys masked by length; then
+// every row decoded at every step, finished or not (:382-436), and only the
+// unfinished rows scored over their candidates with the scalar u8 x i8 dot
+// (select_token, :749-790; q8_arm.rs:50-55).  Same tokens as
+// oracle_translate_ssru.
+// ---------------------------------------------------------------------------
+int oracle_translate_ssru_reference_schedule(
+    const oracle_ssru_model* model, const int32_t* tokens, size_t n_tokens, const uint32_t* offsets,
+    size_t n_offsets, const uint32_t* max_output_tokens, const oracle_limits* limits, uint32_t flags,
+    int order, int threads, const uint32_t* candidates, const uint32_t* cand_offsets,
+    int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
+    size_t err_cap) {
+  Err e{err, err_cap};
+  if (!ssru_model_ok(model)) return e.fail(-2, "invalid model description");
+  oracle_model view{};
+  view.vocab = model->source_vocab;
+  std::vector<uint32_t> lim;
+  int rc = validate(&view, tokens, n_tokens, offsets, n_offsets, max_output_tokens, limits, lim, e);
+  if (rc) return rc;
+  if (!have_avx2()) return e.fail(-2, "the reference x86 schedule needs AVX2");
+  const SsruGeometry g = ssru_geometry(model);
+  const size_t d = g.d, B = n_offsets - 1;
+  if (candidates) {
+    if (!cand_offsets || cand_offsets[0] != 0) return e.fail(-1, "invalid candidate offsets");
+    for (size_t b = 0; b < B; ++b) {
+      if (cand_offsets[b + 1] <= cand_offsets[b])
+        return e.fail(-1, "cannot select from an empty candidate list");
+      for (uint32_t i = cand_offsets[b]; i < cand_offsets[b + 1]; ++i)
+        if (candidates[i] >= g.Vt)
+          return e.fail(-1, "output candidate %u exceeds vocabulary %zu", candidates[i], g.Vt);
+    }
+  }
+  Pool pool(threads);
+  Scratch s;
+  const auto& pos = positions_for(model->dim);
+  std::vector<size_t> len(B);
+  size_t Lmax = 0;
+  for (size_t b = 0; b < B; ++b) {
+    len[b] = offsets[b + 1] - offsets[b];
+    Lmax = std::max(Lmax, len[b]);
+  }
+  const size_t R = B * Lmax;
+  std::vector<float> x(R * d), q(R * d), k(R * d), v(R * d), att(R * d), y(R * d), h(R * g.F),
+      x2(R * d), sc;
+  for (size_t b = 0; b < B; ++b)
+    for (size_t i = 0; i < Lmax; ++i) {
+      const int32_t t = i < len[b] ? tokens[offsets[b] + i] : 0;
+      embed_static(model->encoder_embedding, model->encoder_embedding_mult, d, g.emb_scale, t,
+                   pos.data() + i * d, x.data() + (b * Lmax + i) * d);
+    }
+  auto fail = [&] { return e.fail(-2, "non-finite activation or accumulator overflow"); };
+  for (size_t l = 0; l < g.Le; ++l) {
+    const oracle_ssru_encoder_layer& E = model->encoder[l];
+    if (!linear_static_reference(&pool, s, x.data(), R, d, &E.wq, d, false, q.data()) ||
+        !linear_static_reference(&pool, s, x.data(), R, d, &E.wk, d, false, k.data()) ||
+        !linear_static_reference(&pool, s, x.data(), R, d, &E.wv, d, false, v.data()))
+      return fail();
+    for (size_t b = 0; b < B; ++b)  // every padded query row, keys masked to the length
+      attend_rows(q.data() + b * Lmax * d, k.data() + b * Lmax * d, v.data() + b * Lmax * d, Lmax,
+                  len[b], g, order, att.data() + b * Lmax * d, sc);
+    if (!linear_static_reference(&pool, s, att.data(), R, d, &E.wo, d, false, y.data())) return fail();
+    residual_ln(y.data(), x.data(), E.attn_ln_scale, E.attn_ln_bias, R, d, order, x2.data());
+    if (!linear_static_reference(&pool, s, x2.data(), R, d, &E.w1, g.F, true, h.data()) ||
+        !linear_static_reference(&pool, s, h.data(), R, g.F, &E.w2, d, false, y.data()))
+      return fail();
+    residual_ln(y.data(), x2.data(), E.ffn_ln_scale, E.ffn_ln_bias, R, d, order, x.data());
+  }
+  std::vector<std::vector<float>> ck(g.Ld, std::vector<float>(R * d)), cv(g.Ld, std::vector<float>(R * d));
+  for (size_t l = 0; l < g.Ld; ++l)
+    if (!linear_static_reference(&pool, s, x.data(), R, d, &model->decoder[l].wk, d, false, ck[l].data()) ||
+        !linear_static_reference(&pool, s, x.data(), R, d, &model->decoder[l].wv, d, false, cv[l].data()))
+      return fail();
+
+  uint32_t gen_limit = 0;
+  for (uint32_t l : lim) gen_limit = std::max(gen_limit, l);
+  std::vector<std::vector<float>> state(g.Ld, std::vector<float>(B * d, 0.0f));
+  std::vector<int32_t> prev(B, -1);
+  std::vector<char> finished(B, 0);
+  std::vector<std::vector<int32_t>> gen(B);
+  std::vector<float> dx(B * d), du(B * d), df(B * d), dx1(B * d), dq(B * d), datt(B * d), dy(B * d),
+      dx2(B * d), dh(B * g.F);
+  std::vector<uint8_t> qu(d);
+  const float inv_out = 1.0f / (model->output_act_mult * model->decoder_embedding_mult);
+  for (uint32_t t = 0; t < gen_limit; ++t) {
+    bool all = true;
+    for (size_t b = 0; b < B; ++b) {
+      if (!finished[b] && t >= lim[b]) finished[b] = 1;
+      all = all && finished[b];
+    }
+    if (all) break;
+    for (size_t b = 0; b < B; ++b) {
+      if (prev[b] < 0)
+        std::memcpy(dx.data() + b * d, pos.data() + (size_t)t * d, d * sizeof(float));
+      else
+        embed_static(model->decoder_embedding, model->decoder_embedding_mult, d, g.emb_scale, prev[b],
+                     pos.data() + (size_t)t * d, dx.data() + b * d);
+    }
+    for (size_t l = 0; l < g.Ld; ++l) {
+      const oracle_ssru_decoder_layer& D = model->decoder[l];
+      if (!linear_static_reference(&pool, s, dx.data(), B, d, &D.ssru_w, d, false, du.data()) ||
+          !linear_static_reference(&pool, s, dx.data(), B, d, &D.ssru_wf, d, false, df.data()))
+        return fail();
+      oracle_ssru_layer_norm(du.data(), df.data(), state[l].data(), dx.data(), D.ssru_ln_scale,
+                             D.ssru_ln_bias, B, d, order, dx1.data());
+      if (!linear_static_reference(&pool, s, dx1.data(), B, d, &D.wq, d, false, dq.data())) return fail();
+      for (size_t b = 0; b < B; ++b)
+        attend_rows(dq.data() + b * d, ck[l].data() + b * Lmax * d, cv[l].data() + b * Lmax * d, 1,
+                    len[b], g, order, datt.data() + b * d, sc);
+      if (!linear_static_reference(&pool, s, datt.data(), B, d, &D.wo, d, false, dy.data())) return fail();
+      residual_ln(dy.data(), dx1.data(), D.context_ln_scale, D.context_ln_bias, B, d, order, dx2.data());
+      if (!linear_static_reference(&pool, s, dx2.data(), B, d, &D.w1, g.F, true, dh.data()) ||
+          !linear_static_reference(&pool, s, dh.data(), B, g.F, &D.w2, d, false, dy.data()))
+        return fail();
+      residual_ln(dy.data(), dx2.data(), D.ffn_ln_scale, D.ffn_ln_bias, B, d, order, dx.data());
+    }
+    for (size_t b = 0; b < B; ++b) {
+      if (finished[b]) continue;
+      const float* st = dx.data() + b * d;
+      for (size_t i = 0; i < d; ++i) {
+        if (!std::isfinite(st[i])) return fail();
+        qu[i] = (uint8_t)((int)quantize_one(st[i], model->output_act_mult) + 127);
+      }
+      const uint32_t* c = candidates ? candidates + cand_offsets[b] : nullptr;
+      const size_t nc = candidates ? cand_offsets[b + 1] - cand_offsets[b] : g.Vt;
+      int32_t best = -1;
+      float best_v = -INFINITY;
+      for (size_t i = 0; i < nc; ++i) {
+        const size_t id = c ? c[i] : i;
+        if (!c && generation_masked(id, flags)) continue;
+        const int32_t acc = oracle_dot_u8_i8(qu.data(), model->decoder_embedding + id * d, d);
+        const float lg = (float)acc * inv_out + model->output_bias[id];
+        if (best < 0) best = (int32_t)id;
+        if (lg > best_v) {
+          best_v = lg;
+          best = (int32_t)id;
+        }
+      }
+      const int32_t token = best < 0 ? 0 : best;
+      prev[b] = token;
+      gen[b].push_back(token);
+      if (token == 0 && !(flags & ORACLE_FLAG_IGNORE_EOS)) finished[b] = 1;
+    }
+  }
   return pack_output(gen, out_tokens, out_cap, out_offsets, out_len, e);
 }
 

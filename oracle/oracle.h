@@ -293,6 +293,16 @@ int oracle_translate_ssru(const oracle_ssru_model* model, const int32_t* tokens,
                           uint32_t probe_step, float* enc_out, float* logits_out,
                           uint8_t* active_out);
 
+/* oracle_translate_ssru executed the way the reference x86 engine schedules
+ * the work (padded batch, every row decoded every step, u8 AVX2 GEMMs, scalar
+ * scoring); the same tokens.  Timed CPU baseline. */
+int oracle_translate_ssru_reference_schedule(
+    const oracle_ssru_model* model, const int32_t* tokens, size_t n_tokens, const uint32_t* offsets,
+    size_t n_offsets, const uint32_t* max_output_tokens, const oracle_limits* limits, uint32_t flags,
+    int order, int threads, const uint32_t* candidates, const uint32_t* cand_offsets,
+    int32_t* out_tokens, size_t out_cap, uint32_t* out_offsets, size_t* out_len, char* err,
+    size_t err_cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -136,6 +136,10 @@ _SIG = {
                                         C.POINTER(Limits), C.c_uint32, C.c_int, C.c_int, _P, _P,
                                         _P, _SZ, _P, C.POINTER(_SZ), C.c_char_p, _SZ, C.c_uint32,
                                         _P, _P, _P]),
+    "oracle_translate_ssru_reference_schedule": (C.c_int, [C.POINTER(SsruModelStruct), _P, _SZ, _P, _SZ,
+                                                           _P, C.POINTER(Limits), C.c_uint32, C.c_int,
+                                                           C.c_int, _P, _P, _P, _SZ, _P, C.POINTER(_SZ),
+                                                           C.c_char_p, _SZ]),
     "oracle_last_step_logits": (C.c_int, [C.POINTER(Model), _P, _SZ, C.c_uint32, C.c_uint32,
                                           C.c_int, _P]),
 }
@@ -241,10 +245,13 @@ class OracleSsruModel:
 
 def translate_ssru(model: OracleSsruModel, tokens, offsets, max_output_tokens, limits: dict,
                    flags=0, candidates=None, candidate_offsets=None, probe_step=None,
-                   order=REFERENCE, threads=8):
+                   order=REFERENCE, threads=8, schedule="ragged"):
     """Greedy translation over the Transformer-SSRU graph.  Returns the token
     lists; with probe_step also the encoder states [T, d], the logits [B, Vt]
-    of that step (ids not scored are -inf) and the rows that reached it."""
+    of that step (ids not scored are -inf) and the rows that reached it.
+    schedule="reference" runs the reference x86 engine's schedule instead (a
+    padded batch, every row decoded every step, `threads` splitting the
+    GEMMs' rows; the timed CPU baseline; no probe): the same tokens."""
     lib = load()
     toks = np.ascontiguousarray(tokens, np.int32)
     offs = np.ascontiguousarray(offsets, np.uint32)
@@ -260,6 +267,16 @@ def translate_ssru(model: OracleSsruModel, tokens, offsets, max_output_tokens, l
     cand = None if candidates is None else np.ascontiguousarray(candidates, np.uint32)
     coff = None if candidate_offsets is None else np.ascontiguousarray(candidate_offsets, np.uint32)
     enc = logits = active = None
+    if schedule != "ragged":
+        if schedule != "reference" or probe_step is not None:
+            raise ValueError("schedule is 'ragged' or 'reference' (the latter without a probe)")
+        rc = lib.oracle_translate_ssru_reference_schedule(
+            C.byref(model.struct), _ptr(toks) if toks.size else None, toks.size, _ptr(offs), offs.size,
+            _ptr(req), C.byref(lim), flags, order, threads, _ptr(cand), _ptr(coff), _ptr(out), cap,
+            _ptr(out_offs), C.byref(n), err, 512)
+        if rc != 0:
+            raise OracleError(rc, err.value.decode())
+        return [out[out_offs[i]:out_offs[i + 1]].tolist() for i in range(B)]
     if probe_step is not None:
         enc = np.zeros((max(toks.size, 1), g.dim), np.float32)
         logits = np.zeros((max(B, 1), g.target_vocab), np.float32)

@@ -58,17 +58,17 @@ def test_fast_probe_row_thresholds(pkg, orc, small, rows):
     assert check(f"fast, rows={rows}", res) == rows
 
 
-@pytest.mark.parametrize("step", [127, 128])
+@pytest.mark.parametrize("step", [127, 128, 200])
 def test_fast_probe_self_key_threshold(pkg, orc, small, step):
     engine, om, V = small
     rng = np.random.default_rng(17)
     toks, offs = sentences(rng, 2, 10, 30, V)
-    res = probe_fast(pkg, orc, engine, om, toks, offs, [200, 200], pkg.FLAG_IGNORE_EOS, step,
+    res = probe_fast(pkg, orc, engine, om, toks, offs, [step + 1, step + 1], pkg.FLAG_IGNORE_EOS, step,
                      pkg.LIFTED_LIMITS)
     assert check(f"fast, self keys={step + 1}", res) == 2
 
 
-@pytest.mark.parametrize("src_len", [128, 129])
+@pytest.mark.parametrize("src_len", [128, 129, 300, 512, 513])
 def test_fast_probe_cross_key_threshold(pkg, orc, small, src_len):
     engine, om, V = small
     rng = np.random.default_rng(1000 + src_len)

@@ -10,7 +10,9 @@ down-projection that quantizes its fp32 input, the attention-output
 projection with its 16-row groups, and the vocabulary kernel with and without
 its LayerNorm prologue.  The cases straddle every row and key threshold at
 which the engine switches kernels: 1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64 and
-65 active rows; 128 and 129 cached keys; 128 and 129 source tokens.
+65 active rows; 128, 129 and 201 cached keys; 128, 129, 300, 512 and 513
+source tokens (one wave per (row, head) up to 128 keys, eight waves up to
+512, 64-key chunks past that), at head widths 64 and 48.
 
 Limits are capped at probe_step + 1 on both sides: a row is active at the
 probed step, and its logits there are the same, whatever happens afterwards.
@@ -72,17 +74,17 @@ def test_probe_row_thresholds(pkg, orc, small, rows):
     assert check(f"rows={rows}", res) == rows
 
 
-@pytest.mark.parametrize("step", [127, 128])
+@pytest.mark.parametrize("step", [127, 128, 200])
 def test_probe_self_key_threshold(pkg, orc, small, step):
     engine, om, V = small
     rng = np.random.default_rng(7)
     toks, offs = sentences(rng, 2, 10, 30, V)
-    res = probe_both(pkg, orc, engine, om, toks, offs, [200, 200], pkg.FLAG_IGNORE_EOS, step,
+    res = probe_both(pkg, orc, engine, om, toks, offs, [step + 1, step + 1], pkg.FLAG_IGNORE_EOS, step,
                      pkg.LIFTED_LIMITS)
     assert check(f"self keys={step + 1}", res) == 2
 
 
-@pytest.mark.parametrize("src_len", [128, 129])
+@pytest.mark.parametrize("src_len", [128, 129, 300, 512, 513])
 def test_probe_cross_key_threshold(pkg, orc, small, src_len):
     engine, om, V = small
     rng = np.random.default_rng(src_len)
@@ -93,6 +95,24 @@ def test_probe_cross_key_threshold(pkg, orc, small, src_len):
     res = probe_both(pkg, orc, engine, om, toks, offs, [6] * 4, pkg.FLAG_IGNORE_EOS, 2,
                      pkg.LIFTED_LIMITS)
     assert check(f"source tokens={src_len}", res) == 4
+
+
+@pytest.mark.parametrize("src_len, step", [(129, 2), (300, 2), (512, 2), (40, 150)])
+def test_probe_long_keys_head_width_48(pkg, orc, src_len, step):
+    """Eight heads of width 48 (d = 384): cross-attention over long sources and
+    self-attention past 128 cached keys."""
+    g = pkg.Geometry(vocab=3000, encoder_layers=1, decoder_layers=2, dim=384, heads=8, ffn_dim=768)
+    model = pkg.seeded_model(seed=23, geometry=g)
+    om = orc.OracleModel(model)
+    rng = np.random.default_rng(src_len + step)
+    toks, offs = sentences(rng, 3, 5, 30, g.vocab)
+    long = rng.integers(3, g.vocab, size=src_len).astype(np.int32)
+    toks = np.concatenate([toks, long])
+    offs = np.append(offs, offs[-1] + src_len).astype(np.uint32)
+    with pkg.HipEngine(model, limits=pkg.LIFTED_LIMITS) as e:
+        res = probe_both(pkg, orc, e, om, toks, offs, [step + 1] * 4, pkg.FLAG_IGNORE_EOS, step,
+                         pkg.LIFTED_LIMITS)
+        assert check(f"head width 48, source tokens={src_len}, step {step}", res) == 4
 
 
 def test_probe_without_generation_mask(pkg, orc, small):

@@ -221,3 +221,35 @@ def test_candidate_and_input_errors(pkg, orc, rmodel):
     bad[0] = rmodel.geometry.source_vocab  # source id checked against the source vocabulary
     with pytest.raises(orc.OracleError):
         orc.translate_ssru(om, bad, offs, [3, 3], pkg.LIFTED_LIMITS)
+
+
+@pytest.mark.parametrize("scoring", ["full", "shortlist"])
+@pytest.mark.parametrize("flags", [0, 1])
+def test_reference_schedule_gives_the_same_tokens(pkg, orc, sl, rmodel, scoring, flags):
+    """The padded, all-rows schedule (the timed CPU baseline: keys masked by
+    length, finished rows still decoded, u8 AVX2 GEMMs) against the
+    per-sentence restatement, with end-of-sentence stops on and off.  With
+    stops on, the EOS id's bias is raised so that two sentences end at their
+    first token while the others run to their limits."""
+    m = rmodel
+    if flags == 0:
+        m = copy.deepcopy(rmodel)
+        m.output_bias[0] += 1.5
+    om = orc.OracleSsruModel(m)
+    toks, offs = batch(n=7, seed=31)
+    g = rmodel.geometry
+    cand = coff = None
+    if scoring == "shortlist":
+        cand, coff, _ = shortlist_for(sl, toks, offs, g.source_vocab, g.target_vocab, seed=8)
+    req = np.array([9, 3, 12, 1, 7, 12, 5], np.uint32)
+    ragged = orc.translate_ssru(om, toks, offs, req, pkg.LIFTED_LIMITS, flags=flags,
+                                candidates=cand, candidate_offsets=coff)
+    padded = orc.translate_ssru(om, toks, offs, req, pkg.LIFTED_LIMITS, flags=flags,
+                                candidates=cand, candidate_offsets=coff, threads=4,
+                                schedule="reference")
+    print(f"{scoring}, flags {flags}: lengths {[len(r) for r in ragged]}")
+    assert padded == ragged
+    stopped = [len(r) < int(n) and r[-1] == 0 for r, n in zip(ragged, req)]
+    assert any(stopped) == (flags == 0) and not all(stopped)
+    with pytest.raises(ValueError):
+        orc.translate_ssru(om, toks, offs, req, pkg.LIFTED_LIMITS, schedule="reference", probe_step=1)
