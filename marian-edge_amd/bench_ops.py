@@ -136,6 +136,38 @@ def copy_calibration(mb: int, reps: int) -> None:
     print(f"copied {mb} MiB x {reps}", flush=True)
 
 
+def memory_rates(mb: int, reps: int) -> dict:
+    """The runtime's fill and device-to-device copy kernels on `mb` MiB
+    buffers, `reps` calls each between two events: the practical write-only
+    and read+write rates of this device, next to the 8 TB/s peak."""
+    pkg = _load_package()
+    from importlib import import_module
+
+    dev = import_module(pkg.__name__ + ".device")
+    n = mb * 1024 * 1024
+    a = dev.DeviceArray((n // 4,), np.float32)
+    b = dev.DeviceArray((n // 4,), np.float32)
+    out = {"mib": mb, "calls": reps}
+    for name, fn, moved in (("fill", lambda: a.fill_bytes(1), n), ("copy", lambda: dev.copy(b, a), 2 * n)):
+        fn()
+        fn()
+        dev.synchronize()
+        e0, e1 = dev.Event(), dev.Event()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.sync()
+        us = e0.elapsed_ms(e1) / reps * 1000.0
+        out[name] = {"us_per_call": round(us, 1), "bytes_moved": moved,
+                     "gb_per_s": round(moved / us / 1e3, 0), "frac_of_8tbs": round(moved / us / 1e3 / 8000, 3)}
+        e0.close()
+        e1.close()
+    a.free()
+    b.free()
+    return out
+
+
 def pmc_summary(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_csv: str,
                 copy_mb: int, workload: str) -> dict:
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the decode kernels from
@@ -308,7 +340,26 @@ def step_breakdown(trace_csv: str, steps_per_batch: int, batches: int, rows_at: 
     return "\n".join(out)
 
 
-def summarize(run_path: str, trace_path: str) -> str:
+def _mfma_ops_per_dispatch(counter_csv: str) -> list:
+    """int8 MFMA operations (SQ_INSTS_VALU_MFMA_MOPS_I8 x 512) of every
+    marian-hip dispatch of a rocprofv3 --pmc run, in dispatch order."""
+    per: dict = {}
+    with open(counter_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            if "mh::" not in r["Kernel_Name"] or r["Counter_Name"] != "SQ_INSTS_VALU_MFMA_MOPS_I8":
+                continue
+            d = int(r.get("Dispatch_Id") or r.get("Correlation_Id"))
+            per[d] = per.get(d, 0.0) + float(r["Counter_Value"])
+    return [per[d] * 512 for d in sorted(per)]
+
+
+def summarize(run_path: str, trace_path: str, counter_csv: str | None = None) -> str:
+    """The op sweep's table from the run's case list and a kernel trace of
+    the same command; with the counter file of a `--pmc
+    SQ_INSTS_VALU_MFMA_MOPS_I8` run of it, also the int8 operations the
+    matrix cores executed per call and the fraction of the dense peak they
+    make at the traced time (the counted operations include the tiles' zero
+    padding past M and N)."""
     spec = json.loads(Path(run_path).read_text())
     rows = []
     with open(trace_path, newline="") as f:
@@ -319,14 +370,23 @@ def summarize(run_path: str, trace_path: str) -> str:
     need = sum(c["calls"] * c["kernels_per_call"] for c in spec["cases"])
     if len(rows) != need:
         raise SystemExit(f"trace holds {len(rows)} marian-hip dispatches, the run made {need}")
-    out = ["| case | kernels | median us / call | algorithmic MB | GB/s | frac of 8 TB/s | int8 MFMA frac |",
-           "|---|---|---:|---:|---:|---:|---:|"]
+    ops = _mfma_ops_per_dispatch(counter_csv) if counter_csv else None
+    if ops is not None and len(ops) != need:
+        raise SystemExit(f"counter file holds {len(ops)} marian-hip dispatches, the run made {need}")
+    head = "| case | kernels | median us / call | algorithmic MB | GB/s | frac of 8 TB/s | int8 MFMA frac |"
+    rule = "|---|---|---:|---:|---:|---:|---:|"
+    if ops is not None:
+        head += " counted int8 GOP / call | counted MFMA frac |"
+        rule += "---:|---:|"
+    out = [head, rule]
     i = 0
     for c in spec["cases"]:
-        per_call = []
+        per_call, per_ops = [], []
         names = set()
         for _ in range(c["calls"]):
             ks = rows[i:i + c["kernels_per_call"]]
+            if ops is not None:
+                per_ops.append(sum(ops[i:i + c["kernels_per_call"]]))
             i += c["kernels_per_call"]
             per_call.append(sum(e - s for s, e, _ in ks) / 1000.0)
             names.update(n.replace("mh::(anonymous namespace)::", "").replace("void ", "").split("(")[0]
@@ -334,9 +394,16 @@ def summarize(run_path: str, trace_path: str) -> str:
         us = statistics.median(per_call[1:] if len(per_call) > 1 else per_call)
         gbs = c["bytes"] / (us * 1e-6) / 1e9
         mf = c["flops"] / (us * 1e-6) / INT8_PEAK if c["kind"] == "gemm" else float("nan")
-        out.append(f"| {c['label']} | {', '.join(sorted(names))} | {us:.2f} | {c['bytes'] / 1e6:.3f} | "
-                   f"{gbs:.0f} | {gbs * 1e9 / HBM_PEAK:.3f} | "
-                   + (f"{mf:.4f} |" if c["kind"] == "gemm" else "- |"))
+        line = (f"| {c['label']} | {', '.join(sorted(names))} | {us:.2f} | {c['bytes'] / 1e6:.3f} | "
+                f"{gbs:.0f} | {gbs * 1e9 / HBM_PEAK:.3f} | "
+                + (f"{mf:.4f} |" if c["kind"] == "gemm" else "- |"))
+        if ops is not None:
+            if c["kind"] == "gemm":
+                o = statistics.median(per_ops)
+                line += f" {o / 1e9:.3f} | {o / (us * 1e-6) / INT8_PEAK:.4f} |"
+            else:
+                line += " - | - |"
+        out.append(line)
     return "\n".join(out)
 
 
@@ -349,9 +416,14 @@ def main(argv=None) -> int:
     s = sub.add_parser("summarize")
     s.add_argument("run_json")
     s.add_argument("trace_csv")
+    s.add_argument("--counters", default=None,
+                   help="counter_collection.csv of a --pmc SQ_INSTS_VALU_MFMA_MOPS_I8 run of the same command")
     c = sub.add_parser("copy")
     c.add_argument("--mb", type=int, default=64)
     c.add_argument("--reps", type=int, default=5)
+    mr = sub.add_parser("rates", help="the runtime's fill and copy rates (events around the calls)")
+    mr.add_argument("--mb", type=int, default=512)
+    mr.add_argument("--reps", type=int, default=10)
     pm = sub.add_parser("pmc")
     pm.add_argument("fetch_csv")
     pm.add_argument("write_csv")
@@ -378,6 +450,8 @@ def main(argv=None) -> int:
         run(a.out, a.reps)
     elif a.cmd == "copy":
         copy_calibration(a.mb, a.reps)
+    elif a.cmd == "rates":
+        print(json.dumps(memory_rates(a.mb, a.reps)))
     elif a.cmd == "pmc":
         print(json.dumps(pmc_summary(a.fetch_csv, a.write_csv, a.copy_fetch_csv, a.copy_write_csv,
                                      a.copy_mb, a.workload), indent=1))
@@ -393,7 +467,7 @@ def main(argv=None) -> int:
     elif a.cmd == "counters":
         print(json.dumps(counter_summary(a.csv, a.trace), indent=1))
     else:
-        print(summarize(a.run_json, a.trace_csv))
+        print(summarize(a.run_json, a.trace_csv, a.counters))
     return 0
 
 

@@ -92,8 +92,11 @@ def test_quantize_rows_matches_oracle(pkg, orc, dev):
 def test_q8_linear_edges(pkg, orc, dev):
     rng = np.random.default_rng(12)
     # column tail (N not a multiple of 16/64), odd M on both kernels, ReLU,
-    # full-range weights including -128 (exact in the int8 matrix core)
-    for M, K, N in [(3, 64, 100), (77, 128, 130), (200, 192, 65), (130, 64, 1)]:
+    # full-range weights including -128 (exact in the int8 matrix core); the
+    # last two are wide grids (more than 64 column tiles) whose tiles go in
+    # groups of eight row tiles, with a partial group and ragged edges
+    for M, K, N in [(3, 64, 100), (77, 128, 130), (200, 192, 65), (130, 64, 1), (200, 64, 4170),
+                    (610, 128, 4500)]:
         print(f"edge M={M} K={K} N={N}", flush=True)
         a = rng.standard_normal((M, K)).astype(np.float32)
         w = rng.integers(-128, 128, size=(N, K)).astype(np.int8)
