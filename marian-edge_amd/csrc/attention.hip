@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
     __builtin_amdgcn_wave_barrier();
-    const float inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, (Lc + 15) >> 4, 0.0f);
+    const float inv = 1.0f / seq_fold_lds_upto<kTileMaxKeys / 16>((const float4*)sP, (Lc + 15) >> 4, 0.0f);
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int c = 0; c < kTileMaxKeys / 64; ++c)
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
       sum = tree_combine_wave(sum);
     } else {
       // keys in order from 0.0, whole batches of 16 (zeros past the last key)
-      sum = seq_fold_lds_batches<4>((const float4*)sE, (nk + 15) >> 4, 0.0f);
+      sum = seq_fold_lds_upto<kLongMaxKeys / 16>((const float4*)sE, (nk + 15) >> 4, 0.0f);
     }
     if (lane == 0) sInv = 1.0f / sum;
   }

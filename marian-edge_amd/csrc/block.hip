@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       // Denominator: keys in order from 0.0 (softmax_in_place), folded over
       // whole batches of 16 entries: past the last key they hold +0.0, which
       // leaves the (non-negative) sum unchanged.
-      inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, n16, 0.0f);
+      inv = 1.0f / seq_fold_lds_upto<kBlkMaxKeys / 16>((const float4*)sP, n16, 0.0f);
       __builtin_amdgcn_wave_barrier();
     }
     // p_k = e_k * inv (scale_in_place)
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   }
   wg_lds_barrier();  // the products are in LDS
   if (wave != 0) return;
-  const float o = seq_fold_lds_batches<4>((const float4*)(sPv + lane * kPvRow), n16, 0.0f);
+  const float o = seq_fold_lds_upto<kBlkMaxKeys / 16>((const float4*)(sPv + lane * kPvRow), n16, 0.0f);
   b.out[(int64_t)r * b.ldo + h * kHeadDim + lane] = o;
   const bool bad = !isfinite(o);
   const float am = wave_max(fabsf(o));

@@ -133,6 +133,9 @@ __device__ __forceinline__ float seq_fold_lds(const float4* p, float init) {
       s = s + A[b].z;
       s = s + A[b].w;
     }
+    // A is consumed before it is reloaded: without this the compiler hoists
+    // the reload into fresh registers and copies them back every iteration.
+    asm volatile("" : "+v"(s)::"memory");
 #pragma unroll
     for (int b = 0; b < NB; ++b) A[b] = p[(k + 2) * NB + b];
     __builtin_amdgcn_sched_barrier(0);
@@ -205,42 +208,38 @@ __device__ __forceinline__ void wave_sum2(float& a, float& b) {
       (__int_as_float(__builtin_amdgcn_readlane(ib, 32)) + __int_as_float(__builtin_amdgcn_readlane(ib, 48)));
 }
 
-// The same fold over the first nb batches of NB float4 (nb >= 1, a value
-// known only at run time).  The read-ahead is unconditional (past the last
-// batch it re-reads that batch, unused), so every wait is for the batch being
-// added.  NB trades registers (8 x NB) for fewer waits.
-template <int NB = 8>
-__device__ __forceinline__ float seq_fold_lds_batches(const float4* p, int nb, float init) {
-  float4 A[NB], B[NB];
+// The same fold over the first nb (1 <= nb <= NBMAX, the same in every lane)
+// batches of NB float4: straight-line code whose only branches are the exits
+// after each batch.  The read-ahead past the end re-reads the last batch.
+template <int NBMAX, int NB = 4, int LA = 1>
+__device__ __forceinline__ float seq_fold_lds_upto(const float4* p, int nb, float init) {
+  nb = __builtin_amdgcn_readfirstlane(nb);
+  float4 buf[LA + 1][NB];
   float s = init;
 #pragma unroll
-  for (int b = 0; b < NB; ++b) A[b] = p[b];
-#pragma unroll 1
-  for (int k = 0;;) {
-    const int kb = min(k + 1, nb - 1);
+  for (int k = 0; k < LA && k < NBMAX; ++k) {
+    const int kn = min(k, nb - 1);
 #pragma unroll
-    for (int b = 0; b < NB; ++b) B[b] = p[kb * NB + b];
-    __builtin_amdgcn_sched_barrier(0);
+    for (int b = 0; b < NB; ++b) buf[k][b] = p[kn * NB + b];
+  }
+#pragma unroll
+  for (int k = 0; k < NBMAX; ++k) {
+    if (k + LA < NBMAX) {
+      const int kn = min(k + LA, nb - 1);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) buf[(k + LA) % (LA + 1)][b] = p[kn * NB + b];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the adds
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      s = s + A[b].x;
-      s = s + A[b].y;
-      s = s + A[b].z;
-      s = s + A[b].w;
+      const float4 v = buf[k % (LA + 1)][b];
+      s = s + v.x;
+      s = s + v.y;
+      s = s + v.z;
+      s = s + v.w;
     }
-    if (++k >= nb) break;
-    const int ka = min(k + 1, nb - 1);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) A[b] = p[ka * NB + b];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      s = s + B[b].x;
-      s = s + B[b].y;
-      s = s + B[b].z;
-      s = s + B[b].w;
-    }
-    if (++k >= nb) break;
+    asm volatile("" : "+v"(s)::"memory");  // this batch is consumed before its buffer is reloaded
+    if (k + 1 >= nb) break;
   }
   return s;
 }

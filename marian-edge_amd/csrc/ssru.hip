@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kSbThreads) void k_ssru_block(SsruBlockArgs a) {
   __builtin_amdgcn_wave_barrier();
   // Denominator: the probabilities in key order from 0.0 (keys past the last
   // hold +0.0, which leaves the non-negative sum unchanged), 16 at a time.
-  const float inv = 1.0f / seq_fold_lds_batches<4>((const float4*)sP, (nk + 15) >> 4, 0.0f);
+  const float inv = 1.0f / seq_fold_lds_upto<kSsruBlockMaxKeys / 16>((const float4*)sP, (nk + 15) >> 4, 0.0f);
   // out_d = sum_j v[j][d] * (e_j * inv) in key order from 0.0; lane = d.
   // Sixteen keys per batch in two alternating register sets: the next batch
   // is read while this one is added.  Keys past the last have e = +0.0 and
