@@ -151,15 +151,15 @@ def test_probe_ragged_64(pkg, orc, full, step):
 
 def test_vocabulary_over_32768_ids_token_exact(pkg, orc):
     """A 40000-id vocabulary: 313 argmax partials per row, more than the
-    finalizer's first pass of 4 x 64 per lane requests.  70 sentences, so the
-    steps run every finalizer (the workgroup scan above 64 rows, one wave per
-    8 rows up to 64, the 4- and 8-row single waves); tokens and one step's
-    logits against the oracle."""
+    finalizer's first pass of 4 x 64 per lane requests.  260 sentences, so the
+    steps run every finalizer (the workgroup scan above 64 rows, over several
+    64-row passes above 256, one wave per 8 rows up to 64, the 4- and 8-row
+    single waves); tokens and one step's logits against the oracle."""
     g = pkg.Geometry(vocab=40000, dim=256, heads=4, ffn_dim=1024, encoder_layers=1,
                      decoder_layers=2)
     model = pkg.seeded_model(seed=17, geometry=g)
     om = orc.OracleModel(model)
-    b = pkg.ragged_batch(seed=41, n=70, vocab=g.vocab)
+    b = pkg.ragged_batch(seed=41, n=260, vocab=g.vocab)
     with pkg.HipEngine(model, limits=b.limits) as e:
         got = e.translate_token_ids(b.tokens, b.offsets, b.max_output_tokens, b.flags).rows()
         want = orc.translate(om, b.tokens, b.offsets, b.max_output_tokens, b.limits, b.flags,
