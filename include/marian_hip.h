@@ -54,8 +54,10 @@
  *                              (shortlist.rs:150-198)
  *   marian_hip_positions       sinusoidal_positions crates/marian-model/src/position.rs:5-21
  * The op-level entry points that need intermediate device buffers keep them
- * in library scratch, one set per device: use one stream per device at a time
- * (calls that overlap on one device race on that scratch).
+ * in library scratch, one set per (device, stream), kept until the process
+ * ends: calls on different streams do not share it, and calls on one stream
+ * are ordered by that stream (two threads that issue calls on the same
+ * stream at once must serialize their calls themselves).
  * marian_hip_vocab_argmax_noalloc has no reference counterpart (see there).
  *
  * Threading: one engine handle belongs to one owner thread (the reference

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -28,25 +29,26 @@ int op_status(hipError_t e, const char* what) {
 
 // Library scratch for the op-level entry points that need intermediate
 // buffers (quantized activations, argmax partials).  Grow-only, one set per
-// device; calls that overlap on one device race on it (the entry points are
-// for one stream per device at a time).  A buffer that grows is freed only
-// after the whole device is idle, so no kernel on any stream still uses it.
+// (device, stream), so calls on different streams never share a buffer; a
+// call's kernels run in its stream's order, so calls on one stream reuse the
+// set safely.  A buffer that grows is freed once its stream has drained.
+// Sets live until the process ends (a stream that is destroyed leaves its
+// set behind).
 struct OpScratch {
   void* p[4] = {nullptr, nullptr, nullptr, nullptr};
   size_t cap[4] = {0, 0, 0, 0};
 };
 std::mutex g_scratch_mu;
-OpScratch g_scratch[64];
+std::map<std::pair<int, uintptr_t>, OpScratch> g_scratch;
 
 void* op_scratch(int which, size_t bytes, hipStream_t s) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
   std::lock_guard<std::mutex> g(g_scratch_mu);
-  OpScratch& S = g_scratch[dev];
+  OpScratch& S = g_scratch[{dev, (uintptr_t)s}];
   if (S.cap[which] >= bytes && S.p[which]) return S.p[which];
   if (S.p[which]) {
-    (void)s;
-    hipDeviceSynchronize();
+    hipStreamSynchronize(s);  // the stream's earlier calls are done with it
     hipFree(S.p[which]);
     S.p[which] = nullptr;
     S.cap[which] = 0;

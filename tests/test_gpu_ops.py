@@ -67,6 +67,42 @@ def test_q8_linear_long_k_row_groups(pkg, orc, dev, M, K, N):
     assert np.array_equal(df.host().view(np.uint32), y_ref.view(np.uint32))
 
 
+def test_q8_linear_on_two_streams_at_once(pkg, orc, dev):
+    """The op-level entry points keep their intermediate buffers (here the
+    quantized activations of an fp32 input) per (device, stream): two streams
+    that issue calls at the same time, with different row counts and no
+    synchronization between them, each get the oracle's result bit for bit."""
+    K, N = 512, 512
+    shapes = {"a": 2048, "b": 96}
+    print("q8_linear on two streams: rows " + ", ".join(map(str, shapes.values())), flush=True)
+    w, mult, bias = None, None, None
+    inputs, refs = {}, {}
+    for i, (key, M) in enumerate(shapes.items()):
+        a, w_i, mult_i, bias_i = pkg.gemm_inputs(M, K, N, seed=100 + i)
+        if w is None:
+            w, mult, bias = w_i, mult_i, bias_i
+        inputs[key] = a
+        refs[key] = orc.linear_forward(a, w, mult, bias, threads=16)[0]
+    dw, dm, db = (dev.DeviceArray.from_host(x) for x in (w, mult, bias))
+    streams = {k: dev.Stream() for k in shapes}
+    try:
+        din = {k: dev.DeviceArray.from_host(inputs[k]) for k in shapes}
+        outs = {k: [dev.DeviceArray.zeros((shapes[k], N), np.float32) for _ in range(4)] for k in shapes}
+        err = dev.DeviceArray.zeros(1, np.int32)
+        for rep in range(4):  # interleaved, never waiting
+            for k in shapes:
+                dev.q8_linear(din[k], dw, dm, db, None, outs[k][rep], err=err, stream=streams[k].handle)
+        for st in streams.values():
+            st.sync()
+        assert err.host()[0] == 0
+        for k in shapes:
+            for rep in range(4):
+                assert np.array_equal(outs[k][rep].host().view(np.uint32), refs[k].view(np.uint32)), (k, rep)
+    finally:
+        for st in streams.values():
+            st.close()
+
+
 def test_quantize_rows_matches_oracle(pkg, orc, dev):
     rng = np.random.default_rng(11)
     x = (rng.standard_normal((300, 2048)) * rng.uniform(0.01, 50, size=(300, 1))).astype(np.float32)
