@@ -199,13 +199,17 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
     for (int c = 0; c < CH; ++c)
       if (c < nch) tile[c * 64 + lane] = s[c];
     __syncthreads();
+    if constexpr (CH <= 8) {
+      sum = seq_fold_lds_upto<CH * 4>((const float4*)tile, nch * 4, 0.0f);
+    } else {  // long ranges: a rolled loop keeps the code small
 #pragma unroll 4
-    for (int j = 0; j < nch * 64; j += 4) {
-      const float4 v = *(const float4*)(tile + j);
-      sum = sum + v.x;
-      sum = sum + v.y;
-      sum = sum + v.z;
-      sum = sum + v.w;
+      for (int j = 0; j < nch * 64; j += 4) {
+        const float4 v = *(const float4*)(tile + j);
+        sum = sum + v.x;
+        sum = sum + v.y;
+        sum = sum + v.z;
+        sum = sum + v.w;
+      }
     }
   }
   const float inv = 1.0f / sum;
@@ -402,8 +406,8 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   }
 
   // out_d = sum_k v_k[d] * p_k in key order, chunk by chunk, in batches of 8
-  // keys read one batch ahead (clamped inside the chunk; past the last key p
-  // is +0 and the rows are zero, so the added products are +0).
+  // keys read one batch ahead (past the last key p is +0 and the rows are
+  // zero, so the added products are +0).
   float o = 0.0f;
 #pragma unroll
   for (int c = 0; c < kTileMaxKeys / 64; ++c) {
@@ -413,41 +417,37 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
       __syncthreads();
       if (c + 1 < nch) pre = ld(a.v, c + 1);
       if (live) {
-        const int kend = min(64, lpad - c * 64);  // a multiple of 8
-        const int nbat = kend >> 3;
-        float va[8], vb[8];
-        float4 pa0, pa1, pb0, pb1;
-        auto load8 = [&](int k0, float (&v)[8], float4& p0, float4& p1) {
+        // Straight-line batches of 8 keys with an exit after each: every read
+        // has a constant offset, so no address register is rewritten while a
+        // read into it is pending.  Reads stay inside the staged chunk.
+        const int nbat = __builtin_amdgcn_readfirstlane(min(64, lpad - c * 64) >> 3);  // >= 1
+        const float* sv = stage + lane;
+        const float* pc = sP + c * 64;
+        float v[2][8];
+        float4 p[2][2];
+        auto load8 = [&](int k0, float (&vv)[8], float4 (&pp)[2]) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = stage[(k0 + i) * kKRow + lane];
-          p0 = *(const float4*)(sP + c * 64 + k0);
-          p1 = *(const float4*)(sP + c * 64 + k0 + 4);
+          for (int i = 0; i < 8; ++i) vv[i] = sv[(k0 + i) * kKRow];
+          pp[0] = *(const float4*)(pc + k0);
+          pp[1] = *(const float4*)(pc + k0 + 4);
         };
-        load8(0, va, pa0, pa1);
-#pragma unroll 1
-        for (int bt = 0;;) {
-          load8(min((bt + 1) * 8, kend - 8), vb, pb0, pb1);
+        load8(0, v[0], p[0]);
+#pragma unroll
+        for (int bt = 0; bt < 8; ++bt) {
+          if (bt + 1 < 8) load8((bt + 1) * 8, v[(bt + 1) & 1], p[(bt + 1) & 1]);
           __builtin_amdgcn_sched_barrier(0);
-          o = o + va[0] * pa0.x;
-          o = o + va[1] * pa0.y;
-          o = o + va[2] * pa0.z;
-          o = o + va[3] * pa0.w;
-          o = o + va[4] * pa1.x;
-          o = o + va[5] * pa1.y;
-          o = o + va[6] * pa1.z;
-          o = o + va[7] * pa1.w;
-          if (++bt >= nbat) break;
-          load8(min((bt + 1) * 8, kend - 8), va, pa0, pa1);
-          __builtin_amdgcn_sched_barrier(0);
-          o = o + vb[0] * pb0.x;
-          o = o + vb[1] * pb0.y;
-          o = o + vb[2] * pb0.z;
-          o = o + vb[3] * pb0.w;
-          o = o + vb[4] * pb1.x;
-          o = o + vb[5] * pb1.y;
-          o = o + vb[6] * pb1.z;
-          o = o + vb[7] * pb1.w;
-          if (++bt >= nbat) break;
+          const float(&vv)[8] = v[bt & 1];
+          const float4(&pp)[2] = p[bt & 1];
+          o = o + vv[0] * pp[0].x;
+          o = o + vv[1] * pp[0].y;
+          o = o + vv[2] * pp[0].z;
+          o = o + vv[3] * pp[0].w;
+          o = o + vv[4] * pp[1].x;
+          o = o + vv[5] * pp[1].y;
+          o = o + vv[6] * pp[1].z;
+          o = o + vv[7] * pp[1].w;
+          asm volatile("" : "+v"(o)::"memory");  // this batch is consumed before its buffer is reloaded
+          if (bt + 1 >= nbat) break;
         }
       }
     }
