@@ -109,6 +109,11 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   // Keys of a stale row may run past the buffer: its last readable key.
   const int nk_ld = a.mode == ATT_SEQ ? nk : (int)min((int64_t)nk, a.max_row - key0);
 
+  // q of this head, one element per lane (broadcast 16 values at a time),
+  // requested first and waited for before the chunk loop (below): a wait
+  // for it inside the loop, after a chunk's conditional prefetch, would
+  // have to drain every load in flight.
+  const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * DH + min(lane, DH - 1)));
   // Chunk 0's V rows are loaded now (used after the softmax), then K.
   float4 vreg[16], kreg[16], kreg1[PRE ? 16 : 1], vreg1[PRE ? 16 : 1];
   MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 0, nk_ld, lane, vreg)
@@ -119,11 +124,10 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
       MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 64, nk_ld, lane, vreg1)
     }
   }
-  // q of this head, one element per lane; broadcast 16 values at a time.
-  const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * DH + min(lane, DH - 1)));
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
   if (r >= n) return;
   if (too_long && threadIdx.x == 0 && a.err) *a.err = 2;
+  asm volatile("" ::"v"(qv));  // q has arrived (the K/V loads stay in flight)
 
   // Scores: lane = key within the chunk, DH-term dot in dimension order.  The
   // next chunk's K rows are loaded while this chunk's dot runs.

@@ -195,20 +195,27 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
   __shared__ float sA;
   __shared__ float sS[64];
 
+  touch_kernargs<sizeof(BlockArgs)>();
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Row-major ids: workgroups are dealt to the 8 XCDs in turn, so head h of
   // every row runs on XCD h and each XCD reads one head's weights.
   const int h = blockIdx.x % b.heads, r = blockIdx.x / b.heads;  // r < b.rows (host bound)
-  const int n = b.rows_dev ? *b.rows_dev : b.rows;
   const int step = b.step;
   // Key range of this row (read before the device row count is known; rows
-  // past it read clamped stale ranges and are discarded below).
-  int64_t key0 = b.row_key0[r];
-  const int nk_row = SELF ? step : b.row_nk[r];
-  key0 = min(max(key0, (int64_t)0), b.max_row - 1);
-  const int nkm = max(min(nk_row, kBlkMaxKeys - (SELF ? 1 : 0)), SELF ? 0 : 1);  // keys from memory
-  const int nk_ld = (int)min((int64_t)nkm, b.max_row - key0);                   // readable rows
-  const int nkey = SELF ? nkm + 1 : nkm;                                       // keys attended
+  // past it read clamped stale ranges and are discarded below).  Each wave
+  // reads it, and the device row count, only after its first loads are
+  // issued: a load whose value a branch needs is waited for there, and the
+  // compiler would otherwise sink the wave's other loads below that wait.
+  int64_t key0;
+  int nk_row, nkm, nk_ld, nkey;
+  auto key_range = [&]() {
+    key0 = b.row_key0[r];
+    nk_row = SELF ? step : b.row_nk[r];
+    key0 = min(max(key0, (int64_t)0), b.max_row - 1);
+    nkm = max(min(nk_row, kBlkMaxKeys - (SELF ? 1 : 0)), SELF ? 0 : 1);  // keys from memory
+    nk_ld = (int)min((int64_t)nkm, b.max_row - key0);                   // readable rows
+    nkey = SELF ? nkm + 1 : nkm;                                       // keys attended
+  };
 
   if (wave < kBlkRowWaves) {
     // ---- the input row ----------------------------------------------------------
@@ -227,7 +234,9 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
         gv[j] = b.pro.gamma[lane + 64 * j];
         bv[j] = b.pro.beta[lane + 64 * j];
       }
-      if (r >= n) return;
+      asm volatile("" ::: "memory");  // the row loads are issued first
+      if (r >= bounded_rows(b.rows_dev, b.rows)) return;
+      key_range();
       float z[PER], o[PER];
 #pragma unroll
       for (int j = 0; j < PER; ++j) z[j] = y[j] + rr[j];  // add_slices
@@ -249,7 +258,9 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
     } else {
       RowLoads<PK> in;
       row_load<PK>(b.pro, r, step, lane, in);
-      if (r >= n) return;
+      asm volatile("" ::: "memory");  // the row loads are issued first
+      if (r >= bounded_rows(b.rows_dev, b.rows)) return;
+      key_range();
       f4v o[2];
       row_build<PK>(b.pro, in, sZ, lane, o);
       a_row = row_quantize(o, sX, lane, bad);
@@ -280,6 +291,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
       wm[i] = b.wmult[n_w];
       bi[i] = b.bias[n_w];
     }
+    asm volatile("" ::: "memory");  // the weight loads are issued first
+    key_range();
     // Key and value rows go straight from memory into the padded LDS rows
     // (global_load_lds, 16 bytes per lane, no registers): an LDS row is 17
     // 16-byte slots, the last one padding.  Wave instruction i fills slots
@@ -298,7 +311,7 @@ __global__ __launch_bounds__(kBlkThreads) void k_attn_block(BlockArgs b) {
                                          (__attribute__((address_space(3))) void*)(sV + 256 * i), 16, 0, 0);
       }
     }
-    if (r >= n) {
+    if (r >= bounded_rows(b.rows_dev, b.rows)) {
       __builtin_amdgcn_s_waitcnt(0);  // no LDS write may land after the workgroup ends
       return;
     }
@@ -471,6 +484,7 @@ static_assert(kLgTiles % kBlkLoadWaves == 0, "every loader wave owns whole tiles
 
 template <bool FAST>
 __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
+  touch_kernargs<sizeof(LnGemmArgs)>();
   constexpr int PER = kBlkD / 64;  // lane l holds row elements l + 64j
   __shared__ __attribute__((aligned(16))) float sZ[kLnRow<PER>];
   __shared__ __attribute__((aligned(16))) int8_t sX[kBlkD];
@@ -478,7 +492,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int slices = a.N / kLgCols;
   const int slice = blockIdx.x % slices, r = blockIdx.x / slices;  // r < a.rows (host bound)
-  const int n = a.rows_dev ? *a.rows_dev : a.rows;
+  // The device row count is read after each wave's loads are issued (the
+  // compiler would otherwise sink the loads below the wait for it).
   if (wave < kBlkRowWaves) {
     if (wave != 0) return;  // wave 0 builds the row with the one-wave folds
     float y[PER], rr[PER], gv[PER], bv[PER];
@@ -490,7 +505,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
       gv[j] = a.pro.gamma[lane + 64 * j];
       bv[j] = a.pro.beta[lane + 64 * j];
     }
-    if (r >= n) return;
+    asm volatile("" ::: "memory");  // the row loads are issued first
+    if (r >= bounded_rows(a.rows_dev, a.rows)) return;
     float z[PER], o[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) z[j] = y[j] + rr[j];  // add_slices
@@ -527,7 +543,8 @@ __global__ __launch_bounds__(kBlkThreads) void k_ln_gemm_block(LnGemmArgs a) {
     wm[i] = a.wmult[col];
     bi[i] = a.bias[col];
   }
-  if (r >= n) return;
+  asm volatile("" ::: "memory");  // the weight loads are issued first
+  if (r >= bounded_rows(a.rows_dev, a.rows)) return;
   __syncthreads();  // the quantized row is in LDS
   const float a_row = sA;
   float inv[kLgTpw];

@@ -33,6 +33,34 @@ constexpr float kLayerNormEpsilon = 1.0e-6f;  // tensor.rs:3
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// min(device row count, host bound) when the launch carries a device row
+// count, else the host bound.  The count is read through a selected pointer
+// (an absent count reads kNoRowCount), so no branch splits the kernel's
+// prologue: a load behind a branch is waited for inside it, which would put
+// a memory round trip between the loads issued before and after it.
+static __device__ int kNoRowCount = 0x7fffffff;
+__device__ __forceinline__ int bounded_rows(const int* rows_dev, int rows) {
+  return min(*(rows_dev ? rows_dev : &kNoRowCount), rows);
+}
+
+// Requests every 64-byte line of the first BYTES bytes of the kernel's
+// arguments in one batch of scalar loads at the start of the kernel.  The
+// compiler loads an argument where it is first used, in several batches,
+// and a scalar load's wait covers every scalar load in flight; with the
+// lines already in the scalar cache, the later batches hit it instead of
+// each waiting for a miss.
+template <int BYTES>
+__device__ __forceinline__ void touch_kernargs() {
+  constexpr int kLines = (BYTES + 63) / 64;
+  static_assert(kLines >= 1 && kLines <= 8, "one to eight lines");
+  typedef const __attribute__((address_space(4))) uint32_t* karg_ptr;
+  const karg_ptr k = (karg_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t t[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t[i] = i < kLines ? k[16 * i] : 0u;
+  asm volatile("" ::"s"(t[0]), "s"(t[1]), "s"(t[2]), "s"(t[3]), "s"(t[4]), "s"(t[5]), "s"(t[6]), "s"(t[7]));
+}
+
 // Value of lane (l ^ off) for lane l, for off = 1, 2 (DPP quad permutes),
 // 4, 8, 16 (ds_swizzle lane swaps within 32) and 32 (v_permlane32_swap).
 // Exactly the xor pairing of __shfl_xor, without the LDS crossbar.

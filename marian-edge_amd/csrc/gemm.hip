@@ -32,13 +32,16 @@ __device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
 // threads write consecutive columns.
 // ---------------------------------------------------------------------------
 // Row multiplier of row m of an fp32 A source from its producer's partial
-// maxima (`parts` per row, one per attention head; eight of them are read as
-// two 16-byte vectors so the loads issue together).
+// maxima (`parts` per row, one per attention head).  EIGHT: exactly eight
+// parts, read as two 16-byte vectors with no branch, so that the loads issue
+// together with the kernel's other prologue loads (a load behind a branch
+// is waited for inside the branch).
 constexpr int kAfParts = 8;
 constexpr int kAfMaxParts = 16;
+template <bool EIGHT>
 __device__ __forceinline__ float af_row_mult(const float* amax, int m, int parts) {
   float mx = 0.0f;
-  if (parts == kAfParts) {
+  if constexpr (EIGHT) {
     const float4* p = (const float4*)(amax + (int64_t)m * kAfParts);
     const float4 u = p[0], v = p[1];
     mx = fmaxf(fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)), fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
@@ -63,18 +66,21 @@ __device__ __forceinline__ v4i quantize_frag16(const float4 (&f)[4], float a) {
 constexpr int kAfRows = 16;  // fp32 A source: one MFMA row tile per workgroup
 
 // A sources of the skinny kernel: int8 rows with their multipliers, or fp32
-// rows quantized while loading, with the row maxima of the producer (A_F32)
-// or found here over all of K (A_F32_MAX).  A_I8_RG: int8 rows in 16-row
-// groups over blockIdx.y, as the fp32 sources are (plain stores only).
-enum ASrc { A_I8 = 0, A_F32 = 1, A_F32_MAX = 2, A_I8_RG = 3 };
+// rows quantized while loading, with the row maxima of the producer in eight
+// parts (A_F32) or in another number of parts (A_F32_P), or found here over
+// all of K (A_F32_MAX).  A_I8_RG: int8 rows in 16-row groups over
+// blockIdx.y, as the fp32 sources are (plain stores only).
+enum ASrc { A_I8 = 0, A_F32 = 1, A_F32_MAX = 2, A_I8_RG = 3, A_F32_P = 4 };
 
 // FULL: K is exactly NW x KSW k-steps (every shape the engine uses), so no
 // k-step needs a guard and every prologue load is unconditional (guarded
 // loads become branches that the compiler waits on one by one).
 template <int MODE, int CT, int NW, int KSW, int ASRC, bool FULL>
 __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e) {
-  constexpr bool AF = ASRC == A_F32 || ASRC == A_F32_MAX;  // fp32 A, quantized while loading
+  touch_kernargs<sizeof(GemmArgs) + sizeof(Epilogue)>();
+  constexpr bool AF = ASRC == A_F32 || ASRC == A_F32_MAX || ASRC == A_F32_P;  // fp32 A, quantized while loading
   constexpr bool AX = ASRC == A_F32_MAX;   // ... with the row maxima found here
+  constexpr bool A8 = ASRC == A_F32;       // ... with the producer's maxima in eight parts
   constexpr bool RG = ASRC != A_I8;        // one 16-row group per workgroup
   constexpr int NT = NW * 64;
   constexpr int COLS = CT * 16;
@@ -92,7 +98,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   const float* Af = AF ? g.Af + (int64_t)r0 * g.ldaf : nullptr;
   const int8_t* Ai = AF ? nullptr : g.A + (int64_t)r0 * g.lda;
   const float* ai = AF ? nullptr : g.a + r0;
-  const float* Aamax = ASRC == A_F32 ? g.Aamax + (int64_t)r0 * g.amax_parts : nullptr;
+  const float* Aamax = AF && !AX ? g.Aamax + (int64_t)r0 * g.amax_parts : nullptr;
   float* out = e.out ? e.out + (int64_t)r0 * e.ldo : nullptr;
   // g.M bounds the rows on the host side; every row below it is allocated,
   // so the first row chunk's activations are loaded before the device row
@@ -118,6 +124,22 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       bf[i][ct] = FULL || s < ksteps ? v : zero4();
     }
   }
+  // Epilogue operands (each thread always handles the same column) and the
+  // row multipliers are requested with the weights, so that they arrive in
+  // the same memory round trip.
+  const int ec = tid % COLS;
+  const int en = min(n0 + ec, g.N - 1);
+  const float ewm = g.wmult[en], ebias = g.bias[en];
+  float am[ROWS_PER_THREAD];
+  int64_t crow[MODE == EPI_QKV_CACHE ? ROWS_PER_THREAD : 1];
+#pragma unroll
+  for (int k = 0; k < ROWS_PER_THREAD; ++k) {
+    const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
+    if constexpr (!AX) am[k] = AF ? af_row_mult<A8>(Aamax, m, g.amax_parts) : ai[m];
+    if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
+  }
+  int Md;  // the device row count, read after the activation loads are issued
+
   // First chunk's activation fragments.
   v4i af[KSW][4];
   bool xbad = false;  // A_F32_MAX: a non-finite value in this lane's row (row lane % 16)
@@ -133,7 +155,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
       for (int w = 0; w < 4; ++w) raw[i][w] = *(const float4*)(ar + s * 64 + 4 * w);
     }
-    float a_m;
+    float a_m = AX ? 0.0f : af_row_mult<A8>(Aamax, m, g.amax_parts);
+    asm volatile("" ::: "memory");  // the loads above are issued first
+    Md = bounded_rows(g.M_dev, g.M);
     if constexpr (AX) {
       // Row |max| over all of K: this lane's 16 values per k-step, the four
       // lanes of the row (its k-offsets), then the waves through LDS.
@@ -156,8 +180,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
 #pragma unroll
       for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + (lane & 15)]);
       a_m = row_multiplier(rm);
-    } else {
-      a_m = af_row_mult(Aamax, m, g.amax_parts);
     }
 #pragma unroll
     for (int i = 0; i < KSW; ++i) {
@@ -177,27 +199,19 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
         af[i][mt] = ((FULL || s < ksteps) && mt * 16 < Mh) ? v : zero4();
       }
     }
+    asm volatile("" ::: "memory");  // the loads above are issued first
+    Md = bounded_rows(g.M_dev, g.M);
   }
-  // Epilogue operands: each thread always handles the same column.
-  const int ec = tid % COLS;
-  const int en = min(n0 + ec, g.N - 1);
-  const float ewm = g.wmult[en], ebias = g.bias[en];
-  float am[ROWS_PER_THREAD];
-  int64_t crow[MODE == EPI_QKV_CACHE ? ROWS_PER_THREAD : 1];
+  if constexpr (AX) {
 #pragma unroll
-  for (int k = 0; k < ROWS_PER_THREAD; ++k) {
-    const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
-    if constexpr (AX) {
+    for (int k = 0; k < ROWS_PER_THREAD; ++k) {
+      const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
       float rm = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) rm = fmaxf(rm, sRowMax[w * kAfRows + m]);
       am[k] = row_multiplier(rm);
-    } else {
-      am[k] = AF ? af_row_mult(Aamax, m, g.amax_parts) : ai[m];
     }
-    if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
   }
-  const int Md = g.M_dev ? min(*g.M_dev, g.M) : g.M;
   const int M = RG ? min(Md - r0, kAfRows) : Md;  // this workgroup's rows
   // Non-finite values count only in rows below the device row count, as in
   // the row quantization.
@@ -315,6 +329,7 @@ constexpr int kVocabLds = kVocabMaxK + 16;        // padded LDS row (bytes)
 // FAST (with LNP): the LayerNorm sums in the fast-reduction tree order.
 template <bool FULL, bool LNP, bool FAST = false>
 __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs g, Epilogue e) {
+  touch_kernargs<sizeof(GemmArgs) + sizeof(Epilogue)>();
   constexpr int kVocabThreads = 64 * kVocabWaves<LNP>;
   constexpr int kVocabCT = kVocabCols / (16 * kVocabWaves<LNP>);  // column tiles per wave
   constexpr int KEYS = kVocabWaves<LNP> * 16;  // per row: one key per (wave, lane column)
@@ -914,7 +929,8 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
         g.ldaf % 4 || e.out_i32 ||
         g.M > 65535 * kAfRows)
       return hipErrorInvalidValue;
-    return launch_skinny_k<MODE, 8, 1, A_F32>(g, e, s);
+    return g.amax_parts == kAfParts ? launch_skinny_k<MODE, 8, 1, A_F32>(g, e, s)
+                                    : launch_skinny_k<MODE, 8, 1, A_F32_P>(g, e, s);
   }
   if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1, A_I8>(g, e, s);
   if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2, A_I8>(g, e, s);

@@ -308,6 +308,7 @@ __device__ __forceinline__ uint64_t rows_max_u64(uint64_t (&b)[R], int lane) {
 
 template <int W, int R>
 __global__ __launch_bounds__(W * 64) void k_finalize_wave(FinalizeArgs f) {
+  touch_kernargs<sizeof(FinalizeArgs)>();
   constexpr int KP = 4;  // partials per row and lane requested up front
   __shared__ int s_cnt[W];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
