@@ -21,6 +21,16 @@ constexpr int kSkinnyMaxK = 2048;  // 8 waves x 4 k-steps x 64
 
 
 __device__ __forceinline__ v4i zero4() { return v4i{0, 0, 0, 0}; }
+// v where keep holds, else zero, with v's load issued either way (its address
+// must be valid).  The mask goes through an empty asm so that the compiler
+// cannot turn the choice back into a select, which it lowers to a branch
+// around the load; a load behind a branch is waited for inside it, which
+// serializes the loads issued before and after it.
+__device__ __forceinline__ v4i keep_or_zero(v4i v, bool keep) {
+  int m = keep ? -1 : 0;
+  asm("" : "+v"(m));
+  return v & v4i{m, m, m, m};
+}
 
 // ---------------------------------------------------------------------------
 // Skinny GEMM (decode and small M).  One workgroup owns CT*16 output columns
@@ -600,23 +610,28 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmArgs g, Epilogue e, int t
     n0 = in_g / gm * kTm;
   }
 
+  // Every load is issued (from an in-bounds address); pieces past M, N or
+  // the chunk's K are zeroed when they are stored to LDS.
   v4i ra[CH], rb[CH];
+  bool ka[CH], kb[CH];
   auto gload = [&](int k0, int kc) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * 256, row = c / ROW_CH, col = c % ROW_CH * 16;
       const int m = m0 + row, n = n0 + row;
-      const bool in_k = col < kc;
-      ra[i] = in_k && m < M ? *(const v4i*)(g.A + (int64_t)m * g.lda + k0 + col) : zero4();
-      rb[i] = in_k && n < N ? *(const v4i*)(g.W + (int64_t)n * K + k0 + col) : zero4();
+      const int cl = min(col, kc - 16);
+      ra[i] = *(const v4i*)(g.A + (int64_t)min(m, M - 1) * g.lda + k0 + cl);
+      rb[i] = *(const v4i*)(g.W + (int64_t)min(n, N - 1) * K + k0 + cl);
+      ka[i] = col < kc && m < M;
+      kb[i] = col < kc && n < N;
     }
   };
   auto lstore = [&]() {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * 256, row = c / ROW_CH, col = c % ROW_CH * 16;
-      *(v4i*)(sA + row * LDS_ROW + col) = ra[i];
-      *(v4i*)(sB + row * LDS_ROW + col) = rb[i];
+      *(v4i*)(sA + row * LDS_ROW + col) = keep_or_zero(ra[i], ka[i]);
+      *(v4i*)(sB + row * LDS_ROW + col) = keep_or_zero(rb[i], kb[i]);
     }
   };
 
