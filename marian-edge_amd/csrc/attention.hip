@@ -276,9 +276,22 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 // k_attention's: lane = key for the sequential 64-term dots, wave max, the
 // restated expf, the denominator folded in key order from 0.0 through LDS,
 // PV in key order with lane = dimension.  Sequences of up to kTileMaxKeys.
+// A sequence of at most kPairKeys keys is one tile of all its queries, two per
+// wave (its 64-lane chunk would leave half the score lanes idle): lanes 0-31
+// take query 2w and lanes 32-63 query 2w + 1, each half computing its query's
+// scores (lane = key), maximum, exponentials and key-order denominator, and
+// each lane the PV sums of dimensions l % 32 and l % 32 + 32 of its half's
+// query, both in key order.  The arithmetic per query is unchanged.
 // ---------------------------------------------------------------------------
 constexpr int kTileQ = 16;          // queries (waves) per workgroup
 constexpr int kTileMaxKeys = 256;   // keys staged in LDS
+constexpr int kPairKeys = 32;       // sequences up to this length: two queries per wave
+
+// Tiles of a sequence of L queries: one tile of the whole sequence when it is
+// short enough for two queries per wave, else tiles of kTileQ queries.
+__device__ __forceinline__ int seq_tile_count(int L) {
+  return L <= 0 ? 0 : (L <= kPairKeys ? 1 : (L + kTileQ - 1) / kTileQ);
+}
 
 __global__ __launch_bounds__(1024) void k_seq_tiles(const uint32_t* cu, int nseq, uint32_t* tiles,
                                                     int cap) {
@@ -289,7 +302,7 @@ __global__ __launch_bounds__(1024) void k_seq_tiles(const uint32_t* cu, int nseq
   const int per = (nseq + 1023) / 1024;
   const int s0 = tid * per, s1 = min(s0 + per, nseq);
   int cnt = 0;
-  for (int q = s0; q < s1; ++q) cnt += (int)((cu[q + 1] - cu[q] + kTileQ - 1) / kTileQ);
+  for (int q = s0; q < s1; ++q) cnt += seq_tile_count((int)(cu[q + 1] - cu[q]));
   int incl = cnt;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
@@ -311,7 +324,8 @@ __global__ __launch_bounds__(1024) void k_seq_tiles(const uint32_t* cu, int nseq
   int pos = s_wsum[wave] + incl - cnt;
   for (int q = s0; q < s1; ++q) {
     const int L = (int)(cu[q + 1] - cu[q]);
-    for (int q0 = 0; q0 < L; q0 += kTileQ, ++pos) {
+    const int step = L <= kPairKeys ? kPairKeys : kTileQ;
+    for (int q0 = 0; q0 < L; q0 += step, ++pos) {
       if (pos < cap) {
         tiles[1 + 2 * pos] = (uint32_t)q;
         tiles[2 + 2 * pos] = (uint32_t)q0;
@@ -326,7 +340,7 @@ template <typename T, int DH>
 __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_attn_tiles(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float stage[64 * kKRow];            // one 64-key chunk
   __shared__ __attribute__((aligned(16))) float sPall[kTileQ * kTileMaxKeys];  // per-wave probabilities
-  __shared__ __attribute__((aligned(16))) float sQall[kTileQ * kHeadDim];     // per-wave query
+  __shared__ __attribute__((aligned(16))) float sQall[2 * kTileQ * kHeadDim];  // per-query query rows
   __shared__ uint64_t sTab[32];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int h = blockIdx.x % a.heads, ti = blockIdx.x / a.heads;
@@ -334,7 +348,6 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   const int sq = (int)a.tiles[1 + 2 * ti], q0 = (int)a.tiles[2 + 2 * ti];
   const int64_t key0 = a.cu[sq];
   const int L = (int)(a.cu[sq + 1] - key0);
-  const int nq = min(kTileQ, L - q0);
   // A range past kTileMaxKeys is cut to it (and flagged).
   const int Lc = min(L, kTileMaxKeys);
   const int nch = (Lc + 63) >> 6;
@@ -343,6 +356,7 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
   const int64_t base = key0 * a.ldkv + h * DH;
   if (tid < 32) sTab[tid] = kExp2Tab[tid];
   if (L > Lc && tid == 0 && a.err) *a.err = 2;
+  const float scale = 1.0f / sqrtf((float)DH);
 
   // Chunk rows: thread t moves float4 t % 16 of key t / 16 of the chunk; keys
   // past the last are zero.  The next chunk is requested while this one is used.
@@ -351,15 +365,98 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
     return key < Lc ? load_row4<T>(src, base + (int64_t)key * a.ldkv + min((tid & 15) * 4, DH - 4))
                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   };
+  float* srow = stage + (tid >> 4) * kKRow + (tid & 15) * 4;
+
+  if (L <= kPairKeys) {  // the whole sequence, two queries per wave (q0 = 0)
+    const int hf = lane >> 5, kl = lane & 31;
+    const int qi = 2 * w + hf;  // this half's query
+    const bool qlive = qi < L;
+    *(float4*)srow = ld(a.k, 0);
+    for (int i = tid; i < L * kHeadDim; i += kTileQ * 64) {
+      const int q = i / kHeadDim, d = i % kHeadDim;
+      if (d < DH) sQall[i] = Io<T>::at(a.q, (key0 + q) * a.ldq + h * DH + d);
+    }
+    const float4 vpre = ld(a.v, 0);
+    __syncthreads();  // K rows, queries and the expf table are in LDS
+    // Scores: lane = key, the DH-term dot in dimension order (the query read
+    // from LDS, one address per half).
+    float sc = -INFINITY;
+    if (qlive) {
+      const float* kr = stage + min(kl, Lc - 1) * kKRow;
+      const float* sQ = sQall + qi * kHeadDim;
+      float dot = -0.0f;
+#pragma unroll
+      for (int i = 0; i < DH; i += 4) {
+        const float4 kk = *(const float4*)(kr + i);
+        const float4 qq = *(const float4*)(sQ + i);
+        dot = dot + qq.x * kk.x;
+        dot = dot + qq.y * kk.y;
+        dot = dot + qq.z * kk.z;
+        dot = dot + qq.w * kk.w;
+      }
+      if (kl < Lc) sc = dot * scale;
+    }
+    const float mx = half_wave_max(sc);
+    const float e = qlive && kl < Lc ? ref_expf(sc - mx, sTab) : 0.0f;
+    // The half's exponentials in key order (+0.0 past the last key), folded
+    // from 0.0 by each of its lanes; then p = e / sum.
+    float* sPh = sP + hf * (kTileMaxKeys / 2);
+    sPh[kl] = e;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes land
+    __builtin_amdgcn_wave_barrier();
+    const float inv = 1.0f / seq_fold_lds_upto<kPairKeys / 16>((const float4*)sPh, (Lc + 15) >> 4, 0.0f);
+    __builtin_amdgcn_wave_barrier();
+    sPh[kl] = e * inv;
+    __syncthreads();  // every wave has read the K rows
+    *(float4*)srow = vpre;
+    __syncthreads();  // V rows (zero past the last key) and this wave's p are in LDS
+    if (!qlive) return;
+    // PV: dimensions kl and kl + 32 of the half's query, each a key-order sum
+    // over batches of 8 keys (past the last key p is +0 and the rows are zero).
+    const int nbat = __builtin_amdgcn_readfirstlane((Lc + 7) >> 3);  // 1..4
+    const float* sv = stage + kl;
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int bt = 0; bt < kPairKeys / 8; ++bt) {
+      float v0[8], v1[8];
+      float4 pp[2];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v0[i] = sv[(bt * 8 + i) * kKRow];
+        v1[i] = sv[(bt * 8 + i) * kKRow + 32];
+      }
+      pp[0] = *(const float4*)(sPh + bt * 8);
+      pp[1] = *(const float4*)(sPh + bt * 8 + 4);
+      const float pk[8] = {pp[0].x, pp[0].y, pp[0].z, pp[0].w, pp[1].x, pp[1].y, pp[1].z, pp[1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        o0 = o0 + v0[i] * pk[i];
+        o1 = o1 + v1[i] * pk[i];
+      }
+      if (bt + 1 >= nbat) break;
+    }
+    const int64_t orow = key0 + qi;
+    const bool d1 = kl + 32 < DH;  // kl < DH always (DH >= 48)
+    a.out[orow * a.ldo + h * DH + kl] = o0;
+    if (d1) a.out[orow * a.ldo + h * DH + kl + 32] = o1;
+    if (a.qout) {
+      a.qout[orow * a.ldqout + h * DH + kl] = (int8_t)quantize_one(o0, a.qmult);
+      if (d1) a.qout[orow * a.ldqout + h * DH + kl + 32] = (int8_t)quantize_one(o1, a.qmult);
+      if (kl == 0 && h == 0) a.qa[orow] = a.qmult;
+    }
+    const bool bad = !isfinite(o0) || (d1 && !isfinite(o1));
+    if (__any(bad) && lane == 0 && a.err) *a.err = 1;
+    return;
+  }
+
+  const int nq = min(kTileQ, L - q0);
   float4 pre = ld(a.k, 0);
   const bool live = w < nq;
   const int row = (int)key0 + q0 + w;
   const float* sQ = sQall + w * kHeadDim;
   if (live && lane < DH) sQall[w * kHeadDim + lane] = Io<T>::at(a.q, (int64_t)row * a.ldq + h * DH + lane);
-  float* srow = stage + (tid >> 4) * kKRow + (tid & 15) * 4;
 
   // Scores: lane = key of the chunk, DH-term dot in dimension order.
-  const float scale = 1.0f / sqrtf((float)DH);
   float sc[kTileMaxKeys / 64];
 #pragma unroll
   for (int c = 0; c < kTileMaxKeys / 64; ++c) {

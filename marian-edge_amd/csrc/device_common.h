@@ -112,6 +112,16 @@ __device__ __forceinline__ float wave_max(float p) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Maximum over each 32-lane half of the wave (every lane returns its half's):
+// the row maxima by DPP, then rows 0-1 and 2-3 paired by a lane swap.
+__device__ __forceinline__ float half_wave_max(float p) {
+  p = fmaxf(p, __int_as_float(dpp_mov<0xB1>(__float_as_int(p))));   // quad_perm [1,0,3,2]
+  p = fmaxf(p, __int_as_float(dpp_mov<0x4E>(__float_as_int(p))));   // quad_perm [2,3,0,1]
+  p = fmaxf(p, __int_as_float(dpp_mov<0x124>(__float_as_int(p))));  // row_ror:4
+  p = fmaxf(p, __int_as_float(dpp_mov<0x128>(__float_as_int(p))));  // row_ror:8
+  return fmaxf(p, xor_lane_f<16>(p));
+}
+
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 template <int CTRL>
