@@ -73,6 +73,24 @@ __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
   _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_)                                            \
       *(float4*)((TILE) + (((LANE) >> 4) + 4 * i_) * kKRow + ((LANE)&15) * 4) = IN[i_];
 
+// The decode key range of row r (read before the device row count; rows past
+// it read clamped stale ranges and are discarded): its first cached row and
+// its count (cross-attention: the row's own count; self-attention: step + 1).
+// Both values are requested together and taken by one empty asm, so neither
+// load waits behind the other; the count is read from a valid address in
+// either mode.
+__device__ __forceinline__ void decode_key_range(const AttnArgs& a, int r, int64_t& key0, int& nk) {
+  const int* nkp = a.row_nk ? a.row_nk + r : &kNoRowCount;
+  int64_t k0 = a.row_key0[r];
+  int nkv = *nkp;
+  asm("" : "+v"(k0), "+v"(nkv));
+  nkv = __builtin_amdgcn_readfirstlane(nkv);  // uniform again
+  k0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(k0 >> 32)) << 32) |
+                 (uint32_t)__builtin_amdgcn_readfirstlane((int)k0));
+  nk = max(a.mode == ATT_CROSS ? nkv : a.step + 1, 1);
+  key0 = min(max(k0, (int64_t)0), a.max_row - 1);
+}
+
 // PRE (two chunks only): all four K/V chunks are requested up front, so a
 // decode row waits for one memory round trip after its key range is known.
 template <int CH, typename T, bool PRE, int DH>
@@ -93,11 +111,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
     key0 = a.cu[sq];
     nk = (int)(a.cu[sq + 1] - a.cu[sq]);
   } else {
-    // Speculative: read this row's key range before the device row count.
-    key0 = a.row_key0[r];
-    nk = a.mode == ATT_CROSS ? a.row_nk[r] : a.step + 1;
-    nk = max(nk, 1);
-    key0 = min(max(key0, (int64_t)0), a.max_row - 1);
+    decode_key_range(a, r, key0, nk);
   }
   // A key range longer than this variant holds would overrun the score
   // registers: attend over the first CH*64 keys (flagged below for live rows).
@@ -604,12 +618,9 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
   const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
   const uint64_t tab_v = kExp2Tab[lane & 31];
 
-  // This row's key range, read before the device row count (rows past it
-  // read clamped stale ranges and are discarded below).
-  int64_t key0 = a.row_key0[r];
-  int nk = a.mode == ATT_CROSS ? a.row_nk[r] : a.step + 1;
-  nk = max(nk, 1);
-  key0 = min(max(key0, (int64_t)0), a.max_row - 1);
+  int64_t key0;
+  int nk;
+  decode_key_range(a, r, key0, nk);
   const bool too_long = nk > 64 * nw;
   if (too_long) nk = 64 * nw;
   const int nk_ld = (int)min((int64_t)nk, a.max_row - key0);  // readable rows
