@@ -398,6 +398,11 @@ __global__ __launch_bounds__(W * 64) void k_finalize_wave(FinalizeArgs f) {
 // End of a decode step: reduce each active row's argmax partials to a token,
 // append it, apply the stop rules of q8_engine.rs:383-390, 444-448, and
 // compact the active list in order.  One workgroup; rows <= kMaxRowsPerCall.
+// WIDE: more than 256 partials per row (vocabularies above 32768 ids), the
+// ones past 256 reduced by a loop after the registers' (a loop with loads
+// would make every wait before it drain all loads in flight).
+constexpr int kFinalizeKP = 4;  // partials per row and lane held in registers
+template <bool WIDE>
 __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
   __shared__ int s_slot[kMaxRowsPerCall];
   __shared__ int s_tok[kMaxRowsPerCall];
@@ -409,64 +414,78 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
   __shared__ int s_wsum[16];
   __shared__ int s_total;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // Rows below the host bound are allocated, so their partials and state are
-  // loaded together with the device row count (one memory round trip); rows
-  // at or past the count are dropped afterwards.
+  // Wave w takes rows 4w..4w+3 of each 64-row pass; lane i < 4 owns row
+  // r0 + i.  Rows below the host bound are allocated, so the passes run as a
+  // two-deep pipeline: the next pass's partials and row state are requested
+  // (from clamped, always valid rows) before this pass is reduced, and no
+  // global store is issued before the last load (a store counts among the
+  // memory operations a load's wait covers): the tokens, counts and the
+  // compacted list are written in the second phase, from LDS.
   const int ub = min(f.rows_ub, kMaxRowsPerCall);
   const int np = f.nparts;
-  // The device row count is first needed after the partials are requested;
-  // the stores that report it come last (a store before the loads would make
-  // every load wait for its completion).
-  int n = 0;
-  // Wave w takes rows 4w..4w+3 of each 64-row pass; lane i < 4 owns row r0 + i.
-  for (int r0 = 4 * wave; r0 < ub; r0 += 64) {
+  constexpr int KP = kFinalizeKP;
+  struct Pass {
+    uint64_t v[4][KP];
+    int slot, srcn;
+    int64_t kv0, src0;
+    uint32_t lim;
+  };
+  auto load_pass = [&](int r0, Pass& P) {
     const int rl = min(r0 + (lane & 3), ub - 1);
-    int slot = 0, srcn = 0;
-    int64_t kv0 = 0, src0 = 0;
-    uint32_t lim = 0;
-    if (lane < 4) {
-      slot = f.rows.slot[rl];
-      kv0 = f.rows.kv0[rl];
-      src0 = f.rows.src0[rl];
-      srcn = f.rows.srcn[rl];
-      lim = f.rows.limit[rl];
+    P.slot = f.rows.slot[rl];
+    P.kv0 = f.rows.kv0[rl];
+    P.src0 = f.rows.src0[rl];
+    P.srcn = f.rows.srcn[rl];
+    P.lim = f.rows.limit[rl];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint64_t* pr = f.partials + (int64_t)min(r0 + i, ub - 1) * np;
+#pragma unroll
+      for (int k = 0; k < KP; ++k) P.v[i][k] = pr[min(lane + 64 * k, np - 1)];  // repeats leave the max
     }
-    const uint64_t* p0 = f.partials + (int64_t)r0 * np;
-    const uint64_t* p1 = f.partials + (int64_t)min(r0 + 1, ub - 1) * np;
-    const uint64_t* p2 = f.partials + (int64_t)min(r0 + 2, ub - 1) * np;
-    const uint64_t* p3 = f.partials + (int64_t)min(r0 + 3, ub - 1) * np;
-    uint64_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-#pragma unroll 4
-    for (int p = lane; p < np; p += 64) {
-      b0 = umax64(b0, p0[p]);
-      b1 = umax64(b1, p1[p]);
-      b2 = umax64(b2, p2[p]);
-      b3 = umax64(b3, p3[p]);
+  };
+  auto finish_pass = [&](int r0, const Pass& P, int n) {
+    uint64_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      b[i] = P.v[i][0];
+#pragma unroll
+      for (int k = 1; k < KP; ++k) b[i] = umax64(b[i], P.v[i][k]);
+      if constexpr (WIDE) {
+        const uint64_t* pr = f.partials + (int64_t)min(r0 + i, ub - 1) * np;
+        for (int q = lane + 64 * KP; q < np; q += 64) b[i] = umax64(b[i], pr[q]);
+      }
+      b[i] = wave_max_u64(b[i]);
     }
-    b0 = wave_max_u64(b0);
-    b1 = wave_max_u64(b1);
-    b2 = wave_max_u64(b2);
-    b3 = wave_max_u64(b3);
-    const uint64_t best = lane == 0 ? b0 : lane == 1 ? b1 : lane == 2 ? b2 : b3;
-    n = min(*f.n_active, ub);
+    const uint64_t best = lane == 0 ? b[0] : lane == 1 ? b[1] : lane == 2 ? b[2] : b[3];
     const int r = r0 + lane;
     if (lane < 4 && r < n) {
       const int32_t tok = argmax_key_id(best);
-      f.out_tok[kv0 + f.step] = tok;
-      f.count[slot] = (uint32_t)f.step + 1u;
-      const bool fin = (tok == 0 && !(f.flags & 1u)) || (uint32_t)f.step + 1u >= lim;
-      s_slot[r] = slot;
+      const bool fin = (tok == 0 && !(f.flags & 1u)) || (uint32_t)f.step + 1u >= P.lim;
+      s_slot[r] = P.slot;
       s_tok[r] = tok;
-      s_kv0[r] = kv0;
-      s_src0[r] = src0;
-      s_srcn[r] = srcn;
-      s_lim[r] = lim;
+      s_kv0[r] = P.kv0;
+      s_src0[r] = P.src0;
+      s_srcn[r] = P.srcn;
+      s_lim[r] = P.lim;
       s_keep[r] = fin ? 0 : 1;
     }
+  };
+  const int n_dev = *f.n_active;  // a scalar load: its wait covers no vector load
+  int n = min(n_dev, ub);
+  Pass pa, pb;
+  int r0 = 4 * __builtin_amdgcn_readfirstlane(wave);  // uniform loop: no exec-masked waits
+  load_pass(r0, pa);
+  for (; r0 < ub; r0 += 128) {
+    load_pass(r0 + 64, pb);
+    __builtin_amdgcn_sched_barrier(0);  // the next pass's loads go out before this pass is reduced
+    finish_pass(r0, pa, n);
+    if (r0 + 64 >= ub) break;
+    load_pass(r0 + 128, pa);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_pass(r0 + 64, pb, n);
   }
   __syncthreads();
-  const int n_dev = *f.n_active;
-  n = min(n_dev, ub);
   int cnt = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -495,6 +514,10 @@ __global__ __launch_bounds__(1024) void k_finalize(FinalizeArgs f) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * tid + i;
+    if (r < n) {
+      f.out_tok[s_kv0[r] + f.step] = s_tok[r];
+      f.count[s_slot[r]] = (uint32_t)f.step + 1u;
+    }
     if (r < n && s_keep[r]) {
       f.rows.slot[pos] = s_slot[r];
       f.rows.kv0[pos] = s_kv0[r];
@@ -652,8 +675,10 @@ hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
     hipLaunchKernelGGL((k_finalize_wave<4, 8>), dim3(1), dim3(256), 0, s, f);
   else if (f.rows_ub <= kFinalizeWaveRows)
     hipLaunchKernelGGL((k_finalize_wave<8, 8>), dim3(1), dim3(512), 0, s, f);
+  else if (f.nparts > 64 * kFinalizeKP)
+    hipLaunchKernelGGL(k_finalize<true>, dim3(1), dim3(1024), 0, s, f);
   else
-    hipLaunchKernelGGL(k_finalize, dim3(1), dim3(1024), 0, s, f);
+    hipLaunchKernelGGL(k_finalize<false>, dim3(1), dim3(1024), 0, s, f);
   return hipGetLastError();
 }
 
