@@ -79,7 +79,8 @@ constexpr int kAfRows = 16;  // fp32 A source: one MFMA row tile per workgroup
 // rows quantized while loading, with the row maxima of the producer in eight
 // parts (A_F32) or in another number of parts (A_F32_P), or found here over
 // all of K (A_F32_MAX).  A_I8_RG: int8 rows in 16-row groups over
-// blockIdx.y, as the fp32 sources are (plain stores only).
+// blockIdx.y, as the fp32 sources are (plain stores or the QKV cache; no
+// int32 or quantized copies).
 enum ASrc { A_I8 = 0, A_F32 = 1, A_F32_MAX = 2, A_I8_RG = 3, A_F32_P = 4 };
 
 // FULL: K is exactly NW x KSW k-steps (every shape the engine uses), so no
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
   for (int k = 0; k < ROWS_PER_THREAD; ++k) {
     const int m = min(tid / COLS + k * (NT / COLS), Mh - 1);
     if constexpr (!AX) am[k] = AF ? af_row_mult<A8>(Aamax, m, g.amax_parts) : ai[m];
-    if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
+    if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[r0 + m] + e.step;
   }
   int Md;  // the device row count, read after the activation loads are issued
 
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(GemmArgs g, Epilogue e)
       for (int k = 0; k < ROWS_PER_THREAD; ++k) {
         const int m = min(m0 + tid / COLS + k * (NT / COLS), M - 1);
         am[k] = ai[m];
-        if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[m] + e.step;
+        if constexpr (MODE == EPI_QKV_CACHE) crow[k] = e.row_kv0[r0 + m] + e.step;
       }
     }
     for (int i = tid; i < kSkinnyRows * LDC; i += NT) sAcc[i] = 0;
@@ -947,8 +948,15 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
     return g.amax_parts == kAfParts ? launch_skinny_k<MODE, 8, 1, A_F32>(g, e, s)
                                     : launch_skinny_k<MODE, 8, 1, A_F32_P>(g, e, s);
   }
-  if (ksteps <= 4) return launch_skinny_k<MODE, 4, 1, A_I8>(g, e, s);
-  if (ksteps <= 8) return launch_skinny_k<MODE, 4, 2, A_I8>(g, e, s);
+  // Above 64 rows, K <= 512 takes one 16-row group per workgroup (the groups
+  // run side by side instead of one workgroup walking 64-row chunks, each
+  // waiting for its own activation loads); the QKV cache epilogue indexes its
+  // cache rows by the group's absolute rows.
+  const bool rg8 = !e.out_i32 && !e.out_q && g.M > kSkinnyRows && g.M <= 65535 * kAfRows;
+  if (ksteps <= 4)
+    return rg8 ? launch_skinny_k<MODE, 4, 1, A_I8_RG>(g, e, s) : launch_skinny_k<MODE, 4, 1, A_I8>(g, e, s);
+  if (ksteps <= 8)
+    return rg8 ? launch_skinny_k<MODE, 4, 2, A_I8_RG>(g, e, s) : launch_skinny_k<MODE, 4, 2, A_I8>(g, e, s);
   if (ksteps <= 16) return launch_skinny_k<MODE, 4, 4, A_I8>(g, e, s);
   // K = 1536 (the FFN down-projection of a 1536-wide FFN): 16 waves of two
   // k-steps beat 8 of four (measured); K = 2048 the other way round.  Above
