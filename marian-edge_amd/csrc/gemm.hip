@@ -441,16 +441,6 @@ __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs
 
   for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
-    if (m0 > 0) {
-#pragma unroll
-      for (int j = 0; j < kStage; ++j) {
-        const int c = tid + kVocabThreads * j, row = c >> 5, cc = c & 31;
-        st[j] = (row < rows && cc < cpr)
-                    ? *(const v4i*)(g.A + (int64_t)(m0 + row) * g.lda + cc * 16)
-                    : zero4();
-      }
-      sa = tid < rows ? g.a[m0 + tid] : 0.0f;
-    }
     if constexpr (!LNP) {
 #pragma unroll
       for (int j = 0; j < kStage; ++j) {
@@ -458,6 +448,17 @@ __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs
         *(v4i*)(sA + (c >> 5) * kVocabLds + (c & 31) * 16) = st[j];
       }
       if (tid < kSkinnyRows) sAm[tid] = sa;
+      // The next chunk's rows are requested now, from clamped (allocated)
+      // rows with the pieces past the chunk masked, so they arrive while this
+      // chunk is multiplied instead of after it.
+      const int m1 = m0 + kSkinnyRows, rows1 = M - m1;
+#pragma unroll
+      for (int j = 0; j < kStage; ++j) {
+        const int c = tid + kVocabThreads * j, row = c >> 5, cc = c & 31;
+        st[j] = keep_or_zero(*(const v4i*)(g.A + (int64_t)min(m1 + row, M - 1) * g.lda + min(cc, cpr - 1) * 16),
+                             row < rows1 && cc < cpr);
+      }
+      sa = g.a[min(m1 + tid, M - 1)];  // read only for rows of the chunk
     }
     __syncthreads();
     const int mt_n = (rows + 15) >> 4;
