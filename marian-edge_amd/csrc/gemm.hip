@@ -949,11 +949,11 @@ static hipError_t launch_skinny_mode(const GemmArgs& g, const Epilogue& e, hipSt
     return g.amax_parts == kAfParts ? launch_skinny_k<MODE, 8, 1, A_F32>(g, e, s)
                                     : launch_skinny_k<MODE, 8, 1, A_F32_P>(g, e, s);
   }
-  // Above 64 rows, K <= 512 takes one 16-row group per workgroup (the groups
-  // run side by side instead of one workgroup walking 64-row chunks, each
-  // waiting for its own activation loads); the QKV cache epilogue indexes its
-  // cache rows by the group's absolute rows.
-  const bool rg8 = !e.out_i32 && !e.out_q && g.M > kSkinnyRows && g.M <= 65535 * kAfRows;
+  // Above 16 rows, K <= 512 takes one 16-row group per workgroup (the groups
+  // run side by side instead of one workgroup walking its rows in 64-row
+  // chunks, each waiting for its own activation loads); the QKV cache
+  // epilogue indexes its cache rows by the group's absolute rows.
+  const bool rg8 = !e.out_i32 && !e.out_q && g.M > kAfRows && g.M <= 65535 * kAfRows;
   if (ksteps <= 4)
     return rg8 ? launch_skinny_k<MODE, 4, 1, A_I8_RG>(g, e, s) : launch_skinny_k<MODE, 4, 1, A_I8>(g, e, s);
   if (ksteps <= 8)
