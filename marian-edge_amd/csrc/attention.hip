@@ -773,8 +773,12 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s, hipEvent_t ev_star
   // Decode launches cover few rows: one round trip per row matters more
   // than occupancy.  Encoder launches keep the lighter register budget.
   hipEvent_t e0 = ev_start, e1 = ev_stop;
+  // Up to 128 keys: with at most kLongMaxPairs (row, head) pairs, every chunk
+  // requested up front (one round trip, one wave per SIMD); with more, the
+  // one-chunk-ahead variant, whose two waves per SIMD keep more pairs going.
   if (a.max_keys <= 128)
-    return a.mode == ATT_SEQ ? launch_ch<2>(a, s, e0, e1) : launch_ch<2, true>(a, s, e0, e1);
+    return a.mode == ATT_SEQ || a.rows * a.heads > kLongMaxPairs ? launch_ch<2>(a, s, e0, e1)
+                                                                 : launch_ch<2, true>(a, s, e0, e1);
   if (a.max_keys <= kLongMaxKeys && a.mode != ATT_SEQ && !a.bf16 && !a.qout &&
       a.rows * a.heads <= kLongMaxPairs) {
     const dim3 grid(a.rows * a.heads), block(64 * ((a.max_keys + 63) / 64));

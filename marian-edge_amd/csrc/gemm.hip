@@ -402,21 +402,25 @@ __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs
   // requested at once.
   // The first chunk is requested for the rows below the host bound g.M (all
   // allocated) before the device row count arrives.
+  // Above 64 rows each 64-row group is a row of workgroups (blockIdx.y), so
+  // the groups run side by side; every group reads the weights again (from
+  // the caches: the vocabulary is 16 MB).
   constexpr int kStage = kSkinnyRows * (kVocabMaxK / 16) / kVocabThreads;
+  const int r0 = (int)blockIdx.y * kSkinnyRows;  // this workgroup's first row
   const int cpr = g.K >> 4;
   v4i st[kStage];
   float sa = 0.0f;
-  const int rows_h = min(kSkinnyRows, g.M);
+  const int rows_h = min(kSkinnyRows, g.M - r0);
   if constexpr (!LNP) {
 #pragma unroll
     for (int j = 0; j < kStage; ++j) {
       const int c = tid + kVocabThreads * j, row = c >> 5, cc = c & 31;
-      st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)row * g.lda + cc * 16)
+      st[j] = (row < rows_h && cc < cpr) ? *(const v4i*)(g.A + (int64_t)(r0 + row) * g.lda + cc * 16)
                                          : zero4();
     }
-    if (tid < rows_h) sa = g.a[tid];
+    if (tid < rows_h) sa = g.a[r0 + tid];
   }
-  const int M = g.M_dev ? min(*g.M_dev, g.M) : g.M;
+  const int M = min(g.M_dev ? min(*g.M_dev, g.M) : g.M, r0 + kSkinnyRows);  // rows below this group's end
   if constexpr (LNP) {
     // normalize_row (tensor.rs:372-385), one wave per row.
     if (wave < g.M) {
@@ -439,7 +443,7 @@ __global__ __launch_bounds__(64 * kVocabWaves<LNP>) void k_vocab_argmax(GemmArgs
     }
   }
 
-  for (int m0 = 0; m0 < M; m0 += kSkinnyRows) {
+  for (int m0 = r0; m0 < M; m0 += kSkinnyRows) {
     const int rows = min(kSkinnyRows, M - m0);
     if constexpr (!LNP) {
 #pragma unroll
@@ -987,7 +991,8 @@ hipError_t launch_vocab_argmax(const GemmArgs& g, const Epilogue& e, hipStream_t
                                hipEvent_t ev_start, hipEvent_t ev_stop) {
   if (g.K <= 0 || g.K % 64 || g.K > kVocabMaxK || g.N <= 0) return hipErrorInvalidValue;
   const RowPrologue& p = g.pro;
-  const dim3 grid((g.N + kVocabCols - 1) / kVocabCols),
+  const dim3 grid((g.N + kVocabCols - 1) / kVocabCols,
+                  p.kind == PRO_LN ? 1 : max(1, (g.M + kSkinnyRows - 1) / kSkinnyRows)),
       block(64 * (p.kind == PRO_LN ? kVocabWaves<true> : kVocabWaves<false>));
   if (p.kind != PRO_NONE &&
       (p.kind != PRO_LN || g.K != kVocabMaxK || g.M > kVocabLnMaxRows || !p.y || !p.r || !p.gamma || !p.beta))
