@@ -357,10 +357,12 @@ def test_attention_edges(pkg, orc, dev):
     _attention_case(pkg, orc, dev, q, k, v, cu, 8, False)
 
 
-def test_vocab_argmax_matches_oracle(pkg, orc, dev, full_model):
+@pytest.mark.parametrize("M", [1, 64, 130])
+def test_vocab_argmax_matches_oracle(pkg, orc, dev, full_model, M):
+    """Up to 64 rows one row group; 130 rows run three 64-row groups side
+    by side, the last one holding two rows."""
     m = full_model
-    rng = np.random.default_rng(15)
-    M = 64
+    rng = np.random.default_rng(15 + M)
     x = rng.standard_normal((M, 512)).astype(np.float32)
     q_ref, a_ref = orc.quantize_rows(x)
     logits_ref, _, _, _ = orc.linear_forward(x, m.embedding, m.embedding_mult, m.output_bias)
