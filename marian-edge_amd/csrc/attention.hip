@@ -61,14 +61,39 @@ __device__ __forceinline__ float4 load_row4(const void* p, int64_t off) {
   }
 }
 
-// Lane l loads dims 4*(l%16)..+3 of keys first + l/16 + 4i (i < 16), both
-// clamped (with head_dim 48 the lanes past dim 47 reload dims 44-47 into tile
-// columns that are never read).
-#define MH_LOAD_CHUNK(T, P, BASE, LD, FIRST, NK, LANE, OUT)                                   \
-  _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_) {                                         \
-    const int key_ = min((FIRST) + ((LANE) >> 4) + 4 * i_, (NK)-1);                           \
-    OUT[i_] = load_row4<T>((P), (BASE) + (int64_t)key_ * (LD) + min(((LANE)&15) * 4, DH - 4)); \
+// One head's K or V rows of a row (or sequence) as a raw buffer resource
+// whose range ends where key nk_ld would start: a raw buffer load whose
+// offset lies at or past the range's end returns zeros (the hardware range
+// check on the VGPR offset), so a chunk's loads need no clamped addresses,
+// only one 32-bit byte offset each (a lane part plus a uniform part).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kRawBufferWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rows(const void* p, int64_t elem0, int64_t ld, int nk_ld) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)((const T*)p + elem0), (short)0,
+                                           (int)((int64_t)nk_ld * ld * (int64_t)sizeof(T)), kRawBufferWord3);
+}
+
+template <typename T>
+__device__ __forceinline__ float4 load_rows4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
+  } else {
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u));
   }
+}
+
+// Lane l loads dims 4*(l%16)..+3 of keys first + l/16 + 4i (i < 16): VOFF is
+// the lane's byte offset of key l/16, LDB the bytes per key row.  Keys past
+// the resource's range read as zeros (with head_dim 48 the lanes past dim 47
+// reload dims 44-47 into tile columns that are never read).
+#define MH_LOAD_CHUNK(T, R, VOFF, LDB, FIRST, OUT) \
+  _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_) OUT[i_] = load_rows4<T>((R), (VOFF) + (uint32_t)((FIRST) + 4 * i_) * (LDB));
 #define MH_STORE_CHUNK(TILE, LANE, IN)                                                         \
   _Pragma("unroll") for (int i_ = 0; i_ < 16; ++i_)                                            \
       *(float4*)((TILE) + (((LANE) >> 4) + 4 * i_) * kKRow + ((LANE)&15) * 4) = IN[i_];
@@ -97,8 +122,9 @@ template <int CH, typename T, bool PRE, int DH>
 __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   static_assert(DH == 64 || DH == 48, "head widths");
   static_assert(!PRE || CH == 2, "up-front loads hold two chunks");
-  static_assert(CH * 64 <= 64 * kKRow, "the tile holds every probability of a row");
-  __shared__ __attribute__((aligned(16))) float tile[64 * kKRow];
+  __shared__ __attribute__((aligned(16))) float tile[64 * kKRow];  // one K or V chunk
+  __shared__ __attribute__((aligned(16))) float sP[CH * 64];        // exponentials, then probabilities
+  __shared__ __attribute__((aligned(16))) float sQ[64];             // the query, read as broadcasts
   __shared__ uint64_t sTab[32];
   const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
   const int lane = threadIdx.x;
@@ -122,6 +148,10 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 
   // Keys of a stale row may run past the buffer: its last readable key.
   const int nk_ld = a.mode == ATT_SEQ ? nk : (int)min((int64_t)nk, a.max_row - key0);
+  const __amdgpu_buffer_rsrc_t rk = head_rows<T>(a.k, kbase, a.ldkv, nk_ld);
+  const __amdgpu_buffer_rsrc_t rv = head_rows<T>(a.v, kbase, a.ldkv, nk_ld);
+  const uint32_t ldb = (uint32_t)a.ldkv * (uint32_t)sizeof(T);
+  const uint32_t voff = (uint32_t)(lane >> 4) * ldb + (uint32_t)min((lane & 15) * 4, DH - 4) * (uint32_t)sizeof(T);
 
   // q of this head, one element per lane (broadcast 16 values at a time),
   // requested first and waited for before the chunk loop (below): a wait
@@ -130,18 +160,19 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   const int qv = __float_as_int(Io<T>::at(a.q, (int64_t)r * a.ldq + h * DH + min(lane, DH - 1)));
   // Chunk 0's V rows are loaded now (used after the softmax), then K.
   float4 vreg[16], kreg[16], kreg1[PRE ? 16 : 1], vreg1[PRE ? 16 : 1];
-  MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 0, nk_ld, lane, vreg)
-  MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, 0, nk_ld, lane, kreg)
+  MH_LOAD_CHUNK(T, rv, voff, ldb, 0, vreg)
+  MH_LOAD_CHUNK(T, rk, voff, ldb, 0, kreg)
   if constexpr (PRE) {
     if (nch > 1) {
-      MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, 64, nk_ld, lane, kreg1)
-      MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 64, nk_ld, lane, vreg1)
+      MH_LOAD_CHUNK(T, rk, voff, ldb, 64, kreg1)
+      MH_LOAD_CHUNK(T, rv, voff, ldb, 64, vreg1)
     }
   }
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
   if (r >= n) return;
   if (too_long && threadIdx.x == 0 && a.err) *a.err = 2;
   asm volatile("" ::"v"(qv));  // q has arrived (the K/V loads stay in flight)
+  sQ[lane] = __int_as_float(qv);  // published by the first barrier below
 
   // Scores: lane = key within the chunk, DH-term dot in dimension order.  The
   // next chunk's K rows are loaded while this chunk's dot runs.
@@ -162,7 +193,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
       } else {
         MH_STORE_CHUNK(tile, lane, kreg)
         if (c + 1 < nch) {
-          MH_LOAD_CHUNK(T, a.k, kbase, a.ldkv, (c + 1) * 64, nk_ld, lane, kreg)
+          MH_LOAD_CHUNK(T, rk, voff, ldb, (c + 1) * 64, kreg)
         }
       }
       __syncthreads();
@@ -173,14 +204,16 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; i += 4) {
           const float4 v = *(const float4*)(tile + lane * kKRow + i0 + i);
+          const float4 q4 = *(const float4*)(sQ + i0 + i);
           kr[i] = v.x;
           kr[i + 1] = v.y;
           kr[i + 2] = v.z;
           kr[i + 3] = v.w;
+          qs[i] = q4.x;
+          qs[i + 1] = q4.y;
+          qs[i + 2] = q4.z;
+          qs[i + 3] = q4.w;
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          qs[i] = __int_as_float(__builtin_amdgcn_readlane(qv, i0 + i));
 #pragma unroll
         for (int i = 0; i < 16; ++i) dot = dot + qs[i] * kr[i];
       }
@@ -190,7 +223,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   // V rows of chunk 1 go into the now free K registers (chunk c uses vreg
   // for even c, kreg for odd c).
   if (!PRE && nch > 1) {
-    MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, 64, nk_ld, lane, kreg)
+    MH_LOAD_CHUNK(T, rv, voff, ldb, 64, kreg)
   }
   float mloc = -INFINITY;
 #pragma unroll
@@ -199,8 +232,8 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
 #pragma unroll
   for (int c = 0; c < CH; ++c)
     s[c] = (c < nch && c * 64 + lane < nk) ? ref_expf(s[c] - mx, sTab) : 0.0f;
-  // Denominator in key order from 0.0 (softmax_in_place): the probabilities
-  // pass through the tile and every lane folds them sequentially.  Keys past
+  // Denominator in key order from 0.0 (softmax_in_place): the exponentials
+  // pass through LDS and every lane folds them sequentially.  Keys past
   // the last hold +0.0, which leaves the (non-negative) sum unchanged.
   // With a.fast (decode only) the denominator takes the fast-reduction tree
   // order instead: lane l's keys l, 64 + l, ... in order from 0.0, then the
@@ -212,17 +245,16 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
       if (c < nch) sum = sum + s[c];
     sum = tree_combine_wave(sum);
   } else {
-    __syncthreads();  // the last K chunk has been read
 #pragma unroll
     for (int c = 0; c < CH; ++c)
-      if (c < nch) tile[c * 64 + lane] = s[c];
+      if (c < nch) sP[c * 64 + lane] = s[c];
     __syncthreads();
     if constexpr (CH <= 8) {
-      sum = seq_fold_lds_upto<CH * 4>((const float4*)tile, nch * 4, 0.0f);
+      sum = seq_fold_lds_upto<CH * 4>((const float4*)sP, nch * 4, 0.0f);
     } else {  // long ranges: a rolled loop keeps the code small
 #pragma unroll 4
       for (int j = 0; j < nch * 64; j += 4) {
-        const float4 v = *(const float4*)(tile + j);
+        const float4 v = *(const float4*)(sP + j);
         sum = sum + v.x;
         sum = sum + v.y;
         sum = sum + v.z;
@@ -231,12 +263,16 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
     }
   }
   const float inv = 1.0f / sum;
+  // The probabilities replace the exponentials in LDS (this wave's fold
+  // reads were issued before these writes and LDS keeps a wave's order).
 #pragma unroll
-  for (int c = 0; c < CH; ++c) s[c] = s[c] * inv;
+  for (int c = 0; c < CH; ++c)
+    if (c < nch) sP[c * 64 + lane] = s[c] * inv;
 
-  // out_d = sum_j v[j][d] * p_j in key order; p_j is broadcast from lane
-  // j%64 of chunk j/64 through an SGPR; keys past the last have p = 0, and
-  // adding v * 0 = +-0 leaves the sum bit-identical to skipping them.
+  // out_d = sum_j v[j][d] * p_j in key order; p_j is read from LDS as a
+  // broadcast, four keys at a time; keys past the last have p = 0 and zero
+  // values (or stale ones: p * v = +-0), and adding +-0 to a sum that
+  // started from +0.0 leaves it bit-identical to skipping them.
   float o = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -251,19 +287,23 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
       } else if (c & 1) {
         MH_STORE_CHUNK(tile, lane, kreg)
         if (c + 2 < nch) {
-          MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, (c + 2) * 64, nk_ld, lane, kreg)
+          MH_LOAD_CHUNK(T, rv, voff, ldb, (c + 2) * 64, kreg)
         }
       } else {
         MH_STORE_CHUNK(tile, lane, vreg)
         if (c + 2 < nch) {
-          MH_LOAD_CHUNK(T, a.v, kbase, a.ldkv, (c + 2) * 64, nk_ld, lane, vreg)
+          MH_LOAD_CHUNK(T, rv, voff, ldb, (c + 2) * 64, vreg)
         }
       }
       __syncthreads();
-      const int pc = __float_as_int(s[c]);
 #pragma unroll
-      for (int u = 0; u < 64; ++u)
-        o = o + tile[u * kKRow + lane] * __int_as_float(__builtin_amdgcn_readlane(pc, u));
+      for (int u = 0; u < 64; u += 4) {
+        const float4 p4 = *(const float4*)(sP + c * 64 + u);
+        o = o + tile[u * kKRow + lane] * p4.x;
+        o = o + tile[(u + 1) * kKRow + lane] * p4.y;
+        o = o + tile[(u + 2) * kKRow + lane] * p4.z;
+        o = o + tile[(u + 3) * kKRow + lane] * p4.w;
+      }
     }
   }
 
@@ -595,8 +635,9 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
 //     products (lane = dimension, p broadcast from the score lanes), then the
 //     running sums pass from wave to wave in key order through LDS, one
 //     barrier per 64-key chunk, each wave adding its 64 products in order.
-// Keys past the row's count have p = 0 (their values reloaded from its last
-// key), so their products are +-0 and leave the sums unchanged.
+// Keys past the row's count have p = 0 (their values read as zeros through
+// the buffer resource's range), so their products are +0 and leave the sums,
+// which start from +0.0 and so are never -0.0, unchanged.
 // The workgroup holds its waves through these dependent phases, so it pays
 // where few (row, head) pairs leave the chip idle; with many, the one-wave
 // kernel keeps more loads in flight per CU (launch_attention chooses).
@@ -613,7 +654,7 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
   __shared__ float sMax[kLongWaves];
   __shared__ float sInv;
   __shared__ uint64_t sTab[32];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int nw = blockDim.x >> 6;  // 3..kLongWaves, set by the launch
   const int h = blockIdx.x % a.heads, r = blockIdx.x / a.heads;  // r < a.rows, the host bound
   const uint64_t tab_v = kExp2Tab[lane & 31];
@@ -635,12 +676,12 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
     const int key = min(kc + lane, nk_ld - 1);
 #pragma unroll
     for (int i = 0; i < DH / 4; ++i) kr[i] = *(const f4v*)((const float*)a.k + kbase + (int64_t)key * a.ldkv + 4 * i);
-    const int d = min(lane, DH - 1);
+    // V: one raw buffer load per key, zeros past the readable keys.
+    const __amdgpu_buffer_rsrc_t rv = head_rows<float>(a.v, kbase, a.ldkv, nk_ld);
+    const uint32_t ldb = (uint32_t)a.ldkv * 4u, voff = (uint32_t)min(lane, DH - 1) * 4u;
 #pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      const int kj = min(kc + j, nk_ld - 1);
-      vv[j] = ((const float*)a.v)[kbase + (int64_t)kj * a.ldkv + d];
-    }
+    for (int j = 0; j < 64; ++j)
+      vv[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, voff + (uint32_t)(kc + j) * ldb, 0, 0));
   }
   const int qv = __float_as_int(((const float*)a.q)[(int64_t)r * a.ldq + h * DH + min(lane, DH - 1)]);
   const int n = a.rows_dev ? *a.rows_dev : a.rows;
