@@ -5,14 +5,14 @@
 // Semantics of attention_into (tensor.rs:251-318): score_k = (q . k_k) * 1/sqrt(dh),
 // softmax as max, exp(s - max), sum, multiply by 1/sum, then
 // out = sum_k p_k v_k in key order.  Mapping onto the wave:
-//   * K and V rows arrive by coalesced 16-byte loads and pass through a
-//     per-head LDS tile;
+//   * K and V rows arrive by coalesced 16-byte raw buffer loads and pass
+//     through a per-head LDS tile;
 //   * scores: lane = key (keys lane, lane+64, ...), sequential 64-term dot
-//     with q broadcast from SGPRs;
+//     with q read from LDS as broadcasts;
 //   * softmax: wave max, the C library's expf (ref_expf.h) per key, then the
 //     denominator summed over the keys in order through LDS;
 //   * PV: lane = output dim, keys accumulated in order (the reference order);
-//     probabilities are broadcast from the score lanes through SGPRs.
+//     probabilities are read from LDS as broadcasts, four keys at a time.
 // The score row never leaves the chip.  Sequences are packed (cu_seqlens), so
 // there is no padding and no mask; keys beyond a row's count are never read.
 // The three modes differ only in where a row's keys live: its own sequence
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
   const uint32_t ldb = (uint32_t)a.ldkv * (uint32_t)sizeof(T);
   const uint32_t voff = (uint32_t)(lane >> 4) * ldb + (uint32_t)min((lane & 15) * 4, DH - 4) * (uint32_t)sizeof(T);
 
-  // q of this head, one element per lane (broadcast 16 values at a time),
+  // q of this head, one element per lane (copied to LDS for broadcasts),
   // requested first and waited for before the chunk loop (below): a wait
   // for it inside the loop, after a chunk's conditional prefetch, would
   // have to drain every load in flight.
@@ -627,12 +627,12 @@ __global__ __launch_bounds__(kTileQ * 64) __attribute__((amdgpu_waves_per_eu(8, 
 // memory round trip instead of one per 64-key chunk.  The arithmetic is
 // k_attention's, in the reference order:
 //   * scores: lane = key, the 64-term dot in dimension order from -0.0, the
-//     query broadcast from its lanes;
+//     query read from the wave's LDS copy as broadcasts;
 //   * max over the workgroup (waves' maxima through LDS), the C library's
 //     expf, the denominator folded in key order from 0.0 by wave 0 over the
 //     exponentials in LDS (with FAST: the tree order, as in k_attention);
 //   * PV: out_d = sum_k p_k v_k[d] in key order.  Each wave forms its keys'
-//     products (lane = dimension, p broadcast from the score lanes), then the
+//     products (lane = dimension, p read back from LDS as broadcasts), then the
 //     running sums pass from wave to wave in key order through LDS, one
 //     barrier per 64-key chunk, each wave adding its 64 products in order.
 // Keys past the row's count have p = 0 (their values read as zeros through
@@ -651,6 +651,7 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
   static_assert(DH == 64 || DH == 48, "head widths");
   __shared__ __attribute__((aligned(16))) float sE[kLongMaxKeys];  // exponentials of the keys
   __shared__ float sO[64];                                          // the PV relay
+  __shared__ __attribute__((aligned(16))) float sQw[kLongWaves][64];  // each wave's copy of the query
   __shared__ float sMax[kLongWaves];
   __shared__ float sInv;
   __shared__ uint64_t sTab[32];
@@ -688,6 +689,8 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
   if (r >= n) return;  // the whole workgroup alike
   if (too_long && tid == 0 && a.err) *a.err = 2;
   if (tid < 32) sTab[tid] = tab_v;
+  float* sQ = sQw[w];
+  sQ[lane] = __int_as_float(qv);  // this wave's own copy: its reads below follow in LDS order
 
   // ---- scores and the row maximum ----
   const float scale = 1.0f / sqrtf((float)DH);
@@ -696,8 +699,13 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
   if (mine) {
     float dot = -0.0f;
 #pragma unroll
-    for (int i = 0; i < DH; ++i)
-      dot = dot + __int_as_float(__builtin_amdgcn_readlane(qv, i)) * kr[i >> 2][i & 3];
+    for (int i = 0; i < DH; i += 4) {  // the query read as LDS broadcasts
+      const float4 q4 = *(const float4*)(sQ + i);
+      dot = dot + q4.x * kr[i >> 2][0];
+      dot = dot + q4.y * kr[i >> 2][1];
+      dot = dot + q4.z * kr[i >> 2][2];
+      dot = dot + q4.w * kr[i >> 2][3];
+    }
     if (valid) sc = dot * scale;
   }
   const float wmax = wave_max(sc);
@@ -728,9 +736,17 @@ __global__ __launch_bounds__(64 * kLongWaves) void k_attn_long(AttnArgs a) {
   // ---- PV: products, then the in-order relay across the waves ----
   float o = 0.0f;
   if (mine) {
-    const int pc = __float_as_int(e * inv);  // p of key kc + lane
+    // p of key kc + lane replaces its exponential (wave 0's fold has read
+    // them all: the barrier above), read back as LDS broadcasts.
+    sE[kc + lane] = e * inv;
 #pragma unroll
-    for (int j = 0; j < 64; ++j) vv[j] = vv[j] * __int_as_float(__builtin_amdgcn_readlane(pc, j));
+    for (int j = 0; j < 64; j += 4) {
+      const float4 p4 = *(const float4*)(sE + kc + j);
+      vv[j] = vv[j] * p4.x;
+      vv[j + 1] = vv[j + 1] * p4.y;
+      vv[j + 2] = vv[j + 2] * p4.z;
+      vv[j + 3] = vv[j + 3] * p4.w;
+    }
   }
   for (int c = 0; c < nch; ++c) {  // nch is uniform over the workgroup
     if (w == c) {
